@@ -1,0 +1,238 @@
+// capi.hip -- extern "C" entry points of libmoss_hip.so (declared in include/moss_hip.h).
+// No exception crosses this boundary: failures become status codes plus a
+// thread-local message (moss_hip_last_error).
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "llm_model.h"
+
+using mh::Status;
+
+struct moss_hip_llm {
+    mh::Model *impl;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F>
+int guard(F &&f) {
+    try {
+        f();
+        return MOSS_HIP_OK;
+    } catch (const Status &s) {
+        g_err = s.what();
+        return s.code;
+    } catch (const std::bad_alloc &) {
+        g_err = "host out of memory";
+        return MOSS_HIP_EDEVICE;
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return MOSS_HIP_EDEVICE;
+    }
+}
+
+mh::Model &model_of(moss_hip_llm *m) {
+    if (m == nullptr || m->impl == nullptr) throw Status(MOSS_HIP_EINVAL, "null model handle");
+    mh::hip_check(hipSetDevice(m->impl->device()), "hipSetDevice");
+    return *m->impl;
+}
+
+moss_hip_llm_options defaults(const moss_hip_llm_options *opt) {
+    moss_hip_llm_options o{0, 0, 0, 1};
+    if (opt) o = *opt;
+    return o;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *moss_hip_last_error(void) { return g_err.c_str(); }
+int moss_hip_abi_version(void) { return MOSS_HIP_ABI_VERSION; }
+
+int moss_hip_llm_create(const void *blob, size_t bytes, const moss_hip_llm_options *opt, moss_hip_llm **out) {
+    return guard([&] {
+        if (out == nullptr || blob == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");
+        *out = nullptr;
+        auto *h = new moss_hip_llm{nullptr};
+        try {
+            h->impl = new mh::Model(blob, bytes, defaults(opt));
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+int moss_hip_llm_create_from_file(const char *path, const moss_hip_llm_options *opt, moss_hip_llm **out) {
+    return guard([&] {
+        if (path == nullptr || out == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");
+        std::FILE *f = std::fopen(path, "rb");
+        if (!f) throw Status(MOSS_HIP_EINVAL, std::string("cannot open weights file: ") + path);
+        std::fseek(f, 0, SEEK_END);
+        const long size = std::ftell(f);
+        std::fseek(f, 0, SEEK_SET);
+        std::vector<uint8_t> data(size > 0 ? (size_t)size : 0);
+        const size_t got = data.empty() ? 0 : std::fread(data.data(), 1, data.size(), f);
+        std::fclose(f);
+        if (size <= 16 || got != data.size()) throw Status(MOSS_HIP_EFORMAT, std::string("short weights file: ") + path);
+        const int rc = moss_hip_llm_create(data.data(), data.size(), opt, out);
+        if (rc != MOSS_HIP_OK) throw Status(rc, g_err);
+    });
+}
+
+void moss_hip_llm_destroy(moss_hip_llm *m) {
+    if (!m) return;
+    delete m->impl;
+    delete m;
+}
+
+int moss_hip_llm_reset(moss_hip_llm *m) {
+    return guard([&] { model_of(m).reset(); });
+}
+
+int moss_hip_llm_position(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->position() : -1; }
+
+int moss_hip_llm_get_hidden(moss_hip_llm *m, float *out) {
+    return guard([&] {
+        if (!out) throw Status(MOSS_HIP_EINVAL, "null output");
+        model_of(m).get_hidden(out);
+    });
+}
+
+int moss_hip_llm_set_hidden(moss_hip_llm *m, const float *in) {
+    return guard([&] {
+        if (!in) throw Status(MOSS_HIP_EINVAL, "null input");
+        model_of(m).set_hidden(in);
+    });
+}
+
+int moss_hip_llm_prefill(moss_hip_llm *m, const int32_t *rows, int n_rows, int start) {
+    return guard([&] {
+        if (n_rows < 0 || (n_rows > 0 && !rows)) throw Status(MOSS_HIP_EINVAL, "bad rows");
+        model_of(m).prefill(rows, n_rows, start);
+    });
+}
+
+int moss_hip_llm_global_step(moss_hip_llm *m, const int32_t *row17) {
+    return guard([&] {
+        if (!row17) throw Status(MOSS_HIP_EINVAL, "null row");
+        model_of(m).global_step(row17);
+    });
+}
+
+int moss_hip_llm_generate(moss_hip_llm *m, int max_frames, const moss_hip_sample_params *p, uint64_t seed,
+                          const int32_t *forced, int n_forced, int32_t *out_rows, int *out_frames, double *timing,
+                          float *logits_dump, float *gate_dump, moss_hip_frame_cb cb, void *user) {
+    return guard([&] {
+        if (!p || !out_rows || max_frames < 0) throw Status(MOSS_HIP_EINVAL, "bad arguments");
+        const int n = model_of(m).generate(max_frames, *p, seed, forced, n_forced, out_rows, timing, logits_dump,
+                                           gate_dump, cb, user);
+        if (out_frames) *out_frames = n;
+    });
+}
+
+int moss_hip_llm_set_cancel_flag(moss_hip_llm *m, const volatile uint8_t *flag) {
+    return guard([&] { model_of(m).set_cancel_flag(flag); });
+}
+
+int moss_hip_llm_snapshot_prefix(moss_hip_llm *m) {
+    return guard([&] { model_of(m).snapshot_prefix(); });
+}
+
+int moss_hip_llm_restore_prefix(moss_hip_llm *m) {
+    return guard([&] { model_of(m).restore_prefix(); });
+}
+
+int moss_hip_llm_prefix_pos(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->prefix_pos() : -1; }
+
+int moss_hip_llm_kv_export(moss_hip_llm *m, int n_pos, float *k, float *v) {
+    return guard([&] {
+        if (n_pos > 0 && (!k || !v)) throw Status(MOSS_HIP_EINVAL, "null buffer");
+        model_of(m).kv_export(n_pos, k, v);
+    });
+}
+
+int moss_hip_llm_kv_import(moss_hip_llm *m, int n_pos, const float *k, const float *v, const float *hidden) {
+    return guard([&] {
+        if (n_pos > 0 && (!k || !v)) throw Status(MOSS_HIP_EINVAL, "null buffer");
+        model_of(m).kv_import(n_pos, k, v, hidden);
+    });
+}
+
+// ------------------------------------------------------------------ operators
+
+int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_dtype, void *y, int y_dtype,
+                       void *stream) {
+    return guard([&] {
+        if (!w || !x || !y) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (rows <= 0 || rows % 4 || cols <= 0 || cols % 128 || cols > 4096)
+            throw Status(MOSS_HIP_EINVAL, "shape must satisfy rows % 4 == 0, cols % 128 == 0, cols <= 4096");
+        if ((x_dtype != MOSS_HIP_F32 && x_dtype != MOSS_HIP_F16) || (y_dtype != MOSS_HIP_F32 && y_dtype != MOSS_HIP_F16))
+            throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
+        mh::GemvArgs a;
+        a.w = static_cast<const uint8_t *>(w);
+        a.rows = rows;
+        a.cols = cols;
+        a.x = x;
+        a.y = y;
+        const auto pro = x_dtype == MOSS_HIP_F16 ? mh::PRO_F16 : mh::PRO_F32;
+        const auto epi = y_dtype == MOSS_HIP_F16 ? mh::EPI_F16 : mh::EPI_F32;
+        mh::hip_check(mh::launch_gemv(a, pro, epi, mh::KV_F16, static_cast<hipStream_t>(stream)), "gemv launch");
+    });
+}
+
+int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int32_t *rows_dev, int n, float *out,
+                               void *stream) {
+    return guard([&] {
+        if (!w || !rows_dev || !out || n < 0) throw Status(MOSS_HIP_EINVAL, "bad arguments");
+        if (cols <= 0 || cols % 32 || mat_rows <= 0 || mat_rows % 4) throw Status(MOSS_HIP_EINVAL, "bad matrix shape");
+        mh::hip_check(mh::launch_dequant_rows(static_cast<const uint8_t *>(w), mat_rows, cols, rows_dev, n, out,
+                                              static_cast<hipStream_t>(stream)),
+                      "dequant launch");
+    });
+}
+
+size_t moss_hip_attn_workspace_bytes(int heads, int ctx_stride, int chunk) {
+    if (chunk <= 0) chunk = 64;
+    if (heads <= 0 || ctx_stride <= 0) return 0;
+    const size_t splits = (size_t)(ctx_stride + chunk - 1) / chunk;
+    return (size_t)heads * splits * (mh::kHeadDim + 2) * sizeof(float);
+}
+
+int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
+                         int ctx_stride, int n_keys, int chunk, void *workspace, void *out, int out_dtype,
+                         void *stream) {
+    return guard([&] {
+        if (!q || !k_cache || !v_cache || !workspace || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (chunk <= 0) chunk = 64;
+        if (chunk % 64 || chunk > 256) throw Status(MOSS_HIP_EINVAL, "chunk must be 64, 128, 192 or 256");
+        if (heads <= 0 || ctx_stride <= 0 || n_keys <= 0 || n_keys > ctx_stride)
+            throw Status(MOSS_HIP_EINVAL, "need 0 < n_keys <= ctx_stride");
+        if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
+            throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
+        const int splits = (ctx_stride + chunk - 1) / chunk;
+        float *ws = static_cast<float *>(workspace);
+        mh::AttnArgs a;
+        a.q = q;
+        a.k_cache = k_cache;
+        a.v_cache = v_cache;
+        a.ctx_stride = ctx_stride;
+        a.heads = heads;
+        a.pos_const = n_keys - 1;
+        a.chunk = chunk;
+        a.max_splits = splits;
+        a.part_o = ws;
+        a.part_ml = ws + (size_t)heads * splits * mh::kHeadDim;
+        const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
+        auto s = static_cast<hipStream_t>(stream);
+        mh::hip_check(mh::launch_attn_split(a, kv, s), "attention launch");
+        mh::hip_check(mh::launch_attn_merge(a, out, out_dtype == MOSS_HIP_F16, s), "merge launch");
+    });
+}
+
+}  // extern "C"

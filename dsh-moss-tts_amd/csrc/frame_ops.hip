@@ -1,0 +1,281 @@
+// frame_ops.hip -- the small per-step kernels around the GEMVs (gfx950).
+#include "mh_ops.h"
+
+namespace mh {
+namespace {
+
+// x = deq(wte[row[0]]) + sum over ch of deq(aemb[ch][row[ch+1]]), pads skipped,
+// channels added in order (reference csrc/src/llm.cpp:148-157).  Each element is
+// an independent serial fp32 sum, so this is bit-identical to the reference.
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+    if (a.state != nullptr && a.state->stop) return;
+    const int nb = kHidden / 32;
+    int row[kNVq + 1];
+#pragma unroll
+    for (int i = 0; i <= kNVq; ++i) row[i] = a.row[i];
+    for (int c = threadIdx.x; c < kHidden; c += 256) {
+        float v = q8x4_elem(a.wte, nb, row[0], c);
+#pragma unroll
+        for (int ch = 0; ch < kNVq; ++ch) {
+            const int code = row[ch + 1];
+            if (code == kAudioPad || code < 0 || code >= kCodebook) continue;
+            v = v + q8x4_elem(a.aemb[ch], nb, code, c);
+        }
+        a.x[c] = v;
+    }
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const float *x, const float *w, const float *b, float *out,
+                                                        DevState *state, int bump_pos) {
+    __shared__ float red[4];
+    if (state != nullptr && state->stop) return;
+    const int t = threadIdx.x;
+    float v[3], o[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v[i] = x[t + 256 * i];
+    layernorm_768(v, w, b, o, red);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) out[t + 256 * i] = o[i];
+    if (bump_pos && t == 0) state->pos += 1;
+}
+
+// Rows outside [0, mat_rows) produce NaN instead of reading outside the matrix.
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *w, int mat_rows, int cols, const int *rows,
+                                                           float *out) {
+    const int r = rows[blockIdx.x];
+    const int nb = cols / 32;
+    const bool ok = r >= 0 && r < mat_rows;
+    for (int c = threadIdx.x; c < cols; c += 256)
+        out[(size_t)blockIdx.x * cols + c] = ok ? q8x4_elem(w, nb, r, c) : __int_as_float(0x7fc00000);
+}
+
+// End gate (reference csrc/src/llm.cpp:274-285 + :30-35 + :678):
+//  1. h = LayerNorm(x; local lnf)                     (the local step's output)
+//  2. W8A8 quantisation of h per 32-block            (csrc/src/quant.cpp:28-43):
+//     d = amax/127, id = 1/d, q = clamp(rint(h*id), +-127), scale kept as fp32 d
+//  3. rows 7 (end) and 9 (slot) of wte dotted in the AVX2 order of
+//     row_dot_q8_4x4 (csrc/src/gemv_avx2.cpp:105-121): 8 lane accumulators, lane j
+//     takes the exact int32 sum of bytes 4j..4j+3 of each block, fma'd with
+//     (d_w * d_a); then the 8 lanes are summed as _mm256 hsum does.
+//  4. stop = frame >= min_frames && l_end > l_slot   (greedy end, llm.cpp:31)
+// Integer parts are exact and the fp32 operation order is the reference's, so
+// the gate values are bit-identical to the reference given the same h.
+__global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const float *lnf_w, const float *lnf_b,
+                                                   const uint8_t *wte, DevState *state, float *gate_log) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    __shared__ float hbuf[kHidden];
+    __shared__ int8_t qa[kHidden];
+    __shared__ float da[kHidden / 32];
+    __shared__ float lanes[2][8];
+    if (state->stop) return;
+    const int t = threadIdx.x;
+    float v[3], o[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v[i] = x_raw[t + 256 * i];
+    layernorm_768(v, lnf_w, lnf_b, o, red);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) hbuf[t + 256 * i] = o[i];
+    __syncthreads();
+    const int nb = kHidden / 32;
+    if (t < nb) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float av = fabsf(hbuf[32 * t + i]);
+            amax = amax < av ? av : amax;
+        }
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        da[t] = d;
+        for (int i = 0; i < 32; ++i) {
+            int q = (int)rintf(hbuf[32 * t + i] * id);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            qa[32 * t + i] = (int8_t)q;
+        }
+    }
+    __syncthreads();
+    if (t < 16) {
+        const int which = t >> 3, lane = t & 7;
+        const int r = which == 0 ? kEndToken : kSlotToken;
+        const uint8_t *grp = wte + (size_t)(r >> 2) * nb * kBlockBytes;
+        float acc = 0.0f;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t *blk = grp + (size_t)b * kBlockBytes;
+            const float dw = h2f(*(const uint16_t *)(blk + 2 * (r & 3)));
+            const int8_t *qs = (const int8_t *)(blk + 8 + 32 * (r & 3));
+            int32_t p = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) p += (int32_t)qs[4 * lane + u] * (int32_t)qa[32 * b + 4 * lane + u];
+            const float scale = dw * da[b];
+            acc = fmaf((float)p, scale, acc);
+        }
+        lanes[which][lane] = acc;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float g[2];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const float *a8 = lanes[w];
+            const float s0 = a8[0] + a8[4], s1 = a8[1] + a8[5], s2 = a8[2] + a8[6], s3 = a8[3] + a8[7];
+            const float t0 = s0 + s2, t1 = s1 + s3;
+            g[w] = t0 + t1;
+        }
+        state->gate[0] = g[0];
+        state->gate[1] = g[1];
+        if (gate_log != nullptr) {
+            gate_log[2 * state->frame] = g[0];
+            gate_log[2 * state->frame + 1] = g[1];
+        }
+        if (state->frame >= state->min_frames && g[0] > g[1]) state->stop = 1;
+    }
+}
+
+// Greedy pick with repetition penalty (reference csrc/src/sampler.cpp:9-28):
+// the penalty is applied once per past occurrence of a code (v<0 ? v*p : v/p,
+// repeated), then argmax with the lowest index winning ties.  Then the used code
+// (forced under teacher forcing) is appended to the history, written into the
+// next global-step row, and its aemb row becomes the next local input
+// (llm.cpp:692-697).
+__global__ __launch_bounds__(256) void sample_greedy_kernel(SampleArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ int used_s;
+    DevState *st = a.state;
+    if (st->stop) return;
+    const int t = threadIdx.x;
+    const float p = st->rep_penalty;
+    const int *cnt = a.counts + a.ch * kCodebook;
+    float best = -INFINITY;
+    int besti = kCodebook;
+    for (int i = t; i < kCodebook; i += 256) {  // ascending i per thread
+        float v = a.logits[i];
+        if (p != 1.0f) {
+            const int c = cnt[i];
+            for (int k = 0; k < c; ++k) v = v < 0.0f ? v * p : v / p;
+        }
+        if (v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+    // wave reduction keeping (max value, lowest index)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(besti, off);
+        if (ov > best || (ov == best && oi < besti)) {
+            best = ov;
+            besti = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = besti;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float b = bv[0];
+        int idx = bi[0];
+        for (int w = 1; w < 4; ++w)
+            if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
+                b = bv[w];
+                idx = bi[w];
+            }
+        if (idx >= kCodebook) idx = 0;  // all NaN: the reference's scan keeps index 0
+        const int used = st->forced_on ? a.forced[st->frame * kNVq + a.ch] : idx;
+        st->codes[a.ch] = idx;
+        st->row[a.ch + 1] = used;
+        a.counts[a.ch * kCodebook + used] += 1;
+        used_s = used;
+        if (a.last_channel) {
+            st->row[0] = kSlotToken;
+            st->frame += 1;
+        }
+    }
+    __syncthreads();
+    const int used = used_s;
+    const int nb = kHidden / 32;
+    for (int c = t; c < kHidden; c += 256) a.next_input[c] = q8x4_elem(a.aemb, nb, used, c);
+}
+
+template <int KV>
+__global__ void kv_import_kernel(const float *src, int n_pos, void *dst, int ctx_stride) {
+    const int p = blockIdx.x;
+    for (int e = threadIdx.x; e < kHidden; e += blockDim.x) {
+        const float v = src[(size_t)p * kHidden + e];
+        const size_t idx = ((size_t)(e >> 6) * ctx_stride + p) * kHeadDim + (e & 63);
+        if constexpr (KV == KV_F16)
+            ((__half *)dst)[idx] = __float2half_rn(v);
+        else
+            ((float *)dst)[idx] = v;
+    }
+}
+
+template <int KV>
+__global__ void kv_export_kernel(const void *src, int n_pos, int ctx_stride, float *dst) {
+    const int p = blockIdx.x;
+    for (int e = threadIdx.x; e < kHidden; e += blockDim.x) {
+        const size_t idx = ((size_t)(e >> 6) * ctx_stride + p) * kHeadDim + (e & 63);
+        float v;
+        if constexpr (KV == KV_F16)
+            v = __half2float(((const __half *)src)[idx]);
+        else
+            v = ((const float *)src)[idx];
+        dst[(size_t)p * kHidden + e] = v;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_embed(const EmbedArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, DevState *state,
+                            int bump_pos, hipStream_t s) {
+    hipLaunchKernelGGL(layernorm_kernel, dim3(1), dim3(256), 0, s, x, w, b, out, state, bump_pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_rows(const uint8_t *w, int mat_rows, int cols, const int *rows_dev, int n, float *out,
+                               hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3(n), dim3(256), 0, s, w, mat_rows, cols, rows_dev, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
+                       DevState *state, float *gate_log, hipStream_t s) {
+    hipLaunchKernelGGL(gate_kernel, dim3(1), dim3(256), 0, s, x_raw, lnf_w, lnf_b, wte, state, gate_log);
+    return hipGetLastError();
+}
+
+hipError_t launch_sample_greedy(const SampleArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(sample_greedy_kernel, dim3(1), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_import(const float *src, int n_pos, void *dst, int ctx_stride, KvType kv, hipStream_t s) {
+    if (n_pos <= 0) return hipSuccess;
+    if (n_pos > ctx_stride) return hipErrorInvalidValue;
+    if (kv == KV_F16)
+        hipLaunchKernelGGL(kv_import_kernel<KV_F16>, dim3(n_pos), dim3(256), 0, s, src, n_pos, dst, ctx_stride);
+    else
+        hipLaunchKernelGGL(kv_import_kernel<KV_F32>, dim3(n_pos), dim3(256), 0, s, src, n_pos, dst, ctx_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType kv, float *dst, hipStream_t s) {
+    if (n_pos <= 0) return hipSuccess;
+    if (n_pos > ctx_stride) return hipErrorInvalidValue;
+    if (kv == KV_F16)
+        hipLaunchKernelGGL(kv_export_kernel<KV_F16>, dim3(n_pos), dim3(256), 0, s, src, n_pos, ctx_stride, dst);
+    else
+        hipLaunchKernelGGL(kv_export_kernel<KV_F32>, dim3(n_pos), dim3(256), 0, s, src, n_pos, ctx_stride, dst);
+    return hipGetLastError();
+}
+
+}  // namespace mh

@@ -1,0 +1,111 @@
+// llm_model.h -- the GPU-resident MOSS-TTS-Nano LLM (host driver).
+//
+// Device-side counterpart of moss::LlmModel (reference csrc/include/moss/llm.h:39-90):
+// owns the uploaded .moss blob, the KV cache, the device decode state and the
+// captured hipGraphs of the global step and of a frame's local loop.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/moss_hip.h"
+#include "mh_ops.h"
+
+namespace mh {
+
+struct Status : std::runtime_error {
+    int code;
+    Status(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+void hip_check(hipError_t e, const char *what);
+
+struct LayerW {
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b;
+    const uint8_t *attn_w;
+    const float *attn_b;
+    const uint8_t *proj_w;
+    const float *proj_b;
+    const uint8_t *fc_in_w;
+    const float *fc_in_b;
+    const uint8_t *fc_out_w;
+    const float *fc_out_b;
+};
+
+class Model {
+public:
+    Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt);
+    ~Model();
+    Model(const Model &) = delete;
+    Model &operator=(const Model &) = delete;
+
+    void reset();
+    int position() const { return pos_; }
+    void get_hidden(float *out);
+    void set_hidden(const float *in);
+    void prefill(const int32_t *rows, int n, int start);
+    void global_step(const int32_t *row17);
+    int generate(int max_frames, const moss_hip_sample_params &p, uint64_t seed, const int32_t *forced, int n_forced,
+                 int32_t *out_rows, double *timing, float *logits_dump, float *gate_dump, moss_hip_frame_cb cb,
+                 void *user);
+    void set_cancel_flag(const volatile uint8_t *f) { cancel_ = f; }
+    void snapshot_prefix();
+    void restore_prefix();
+    int prefix_pos() const { return prefix_pos_; }
+    void kv_export(int n_pos, float *k, float *v);
+    void kv_import(int n_pos, const float *k, const float *v, const float *hidden);
+
+    int device() const { return device_; }
+
+private:
+    void enqueue_global_step(hipStream_t s, const int *row_dev);
+    void enqueue_local_step(hipStream_t s, const float *in, int lpos);
+    void enqueue_frame_local(hipStream_t s);
+    void build_graphs();
+    void launch_global(hipStream_t s);
+    void launch_frame_local(hipStream_t s);
+    void write_state_header();
+    void *kv_layer(int which, int layer) const;  // which: 0 = K, 1 = V
+
+    int device_ = 0, max_ctx_ = kMaxCtx, use_graphs_ = 1;
+    KvType kvt_ = KV_F16;
+    size_t kv_esize_ = 2;
+    hipStream_t stream_ = nullptr;
+    hipEvent_t ev_[3] = {};
+
+    uint8_t *blob_ = nullptr;
+    LayerW g_[kLayers] = {}, local_ = {};
+    const float *lnf_w_ = nullptr, *lnf_b_ = nullptr, *llnf_w_ = nullptr, *llnf_b_ = nullptr;
+    const uint8_t *wte_ = nullptr;
+    std::array<const uint8_t *, kNVq> aemb_{};
+
+    // device buffers
+    void *kv_ = nullptr;                 // [2][layers][heads][max_ctx][64]
+    float *lkv_ = nullptr;               // [2][heads][17][64] fp32
+    float *rope_ = nullptr;              // cos [n][32] then sin [n][32]
+    int rope_n_ = 0;
+    float *x_ = nullptr, *q_ = nullptr, *mlp_ = nullptr, *hidden_ = nullptr;
+    float *lres_ = nullptr, *next_in_ = nullptr, *slot_in_ = nullptr;
+    float *part_o_ = nullptr, *part_ml_ = nullptr;
+    int max_splits_ = 0, chunk_ = 64;
+    float *logits_ = nullptr;            // [16][1024]
+    int *counts_ = nullptr;              // [16][1024]
+    int *forced_ = nullptr;              // [max_ctx][16]
+    float *gate_log_ = nullptr;          // [max_ctx][2]
+    int *rows_dev_ = nullptr;            // prefill rows [n][17]
+    int rows_cap_ = 0;
+    DevState *state_ = nullptr;          // device
+    DevState *hstate_ = nullptr;         // pinned host mirror
+    void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]
+
+    hipGraphExec_t g_global_ = nullptr, g_local_ = nullptr;
+
+    int pos_ = 0, prefix_pos_ = 0;
+    const volatile uint8_t *cancel_ = nullptr;
+};
+
+}  // namespace mh

@@ -1,0 +1,575 @@
+// llm_model.hip -- host driver of the GPU-resident LLM (see llm_model.h).
+#include "llm_model.h"
+
+#include <chrono>
+#include <cmath>
+#include <cstddef>
+#include <cstring>
+#include <unordered_map>
+
+namespace mh {
+
+void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw Status(MOSS_HIP_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+struct Entry {
+    uint8_t dtype = 0, ndim = 0;
+    uint32_t dims[3] = {0, 0, 0};
+    uint64_t off = 0, nbytes = 0;
+};
+
+// .moss v1 index (reference csrc/src/weights.cpp:27-125): "MOSW", u32 version = 1,
+// u32 n; 80-byte entries: name[48], u8 dtype, u8 ndim, u32 dims[3] @52, u64 offset
+// @64, u64 nbytes @72.
+std::unordered_map<std::string, Entry> parse_index(const uint8_t *blob, size_t bytes) {
+    if (bytes < 16 || std::memcmp(blob, "MOSW", 4) != 0) throw Status(MOSS_HIP_EFORMAT, "not a .moss file (bad magic)");
+    uint32_t version = 0, n = 0;
+    std::memcpy(&version, blob + 4, 4);
+    std::memcpy(&n, blob + 8, 4);
+    if (version != 1) throw Status(MOSS_HIP_EFORMAT, "unsupported .moss version " + std::to_string(version));
+    if (16 + (size_t)n * 80 > bytes) throw Status(MOSS_HIP_EFORMAT, ".moss index truncated");
+    std::unordered_map<std::string, Entry> out;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint8_t *e = blob + 16 + (size_t)i * 80;
+        char name[49];
+        std::memcpy(name, e, 48);
+        name[48] = 0;
+        Entry en;
+        en.dtype = e[48];
+        en.ndim = e[49];
+        std::memcpy(en.dims, e + 52, 12);
+        std::memcpy(&en.off, e + 64, 8);
+        std::memcpy(&en.nbytes, e + 72, 8);
+        if (en.off + en.nbytes > bytes) throw Status(MOSS_HIP_EFORMAT, std::string("tensor out of range: ") + name);
+        out[name] = en;
+    }
+    return out;
+}
+
+bool is_vector(const Entry &e) { return e.ndim == 1 || (e.dims[0] == 1 && e.dims[2] == 1); }
+
+constexpr size_t kStateRowOff = offsetof(DevState, row);
+
+}  // namespace
+
+Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
+    device_ = opt.device;
+    max_ctx_ = opt.max_ctx > 0 ? opt.max_ctx : kMaxCtx;
+    if (max_ctx_ > 65536) throw Status(MOSS_HIP_EINVAL, "max_ctx too large");
+    kvt_ = opt.kv_dtype == 1 ? KV_F32 : KV_F16;
+    kv_esize_ = kvt_ == KV_F32 ? 4 : 2;
+    use_graphs_ = opt.use_graphs;
+    const uint8_t *b = static_cast<const uint8_t *>(blob);
+    auto idx = parse_index(b, bytes);
+
+    // Resolve every tensor LlmModel::load needs (llm.cpp:44-70) before touching the GPU.
+    std::unordered_map<std::string, uint64_t> off;
+    auto need_vec = [&](const std::string &name, uint32_t n) {
+        auto it = idx.find(name);
+        if (it == idx.end() || !is_vector(it->second)) throw Status(MOSS_HIP_EFORMAT, "missing vector: " + name);
+        if (it->second.dims[0] * it->second.dims[1] != n || it->second.nbytes < (uint64_t)n * 4)
+            throw Status(MOSS_HIP_EFORMAT, "bad vector size: " + name);
+        off[name] = it->second.off;
+    };
+    auto need_mat = [&](const std::string &name, uint32_t rows, uint32_t cols) {
+        auto it = idx.find(name);
+        if (it == idx.end() || is_vector(it->second)) throw Status(MOSS_HIP_EFORMAT, "missing matrix: " + name);
+        if (it->second.dtype != 4)
+            throw Status(MOSS_HIP_EUNSUPPORTED, "matrix " + name + " has dtype " + std::to_string(it->second.dtype) +
+                                                    "; only Q8_0_4X4 (4) is supported");
+        if (it->second.dims[0] != rows || it->second.dims[1] != cols ||
+            it->second.nbytes < (uint64_t)(rows / 4) * (cols / 32) * kBlockBytes)
+            throw Status(MOSS_HIP_EFORMAT, "bad matrix shape: " + name);
+        off[name] = it->second.off;
+    };
+    auto need_layer = [&](const std::string &p) {
+        need_vec(p + "ln1.w", kHidden);
+        need_vec(p + "ln1.b", kHidden);
+        need_vec(p + "ln2.w", kHidden);
+        need_vec(p + "ln2.b", kHidden);
+        need_mat(p + "attn.w", 3 * kHidden, kHidden);
+        need_vec(p + "attn.b", 3 * kHidden);
+        need_mat(p + "proj.w", kHidden, kHidden);
+        need_vec(p + "proj.b", kHidden);
+        need_mat(p + "fc_in.w", kFF, kHidden);
+        need_vec(p + "fc_in.b", kFF);
+        need_mat(p + "fc_out.w", kHidden, kFF);
+        need_vec(p + "fc_out.b", kHidden);
+    };
+    for (int i = 0; i < kLayers; ++i) need_layer("g" + std::to_string(i) + ".");
+    need_layer("local.");
+    need_vec("lnf.w", kHidden);
+    need_vec("lnf.b", kHidden);
+    need_vec("local.lnf.w", kHidden);
+    need_vec("local.lnf.b", kHidden);
+    need_mat("wte", kVocab, kHidden);
+    for (int ch = 0; ch < kNVq; ++ch) need_mat("aemb." + std::to_string(ch), kCodebook, kHidden);
+
+    hip_check(hipSetDevice(device_), "hipSetDevice");
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    for (auto &e : ev_) hip_check(hipEventCreate(&e), "hipEventCreate");
+    hip_check(hipMalloc(&blob_, bytes), "hipMalloc(weights)");
+    hip_check(hipMemcpy(blob_, blob, bytes, hipMemcpyHostToDevice), "upload weights");
+
+    auto V = [&](const std::string &n) { return reinterpret_cast<const float *>(blob_ + off.at(n)); };
+    auto M = [&](const std::string &n) { return static_cast<const uint8_t *>(blob_ + off.at(n)); };
+    auto set_layer = [&](LayerW &L, const std::string &p) {
+        L.ln1_w = V(p + "ln1.w");
+        L.ln1_b = V(p + "ln1.b");
+        L.ln2_w = V(p + "ln2.w");
+        L.ln2_b = V(p + "ln2.b");
+        L.attn_w = M(p + "attn.w");
+        L.attn_b = V(p + "attn.b");
+        L.proj_w = M(p + "proj.w");
+        L.proj_b = V(p + "proj.b");
+        L.fc_in_w = M(p + "fc_in.w");
+        L.fc_in_b = V(p + "fc_in.b");
+        L.fc_out_w = M(p + "fc_out.w");
+        L.fc_out_b = V(p + "fc_out.b");
+    };
+    for (int i = 0; i < kLayers; ++i) set_layer(g_[i], "g" + std::to_string(i) + ".");
+    set_layer(local_, "local.");
+    lnf_w_ = V("lnf.w");
+    lnf_b_ = V("lnf.b");
+    llnf_w_ = V("local.lnf.w");
+    llnf_b_ = V("local.lnf.b");
+    wte_ = M("wte");
+    for (int ch = 0; ch < kNVq; ++ch) aemb_[ch] = M("aemb." + std::to_string(ch));
+
+    // KV cache [K|V][layer][head][pos][64]
+    const size_t kv_bytes = 2ull * kLayers * kHeads * max_ctx_ * kHeadDim * kv_esize_;
+    hip_check(hipMalloc(&kv_, kv_bytes), "hipMalloc(kv)");
+    hip_check(hipMemset(kv_, 0, kv_bytes), "memset(kv)");
+    hip_check(hipMalloc(&lkv_, 2ull * kHeads * kLocalLen * kHeadDim * 4), "hipMalloc(local kv)");
+
+    // RoPE table: angle = pos * 10000^(-2i/64) in double, stored as float
+    // (reference csrc/src/llm.cpp:90-102; identical for every head).
+    rope_n_ = max_ctx_ > kLocalLen ? max_ctx_ : kLocalLen;
+    std::vector<float> rope(2ull * rope_n_ * kRopeHalf);
+    for (int p = 0; p < rope_n_; ++p)
+        for (int i = 0; i < kRopeHalf; ++i) {
+            const double inv = 1.0 / std::pow(10000.0, static_cast<double>(2 * i) / kHeadDim);
+            const double ang = static_cast<double>(p) * inv;
+            rope[(size_t)p * kRopeHalf + i] = static_cast<float>(std::cos(ang));
+            rope[(size_t)(rope_n_ + p) * kRopeHalf + i] = static_cast<float>(std::sin(ang));
+        }
+    hip_check(hipMalloc(&rope_, rope.size() * 4), "hipMalloc(rope)");
+    hip_check(hipMemcpy(rope_, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "upload rope");
+
+    chunk_ = 64;
+    max_splits_ = (max_ctx_ + chunk_ - 1) / chunk_;
+    auto fmalloc = [&](float **p, size_t n) { hip_check(hipMalloc(p, n * 4), "hipMalloc(act)"); };
+    fmalloc(&x_, kHidden);
+    fmalloc(&q_, kHidden);
+    fmalloc(&mlp_, kFF);
+    fmalloc(&hidden_, kHidden);
+    fmalloc(&lres_, kHidden);
+    fmalloc(&next_in_, kHidden);
+    fmalloc(&slot_in_, kHidden);
+    fmalloc(&part_o_, (size_t)kHeads * max_splits_ * kHeadDim);
+    fmalloc(&part_ml_, (size_t)kHeads * max_splits_ * 2);
+    fmalloc(&logits_, (size_t)kNVq * kCodebook);
+    fmalloc(&gate_log_, 2ull * (max_ctx_ + 2));
+    hip_check(hipMalloc(&counts_, sizeof(int) * kNVq * kCodebook), "hipMalloc(counts)");
+    hip_check(hipMalloc(&forced_, sizeof(int) * kNVq * (max_ctx_ + 2)), "hipMalloc(forced)");
+    hip_check(hipMemset(hidden_, 0, kHidden * 4), "memset(hidden)");
+    hip_check(hipMalloc(&state_, sizeof(DevState)), "hipMalloc(state)");
+    hip_check(hipHostMalloc(&hstate_, sizeof(DevState), hipHostMallocDefault), "hipHostMalloc(state)");
+    std::memset(hstate_, 0, sizeof(DevState));
+    hstate_->rep_penalty = 1.0f;
+    hip_check(hipMemcpy(state_, hstate_, sizeof(DevState), hipMemcpyHostToDevice), "init state");
+
+    // The first local input of every channel loop is wte[slot] (llm.cpp:682): dequantise once.
+    rows_cap_ = 1;
+    hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17), "hipMalloc(rows)");
+    const int slot = kSlotToken;
+    hip_check(hipMemcpy(rows_dev_, &slot, sizeof(int), hipMemcpyHostToDevice), "slot row");
+    hip_check(launch_dequant_rows(wte_, kVocab, kHidden, rows_dev_, 1, slot_in_, stream_), "dequant slot row");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    if (use_graphs_) build_graphs();
+}
+
+Model::~Model() {
+    (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (g_global_) (void)hipGraphExecDestroy(g_global_);
+    if (g_local_) (void)hipGraphExecDestroy(g_local_);
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, part_o_, part_ml_,
+                    logits_, counts_, forced_, gate_log_, rows_dev_, state_, snap_};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+    if (hstate_) (void)hipHostFree(hstate_);
+    for (auto &e : ev_)
+        if (e) (void)hipEventDestroy(e);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void *Model::kv_layer(int which, int layer) const {
+    const size_t per = (size_t)kHeads * max_ctx_ * kHeadDim * kv_esize_;
+    return static_cast<uint8_t *>(kv_) + ((size_t)which * kLayers + layer) * per;
+}
+
+// One global step: embed_row -> 12 x block_forward -> ln_f (llm.cpp:248-255).
+// block_forward (llm.cpp:230-246) is five kernels: QKV GEMV with LN1 fused in its
+// prologue and bias + RoPE + KV write in its epilogue; split-KV attention; proj
+// GEMV merging the attention splits in its prologue and adding the residual in
+// its epilogue; fc_in GEMV with LN2 in, bias + gelu out; fc_out GEMV with the
+// residual out.  Every position-dependent kernel reads state->pos.
+void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
+    const int *pos = &state_->pos;
+    EmbedArgs e;
+    e.wte = wte_;
+    for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = aemb_[ch];
+    e.row = row_dev;
+    e.x = x_;
+    e.state = state_;
+    hip_check(launch_embed(e, s), "embed");
+    for (int l = 0; l < kLayers; ++l) {
+        const LayerW &L = g_[l];
+        GemvArgs a;
+        a.w = L.attn_w; a.rows = 3 * kHidden; a.cols = kHidden;
+        a.x = x_; a.ln_w = L.ln1_w; a.ln_b = L.ln1_b;
+        a.bias = L.attn_b; a.q_out = q_;
+        a.k_cache = kv_layer(0, l); a.v_cache = kv_layer(1, l); a.ctx_stride = max_ctx_;
+        a.rope_cos = rope_; a.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
+        a.pos_ptr = pos; a.state = state_;
+        hip_check(launch_gemv(a, PRO_LN, EPI_QKV, kvt_, s), "qkv gemv");
+
+        AttnArgs t;
+        t.q = q_; t.k_cache = a.k_cache; t.v_cache = a.v_cache; t.ctx_stride = max_ctx_;
+        t.pos_ptr = pos; t.chunk = chunk_; t.max_splits = max_splits_;
+        t.part_o = part_o_; t.part_ml = part_ml_; t.state = state_;
+        hip_check(launch_attn_split(t, kvt_, s), "attention");
+
+        GemvArgs p;
+        p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
+        p.part_o = part_o_; p.part_ml = part_ml_; p.max_splits = max_splits_; p.chunk = chunk_; p.pos_ptr = pos;
+        p.y = x_; p.bias = L.proj_b; p.state = state_;
+        hip_check(launch_gemv(p, PRO_MERGE, EPI_RESID, kvt_, s), "proj gemv");
+
+        GemvArgs f1;
+        f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;
+        f1.x = x_; f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
+        f1.y = mlp_; f1.bias = L.fc_in_b; f1.state = state_;
+        hip_check(launch_gemv(f1, PRO_LN, EPI_GELU, kvt_, s), "fc_in gemv");
+
+        GemvArgs f2;
+        f2.w = L.fc_out_w; f2.rows = kHidden; f2.cols = kFF;
+        f2.x = mlp_; f2.y = x_; f2.bias = L.fc_out_b; f2.state = state_;
+        hip_check(launch_gemv(f2, PRO_F32, EPI_RESID, kvt_, s), "fc_out gemv");
+    }
+    hip_check(launch_layernorm(x_, lnf_w_, lnf_b_, hidden_, state_, 1, s), "ln_f");
+}
+
+// local_step (llm.cpp:259-264) without its final ln_f: the residual stream starts
+// as `in` (read by the proj epilogue) and lives in lres_; consumers apply the
+// local ln_f in their own prologue.
+void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
+    const LayerW &L = local_;
+    float *lk = lkv_, *lv = lkv_ + (size_t)kHeads * kLocalLen * kHeadDim;
+    GemvArgs a;
+    a.w = L.attn_w; a.rows = 3 * kHidden; a.cols = kHidden;
+    a.x = in; a.ln_w = L.ln1_w; a.ln_b = L.ln1_b;
+    a.bias = L.attn_b; a.q_out = q_;
+    a.k_cache = lk; a.v_cache = lv; a.ctx_stride = kLocalLen;
+    a.rope_cos = rope_; a.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
+    a.pos_const = lpos; a.state = state_;
+    hip_check(launch_gemv(a, PRO_LN, EPI_QKV, KV_F32, s), "local qkv");
+
+    // At most 17 keys: only split 0 has work (the others exit at once); partials keep
+    // the model-wide head stride of max_splits_ so the proj prologue reads them alike.
+    AttnArgs t;
+    t.q = q_; t.k_cache = lk; t.v_cache = lv; t.ctx_stride = kLocalLen;
+    t.pos_const = lpos; t.chunk = chunk_; t.max_splits = max_splits_;
+    t.part_o = part_o_; t.part_ml = part_ml_; t.state = state_;
+    hip_check(launch_attn_split(t, KV_F32, s), "local attention");
+
+    GemvArgs p;
+    p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
+    p.part_o = part_o_; p.part_ml = part_ml_; p.max_splits = max_splits_; p.chunk = chunk_; p.pos_const = lpos;
+    p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_;
+    hip_check(launch_gemv(p, PRO_MERGE, EPI_RESID, KV_F32, s), "local proj");
+
+    GemvArgs f1;
+    f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;
+    f1.x = lres_; f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
+    f1.y = mlp_; f1.bias = L.fc_in_b; f1.state = state_;
+    hip_check(launch_gemv(f1, PRO_LN, EPI_GELU, KV_F32, s), "local fc_in");
+
+    GemvArgs f2;
+    f2.w = L.fc_out_w; f2.rows = kHidden; f2.cols = kFF;
+    f2.x = mlp_; f2.y = lres_; f2.bias = L.fc_out_b; f2.state = state_;
+    hip_check(launch_gemv(f2, PRO_F32, EPI_RESID, KV_F32, s), "local fc_out");
+}
+
+// The local half of a frame (llm.cpp:648-698): local step on hidden, end gate,
+// then 16 x (local step, audio head of channel ch, greedy pick + next input).
+void Model::enqueue_frame_local(hipStream_t s) {
+    enqueue_local_step(s, hidden_, 0);
+    hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, gate_log_, s), "gate");
+    for (int ch = 0; ch < kNVq; ++ch) {
+        enqueue_local_step(s, ch == 0 ? slot_in_ : next_in_, ch + 1);
+        GemvArgs h;
+        h.w = aemb_[ch]; h.rows = kCodebook; h.cols = kHidden;
+        h.x = lres_; h.ln_w = llnf_w_; h.ln_b = llnf_b_;
+        h.y = logits_ + (size_t)ch * kCodebook; h.state = state_;
+        hip_check(launch_gemv(h, PRO_LN, EPI_F32, KV_F32, s), "audio head");
+        SampleArgs sa;
+        sa.logits = logits_ + (size_t)ch * kCodebook;
+        sa.ch = ch;
+        sa.counts = counts_;
+        sa.forced = forced_;
+        sa.aemb = aemb_[ch];
+        sa.next_input = next_in_;
+        sa.state = state_;
+        sa.last_channel = ch == kNVq - 1;
+        hip_check(launch_sample_greedy(sa, s), "sample");
+    }
+}
+
+void Model::build_graphs() {
+    hipGraph_t g = nullptr;
+    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+    enqueue_global_step(stream_, reinterpret_cast<const int *>(reinterpret_cast<uint8_t *>(state_) + kStateRowOff));
+    hip_check(hipStreamEndCapture(stream_, &g), "end capture");
+    hip_check(hipGraphInstantiate(&g_global_, g, nullptr, nullptr, 0), "instantiate global");
+    (void)hipGraphDestroy(g);
+    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+    enqueue_frame_local(stream_);
+    hip_check(hipStreamEndCapture(stream_, &g), "end capture");
+    hip_check(hipGraphInstantiate(&g_local_, g, nullptr, nullptr, 0), "instantiate local");
+    (void)hipGraphDestroy(g);
+}
+
+void Model::launch_global(hipStream_t s) {
+    if (g_global_)
+        hip_check(hipGraphLaunch(g_global_, s), "graph launch");
+    else
+        enqueue_global_step(s, reinterpret_cast<const int *>(reinterpret_cast<uint8_t *>(state_) + kStateRowOff));
+}
+
+void Model::launch_frame_local(hipStream_t s) {
+    if (g_local_)
+        hip_check(hipGraphLaunch(g_local_, s), "graph launch");
+    else
+        enqueue_frame_local(s);
+}
+
+// Pushes the scalar header (pos .. rep_penalty) of the host mirror to the device.
+void Model::write_state_header() {
+    hstate_->pos = pos_;
+    hip_check(hipMemcpyAsync(state_, hstate_, offsetof(DevState, row), hipMemcpyHostToDevice, stream_), "state h2d");
+}
+
+void Model::reset() { pos_ = 0; }
+
+void Model::get_hidden(float *out) {
+    hip_check(hipMemcpyAsync(out, hidden_, kHidden * 4, hipMemcpyDeviceToHost, stream_), "hidden d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+}
+
+void Model::set_hidden(const float *in) {
+    hip_check(hipMemcpyAsync(hidden_, in, kHidden * 4, hipMemcpyHostToDevice, stream_), "hidden h2d");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+}
+
+// Token ids index wte directly (lookup_row, llm.cpp:149): reject what would read
+// outside the table.  Codes outside [0, 1024) are skipped as pads (llm.cpp:153).
+static void check_rows(const int32_t *rows, int n) {
+    for (int i = 0; i < n; ++i)
+        if (rows[(size_t)i * 17] < 0 || rows[(size_t)i * 17] >= kVocab)
+            throw Status(MOSS_HIP_EINVAL, "row " + std::to_string(i) + ": text id out of [0, 16384)");
+}
+
+void Model::global_step(const int32_t *row) {
+    if (pos_ >= max_ctx_) throw Status(MOSS_HIP_ESTATE, "KV cache full (position == max_ctx)");
+    check_rows(row, 1);
+    hstate_->stop = 0;
+    write_state_header();
+    hip_check(hipMemcpyAsync(reinterpret_cast<uint8_t *>(state_) + kStateRowOff, row, 17 * sizeof(int32_t),
+                             hipMemcpyHostToDevice, stream_),
+              "row h2d");
+    launch_global(stream_);
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    ++pos_;
+}
+
+// LlmModel::prefill (llm.cpp:327-401): rows are embedded and pushed through the
+// layers one position at a time (KV for [start, start+m), hidden = ln_f of the
+// last row).  Same arithmetic as the decode step (W8A16).
+void Model::prefill(const int32_t *rows, int n, int start) {
+    start = start < 0 ? 0 : (start > max_ctx_ ? max_ctx_ : start);
+    const int m = n < max_ctx_ - start ? n : max_ctx_ - start;
+    if (m <= 0) return;
+    check_rows(rows, m);
+    if (m > rows_cap_) {
+        hip_check(hipFree(rows_dev_), "free rows");
+        rows_dev_ = nullptr;
+        hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
+        rows_cap_ = m;
+    }
+    hip_check(hipMemcpyAsync(rows_dev_, rows, sizeof(int) * 17 * (size_t)m, hipMemcpyHostToDevice, stream_), "rows h2d");
+    pos_ = start;
+    hstate_->stop = 0;
+    write_state_header();
+    for (int i = 0; i < m; ++i) enqueue_global_step(stream_, rows_dev_ + 17 * (size_t)i);
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    pos_ = start + m;
+}
+
+int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t seed, const int32_t *forced,
+                    int n_forced, int32_t *out_rows, double *timing, float *logits_dump, float *gate_dump,
+                    moss_hip_frame_cb cb, void *user) {
+    (void)seed;  // greedy decoding draws no random numbers (sampler.cpp:23-28)
+    if (!(p.greedy || p.top_k == 1))
+        throw Status(MOSS_HIP_EUNSUPPORTED, "only greedy decoding runs on the device in this build");
+    if (!p.end_greedy) throw Status(MOSS_HIP_EUNSUPPORTED, "only the greedy end gate runs on the device in this build");
+    if (forced && n_forced < max_frames) max_frames = n_forced;
+    if (max_frames <= 0) return 0;
+    const int cap = max_ctx_ + 1;  // frames beyond this cannot happen: pos reaches max_ctx first
+    const int nf = max_frames < cap ? max_frames : cap;
+    if (forced) {
+        std::vector<int> codes((size_t)nf * kNVq);
+        for (int f = 0; f < nf; ++f)
+            for (int ch = 0; ch < kNVq; ++ch) {
+                const int c = forced[(size_t)f * 17 + ch + 1];
+                if (c < 0 || c >= kCodebook) throw Status(MOSS_HIP_EINVAL, "forced code out of range");
+                codes[(size_t)f * kNVq + ch] = c;
+            }
+        hip_check(hipMemcpyAsync(forced_, codes.data(), codes.size() * sizeof(int), hipMemcpyHostToDevice, stream_),
+                  "forced h2d");
+    }
+    hip_check(hipMemsetAsync(counts_, 0, sizeof(int) * kNVq * kCodebook, stream_), "counts clear");
+    hstate_->frame = 0;
+    hstate_->stop = 0;
+    hstate_->min_frames = p.min_frames;
+    hstate_->forced_on = forced ? 1 : 0;
+    hstate_->rep_penalty = p.repetition_penalty;
+    write_state_header();
+    hip_check(hipStreamSynchronize(stream_), "sync");
+
+    int frames = 0;
+    for (int f = 0; f < max_frames; ++f) {
+        if (pos_ >= max_ctx_) break;
+        if (cancel_ != nullptr && __atomic_load_n(cancel_, __ATOMIC_RELAXED)) break;
+        hip_check(hipEventRecord(ev_[0], stream_), "event");
+        launch_frame_local(stream_);
+        hip_check(hipEventRecord(ev_[1], stream_), "event");
+        const bool do_global = f + 1 < max_frames && pos_ < max_ctx_;
+        if (do_global) launch_global(stream_);
+        hip_check(hipEventRecord(ev_[2], stream_), "event");
+        if (logits_dump)
+            hip_check(hipMemcpyAsync(logits_dump + (size_t)f * kNVq * kCodebook, logits_,
+                                     sizeof(float) * kNVq * kCodebook, hipMemcpyDeviceToHost, stream_),
+                      "logits d2h");
+        hip_check(hipMemcpyAsync(hstate_, state_, sizeof(DevState), hipMemcpyDeviceToHost, stream_), "state d2h");
+        hip_check(hipStreamSynchronize(stream_), "sync");
+        if (gate_dump) {
+            gate_dump[2 * f] = hstate_->gate[0];
+            gate_dump[2 * f + 1] = hstate_->gate[1];
+        }
+        if (hstate_->stop) break;
+        int32_t *row = out_rows + (size_t)f * 17;
+        row[0] = 0;
+        for (int ch = 0; ch < kNVq; ++ch) row[ch + 1] = hstate_->codes[ch];
+        if (timing) {
+            float lm = 0.f, gm = 0.f;
+            hip_check(hipEventElapsedTime(&lm, ev_[0], ev_[1]), "elapsed");
+            hip_check(hipEventElapsedTime(&gm, ev_[1], ev_[2]), "elapsed");
+            timing[2 * f] = do_global ? gm : 0.0;
+            timing[2 * f + 1] = lm;
+        }
+        if (do_global) ++pos_;
+        frames = f + 1;
+        if (cb) cb(user, f, row);
+    }
+    return frames;
+}
+
+void Model::snapshot_prefix() {
+    prefix_pos_ = pos_;
+    if (snap_) {
+        hip_check(hipFree(snap_), "free snapshot");
+        snap_ = nullptr;
+    }
+    if (prefix_pos_ <= 0) return;
+    const size_t width = (size_t)prefix_pos_ * kHeadDim * kv_esize_;
+    hip_check(hipMalloc(&snap_, 2ull * kLayers * kHeads * width), "hipMalloc(snapshot)");
+    for (int w = 0; w < 2; ++w)
+        for (int l = 0; l < kLayers; ++l) {
+            uint8_t *dst = static_cast<uint8_t *>(snap_) + ((size_t)w * kLayers + l) * kHeads * width;
+            hip_check(hipMemcpy2DAsync(dst, width, kv_layer(w, l), (size_t)max_ctx_ * kHeadDim * kv_esize_, width,
+                                       kHeads, hipMemcpyDeviceToDevice, stream_),
+                      "snapshot copy");
+        }
+    hip_check(hipStreamSynchronize(stream_), "sync");
+}
+
+void Model::restore_prefix() {
+    if (prefix_pos_ <= 0 || !snap_) {
+        pos_ = 0;
+        return;
+    }
+    const size_t width = (size_t)prefix_pos_ * kHeadDim * kv_esize_;
+    for (int w = 0; w < 2; ++w)
+        for (int l = 0; l < kLayers; ++l) {
+            const uint8_t *src = static_cast<const uint8_t *>(snap_) + ((size_t)w * kLayers + l) * kHeads * width;
+            hip_check(hipMemcpy2DAsync(kv_layer(w, l), (size_t)max_ctx_ * kHeadDim * kv_esize_, src, width, width,
+                                       kHeads, hipMemcpyDeviceToDevice, stream_),
+                      "restore copy");
+        }
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    pos_ = prefix_pos_;
+}
+
+void Model::kv_export(int n_pos, float *k, float *v) {
+    if (n_pos < 0 || n_pos > max_ctx_) throw Status(MOSS_HIP_EINVAL, "n_pos out of range");
+    if (n_pos == 0) return;
+    float *stage = nullptr;
+    const size_t per = (size_t)n_pos * kHidden;
+    hip_check(hipMalloc(&stage, per * 4), "hipMalloc(stage)");
+    try {
+        for (int w = 0; w < 2; ++w)
+            for (int l = 0; l < kLayers; ++l) {
+                hip_check(launch_kv_export(kv_layer(w, l), n_pos, max_ctx_, kvt_, stage, stream_), "kv export");
+                hip_check(hipMemcpyAsync((w == 0 ? k : v) + (size_t)l * per, stage, per * 4, hipMemcpyDeviceToHost,
+                                         stream_),
+                          "kv d2h");
+                hip_check(hipStreamSynchronize(stream_), "sync");
+            }
+    } catch (...) {
+        (void)hipFree(stage);
+        throw;
+    }
+    (void)hipFree(stage);
+}
+
+void Model::kv_import(int n_pos, const float *k, const float *v, const float *hidden) {
+    if (n_pos < 0 || n_pos > max_ctx_) throw Status(MOSS_HIP_EINVAL, "n_pos out of range");
+    float *stage = nullptr;
+    const size_t per = (size_t)n_pos * kHidden;
+    if (n_pos > 0) {
+        hip_check(hipMalloc(&stage, per * 4), "hipMalloc(stage)");
+        try {
+            for (int w = 0; w < 2; ++w)
+                for (int l = 0; l < kLayers; ++l) {
+                    hip_check(hipMemcpyAsync(stage, (w == 0 ? k : v) + (size_t)l * per, per * 4, hipMemcpyHostToDevice,
+                                             stream_),
+                              "kv h2d");
+                    hip_check(launch_kv_import(stage, n_pos, kv_layer(w, l), max_ctx_, kvt_, stream_), "kv import");
+                    hip_check(hipStreamSynchronize(stream_), "sync");
+                }
+        } catch (...) {
+            (void)hipFree(stage);
+            throw;
+        }
+        (void)hipFree(stage);
+    }
+    if (hidden) set_hidden(hidden);
+    pos_ = n_pos;
+}
+
+}  // namespace mh

@@ -1,0 +1,234 @@
+"""ctypes binding of libmoss_hip.so (C ABI declared in include/moss_hip.h).
+
+The library is the product: if it is missing this module raises instead of
+falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libmoss_hip.so")
+
+OK, EINVAL, EDEVICE, EFORMAT, EUNSUPPORTED, ESTATE = 0, 1, 2, 3, 4, 5
+F32, F16 = 0, 1
+
+EXPORTED = [
+    "moss_hip_last_error", "moss_hip_abi_version",
+    "moss_hip_llm_create", "moss_hip_llm_create_from_file", "moss_hip_llm_destroy", "moss_hip_llm_reset",
+    "moss_hip_llm_position", "moss_hip_llm_get_hidden", "moss_hip_llm_set_hidden", "moss_hip_llm_prefill",
+    "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
+    "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
+    "moss_hip_llm_kv_export", "moss_hip_llm_kv_import",
+    "moss_hip_gemv_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_workspace_bytes", "moss_hip_attn_decode",
+]
+
+
+class MossHipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class Options(C.Structure):
+    _fields_ = [("device", C.c_int), ("max_ctx", C.c_int), ("kv_dtype", C.c_int), ("use_graphs", C.c_int)]
+
+
+class SampleParams(C.Structure):
+    """moss_hip_sample_params == SampleParams (csrc/include/moss/sampler.h:8-22)."""
+    _fields_ = [("greedy", C.c_int), ("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float), ("end_greedy", C.c_int), ("min_frames", C.c_int),
+                ("greedy_frames", C.c_int)]
+
+    @classmethod
+    def make(cls, greedy=True, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0, end_greedy=True,
+             min_frames=0, greedy_frames=0):
+        return cls(int(greedy), temperature, top_k, top_p, repetition_penalty, int(end_greedy), min_frames,
+                   greedy_frames)
+
+
+FRAME_CB = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.POINTER(C.c_int32))
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load libmoss_hip.so (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `make -C dsh-moss-tts_amd` (or __graft_entry__.build())")
+    L = C.CDLL(path)
+    vp, i32, f32p = C.c_void_p, C.c_int, C.POINTER(C.c_float)
+    L.moss_hip_last_error.restype = C.c_char_p
+    L.moss_hip_abi_version.restype = C.c_int
+    L.moss_hip_llm_create.argtypes = [vp, C.c_size_t, C.POINTER(Options), C.POINTER(vp)]
+    L.moss_hip_llm_create_from_file.argtypes = [C.c_char_p, C.POINTER(Options), C.POINTER(vp)]
+    L.moss_hip_llm_destroy.argtypes = [vp]
+    L.moss_hip_llm_destroy.restype = None
+    for n in ("moss_hip_llm_reset", "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix"):
+        getattr(L, n).argtypes = [vp]
+    L.moss_hip_llm_position.argtypes = [vp]
+    L.moss_hip_llm_prefix_pos.argtypes = [vp]
+    L.moss_hip_llm_get_hidden.argtypes = [vp, vp]
+    L.moss_hip_llm_set_hidden.argtypes = [vp, vp]
+    L.moss_hip_llm_prefill.argtypes = [vp, vp, i32, i32]
+    L.moss_hip_llm_global_step.argtypes = [vp, vp]
+    L.moss_hip_llm_generate.argtypes = [vp, i32, C.POINTER(SampleParams), C.c_uint64, vp, i32, vp, C.POINTER(i32),
+                                        vp, vp, vp, FRAME_CB, vp]
+    L.moss_hip_llm_set_cancel_flag.argtypes = [vp, vp]
+    L.moss_hip_llm_kv_export.argtypes = [vp, i32, vp, vp]
+    L.moss_hip_llm_kv_import.argtypes = [vp, i32, vp, vp, vp]
+    L.moss_hip_gemv_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp]
+    L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
+    L.moss_hip_attn_workspace_bytes.argtypes = [i32, i32, i32]
+    L.moss_hip_attn_workspace_bytes.restype = C.c_size_t
+    L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp]
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise MossHipError(rc, load().moss_hip_last_error().decode(errors="replace"))
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- operators (torch device tensors)
+
+def _stream(stream):
+    if stream is not None:
+        return C.c_void_p(stream)
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def gemv_q8x4(w, rows: int, cols: int, x, y, stream=None) -> None:
+    """y = W x on the device.  w: uint8 tensor (Q8_0_4X4), x/y: float32 or float16 tensors."""
+    import torch
+    dt = {torch.float32: F32, torch.float16: F16}
+    check(load().moss_hip_gemv_q8x4(C.c_void_p(w.data_ptr()), rows, cols, C.c_void_p(x.data_ptr()), dt[x.dtype],
+                                    C.c_void_p(y.data_ptr()), dt[y.dtype], _stream(stream)))
+
+
+def dequant_rows_q8x4(w, mat_rows: int, cols: int, rows_idx, out, stream=None) -> None:
+    check(load().moss_hip_dequant_rows_q8x4(C.c_void_p(w.data_ptr()), mat_rows, cols, C.c_void_p(rows_idx.data_ptr()),
+                                            rows_idx.numel(), C.c_void_p(out.data_ptr()), _stream(stream)))
+
+
+def attn_workspace_bytes(heads: int, ctx_stride: int, chunk: int = 64) -> int:
+    return load().moss_hip_attn_workspace_bytes(heads, ctx_stride, chunk)
+
+
+def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, workspace, out, chunk: int = 64,
+                stream=None) -> None:
+    import torch
+    dt = {torch.float32: F32, torch.float16: F16}
+    check(load().moss_hip_attn_decode(C.c_void_p(q.data_ptr()), C.c_void_p(k_cache.data_ptr()),
+                                      C.c_void_p(v_cache.data_ptr()), dt[k_cache.dtype], heads, ctx_stride, n_keys,
+                                      chunk, C.c_void_p(workspace.data_ptr()), C.c_void_p(out.data_ptr()),
+                                      dt[out.dtype], _stream(stream)))
+
+
+# ---------------------------------------------------------------- model
+
+class HipLLM:
+    """Python view of the GPU LlmModel (moss_hip_llm_*)."""
+
+    def __init__(self, blob: bytes, device: int = 0, max_ctx: int = 0, kv_fp32: bool = False, graphs: bool = True):
+        L = self.L = load()
+        self._h = C.c_void_p()
+        buf = np.frombuffer(blob, dtype=np.uint8)
+        opt = Options(device, max_ctx, 1 if kv_fp32 else 0, 1 if graphs else 0)
+        check(L.moss_hip_llm_create(_ptr(buf), buf.size, C.byref(opt), C.byref(self._h)))
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            self.L.moss_hip_llm_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def position(self) -> int:
+        return self.L.moss_hip_llm_position(self._h)
+
+    @property
+    def prefix_pos(self) -> int:
+        return self.L.moss_hip_llm_prefix_pos(self._h)
+
+    def reset(self):
+        check(self.L.moss_hip_llm_reset(self._h))
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(768, np.float32)
+        check(self.L.moss_hip_llm_get_hidden(self._h, _ptr(out)))
+        return out
+
+    def set_hidden(self, h):
+        h = np.ascontiguousarray(h, np.float32)
+        check(self.L.moss_hip_llm_set_hidden(self._h, _ptr(h)))
+
+    def prefill(self, rows, start: int = 0):
+        rows = np.ascontiguousarray(rows, np.int32).reshape(-1, 17)
+        check(self.L.moss_hip_llm_prefill(self._h, _ptr(rows), rows.shape[0], start))
+
+    def global_step(self, row):
+        row = np.ascontiguousarray(row, np.int32).reshape(17)
+        check(self.L.moss_hip_llm_global_step(self._h, _ptr(row)))
+
+    def generate(self, max_frames: int, params: SampleParams | None = None, seed: int = 0, forced=None,
+                 timing: bool = False, logits: bool = False, gate: bool = False, on_frame=None):
+        params = params or SampleParams.make()
+        out = np.zeros((max(max_frames, 1), 17), np.int32)
+        fa = np.ascontiguousarray(forced, np.int32).reshape(-1, 17) if forced is not None else None
+        t = np.zeros((max(max_frames, 1), 2), np.float64) if timing else None
+        ld = np.zeros((max(max_frames, 1), 16, 1024), np.float32) if logits else None
+        gd = np.zeros((max(max_frames, 1), 2), np.float32) if gate else None
+        n = C.c_int(0)
+        cb = FRAME_CB(lambda u, f, row: on_frame(f, np.ctypeslib.as_array(row, (17,)).copy())) if on_frame \
+            else FRAME_CB()
+        check(self.L.moss_hip_llm_generate(self._h, max_frames, C.byref(params), seed,
+                                           _ptr(fa) if fa is not None else None, 0 if fa is None else fa.shape[0],
+                                           _ptr(out), C.byref(n), _ptr(t) if t is not None else None,
+                                           _ptr(ld) if ld is not None else None, _ptr(gd) if gd is not None else None,
+                                           cb, None))
+        res = {"rows": out[:n.value]}
+        if timing:
+            res["timing"] = t[:n.value]
+        if logits:
+            res["logits"] = ld[:n.value]
+        if gate:
+            res["gate"] = gd[:min(n.value + 1, max_frames)]
+        return res
+
+    def set_cancel_flag(self, flag_array: np.ndarray | None):
+        """flag_array: a 1-element uint8 numpy array kept alive by the caller (or None)."""
+        self._cancel = flag_array
+        check(self.L.moss_hip_llm_set_cancel_flag(self._h, _ptr(flag_array) if flag_array is not None else None))
+
+    def snapshot_prefix(self):
+        check(self.L.moss_hip_llm_snapshot_prefix(self._h))
+
+    def restore_prefix(self):
+        check(self.L.moss_hip_llm_restore_prefix(self._h))
+
+    def kv_export(self, n_pos: int):
+        k = np.empty((12, n_pos, 768), np.float32)
+        v = np.empty((12, n_pos, 768), np.float32)
+        check(self.L.moss_hip_llm_kv_export(self._h, n_pos, _ptr(k), _ptr(v)))
+        return k, v
+
+    def kv_import(self, k, v, hidden=None):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        h = np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
+        check(self.L.moss_hip_llm_kv_import(self._h, k.shape[1], _ptr(k), _ptr(v), _ptr(h) if h is not None else None))

@@ -1,0 +1,154 @@
+/*
+ * moss_hip.h -- C ABI of libmoss_hip.so, the MI355X (gfx950) backend of the
+ * MOSS-TTS-Nano LLM decode path.
+ *
+ * Two layers, both plain C (no C++ types, no exceptions cross this boundary):
+ *
+ *  1. Model layer (moss_hip_llm_*): the GPU replacement of moss::LlmModel
+ *     (reference csrc/include/moss/llm.h:39-90).  Host pointers in, host
+ *     pointers out; the library owns the weights, the KV cache and the decode
+ *     state on the device.  A C++ class with LlmModel's public surface sits on
+ *     top of these calls (dsh-moss-tts_amd/host/moss_hip_llm.hpp).
+ *  2. Operator layer (moss_hip_gemv_q8x4, moss_hip_attn_decode, ...): the hot
+ *     kernels on caller-owned device memory, for tests and benchmarks.  Every
+ *     pointer argument is a device pointer; `stream` is a hipStream_t (NULL =
+ *     the default stream).
+ *
+ * Conventions (mirroring csrc/include/moss/tts.h:10-41): every int-returning
+ * call returns MOSS_HIP_OK (0) on success, non-zero on failure; the reason is
+ * available from moss_hip_last_error() on the calling thread.  A model handle
+ * is not thread-safe; calls on it must be serialised (the reference engine
+ * calls prefill on its caller thread and generate on a producer thread, never
+ * concurrently, csrc/src/engine.cpp:460-470).  Every model call makes the
+ * model's device current and uses the model's own stream.
+ */
+#ifndef MOSS_HIP_H
+#define MOSS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOSS_HIP_ABI_VERSION 1
+
+enum {
+    MOSS_HIP_OK = 0,
+    MOSS_HIP_EINVAL = 1,       /* bad argument */
+    MOSS_HIP_EDEVICE = 2,      /* HIP runtime failure */
+    MOSS_HIP_EFORMAT = 3,      /* malformed .moss / missing tensor */
+    MOSS_HIP_EUNSUPPORTED = 4, /* valid request this build does not implement */
+    MOSS_HIP_ESTATE = 5        /* call not valid in the model's current state */
+};
+
+/* Last error message of this thread (cf. moss_last_error, csrc/include/moss/tts.h:40). */
+const char *moss_hip_last_error(void);
+int moss_hip_abi_version(void);
+
+/* ------------------------------------------------------------------ model layer */
+
+typedef struct moss_hip_llm moss_hip_llm;
+
+typedef struct {
+    int device;     /* HIP device ordinal */
+    int max_ctx;    /* KV capacity in positions; 0 = 768 (kMaxCtx, csrc/include/moss/llm.h:28) */
+    int kv_dtype;   /* 0 = fp16 KV cache (default), 1 = fp32 KV cache (the reference's own precision) */
+    int use_graphs; /* 1 = replay the global step and the frame as hipGraphs (default), 0 = direct launches */
+} moss_hip_llm_options;
+
+/* SampleParams (csrc/include/moss/sampler.h:8-22), field for field. */
+typedef struct {
+    int greedy;
+    float temperature;
+    int top_k;
+    float top_p;
+    float repetition_penalty;
+    int end_greedy;
+    int min_frames;
+    int greedy_frames;
+} moss_hip_sample_params;
+
+/* on_frame callback of LlmModel::generate (llm.h:74-77): frame index and its row. */
+typedef void (*moss_hip_frame_cb)(void *user, int frame, const int32_t row[17]);
+
+/* LlmModel::LlmModel + LlmModel::load (llm.h:41-43, csrc/src/llm.cpp:59-110): parses a
+ * .moss v1 blob (csrc/src/weights.cpp:27-125), uploads it once to HBM, allocates the
+ * KV cache and the decode state.  opt may be NULL (defaults).  Only Q8_0_4X4 matrices
+ * are accepted (the release format, scripts/model_lock.json). */
+int moss_hip_llm_create(const void *moss_blob, size_t bytes, const moss_hip_llm_options *opt,
+                        moss_hip_llm **out);
+int moss_hip_llm_create_from_file(const char *path, const moss_hip_llm_options *opt, moss_hip_llm **out);
+void moss_hip_llm_destroy(moss_hip_llm *m);
+
+int moss_hip_llm_reset(moss_hip_llm *m);              /* LlmModel::reset, llm.h:46 */
+int moss_hip_llm_position(const moss_hip_llm *m);     /* LlmModel::position, llm.h:89 */
+int moss_hip_llm_get_hidden(moss_hip_llm *m, float *out768); /* LlmModel::hidden, llm.h:88 */
+int moss_hip_llm_set_hidden(moss_hip_llm *m, const float *in768);
+
+/* LlmModel::prefill (llm.h:50, llm.cpp:327-401): rows [n_rows][17], from `start`.
+ * Computed in W8A16 (the reference with MOSS_A16=1). */
+int moss_hip_llm_prefill(moss_hip_llm *m, const int32_t *rows, int n_rows, int start);
+
+/* LlmModel::global_step (llm.cpp:248-255): embed row -> 12 layers -> ln_f -> hidden; pos += 1. */
+int moss_hip_llm_global_step(moss_hip_llm *m, const int32_t *row17);
+
+/* LlmModel::generate (llm.h:74-77, llm.cpp:634-733).
+ *   forced   [n_forced][17] teacher-forcing rows or NULL; max_frames is clamped to n_forced.
+ *   out_rows [max_frames][17] receives the predicted rows; *out_frames their count.
+ *   timing   [max_frames][2] (global_ms, local_ms) or NULL (FrameTiming, llm.h:34-37).
+ *   logits_dump [max_frames][16][1024] or NULL (set_logits_dump, llm.h:80).
+ *   gate_dump   [max_frames][2] (l_end, l_slot) or NULL (set_gate_dump, llm.h:83).
+ *   cb/user: on_frame.  Greedy decoding (greedy != 0 or top_k == 1) with end_greedy != 0;
+ *   other sampling modes return MOSS_HIP_EUNSUPPORTED. */
+int moss_hip_llm_generate(moss_hip_llm *m, int max_frames, const moss_hip_sample_params *p, uint64_t seed,
+                          const int32_t *forced, int n_forced, int32_t *out_rows, int *out_frames, double *timing,
+                          float *logits_dump, float *gate_dump, moss_hip_frame_cb cb, void *user);
+
+/* LlmModel::set_cancel_flag (llm.h:86): a byte polled (relaxed) once per frame; NULL clears it.
+ * std::atomic<bool> is one byte with bool's representation on the supported ABIs. */
+int moss_hip_llm_set_cancel_flag(moss_hip_llm *m, const volatile uint8_t *flag);
+
+/* Prefix KV (llm.h:52-57, llm.cpp:455-483): device-to-device snapshot / restore. */
+int moss_hip_llm_snapshot_prefix(moss_hip_llm *m);
+int moss_hip_llm_restore_prefix(moss_hip_llm *m);
+int moss_hip_llm_prefix_pos(const moss_hip_llm *m);
+
+/* KV in the reference layout [12][n_pos][768] fp32 (llm.cpp:72-75), for the host
+ * side of save_prefix / save_state (llm.cpp:485-586).  Export converts fp16 -> fp32. */
+int moss_hip_llm_kv_export(moss_hip_llm *m, int n_pos, float *k, float *v);
+/* Import for load_prefix / load_state (llm.cpp:512-632): sets pos = n_pos and, when
+ * hidden768 != NULL, the hidden state.  fp32 values are rounded to fp16 for an fp16 cache. */
+int moss_hip_llm_kv_import(moss_hip_llm *m, int n_pos, const float *k, const float *v, const float *hidden768);
+
+/* ------------------------------------------------------------------ operator layer */
+
+enum { MOSS_HIP_F32 = 0, MOSS_HIP_F16 = 1 };
+
+/* y[rows] = W[rows][cols] x over Q8_0_4X4 weights -- gemv_par (csrc/include/moss/gemv.h:48,
+ * csrc/src/gemv.cpp:245-274) with MOSS_A16 on (row kernel csrc/src/gemv_avx2.cpp:123-150).
+ * x_dtype / y_dtype: MOSS_HIP_F32 or MOSS_HIP_F16.  rows % 4 == 0, cols % 128 == 0, cols <= 4096. */
+int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_dtype, void *y, int y_dtype,
+                       void *stream);
+
+/* Dequantise rows of a mat_rows x cols Q8_0_4X4 matrix to fp32 -- LlmModel::lookup_row
+ * (llm.cpp:114-146) / dequantize_row_q8_0_4x4 (csrc/src/quant.cpp:56-65).  rows_dev: n device
+ * int32 indices; an index outside [0, mat_rows) yields a row of NaN. */
+int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int32_t *rows_dev, int n, float *out,
+                               void *stream);
+
+/* Single-query attention over one layer's cache -- LlmModel::attention_core (llm.cpp:189-217).
+ * q [heads*64] fp32 (post-RoPE); k_cache/v_cache [heads][ctx_stride][64] of kv_dtype; the
+ * first n_keys positions are attended.  out [heads*64] of out_dtype.  workspace: device
+ * memory of moss_hip_attn_workspace_bytes(heads, ctx_stride, chunk) bytes.  chunk: keys
+ * per split (64, 128, 192 or 256; 0 = 64). */
+size_t moss_hip_attn_workspace_bytes(int heads, int ctx_stride, int chunk);
+int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
+                         int ctx_stride, int n_keys, int chunk, void *workspace, void *out, int out_dtype,
+                         void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOSS_HIP_H */

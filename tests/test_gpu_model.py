@@ -1,0 +1,184 @@
+"""The GPU LlmModel (moss_hip_llm_* through the C ABI) vs the CPU oracle (GPU).
+
+The oracle is pinned bit-exactly to the compiled reference (test_oracle_golden),
+so agreement with it is agreement with the reference.  With an fp32 KV cache the
+GPU path differs from the reference only by fp32 summation order; with the fp16
+cache the oracle emulates the fp16 KV rounding (kv_f16).
+"""
+import numpy as np
+import pytest
+from conftest import max_rel
+
+from mosship import HipLLM, SampleParams, lib
+from mosship import moss_format as mf
+from oracle import SampleParams as OSP
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def prefilled(oracle, golden_model):
+    """Oracle prefill (A16) of the golden prompt plus 40 extra rows: KV + hidden to import."""
+    blob, g = golden_model
+    rng = np.random.default_rng(77)
+    rows = np.concatenate([g["rows"], mf.text_rows(rng.integers(0, mf.VOCAB, 40))])
+    rows[10:20, 1:] = rng.integers(0, 1024, (10, 16))
+    m = oracle.model(blob)
+    m.prefill(rows, a16=True)
+    k, v = m.kv_export(len(rows))
+    return blob, rows, k, v, m.hidden()
+
+
+def _oracle_from_state(oracle, blob, k, v, hidden, kv_f16):
+    m = oracle.model(blob, kv_f16=kv_f16)
+    kk = k.astype(np.float16).astype(np.float32) if kv_f16 else k
+    vv = v.astype(np.float16).astype(np.float32) if kv_f16 else v
+    m.kv_import(kk, vv)
+    m.set_hidden(hidden)
+    return m
+
+
+def test_kv_import_export_exact(torch_gpu, prefilled):
+    blob, rows, k, v, h = prefilled
+    for kv32 in (True, False):
+        print(f"kv roundtrip kv32={kv32}", flush=True)
+        g = HipLLM(blob, kv_fp32=kv32)
+        g.kv_import(k, v, h)
+        assert g.position == len(rows)
+        k2, v2 = g.kv_export(len(rows))
+        exp_k = k if kv32 else k.astype(np.float16).astype(np.float32)  # numpy casts round to nearest even
+        exp_v = v if kv32 else v.astype(np.float16).astype(np.float32)
+        assert np.array_equal(k2, exp_k) and np.array_equal(v2, exp_v)
+        assert np.array_equal(g.hidden(), h)
+        g.close()
+
+
+@pytest.mark.parametrize("kv32", [True, False])
+@pytest.mark.parametrize("graphs", [True, False])
+def test_global_step_vs_oracle(torch_gpu, oracle, prefilled, kv32, graphs):
+    blob, rows, k, v, h = prefilled
+    print(f"global step kv32={kv32} graphs={graphs}", flush=True)
+    g = HipLLM(blob, kv_fp32=kv32, graphs=graphs)
+    g.kv_import(k, v, h)
+    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=not kv32)
+    rng = np.random.default_rng(9)
+    for step in range(3):
+        row = np.array([mf.SLOT] + list(rng.integers(0, 1024, 16)), np.int32)
+        if step == 1:
+            row[5] = mf.AUDIO_PAD
+        g.global_step(row)
+        m.global_step(row)
+        assert g.position == m.position
+        assert max_rel(g.hidden(), m.hidden()) <= TOL
+    n = g.position
+    gk, gv = g.kv_export(n)
+    ok, ov = m.kv_export(n)
+    assert np.array_equal(gk[:, :len(rows)], ok[:, :len(rows)])  # imported part untouched
+    assert max_rel(gk[:, len(rows):], ok[:, len(rows):]) <= TOL
+    assert max_rel(gv[:, len(rows):], ov[:, len(rows):]) <= TOL
+    g.close()
+
+
+@pytest.mark.parametrize("kv32", [True, False])
+def test_generate_teacher_forced(torch_gpu, oracle, prefilled, kv32):
+    """Teacher forcing (the reference's own accuracy protocol, main.cpp:146-180):
+    feed the oracle's codes, compare per-step greedy predictions."""
+    blob, rows, k, v, h = prefilled
+    frames = 8
+    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=not kv32)
+    ref = m.generate(frames, OSP.make(greedy=True, min_frames=frames), logits=True)
+    forced = ref["rows"].copy()
+    forced[:, 0] = mf.SLOT
+    g = HipLLM(blob, kv_fp32=kv32)
+    g.kv_import(k, v, h)
+    out = g.generate(frames, SampleParams.make(greedy=True, min_frames=frames), forced=forced, logits=True,
+                     timing=True)
+    assert out["rows"].shape == ref["rows"].shape
+    agree = np.mean(out["rows"][:, 1:] == ref["rows"][:, 1:])
+    print(f"teacher-forced agreement kv32={kv32}: {agree:.4f}")
+    assert agree >= 0.99
+    assert max_rel(out["logits"], ref["logits"]) <= TOL
+    assert g.position == m.position
+    assert (out["timing"][:-1, 0] > 0).all() and out["timing"][-1, 0] == 0.0  # no global step after the last frame
+
+
+def test_generate_free_running_fp32kv(torch_gpu, oracle, prefilled):
+    blob, rows, k, v, h = prefilled
+    frames = 8
+    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=False)
+    ref = m.generate(frames, OSP.make(greedy=True, min_frames=frames, repetition_penalty=1.2))
+    g = HipLLM(blob, kv_fp32=True)
+    g.kv_import(k, v, h)
+    out = g.generate(frames, SampleParams.make(greedy=True, min_frames=frames, repetition_penalty=1.2))
+    agree = np.mean(out["rows"][:, 1:] == ref["rows"][:, 1:])
+    print(f"free-running agreement (rep 1.2): {agree:.4f}")
+    assert agree >= 0.99
+    assert max_rel(g.hidden(), m.hidden()) <= TOL
+
+
+def test_generate_end_gate_matches_oracle(torch_gpu, oracle, prefilled):
+    """min_frames = 0: the W8A8 end gate decides when to stop; frame count and the
+    gate logits follow the oracle."""
+    blob, rows, k, v, h = prefilled
+    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=False)
+    ref = m.generate(6, OSP.make(greedy=True, min_frames=0), gate=True)
+    g = HipLLM(blob, kv_fp32=True)
+    g.kv_import(k, v, h)
+    out = g.generate(6, SampleParams.make(greedy=True, min_frames=0), gate=True)
+    assert len(out["rows"]) == len(ref["rows"])
+    ng = min(len(out["gate"]), len(ref["gate"]))
+    assert max_rel(out["gate"][:ng], ref["gate"][:ng]) <= TOL
+
+
+def test_prefill_vs_oracle(torch_gpu, oracle, golden_model):
+    blob, g = golden_model
+    rows = g["rows"]
+    gm = HipLLM(blob, kv_fp32=True)
+    gm.prefill(rows)
+    assert gm.position == len(rows)
+    assert max_rel(gm.hidden(), g["hidden_prefill_a16"]) <= TOL
+    m = oracle.model(blob)
+    m.prefill(rows, a16=True)
+    gk, gv = gm.kv_export(len(rows))
+    ok, ov = m.kv_export(len(rows))
+    assert max_rel(gk, ok) <= TOL and max_rel(gv, ov) <= TOL
+    # continue from start = position (multi-chunk prompts, engine.cpp:463)
+    extra = mf.text_rows(np.arange(5))
+    gm.prefill(extra, start=gm.position)
+    m.prefill(extra, start=m.position, a16=True)
+    assert gm.position == m.position
+    assert max_rel(gm.hidden(), m.hidden()) <= TOL
+
+
+def test_snapshot_restore_prefix(torch_gpu, prefilled):
+    blob, rows, k, v, h = prefilled
+    g = HipLLM(blob)
+    g.kv_import(k, v, h)
+    g.snapshot_prefix()
+    assert g.prefix_pos == len(rows)
+    k0, v0 = g.kv_export(len(rows))
+    g.global_step(np.array([mf.SLOT] + [1] * 16, np.int32))
+    g.global_step(np.array([mf.SLOT] + [2] * 16, np.int32))
+    g.restore_prefix()
+    assert g.position == len(rows)
+    k1, v1 = g.kv_export(len(rows))
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+
+
+def test_model_errors(torch_gpu, golden_model):
+    blob, _ = golden_model
+    with pytest.raises(lib.MossHipError) as e:
+        HipLLM(b"NOPE" + bytes(100))
+    assert e.value.code == lib.EFORMAT
+    with pytest.raises(lib.MossHipError) as e:
+        HipLLM(mf.synth_model(3, drop="g5.fc_in.b"))
+    assert e.value.code == lib.EFORMAT and "g5.fc_in.b" in str(e.value)
+    g = HipLLM(blob)
+    with pytest.raises(lib.MossHipError) as e:
+        g.generate(2, SampleParams.make(greedy=False, top_k=25, temperature=0.8))
+    assert e.value.code == lib.EUNSUPPORTED
+    bad = np.full((2, 17), 2000, np.int32)
+    with pytest.raises(lib.MossHipError) as e:
+        g.generate(2, SampleParams.make(), forced=bad)
+    assert e.value.code == lib.EINVAL

@@ -1,0 +1,151 @@
+"""HIP operators through the C ABI vs the CPU oracle (GPU).
+
+Tolerance: max|y - ref| / max|ref| <= 1e-3 for every floating-point output
+(the W8A16 GEMV and attention contract); dequantisation is bit-exact.
+"""
+import numpy as np
+import pytest
+from conftest import max_rel
+
+from mosship import lib
+from mosship import moss_format as mf
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("rows,cols", [(2304, 768), (768, 768), (3072, 768), (768, 3072), (1024, 768), (8, 768),
+                                       (4, 128), (16384, 768)])
+def test_gemv_f32_vs_oracle(torch_gpu, oracle, rows, cols):
+    torch = torch_gpu
+    print(f"gemv f32 rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols)
+    w = mf.synth_q8x4(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    lib.gemv_q8x4(_dev(torch, w), rows, cols, _dev(torch, x), y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle.gemv(w, rows, cols, x)
+    assert max_rel(got, ref) <= TOL
+    # and against the exact fp64 product of the exactly dequantised matrix
+    truth = mf.dequant_q8x4(w, rows, cols).astype(np.float64) @ x.astype(np.float64)
+    assert max_rel(got, truth) <= 1e-5
+
+
+def test_gemv_config0_f16(torch_gpu, oracle):
+    """K=768, N=2304, x fp16 N(0,1), y fp16 with fp32 accumulation."""
+    torch = torch_gpu
+    rows, cols = 2304, 768
+    rng = np.random.default_rng(2304)
+    w = mf.synth_q8x4(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float16)
+    y = torch.empty(rows, dtype=torch.float16, device="cuda")
+    lib.gemv_q8x4(_dev(torch, w), rows, cols, _dev(torch, x), y)
+    torch.cuda.synchronize()
+    ref = oracle.gemv(w, rows, cols, x.astype(np.float32))
+    assert max_rel(y.cpu().numpy().astype(np.float32), ref) <= TOL
+
+
+def test_gemv_large_n_sampled(torch_gpu, oracle):
+    """N = 262144 (213 MB of weights): every sampled 4-row group checked against the oracle."""
+    torch = torch_gpu
+    rows, cols = 262144, 768
+    rng = np.random.default_rng(5)
+    w = mf.synth_q8x4(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    lib.gemv_q8x4(_dev(torch, w), rows, cols, _dev(torch, x), y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    groups = np.unique(np.concatenate([[0, rows // 4 - 1], rng.integers(0, rows // 4, 400)]))
+    sub = w.reshape(rows // 4, -1)[groups]
+    ref = oracle.gemv(sub, 4 * len(groups), cols, x)
+    got_sub = got.reshape(-1, 4)[groups].ravel()
+    assert max_rel(got_sub, ref) <= TOL
+    assert np.isfinite(got).all()
+
+
+def test_dequant_rows_bit_exact(torch_gpu, oracle):
+    torch = torch_gpu
+    rng = np.random.default_rng(11)
+    rows, cols = 1024, 768
+    w = mf.synth_q8x4(rng, rows, cols)
+    idx = np.array([0, 1, 2, 3, 4, 511, 1023, 9, 7, -1, 1024], np.int32)
+    out = torch.empty((len(idx), cols), dtype=torch.float32, device="cuda")
+    lib.dequant_rows_q8x4(_dev(torch, w), rows, cols, _dev(torch, idx), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isnan(got[-2:]).all()  # out-of-range indices are flagged, never read
+    groups = w.reshape(rows // 4, -1)
+    for i, r in enumerate(idx[:-2]):
+        assert np.array_equal(got[i].view(np.uint32), oracle.dequant_row(groups[r // 4], cols // 32, r % 4).view(np.uint32))
+
+
+def _attn_case(oracle, ctx, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(768).astype(np.float32)
+    k = rng.standard_normal((ctx, 768)).astype(np.float32)
+    v = rng.standard_normal((ctx, 768)).astype(np.float32)
+    cos_t, sin_t = oracle.rope_tables(max(ctx, 1))
+    for p in range(ctx):  # K stored post-RoPE at its position, q at ctx-1
+        k[p] = oracle.rope_apply(k[p], p, cos_t, sin_t)
+    q = oracle.rope_apply(q, ctx - 1, cos_t, sin_t)
+    return q, k, v
+
+
+def _to_cache(rows_768, ctx_stride, dtype):
+    n = rows_768.shape[0]
+    c = np.zeros((12, ctx_stride, 64), dtype)
+    c[:, :n, :] = rows_768.reshape(n, 12, 64).transpose(1, 0, 2).astype(dtype)
+    return c
+
+
+@pytest.mark.parametrize("ctx", [1, 33, 128, 512, 1024, 2048])
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+@pytest.mark.parametrize("chunk", [64, 256])
+def test_attention_decode_vs_oracle(torch_gpu, oracle, ctx, kv, chunk):
+    torch = torch_gpu
+    print(f"attention ctx={ctx} kv={kv} chunk={chunk}", flush=True)
+    q, k, v = _attn_case(oracle, ctx, ctx)
+    npdt = np.float16 if kv == "f16" else np.float32
+    stride = ctx + 5
+    kc, vc = _to_cache(k, stride, npdt), _to_cache(v, stride, npdt)
+    ws = torch.empty(lib.attn_workspace_bytes(12, stride, chunk), dtype=torch.uint8, device="cuda")
+    out = torch.empty(768, dtype=torch.float32, device="cuda")
+    lib.attn_decode(_dev(torch, q), _dev(torch, kc), _dev(torch, vc), 12, stride, ctx, ws, out, chunk=chunk)
+    out16 = torch.empty(768, dtype=torch.float16, device="cuda")
+    lib.attn_decode(_dev(torch, q), _dev(torch, kc), _dev(torch, vc), 12, stride, ctx, ws, out16, chunk=chunk)
+    torch.cuda.synchronize()
+    ref = oracle.attention(k.astype(npdt).astype(np.float32), v.astype(npdt).astype(np.float32), q)
+    assert max_rel(out.cpu().numpy(), ref) <= TOL
+    assert max_rel(out16.cpu().numpy().astype(np.float32), ref) <= TOL
+
+
+def test_attention_single_key_returns_v(torch_gpu):
+    """ctx = 1: softmax over one key is 1, so the output is that key's v exactly."""
+    torch = torch_gpu
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(768).astype(np.float32)
+    k = rng.standard_normal((1, 768)).astype(np.float32)
+    v = rng.standard_normal((1, 768)).astype(np.float32)
+    ws = torch.empty(lib.attn_workspace_bytes(12, 1, 64), dtype=torch.uint8, device="cuda")
+    out = torch.empty(768, dtype=torch.float32, device="cuda")
+    lib.attn_decode(_dev(torch, q), _dev(torch, _to_cache(k, 1, np.float32)), _dev(torch, _to_cache(v, 1, np.float32)),
+                    12, 1, 1, ws, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), v[0])
+
+
+def test_operator_errors(torch_gpu):
+    torch = torch_gpu
+    w = torch.zeros(3264, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(768, dtype=torch.float32, device="cuda")
+    y = torch.zeros(6, dtype=torch.float32, device="cuda")
+    with pytest.raises(lib.MossHipError) as e:
+        lib.gemv_q8x4(w, 6, 768, x, y)  # rows % 4 != 0
+    assert e.value.code == lib.EINVAL

@@ -1,0 +1,71 @@
+"""Randomised bit-exact agreement of the C oracle with the compiled reference (CPU;
+skipped where oracle/_ref was not built)."""
+import numpy as np
+import pytest
+
+from mosship import moss_format as mf
+from oracle import SampleParams
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_gemv_bit_exact(oracle, ref, seed):
+    rng = np.random.default_rng(seed)
+    for rows, cols in [(2304, 768), (768, 3072), (1024, 768)]:
+        w = mf.synth_q8x4(rng, rows, cols)
+        x = (rng.standard_normal(cols) * 4).astype(np.float32)
+        assert np.array_equal(oracle.gemv(w, rows, cols, x).view(np.uint32),
+                              ref.gemv(w, rows, cols, x, threads=4).view(np.uint32))
+
+
+def test_thread_count_does_not_change_output(ref):
+    """Reference invariant (AGENTS.md:164): thread count never changes the result."""
+    rng = np.random.default_rng(9)
+    w = mf.synth_q8x4(rng, 3072, 768)
+    x = rng.standard_normal(768).astype(np.float32)
+    assert np.array_equal(ref.gemv(w, 3072, 768, x, threads=1), ref.gemv(w, 3072, 768, x, threads=7))
+
+
+def test_quantize_bit_exact(oracle, ref):
+    rng = np.random.default_rng(3)
+    for scale in (1e-3, 1.0, 50.0):
+        x = (rng.standard_normal(3072) * scale).astype(np.float32)
+        qo, dho, do = oracle.quantize_row(x)
+        qr, dhr, dr = ref.quantize_row(x)
+        assert np.array_equal(qo, qr) and np.array_equal(dho, dhr) and np.array_equal(do, dr)
+
+
+def test_sampler_bit_exact(oracle, ref):
+    rng = np.random.default_rng(4)
+    for trial in range(30):
+        logits = (rng.standard_normal(1024) * 3).astype(np.float32)
+        prev = rng.integers(0, 1024, rng.integers(0, 60)).astype(np.int32)
+        p = SampleParams.make(greedy=bool(trial % 3 == 0), temperature=float(rng.choice([0.5, 0.8, 1.0, 1.3])),
+                              top_k=int(rng.choice([0, 1, 5, 25])), top_p=float(rng.choice([0.5, 0.95, 1.0])),
+                              repetition_penalty=float(rng.choice([1.0, 1.2])))
+        seed = int(rng.integers(0, 2**32))
+        assert oracle.sample_token(logits, p, prev, seed=seed) == ref.sample_token(logits, p, prev, seed=seed)
+
+
+def test_model_steps_bit_exact(oracle, ref, golden_model):
+    """Prefill (W8A8), then greedy frames with the 1.2 repetition penalty: rows and
+    hidden state bit-identical between the restatement and the reference."""
+    blob, g = golden_model
+    rng = np.random.default_rng(11)
+    rows = mf.text_rows(rng.integers(0, mf.VOCAB, 20))
+    rows[5:9, 1:] = rng.integers(0, 1024, (4, 16))
+    o = oracle.model(blob)
+    r = ref.model(blob, threads=3)
+    o.prefill(rows)
+    r.prefill(rows)
+    assert np.array_equal(o.hidden(), r.hidden())
+    p = SampleParams.make(greedy=True, repetition_penalty=1.2, min_frames=6)
+    go = o.generate(6, p)
+    gr = r.generate(6, p)
+    assert np.array_equal(go["rows"], gr["rows"])
+    assert np.array_equal(o.hidden(), r.hidden())
+    # teacher forcing with arbitrary codes
+    forced = np.concatenate([np.full((4, 1), mf.SLOT), rng.integers(0, 1024, (4, 16))], axis=1).astype(np.int32)
+    fo = o.generate(4, p, forced=forced)
+    fr = r.generate(4, p, forced=forced)
+    assert np.array_equal(fo["rows"], fr["rows"])
+    assert np.array_equal(o.hidden(), r.hidden())
