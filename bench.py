@@ -1,0 +1,257 @@
+"""Benchmark of the MOSS-TTS-Nano LLM decode hot path on one MI355X.
+
+Workload (one "step" = one decoded frame): batch 1, a seeded random-init model
+with the reference's dims (12 layers, d 768, 12x64 heads, FF 3072, vocab 16384,
+W8A16 Q8_0_4X4 weights), KV cache prefilled to context 512 with N(0,1) values
+(fp16 cache), greedy decoding (min_frames = steps, so the end gate never stops
+it) replayed as hipGraphs.  A frame is what the reference's "ms/frame" counts:
+local 1-layer transformer x 17, 16 audio heads + greedy picks, the W8A8 end
+gate, and the 12-layer global step.  The global step alone is also reported.
+
+The roofline object describes the W8A16 GEMV kernel at large N (K = 768,
+N = 262144, weights cycled through a 1 GiB pool so they stream from HBM, not
+the 256 MB Infinity Cache): algorithmic bytes (N/4)(K/32)*136 + 2K + 2N per
+launch over its average duration from HIP events on its stream.
+
+cpu_baseline: the reference's own AVX2 CPU path (oracle/_ref, compiled from the
+reference sources) decoding from the same context-512 state on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu] [--mode full|gemv|decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dsh-moss-tts_amd"))
+
+HBM_PEAK_GBS = 8000.0
+CTX = 512
+GEMV_N, GEMV_K = 262144, 768
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_state(seed: int = 2024):
+    from mosship import moss_format as mf
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((12, CTX, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((12, CTX, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    hidden = rng.standard_normal(768, dtype=np.float32)
+    rows = mf.text_rows(rng.integers(0, mf.VOCAB, CTX))
+    return k, v, hidden, rows
+
+
+def bench_decode(blob, state, steps, warmup):
+    import torch
+
+    from mosship import HipLLM, SampleParams
+    k, v, hidden, _ = state
+    m = HipLLM(blob, device=0)
+    m.kv_import(k, v, hidden)
+    m.snapshot_prefix()
+    p = SampleParams.make(greedy=True, min_frames=max(steps, warmup))
+    if warmup:
+        m.generate(warmup, p)
+        m.restore_prefix()
+    m.set_hidden(hidden)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = m.generate(steps, p, timing=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    frames = len(out["rows"])
+    assert frames == steps, f"decoded {frames} of {steps} frames"
+    t = out["timing"]
+    res = {
+        "ms_per_frame": (t1 - t0) * 1e3 / frames,
+        "global_ms_event": float(np.mean(t[:-1, 0])) if frames > 1 else 0.0,
+        "local_ms_event": float(np.mean(t[:, 1])),
+        "frames": frames,
+        "end_position": m.position,
+    }
+    m.close()
+    return res
+
+
+def bench_gemv(reps: int = 60):
+    """Large-N W8A16 GEMV on torch's current stream, timed with HIP events around
+    `reps` launches; weights rotate through a pool larger than the MALL (cold) and,
+    separately, one buffer is reused (warm)."""
+    import torch
+
+    from mosship import lib
+    from mosship import moss_format as mf
+    rows, cols = GEMV_N, GEMV_K
+    wbytes = (rows // 4) * (cols // 32) * 136
+    algo = wbytes + 2 * cols + 2 * rows
+    rng = np.random.default_rng(42)
+    host = mf.synth_q8x4(rng, rows, cols)
+    pool_n = max(2, -(-(1 << 30) // wbytes))  # >= 1 GiB of distinct weights
+    base = torch.from_numpy(host.reshape(-1)).cuda()
+    pool = [base] + [torch.roll(base, 136 * 4 * (i + 1)) for i in range(pool_n - 1)]
+    x = torch.from_numpy(rng.standard_normal(cols).astype(np.float16)).cuda()
+    y = torch.empty(rows, dtype=torch.float16, device="cuda")
+    s = torch.cuda.current_stream()
+    for w in pool:
+        lib.gemv_q8x4(w, rows, cols, x, y)
+    torch.cuda.synchronize()
+    out = {}
+    for mode in ("cold", "warm"):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(reps):
+            lib.gemv_q8x4(pool[i % pool_n] if mode == "cold" else pool[0], rows, cols, x, y)
+        e1.record(s)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        out[mode] = {"us": us, "GBps": algo / us / 1e3}
+    out["algo_bytes"] = algo
+    out["pool_buffers"] = pool_n
+    # config 0 shape (K=768, N=2304): latency-bound, reported for completeness
+    w0 = torch.from_numpy(mf.synth_q8x4(rng, 2304, 768).reshape(-1)).cuda()
+    y0 = torch.empty(2304, dtype=torch.float16, device="cuda")
+    for _ in range(10):
+        lib.gemv_q8x4(w0, 2304, 768, x, y0)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(200):
+        lib.gemv_q8x4(w0, 2304, 768, x, y0)
+    e1.record(s)
+    torch.cuda.synchronize()
+    us0 = e0.elapsed_time(e1) * 1e3 / 200
+    out["config0"] = {"us": us0, "GBps": 1886208 / us0 / 1e3}
+    return out
+
+
+def cpu_baseline(blob, state, frames: int = 48):
+    """The compiled reference (oracle/_ref) decoding from the same ctx-512 state."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import REF_SO, RefCpu, SampleParams
+
+    from mosship import moss_format as mf
+    if not os.path.exists(REF_SO):
+        return None
+    k, v, hidden, rows = state
+    threads = 4  # the reference's published setting (README.md:40)
+    r = RefCpu(a16_mode="decode")
+    m = r.model(blob, threads=threads)
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "ctx512.state")
+        with open(path, "wb") as f:
+            f.write(mf.write_state(k, v, hidden, rows, mf.fp_weights(blob)))
+        m.load_state(path, rows, ignore_fp=False)
+        p = SampleParams.make(greedy=True, min_frames=frames)
+        m.generate(3, p)  # 3-frame warmup (the reference's protocol)
+        m.load_state(path, rows, ignore_fp=False)
+        t0 = time.perf_counter()
+        out = m.generate(frames, p, timing=True)
+        t1 = time.perf_counter()
+    n = len(out["rows"])
+    t = out["timing"]
+    m.close()
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {
+        "value": (t1 - t0) * 1e3 / n,
+        "unit": "ms/frame",
+        "cores": threads,
+        "kind": "reference",
+        "sample": f"{n} greedy frames from the ctx-512 state, MOSS_A16=decode, {threads} threads, "
+                  f"global {np.mean(t[:-1, 0]) * n / max(n - 1, 1):.2f} + local {np.mean(t[:, 1]):.2f} ms/frame; "
+                  f"host {cpu_model}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mode", choices=["full", "gemv", "decode"], default="full")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 2 or args.steps > 256:
+        sys.exit("--steps must be in [2, 256]: the ctx-512 cache holds 256 more positions (kMaxCtx 768)")
+    import torch
+    if not torch.cuda.is_available():
+        sys.exit("no GPU visible")
+    from mosship import moss_format as mf
+
+    if args.mode == "gemv":
+        g = bench_gemv()
+        print(json.dumps({"gemv": g}), flush=True)
+        return
+
+    log("generating synthetic model + ctx-512 state")
+    blob = mf.synth_model(1234)
+    state = make_state()
+    log("decode")
+    d = bench_decode(blob, state, args.steps, args.warmup)
+    if args.mode == "decode":
+        print(json.dumps({"decode": d}), flush=True)
+        return
+    log("gemv roofline")
+    g = bench_gemv()
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (reference)")
+        cpu = cpu_baseline(blob, state)
+    # global step at position 512: weights + vectors + embed + fp16 KV read/write
+    global_bytes = 90243072 + 485376 + 13872 + 36864 * (CTX + 1) + 36864
+    line = {
+        "metric": "LLM decode ms/frame (bs1, ctx 512); frames/s @64 streams; GEMV GB/s",
+        "value": round(d["ms_per_frame"], 4),
+        "unit": "ms/frame",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_frame"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w8a16 (int8 weights, fp32 activations/accumulation, fp16 KV)",
+        "data": "synthetic (seeded random-init weights with the reference's dims; N(0,1) fp16 KV at ctx 512)",
+        "config": {"workload": "LLM decode, batch 1, ctx 512 -> 767, 256 greedy frames under hipGraph "
+                               "(full frame = 17 local steps + 16 heads + end gate + 12-layer global step)",
+                   "global_batch": 1, "seq_len": CTX, "parallelism": "none (1 GPU)"},
+        "frames_per_s": round(1e3 / d["ms_per_frame"], 1),
+        "global_step_ms": round(d["global_ms_event"], 4),
+        "local_ms_per_frame": round(d["local_ms_event"], 4),
+        "global_step_GBps": round(global_bytes / (d["global_ms_event"] * 1e-3) / 1e9, 1),
+        "gemv": {"cold_GBps": round(g["cold"]["GBps"], 1), "warm_GBps": round(g["warm"]["GBps"], 1),
+                 "config0_us": round(g["config0"]["us"], 3), "config0_GBps": round(g["config0"]["GBps"], 1)},
+        "roofline": {
+            "kernel": f"gemv_q8x4 (fp16 in/out), N={GEMV_N} K={GEMV_K}, weights cycled over "
+                      f"{g['pool_buffers']} buffers (cold)",
+            "bound": "hbm",
+            "achieved": round(g["cold"]["GBps"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g["cold"]["GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

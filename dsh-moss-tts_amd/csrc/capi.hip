@@ -197,26 +197,15 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
     });
 }
 
-size_t moss_hip_attn_workspace_bytes(int heads, int ctx_stride, int chunk) {
-    if (chunk <= 0) chunk = 64;
-    if (heads <= 0 || ctx_stride <= 0) return 0;
-    const size_t splits = (size_t)(ctx_stride + chunk - 1) / chunk;
-    return (size_t)heads * splits * (mh::kHeadDim + 2) * sizeof(float);
-}
-
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
-                         int ctx_stride, int n_keys, int chunk, void *workspace, void *out, int out_dtype,
-                         void *stream) {
+                         int ctx_stride, int n_keys, void *out, int out_dtype, void *stream) {
     return guard([&] {
-        if (!q || !k_cache || !v_cache || !workspace || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
-        if (chunk <= 0) chunk = 64;
-        if (chunk % 64 || chunk > 256) throw Status(MOSS_HIP_EINVAL, "chunk must be 64, 128, 192 or 256");
+        if (!q || !k_cache || !v_cache || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
         if (heads <= 0 || ctx_stride <= 0 || n_keys <= 0 || n_keys > ctx_stride)
             throw Status(MOSS_HIP_EINVAL, "need 0 < n_keys <= ctx_stride");
+        if (n_keys > mh::attn_max_keys()) throw Status(MOSS_HIP_EINVAL, "n_keys above 4096");
         if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
             throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
-        const int splits = (ctx_stride + chunk - 1) / chunk;
-        float *ws = static_cast<float *>(workspace);
         mh::AttnArgs a;
         a.q = q;
         a.k_cache = k_cache;
@@ -224,14 +213,11 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
         a.ctx_stride = ctx_stride;
         a.heads = heads;
         a.pos_const = n_keys - 1;
-        a.chunk = chunk;
-        a.max_splits = splits;
-        a.part_o = ws;
-        a.part_ml = ws + (size_t)heads * splits * mh::kHeadDim;
+        a.max_keys = n_keys;
+        a.out = out;
+        a.out_f16 = out_dtype == MOSS_HIP_F16;
         const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
-        auto s = static_cast<hipStream_t>(stream);
-        mh::hip_check(mh::launch_attn_split(a, kv, s), "attention launch");
-        mh::hip_check(mh::launch_attn_merge(a, out, out_dtype == MOSS_HIP_F16, s), "merge launch");
+        mh::hip_check(mh::launch_attn_decode(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
     });
 }
 

@@ -7,22 +7,26 @@ namespace {
 // x = deq(wte[row[0]]) + sum over ch of deq(aemb[ch][row[ch+1]]), pads skipped,
 // channels added in order (reference csrc/src/llm.cpp:148-157).  Each element is
 // an independent serial fp32 sum, so this is bit-identical to the reference.
-__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+// One thread per column (12 workgroups of 64); the 17 gathers are issued
+// unconditionally (skipped channels read row 0 and are not added) so they are
+// all in flight together.
+__global__ __launch_bounds__(64) void embed_kernel(EmbedArgs a) {
     if (a.state != nullptr && a.state->stop) return;
     const int nb = kHidden / 32;
-    int row[kNVq + 1];
+    const int c = blockIdx.x * 64 + threadIdx.x;
+    float e[kNVq];
+    bool use[kNVq];
 #pragma unroll
-    for (int i = 0; i <= kNVq; ++i) row[i] = a.row[i];
-    for (int c = threadIdx.x; c < kHidden; c += 256) {
-        float v = q8x4_elem(a.wte, nb, row[0], c);
-#pragma unroll
-        for (int ch = 0; ch < kNVq; ++ch) {
-            const int code = row[ch + 1];
-            if (code == kAudioPad || code < 0 || code >= kCodebook) continue;
-            v = v + q8x4_elem(a.aemb[ch], nb, code, c);
-        }
-        a.x[c] = v;
+    for (int ch = 0; ch < kNVq; ++ch) {
+        const int code = a.row[ch + 1];
+        use[ch] = !(code == kAudioPad || code < 0 || code >= kCodebook);
+        e[ch] = q8x4_elem(a.aemb[ch], nb, use[ch] ? code : 0, c);
     }
+    float v = q8x4_elem(a.wte, nb, a.row[0], c);
+#pragma unroll
+    for (int ch = 0; ch < kNVq; ++ch)
+        if (use[ch]) v = v + e[ch];
+    a.x[c] = v;
 }
 
 __global__ __launch_bounds__(256) void layernorm_kernel(const float *x, const float *w, const float *b, float *out,
@@ -230,7 +234,7 @@ __global__ void kv_export_kernel(const void *src, int n_pos, int ctx_stride, flo
 }  // namespace
 
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(embed_kernel, dim3(kHidden / 64), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -14,8 +14,8 @@
 // lanes of a row.  SPLIT waves may share one group (split-K), reduced through
 // LDS in a fixed order, so results never depend on the launch shape's timing.
 //
-// Prologues stage the activation: plain fp32/fp16, LayerNorm (llm.cpp:159-171)
-// or the split-KV attention merge; epilogues fuse what block_forward
+// Prologues stage the activation: plain fp32/fp16 or LayerNorm (llm.cpp:159-171);
+// epilogues fuse what block_forward
 // (llm.cpp:230-246) does next to each GEMV: bias + RoPE + KV write (QKV),
 // residual add (proj, fc_out), bias + gelu_new (fc_in).
 #include "mh_ops.h"
@@ -45,23 +45,6 @@ __device__ __forceinline__ void stage_activation(const GemvArgs &a, float *act, 
         layernorm_768(v, a.ln_w, a.ln_b, o, red);
 #pragma unroll
         for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
-    } else {  // PRO_MERGE: K = heads * 64
-        const int n = (a.pos_ptr ? *a.pos_ptr : a.pos_const) + 1;
-        const int nsplit = (n + a.chunk - 1) / a.chunk;
-        for (int e = t; e < K; e += 256) {
-            const int h = e >> 6, d = e & 63;
-            const float *ml = a.part_ml + (size_t)h * a.max_splits * 2;
-            const float *po = a.part_o + (size_t)h * a.max_splits * 64 + d;
-            float m = -INFINITY;
-            for (int s = 0; s < nsplit; ++s) m = fmaxf(m, ml[2 * s]);
-            float l = 0.0f, o = 0.0f;
-            for (int s = 0; s < nsplit; ++s) {
-                const float w = expf(ml[2 * s] - m);
-                l = fmaf(ml[2 * s + 1], w, l);
-                o = fmaf(po[(size_t)s * 64], w, o);
-            }
-            act[e] = o / l;
-        }
     }
 }
 
@@ -110,15 +93,56 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int r, float v, fl
     }
 }
 
-template <int PRO, int EPI, int SPLIT, int KV>
+// Up to NB blocks per lane are in flight at once: all loads of a batch are
+// issued before the first is consumed.  NB is picked per shape so a wave's
+// K-slice is one batch whenever it is at most 32 blocks.
+//
+// Loads are unconditional (the block index is clamped to the wave's last block,
+// so every address is valid): guarded loads would make the compiler wait on
+// each one in turn.
+template <int NB>
+__device__ __forceinline__ void load_batch(const uint8_t *grp, int first_b, int b1, int u, int kk, uint2 (&qv)[NB],
+                                           uint16_t (&dh)[NB]) {
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+        const int b = min(first_b + 4 * it, b1 - 1);
+        const uint8_t *blk = grp + (size_t)b * kBlockBytes;
+        const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 8 * u));
+        qv[it] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
+        dh[it] = *(const uint16_t *)(blk + 2 * kk);
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1, int j, const uint2 (&qv)[NB],
+                                           const uint16_t (&dh)[NB], float acc) {
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+        const int b = first_b + 4 * it;
+        if (b < b1) {
+            const float4 x0 = *(const float4 *)(act + b * 32 + 8 * j);
+            const float4 x1 = *(const float4 *)(act + b * 32 + 8 * j + 4);
+            const uint2 q = qv[it];
+            float s = (float)(int8_t)(q.x) * x0.x;
+            s = fmaf((float)(int8_t)(q.x >> 8), x0.y, s);
+            s = fmaf((float)(int8_t)(q.x >> 16), x0.z, s);
+            s = fmaf((float)(int8_t)(q.x >> 24), x0.w, s);
+            s = fmaf((float)(int8_t)(q.y), x1.x, s);
+            s = fmaf((float)(int8_t)(q.y >> 8), x1.y, s);
+            s = fmaf((float)(int8_t)(q.y >> 16), x1.z, s);
+            s = fmaf((float)(int8_t)(q.y >> 24), x1.w, s);
+            acc = fmaf(s, h2f(dh[it]), acc);
+        }
+    }
+    return acc;
+}
+
+template <int PRO, int EPI, int SPLIT, int KV, int NB>
 __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     extern __shared__ float act[];
     __shared__ float red[4];
     __shared__ float part[4][4];
     if (a.state != nullptr && a.state->stop) return;
-
-    stage_activation<PRO>(a, act, red);
-    __syncthreads();
 
     constexpr int GPW = 4 / SPLIT;  // groups per workgroup pass
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -128,29 +152,26 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     const int bl = lane >> 4, u = lane & 15, kk = u >> 2, j = u & 3;
     const int per = (nb + SPLIT - 1) / SPLIT;
     const int b0 = ks * per, b1 = min(nb, b0 + per);
+    const int gfirst = blockIdx.x * GPW;
 
-    for (int gb = blockIdx.x * GPW; gb < ngroups; gb += gridDim.x * GPW) {
+    // The weights do not depend on the activation: start streaming this wave's
+    // first batch before the prologue (activation load, LayerNorm) runs.
+    uint2 qv[NB];
+    uint16_t dh[NB];
+    if (gfirst + gslot < ngroups) load_batch<NB>(a.w + (size_t)(gfirst + gslot) * nb * kBlockBytes, b0 + bl, b1, u, kk, qv, dh);
+
+    stage_activation<PRO>(a, act, red);
+    __syncthreads();
+
+    for (int gb = gfirst; gb < ngroups; gb += gridDim.x * GPW) {
         const int g = gb + gslot;
         const bool valid = g < ngroups;
         float acc = 0.0f;
         if (valid) {
             const uint8_t *grp = a.w + (size_t)g * nb * kBlockBytes;
-#pragma unroll 4
-            for (int b = b0 + bl; b < b1; b += 4) {
-                const uint8_t *blk = grp + (size_t)b * kBlockBytes;
-                const uint2 qv = *(const uint2 *)(blk + 8 + 8 * u);
-                const float d = h2f(*(const uint16_t *)(blk + 2 * kk));
-                const float4 x0 = *(const float4 *)(act + b * 32 + 8 * j);
-                const float4 x1 = *(const float4 *)(act + b * 32 + 8 * j + 4);
-                float s = (float)(int8_t)(qv.x) * x0.x;
-                s = fmaf((float)(int8_t)(qv.x >> 8), x0.y, s);
-                s = fmaf((float)(int8_t)(qv.x >> 16), x0.z, s);
-                s = fmaf((float)(int8_t)(qv.x >> 24), x0.w, s);
-                s = fmaf((float)(int8_t)(qv.y), x1.x, s);
-                s = fmaf((float)(int8_t)(qv.y >> 8), x1.y, s);
-                s = fmaf((float)(int8_t)(qv.y >> 16), x1.z, s);
-                s = fmaf((float)(int8_t)(qv.y >> 24), x1.w, s);
-                acc = fmaf(s, d, acc);
+            for (int base = b0; base < b1; base += 4 * NB) {
+                if (base != b0 || gb != gfirst) load_batch<NB>(grp, base + bl, b1, u, kk, qv, dh);
+                acc = dot_batch<NB>(act, base + bl, b1, j, qv, dh, acc);
             }
         }
         acc += __shfl_xor(acc, 1);
@@ -171,26 +192,33 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     }
 }
 
-template <int PRO, int EPI, int KV>
-hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
+template <int PRO, int EPI, int SPLIT, int KV>
+hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
     const int ngroups = a.rows / 4;
+    constexpr int GPW = 4 / SPLIT;
+    int grid = (ngroups + GPW - 1) / GPW;
+    grid = grid > 4096 ? 4096 : grid;
     const size_t lds = (size_t)a.cols * sizeof(float);
-    auto grid_for = [&](int gpw) {
-        int g = (ngroups + gpw - 1) / gpw;
-        return g > 4096 ? 4096 : g;
-    };
-    switch (split) {
-        case 4:
-            hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, 4, KV>), dim3(grid_for(1)), dim3(256), lds, s, a);
-            break;
-        case 2:
-            hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, 2, KV>), dim3(grid_for(2)), dim3(256), lds, s, a);
-            break;
-        default:
-            hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, 1, KV>), dim3(grid_for(4)), dim3(256), lds, s, a);
-            break;
+    switch (nbatch) {
+        case 2: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 2>), dim3(grid), dim3(256), lds, s, a); break;
+        case 3: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 3>), dim3(grid), dim3(256), lds, s, a); break;
+        case 6: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 6>), dim3(grid), dim3(256), lds, s, a); break;
+        default: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 8>), dim3(grid), dim3(256), lds, s, a); break;
     }
     return hipGetLastError();
+}
+
+template <int PRO, int EPI, int KV>
+hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
+    // blocks per wave -> batch size (iterations of 4 blocks), one of 2, 3, 6, 8
+    const int per = (a.cols / 32 + split - 1) / split;
+    const int its = (per + 3) / 4;
+    const int nbatch = its <= 2 ? 2 : its <= 3 ? 3 : its <= 6 ? 6 : 8;
+    switch (split) {
+        case 4: return launch_nb<PRO, EPI, 4, KV>(a, nbatch, s);
+        case 2: return launch_nb<PRO, EPI, 2, KV>(a, nbatch, s);
+        default: return launch_nb<PRO, EPI, 1, KV>(a, nbatch, s);
+    }
 }
 
 // Waves per 4-row group: enough workgroups to cover the 256 CUs at small N,
@@ -208,7 +236,7 @@ int pick_split(int rows, int cols) {
 
 hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv, hipStream_t s) {
     if (a.rows % 4 != 0 || a.cols % 128 != 0 || a.cols > 4096 || a.rows <= 0) return hipErrorInvalidValue;
-    if ((pro == PRO_LN || pro == PRO_MERGE) && a.cols != kHidden) return hipErrorInvalidValue;
+    if (pro == PRO_LN && a.cols != kHidden) return hipErrorInvalidValue;
     if (epi == EPI_QKV && a.rows != 3 * kHidden) return hipErrorInvalidValue;
     const int split = pick_split(a.rows, a.cols);
 #define MH_CASE(P, E)                                                                         \
@@ -221,7 +249,6 @@ hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv,
     MH_CASE(PRO_F16, EPI_F32)
     MH_CASE(PRO_F32, EPI_F16)
     MH_CASE(PRO_LN, EPI_QKV)
-    MH_CASE(PRO_MERGE, EPI_RESID)
     MH_CASE(PRO_LN, EPI_GELU)
     MH_CASE(PRO_F32, EPI_RESID)
     MH_CASE(PRO_LN, EPI_F32)

@@ -90,8 +90,7 @@ private:
     int rope_n_ = 0;
     float *x_ = nullptr, *q_ = nullptr, *mlp_ = nullptr, *hidden_ = nullptr;
     float *lres_ = nullptr, *next_in_ = nullptr, *slot_in_ = nullptr;
-    float *part_o_ = nullptr, *part_ml_ = nullptr;
-    int max_splits_ = 0, chunk_ = 64;
+    float *attn_out_ = nullptr;
     float *logits_ = nullptr;            // [16][1024]
     int *counts_ = nullptr;              // [16][1024]
     int *forced_ = nullptr;              // [max_ctx][16]

@@ -159,8 +159,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     hip_check(hipMalloc(&rope_, rope.size() * 4), "hipMalloc(rope)");
     hip_check(hipMemcpy(rope_, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "upload rope");
 
-    chunk_ = 64;
-    max_splits_ = (max_ctx_ + chunk_ - 1) / chunk_;
+    if (max_ctx_ > attn_max_keys()) throw Status(MOSS_HIP_EINVAL, "max_ctx above the attention kernel's key capacity");
     auto fmalloc = [&](float **p, size_t n) { hip_check(hipMalloc(p, n * 4), "hipMalloc(act)"); };
     fmalloc(&x_, kHidden);
     fmalloc(&q_, kHidden);
@@ -169,8 +168,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     fmalloc(&lres_, kHidden);
     fmalloc(&next_in_, kHidden);
     fmalloc(&slot_in_, kHidden);
-    fmalloc(&part_o_, (size_t)kHeads * max_splits_ * kHeadDim);
-    fmalloc(&part_ml_, (size_t)kHeads * max_splits_ * 2);
+    fmalloc(&attn_out_, kHidden);
     fmalloc(&logits_, (size_t)kNVq * kCodebook);
     fmalloc(&gate_log_, 2ull * (max_ctx_ + 2));
     hip_check(hipMalloc(&counts_, sizeof(int) * kNVq * kCodebook), "hipMalloc(counts)");
@@ -197,8 +195,7 @@ Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, part_o_, part_ml_,
-                    logits_, counts_, forced_, gate_log_, rows_dev_, state_, snap_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, logits_, counts_, forced_, gate_log_, rows_dev_, state_, snap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -214,9 +211,9 @@ void *Model::kv_layer(int which, int layer) const {
 
 // One global step: embed_row -> 12 x block_forward -> ln_f (llm.cpp:248-255).
 // block_forward (llm.cpp:230-246) is five kernels: QKV GEMV with LN1 fused in its
-// prologue and bias + RoPE + KV write in its epilogue; split-KV attention; proj
-// GEMV merging the attention splits in its prologue and adding the residual in
-// its epilogue; fc_in GEMV with LN2 in, bias + gelu out; fc_out GEMV with the
+// prologue and bias + RoPE + KV write in its epilogue; attention (one workgroup
+// per head, split-KV over its waves); proj GEMV adding bias and residual in its
+// epilogue; fc_in GEMV with LN2 in, bias + gelu out; fc_out GEMV with the
 // residual out.  Every position-dependent kernel reads state->pos.
 void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
     const int *pos = &state_->pos;
@@ -240,15 +237,13 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
 
         AttnArgs t;
         t.q = q_; t.k_cache = a.k_cache; t.v_cache = a.v_cache; t.ctx_stride = max_ctx_;
-        t.pos_ptr = pos; t.chunk = chunk_; t.max_splits = max_splits_;
-        t.part_o = part_o_; t.part_ml = part_ml_; t.state = state_;
-        hip_check(launch_attn_split(t, kvt_, s), "attention");
+        t.pos_ptr = pos; t.max_keys = max_ctx_; t.out = attn_out_; t.state = state_;
+        hip_check(launch_attn_decode(t, kvt_, s), "attention");
 
         GemvArgs p;
         p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
-        p.part_o = part_o_; p.part_ml = part_ml_; p.max_splits = max_splits_; p.chunk = chunk_; p.pos_ptr = pos;
-        p.y = x_; p.bias = L.proj_b; p.state = state_;
-        hip_check(launch_gemv(p, PRO_MERGE, EPI_RESID, kvt_, s), "proj gemv");
+        p.x = attn_out_; p.y = x_; p.bias = L.proj_b; p.state = state_;
+        hip_check(launch_gemv(p, PRO_F32, EPI_RESID, kvt_, s), "proj gemv");
 
         GemvArgs f1;
         f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;
@@ -279,19 +274,16 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
     a.pos_const = lpos; a.state = state_;
     hip_check(launch_gemv(a, PRO_LN, EPI_QKV, KV_F32, s), "local qkv");
 
-    // At most 17 keys: only split 0 has work (the others exit at once); partials keep
-    // the model-wide head stride of max_splits_ so the proj prologue reads them alike.
+    // At most 17 keys: a single split per head, normalised in place.
     AttnArgs t;
     t.q = q_; t.k_cache = lk; t.v_cache = lv; t.ctx_stride = kLocalLen;
-    t.pos_const = lpos; t.chunk = chunk_; t.max_splits = max_splits_;
-    t.part_o = part_o_; t.part_ml = part_ml_; t.state = state_;
-    hip_check(launch_attn_split(t, KV_F32, s), "local attention");
+    t.pos_const = lpos; t.max_keys = kLocalLen; t.out = attn_out_; t.state = state_;
+    hip_check(launch_attn_decode(t, KV_F32, s), "local attention");
 
     GemvArgs p;
     p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
-    p.part_o = part_o_; p.part_ml = part_ml_; p.max_splits = max_splits_; p.chunk = chunk_; p.pos_const = lpos;
-    p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_;
-    hip_check(launch_gemv(p, PRO_MERGE, EPI_RESID, KV_F32, s), "local proj");
+    p.x = attn_out_; p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_;
+    hip_check(launch_gemv(p, PRO_F32, EPI_RESID, KV_F32, s), "local proj");
 
     GemvArgs f1;
     f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;

@@ -13,7 +13,6 @@ enum Prologue : int {
     PRO_F32 = 0,    // x: float[cols]
     PRO_F16 = 1,    // x: half[cols]
     PRO_LN = 2,     // x: float[768], LayerNorm(ln_w, ln_b) applied in the prologue
-    PRO_MERGE = 3,  // x: split-KV attention partials, log-sum-exp merged in the prologue
 };
 
 // What happens to each output row.
@@ -33,8 +32,6 @@ struct GemvArgs {
     // prologue
     const void *x = nullptr;
     const float *ln_w = nullptr, *ln_b = nullptr;
-    const float *part_o = nullptr, *part_ml = nullptr;  // PRO_MERGE: [heads][max_splits][64], [heads][max_splits][2]
-    int max_splits = 0, chunk = 0;
     // epilogue
     void *y = nullptr;
     const float *resid_in = nullptr;  // EPI_RESID reads the residual from here (nullptr: from y)
@@ -43,7 +40,7 @@ struct GemvArgs {
     void *k_cache = nullptr, *v_cache = nullptr;  // [heads][ctx_stride][64]
     int ctx_stride = 0;
     const float *rope_cos = nullptr, *rope_sin = nullptr;  // [pos][32]
-    // position: *pos_ptr when non-null, else pos_const (MERGE uses pos + 1 keys)
+    // position (EPI_QKV): *pos_ptr when non-null, else pos_const
     const int *pos_ptr = nullptr;
     int pos_const = 0;
     const DevState *state = nullptr;  // when non-null, the kernel is a no-op once state->stop is set
@@ -53,20 +50,20 @@ struct GemvArgs {
 hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv, hipStream_t s);
 
 struct AttnArgs {
-    const float *q = nullptr;                       // [heads*64] fp32 (post-RoPE)
+    const float *q = nullptr;                           // [heads*64] fp32 (post-RoPE)
     const void *k_cache = nullptr, *v_cache = nullptr;  // [heads][ctx_stride][64]
     int ctx_stride = 0;
     int heads = kHeads;
     const int *pos_ptr = nullptr;  // keys = *pos_ptr + 1 (or pos_const + 1)
     int pos_const = 0;
-    int chunk = 64;                // positions per split (multiple of 64, <= 256)
-    int max_splits = 0;            // grid.x; splits beyond the live key count exit at once
-    float *part_o = nullptr, *part_ml = nullptr;
+    int max_keys = 0;              // capacity the launch shape is sized for (<= attn_max_keys())
+    void *out = nullptr;           // [heads*64] normalised output
+    int out_f16 = 0;               // out is half (else float)
     const DevState *state = nullptr;
 };
-hipError_t launch_attn_split(const AttnArgs &a, KvType kv, hipStream_t s);
-// Standalone merge: out[heads*64] (fp32 or fp16) from the partials.
-hipError_t launch_attn_merge(const AttnArgs &a, void *out, int out_f16, hipStream_t s);
+// Decode attention, one workgroup per head (split-KV across its waves, LDS merge).
+int attn_max_keys();
+hipError_t launch_attn_decode(const AttnArgs &a, KvType kv, hipStream_t s);
 
 // ---- frame / step kernels (frame_ops.hip)
 struct EmbedArgs {

@@ -23,7 +23,7 @@ EXPORTED = [
     "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
     "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
     "moss_hip_llm_kv_export", "moss_hip_llm_kv_import",
-    "moss_hip_gemv_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_workspace_bytes", "moss_hip_attn_decode",
+    "moss_hip_gemv_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
 ]
 
 
@@ -85,9 +85,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_llm_kv_import.argtypes = [vp, i32, vp, vp, vp]
     L.moss_hip_gemv_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp]
     L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
-    L.moss_hip_attn_workspace_bytes.argtypes = [i32, i32, i32]
-    L.moss_hip_attn_workspace_bytes.restype = C.c_size_t
-    L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp, vp, i32, vp]
+    L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
     _lib = L
     return L
 
@@ -123,18 +121,12 @@ def dequant_rows_q8x4(w, mat_rows: int, cols: int, rows_idx, out, stream=None) -
                                             rows_idx.numel(), C.c_void_p(out.data_ptr()), _stream(stream)))
 
 
-def attn_workspace_bytes(heads: int, ctx_stride: int, chunk: int = 64) -> int:
-    return load().moss_hip_attn_workspace_bytes(heads, ctx_stride, chunk)
-
-
-def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, workspace, out, chunk: int = 64,
-                stream=None) -> None:
+def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, out, stream=None) -> None:
     import torch
     dt = {torch.float32: F32, torch.float16: F16}
     check(load().moss_hip_attn_decode(C.c_void_p(q.data_ptr()), C.c_void_p(k_cache.data_ptr()),
                                       C.c_void_p(v_cache.data_ptr()), dt[k_cache.dtype], heads, ctx_stride, n_keys,
-                                      chunk, C.c_void_p(workspace.data_ptr()), C.c_void_p(out.data_ptr()),
-                                      dt[out.dtype], _stream(stream)))
+                                      C.c_void_p(out.data_ptr()), dt[out.dtype], _stream(stream)))
 
 
 # ---------------------------------------------------------------- model

@@ -140,13 +140,9 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
 
 /* Single-query attention over one layer's cache -- LlmModel::attention_core (llm.cpp:189-217).
  * q [heads*64] fp32 (post-RoPE); k_cache/v_cache [heads][ctx_stride][64] of kv_dtype; the
- * first n_keys positions are attended.  out [heads*64] of out_dtype.  workspace: device
- * memory of moss_hip_attn_workspace_bytes(heads, ctx_stride, chunk) bytes.  chunk: keys
- * per split (64, 128, 192 or 256; 0 = 64). */
-size_t moss_hip_attn_workspace_bytes(int heads, int ctx_stride, int chunk);
+ * first n_keys (<= 4096) positions are attended.  out [heads*64] of out_dtype. */
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
-                         int ctx_stride, int n_keys, int chunk, void *workspace, void *out, int out_dtype,
-                         void *stream);
+                         int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
 
 #ifdef __cplusplus
 }
