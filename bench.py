@@ -16,7 +16,12 @@ launch over its average duration from HIP events on its stream.
 cpu_baseline: the reference's own AVX2 CPU path (oracle/_ref, compiled from the
 reference sources) decoding from the same context-512 state on this host.
 
-Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu] [--mode full|gemv|decode]
+Also reported: the 256-row prefill (ms, TFLOP/s against the 2.5 PFLOP/s fp16
+MFMA peak) and 64 streams with contexts ~ U[64, 1024] decoded 128 frames in
+lock-step (aggregate frames/s), each next to the reference on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
+                       [--mode full|gemv|decode|prefill|streams]
 """
 from __future__ import annotations
 
@@ -133,6 +138,161 @@ def bench_gemv(reps: int = 60):
     return out
 
 
+PREFILL_ROWS = 256
+PREFILL_FLOP = 44_699_222_016  # 2*256*84,934,656 (GEMMs) + 144*256*32,896 (causal attention)
+MFMA_F16_PEAK_TFLOPS = 2500.0
+STREAMS, STREAM_STEPS = 64, 128
+
+
+def prefill_rows(seed: int = 7):
+    from mosship import moss_format as mf
+    rng = np.random.default_rng(seed)
+    return mf.text_rows(rng.integers(0, mf.VOCAB, PREFILL_ROWS))  # codes = pad, as make_text_row
+
+
+def bench_prefill(blob, reps: int = 5):
+    """256-row prefill from position 0 (KV written for decode), MFMA W8A16 GEMMs."""
+    import torch
+
+    from mosship import HipLLM
+    rows = prefill_rows()
+    m = HipLLM(blob, device=0)
+    for _ in range(2):
+        m.prefill(rows)
+    times = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill(rows)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    m.close()
+    ms = float(np.median(times)) * 1e3
+    tflops = PREFILL_FLOP / (ms * 1e-3) / 1e12
+    return {"ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
+
+
+def stream_contexts(seed: int = 64, lo: int = 64, hi: int = 1024):
+    return np.random.default_rng(seed).integers(lo, hi + 1, STREAMS)
+
+
+def bench_streams(blob, steps: int = STREAM_STEPS):
+    """64 independent streams, contexts ~ U[64, 1024], paged fp16 KV, `steps` greedy frames in lock-step."""
+    from mosship import HipBatch, HipLLM, SampleParams
+    ctx = stream_contexts()
+    rng = np.random.default_rng(99)
+    kmax = int(ctx.max())
+    # N(0,1) fp16-representable KV; stream s uses the first ctx[s] positions
+    k = rng.standard_normal((12, kmax, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((12, kmax, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    m = HipLLM(blob, device=0)
+    b = HipBatch(m, max_streams=STREAMS, capacity=kmax + steps + 1)
+    for s in range(STREAMS):
+        b.set_stream(s, k[:, :ctx[s]], v[:, :ctx[s]], rng.standard_normal(768, dtype=np.float32))
+    p = SampleParams.make(greedy=True, min_frames=steps)
+    b.generate(STREAMS, 2, p)  # warm-up (captures the graphs)
+    for s in range(STREAMS):
+        b.set_stream(s, k[:, :ctx[s]], v[:, :ctx[s]], rng.standard_normal(768, dtype=np.float32))
+    out = b.generate(STREAMS, steps, p)
+    assert (out["frames"] == steps).all()
+    b.close()
+    m.close()
+    kv_bytes = int(np.sum(36864 * (ctx + steps // 2 + 1)))  # mean context over the run, fp16 K+V, 12 layers
+    step_bytes = 90728448 + STREAMS * 13872 + kv_bytes
+    return {"ms_total": out["ms"], "frames_per_s": STREAMS * steps / (out["ms"] * 1e-3),
+            "ms_per_step": out["ms"] / steps, "global_stack_GBps": step_bytes / (out["ms"] / steps * 1e-3) / 1e9}
+
+
+def _cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        return ""
+
+
+def cpu_prefill(blob):
+    """Reference prefill of the same 256 rows: W8A8 (its release default) in this process,
+    A16 (MOSS_A16=1, the numerics the GPU path follows) in a child process."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import REF_SO, RefCpu
+    if not os.path.exists(REF_SO):
+        return None
+    rows = prefill_rows()
+    r = RefCpu(a16_mode="decode")
+    m = r.model(blob, threads=4)
+    t0 = time.perf_counter()
+    m.prefill(rows)
+    w8a8 = (time.perf_counter() - t0) * 1e3
+    m.close()
+    code = ("import sys, time, numpy as np; sys.path[:0] = [%r, %r]; from oracle import RefCpu;"
+            "from mosship import moss_format as mf; r = RefCpu(a16_mode='1'); blob = open(sys.argv[1], 'rb').read();"
+            "rows = np.load(sys.argv[2]); m = r.model(blob, threads=4); t0 = time.perf_counter(); m.prefill(rows);"
+            "print((time.perf_counter() - t0) * 1e3)" % (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "dsh-moss-tts_amd")))
+    import subprocess
+    with tempfile.TemporaryDirectory() as td:
+        bp, rp = os.path.join(td, "w.moss"), os.path.join(td, "rows.npy")
+        with open(bp, "wb") as f:
+            f.write(blob)
+        np.save(rp, rows)
+        a16 = float(subprocess.run([sys.executable, "-c", code, bp, rp], check=True, capture_output=True,
+                                   text=True).stdout.strip().splitlines()[-1])
+    return {"w8a8_ms": w8a8, "a16_ms": a16, "threads": 4}
+
+
+def cpu_streams(blob, frames: int = 12, threads: int = 4):
+    """P = floor(cores / T) concurrent reference LlmModels (T threads each) decoding greedy
+    frames from their own states; contexts ~ U[64, 640] (the reference caps at 768)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import threading
+
+    from oracle import REF_SO, RefCpu, SampleParams
+
+    from mosship import moss_format as mf
+    if not os.path.exists(REF_SO):
+        return None
+    cores = min(os.cpu_count() or 1, 16)
+    procs = max(1, cores // threads)
+    ctx = stream_contexts(lo=64, hi=640)[:procs]
+    rng = np.random.default_rng(99)
+    r = RefCpu(a16_mode="decode")
+    models, paths = [], []
+    td = tempfile.mkdtemp(prefix="mossref_streams_")
+    for i in range(procs):
+        n = int(ctx[i])
+        k = rng.standard_normal((12, n, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+        v = rng.standard_normal((12, n, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+        rows = mf.text_rows(rng.integers(0, mf.VOCAB, n))
+        path = os.path.join(td, f"s{i}.state")
+        with open(path, "wb") as f:
+            f.write(mf.write_state(k, v, rng.standard_normal(768, dtype=np.float32), rows, mf.fp_weights(blob)))
+        mm = r.model(blob, threads=threads)
+        mm.load_state(path, rows, ignore_fp=False)
+        models.append(mm)
+        paths.append(path)
+    p = SampleParams.make(greedy=True, min_frames=frames)
+    counts = [0] * procs
+
+    def run(i):
+        counts[i] = len(models[i].generate(frames, p)["rows"])
+
+    ths = [threading.Thread(target=run, args=(i,)) for i in range(procs)]
+    t0 = time.perf_counter()
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    wall = time.perf_counter() - t0
+    for mm in models:
+        mm.close()
+    for pth in paths:
+        os.remove(pth)
+    os.rmdir(td)
+    return {"frames_per_s": sum(counts) / wall, "instances": procs, "threads_each": threads, "cores": procs * threads,
+            "sample": f"{procs} concurrent LlmModel x {threads} threads, {frames} greedy frames each, "
+                      f"ctx {ctx.tolist()}"}
+
+
 def cpu_baseline(blob, state, frames: int = 48):
     """The compiled reference (oracle/_ref) decoding from the same ctx-512 state."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -159,12 +319,7 @@ def cpu_baseline(blob, state, frames: int = 48):
     n = len(out["rows"])
     t = out["timing"]
     m.close()
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu_model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
+    cpu_model = _cpu_model_name()
     return {
         "value": (t1 - t0) * 1e3 / n,
         "unit": "ms/frame",
@@ -182,7 +337,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "decode"], default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "decode", "prefill", "streams"], default="full")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -203,6 +358,12 @@ def main():
     log("generating synthetic model + ctx-512 state")
     blob = mf.synth_model(1234)
     state = make_state()
+    if args.mode == "prefill":
+        print(json.dumps({"prefill": bench_prefill(blob)}), flush=True)
+        return
+    if args.mode == "streams":
+        print(json.dumps({"streams": bench_streams(blob)}), flush=True)
+        return
     log("decode")
     d = bench_decode(blob, state, args.steps, args.warmup)
     if args.mode == "decode":
@@ -210,10 +371,16 @@ def main():
         return
     log("gemv roofline")
     g = bench_gemv()
-    cpu = None
+    log("prefill (256 rows)")
+    pf = bench_prefill(blob)
+    log("64 streams")
+    st = bench_streams(blob)
+    cpu = cpu_pf = cpu_st = None
     if not args.no_cpu:
         log("cpu baseline (reference)")
         cpu = cpu_baseline(blob, state)
+        cpu_pf = cpu_prefill(blob)
+        cpu_st = cpu_streams(blob)
     # global step at position 512: weights + vectors + embed + fp16 KV read/write
     global_bytes = 90243072 + 485376 + 13872 + 36864 * (CTX + 1) + 36864
     line = {
@@ -248,6 +415,11 @@ def main():
             "frac": round(g["cold"]["GBps"] / HBM_PEAK_GBS, 4),
             "traffic": None,
         },
+        "prefill_256": {"ms": round(pf["ms"], 3), "TFLOP/s": round(pf["TFLOPs"], 2),
+                        "mfma_frac": round(pf["mfma_frac"], 4), "cpu_ref": cpu_pf},
+        "streams_64": {"frames_per_s": round(st["frames_per_s"], 1), "ms_per_step": round(st["ms_per_step"], 4),
+                       "global_stack_GBps": round(st["global_stack_GBps"], 1), "cpu_ref": cpu_st,
+                       "vs_cpu": round(st["frames_per_s"] / cpu_st["frames_per_s"], 1) if cpu_st else None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

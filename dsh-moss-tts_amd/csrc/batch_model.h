@@ -1,0 +1,79 @@
+// batch_model.h -- batched multi-stream decode on one GPU.
+//
+// Many independent TTS streams (each one LlmModel state in the reference,
+// csrc/include/moss/llm.h:39-90, which is single-stream) decoded in lock-step:
+// every projection is one W8A16 GEMM over all streams on the matrix cores, the
+// global KV cache is paged (per layer a pool of 64-position pages, one block
+// table row per stream), attention runs per (head, stream) over that stream's
+// pages, and the local transformer, heads, greedy picks and end gate run per
+// stream.  Weights are the model's own device copy.
+#pragma once
+
+#include <map>
+#include <vector>
+
+#include "llm_model.h"
+
+namespace mh {
+
+class Batch {
+public:
+    static constexpr int kPage = 64;
+
+    Batch(Model &model, int max_streams, int capacity, KvType kv);
+    ~Batch();
+    Batch(const Batch &) = delete;
+    Batch &operator=(const Batch &) = delete;
+
+    int max_streams() const { return S_; }
+    int capacity() const { return cap_; }
+    int position(int s) const { return pos_[s]; }
+    int device() const { return model_.device(); }
+    // Loads one stream's state: K/V [12][n_pos][768] fp32 (reference layout) and hidden[768].
+    void set_stream(int s, int n_pos, const float *k, const float *v, const float *hidden);
+    void get_hidden(int s, float *out);
+    void kv_export(int s, int n_pos, float *k, float *v);
+    // One global step for streams [0, n): rows [n][17].
+    void global_step(int n, const int32_t *rows);
+    // Greedy frames for streams [0, n) (llm.cpp:634-733 per stream, in lock-step).
+    // out_rows [frames][n][17]; out_frames[s] = frames stream s produced.  Returns elapsed ms.
+    double generate(int n, int frames, const moss_hip_sample_params &p, int32_t *out_rows, int *out_frames);
+
+private:
+    struct Graphs {
+        hipGraphExec_t local = nullptr, global = nullptr;
+    };
+    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos);
+    void enqueue_frame_local(hipStream_t s, int n);
+    void enqueue_global(hipStream_t s, int n);
+    Graphs &graphs_for(int n);
+    StreamState state() const;
+    void write_ctrl(int frame, int min_frames, float rep);
+
+    Model &model_;
+    Model::Weights w_;
+    int S_ = 0, cap_ = 0, pages_ = 0;
+    KvType kvt_ = KV_F16;
+    size_t esize_ = 2;
+    hipStream_t stream_ = nullptr;
+    hipEvent_t ev_[2] = {};
+
+    void *kpool_ = nullptr, *vpool_ = nullptr;  // [layer][S*pages][heads][64][64]
+    size_t layer_pool_elems_ = 0;
+    float *lkv_ = nullptr;                      // local K then V: [S][heads][17][64] fp32 each
+    int *table_ = nullptr;                      // [S][pages]
+    float *rope_ = nullptr;                     // cos [cap+1][32] then sin
+    int rope_n_ = 0;
+    float *x_ = nullptr, *a_ = nullptr, *q_ = nullptr, *o_ = nullptr, *h_ = nullptr;
+    float *hidden_ = nullptr, *lres_ = nullptr, *next_in_ = nullptr, *logits_ = nullptr;
+    int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr, *ctrl_ = nullptr;
+    unsigned char *active_ = nullptr;
+    float *gate_ = nullptr;
+    int *hist_codes_ = nullptr;                 // [cap+1][S][16] codes per frame
+    unsigned char *hist_active_ = nullptr;      // [cap+1][S] active after each frame's gate
+    int *ctrl_h_ = nullptr;                     // pinned host staging for ctrl
+    std::vector<int> pos_;
+    std::map<int, Graphs> graphs_;
+};
+
+}  // namespace mh

@@ -1,0 +1,356 @@
+// batch_model.hip -- batched multi-stream decode (see batch_model.h).
+#include "batch_model.h"
+
+#include <cmath>
+#include <cstring>
+
+namespace mh {
+
+Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
+    : model_(model), w_(model.weights()), S_(max_streams), cap_(capacity), kvt_(kv) {
+    if (S_ <= 0 || S_ > 1024) throw Status(MOSS_HIP_EINVAL, "max_streams must be in [1, 1024]");
+    if (cap_ <= kLocalLen || cap_ > 65536) throw Status(MOSS_HIP_EINVAL, "capacity must be in (17, 65536]");
+    esize_ = kvt_ == KV_F32 ? 4 : 2;
+    pages_ = (cap_ + kPage - 1) / kPage;
+    hip_check(hipSetDevice(model.device()), "hipSetDevice");
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    for (auto &e : ev_) hip_check(hipEventCreate(&e), "hipEventCreate");
+
+    layer_pool_elems_ = (size_t)S_ * pages_ * kHeads * kPage * kHeadDim;
+    const size_t pool_bytes = layer_pool_elems_ * kLayers * esize_;
+    hip_check(hipMalloc(&kpool_, pool_bytes), "hipMalloc(k pages)");
+    hip_check(hipMalloc(&vpool_, pool_bytes), "hipMalloc(v pages)");
+    hip_check(hipMemset(kpool_, 0, pool_bytes), "memset(k pages)");
+    hip_check(hipMemset(vpool_, 0, pool_bytes), "memset(v pages)");
+    const size_t lkv = (size_t)S_ * kHeads * kLocalLen * kHeadDim;
+    hip_check(hipMalloc(&lkv_, 2 * lkv * sizeof(float)), "hipMalloc(local kv)");
+    hip_check(hipMemset(lkv_, 0, 2 * lkv * sizeof(float)), "memset(local kv)");
+
+    // Block table: page j of stream s is page j*S + s of the pool, so a stream's
+    // pages are spread over the pool and every access goes through the table.
+    std::vector<int> table((size_t)S_ * pages_);
+    for (int s = 0; s < S_; ++s)
+        for (int j = 0; j < pages_; ++j) table[(size_t)s * pages_ + j] = j * S_ + s;
+    hip_check(hipMalloc(&table_, table.size() * sizeof(int)), "hipMalloc(table)");
+    hip_check(hipMemcpy(table_, table.data(), table.size() * sizeof(int), hipMemcpyHostToDevice), "table h2d");
+
+    // RoPE table for positions [0, cap] (llm.cpp:90-102 formula; a stream parked at
+    // capacity still evaluates row `cap`)
+    rope_n_ = cap_ + 1;
+    std::vector<float> rope(2ull * rope_n_ * kRopeHalf);
+    for (int p = 0; p < rope_n_; ++p)
+        for (int i = 0; i < kRopeHalf; ++i) {
+            const double inv = 1.0 / std::pow(10000.0, static_cast<double>(2 * i) / kHeadDim);
+            const double ang = static_cast<double>(p) * inv;
+            rope[(size_t)p * kRopeHalf + i] = static_cast<float>(std::cos(ang));
+            rope[(size_t)(rope_n_ + p) * kRopeHalf + i] = static_cast<float>(std::sin(ang));
+        }
+    hip_check(hipMalloc(&rope_, rope.size() * 4), "hipMalloc(rope)");
+    hip_check(hipMemcpy(rope_, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "rope h2d");
+
+    auto fm = [&](float **p, size_t n) {
+        hip_check(hipMalloc(p, n * sizeof(float)), "hipMalloc(batch)");
+        hip_check(hipMemset(*p, 0, n * sizeof(float)), "memset(batch)");
+    };
+    fm(&x_, (size_t)S_ * kHidden);
+    fm(&a_, (size_t)S_ * kHidden);
+    fm(&q_, (size_t)S_ * kHidden);
+    fm(&o_, (size_t)S_ * kHidden);
+    fm(&h_, (size_t)S_ * kFF);
+    fm(&hidden_, (size_t)S_ * kHidden);
+    fm(&lres_, (size_t)S_ * kHidden);
+    fm(&next_in_, (size_t)S_ * kHidden);
+    fm(&logits_, (size_t)S_ * kCodebook);
+    fm(&gate_, (size_t)S_ * 2);
+    auto im = [&](int **p, size_t n) {
+        hip_check(hipMalloc(p, n * sizeof(int)), "hipMalloc(batch)");
+        hip_check(hipMemset(*p, 0, n * sizeof(int)), "memset(batch)");
+    };
+    im(&pos_d_, S_);
+    im(&codes_, (size_t)S_ * kNVq);
+    im(&row_, (size_t)S_ * (kNVq + 1));
+    im(&counts_, (size_t)S_ * kNVq * kCodebook);
+    im(&ctrl_, 4);
+    im(&hist_codes_, (size_t)(cap_ + 1) * S_ * kNVq);
+    hip_check(hipMalloc(&active_, S_), "hipMalloc(active)");
+    hip_check(hipMemset(active_, 0, S_), "memset(active)");
+    hip_check(hipMalloc(&hist_active_, (size_t)(cap_ + 1) * S_), "hipMalloc(history)");
+    hip_check(hipHostMalloc(&ctrl_h_, 4 * sizeof(int), hipHostMallocDefault), "hipHostMalloc(ctrl)");
+    pos_.assign(S_, 0);
+}
+
+Batch::~Batch() {
+    (void)hipSetDevice(model_.device());
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (auto &kv : graphs_) {
+        if (kv.second.local) (void)hipGraphExecDestroy(kv.second.local);
+        if (kv.second.global) (void)hipGraphExecDestroy(kv.second.global);
+    }
+    void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
+                    gate_, pos_d_, codes_, row_, counts_, ctrl_, hist_codes_, active_, hist_active_};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+    if (ctrl_h_) (void)hipHostFree(ctrl_h_);
+    for (auto &e : ev_)
+        if (e) (void)hipEventDestroy(e);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+StreamState Batch::state() const {
+    StreamState st;
+    st.pos = pos_d_;
+    st.active = active_;
+    st.codes = codes_;
+    st.row = row_;
+    st.gate = gate_;
+    st.counts = counts_;
+    st.ctrl = ctrl_;
+    st.capacity = cap_;
+    return st;
+}
+
+void Batch::write_ctrl(int frame, int min_frames, float rep) {
+    ctrl_h_[0] = frame;
+    ctrl_h_[1] = min_frames;
+    std::memcpy(&ctrl_h_[2], &rep, 4);
+    ctrl_h_[3] = 0;
+    hip_check(hipMemcpyAsync(ctrl_, ctrl_h_, 4 * sizeof(int), hipMemcpyHostToDevice, stream_), "ctrl h2d");
+}
+
+void Batch::set_stream(int s, int n_pos, const float *k, const float *v, const float *hidden) {
+    if (s < 0 || s >= S_) throw Status(MOSS_HIP_EINVAL, "stream out of range");
+    if (n_pos < 0 || n_pos > cap_) throw Status(MOSS_HIP_EINVAL, "n_pos above the batch capacity");
+    hip_check(hipSetDevice(model_.device()), "hipSetDevice");
+    if (n_pos > 0) {
+        float *stage = nullptr;
+        const size_t per = (size_t)n_pos * kHidden;
+        hip_check(hipMalloc(&stage, per * 4), "hipMalloc(stage)");
+        try {
+            for (int w = 0; w < 2; ++w)
+                for (int l = 0; l < kLayers; ++l) {
+                    uint8_t *pool = static_cast<uint8_t *>(w == 0 ? kpool_ : vpool_) + l * layer_pool_elems_ * esize_;
+                    hip_check(hipMemcpyAsync(stage, (w == 0 ? k : v) + (size_t)l * per, per * 4, hipMemcpyHostToDevice,
+                                             stream_),
+                              "kv h2d");
+                    hip_check(launch_kv_import_paged(stage, n_pos, pool, table_ + (size_t)s * pages_, kPage, kvt_, stream_),
+                              "kv import");
+                    hip_check(hipStreamSynchronize(stream_), "sync");
+                }
+        } catch (...) {
+            (void)hipFree(stage);
+            throw;
+        }
+        (void)hipFree(stage);
+    }
+    if (hidden)
+        hip_check(hipMemcpyAsync(hidden_ + (size_t)s * kHidden, hidden, kHidden * 4, hipMemcpyHostToDevice, stream_),
+                  "hidden h2d");
+    hip_check(hipMemcpyAsync(pos_d_ + s, &n_pos, sizeof(int), hipMemcpyHostToDevice, stream_), "pos h2d");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    pos_[s] = n_pos;
+}
+
+void Batch::get_hidden(int s, float *out) {
+    if (s < 0 || s >= S_) throw Status(MOSS_HIP_EINVAL, "stream out of range");
+    hip_check(hipMemcpyAsync(out, hidden_ + (size_t)s * kHidden, kHidden * 4, hipMemcpyDeviceToHost, stream_), "d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+}
+
+void Batch::kv_export(int s, int n_pos, float *k, float *v) {
+    if (s < 0 || s >= S_ || n_pos < 0 || n_pos > cap_) throw Status(MOSS_HIP_EINVAL, "bad stream / n_pos");
+    if (n_pos == 0) return;
+    float *stage = nullptr;
+    const size_t per = (size_t)n_pos * kHidden;
+    hip_check(hipMalloc(&stage, per * 4), "hipMalloc(stage)");
+    try {
+        for (int w = 0; w < 2; ++w)
+            for (int l = 0; l < kLayers; ++l) {
+                const uint8_t *pool = static_cast<const uint8_t *>(w == 0 ? kpool_ : vpool_) + l * layer_pool_elems_ * esize_;
+                hip_check(launch_kv_export_paged(pool, table_ + (size_t)s * pages_, kPage, n_pos, kvt_, stage, stream_),
+                          "kv export");
+                hip_check(hipMemcpyAsync((w == 0 ? k : v) + (size_t)l * per, stage, per * 4, hipMemcpyDeviceToHost,
+                                         stream_),
+                          "kv d2h");
+                hip_check(hipStreamSynchronize(stream_), "sync");
+            }
+    } catch (...) {
+        (void)hipFree(stage);
+        throw;
+    }
+    (void)hipFree(stage);
+}
+
+// block_forward (llm.cpp:230-246) of the local layer for n streams at local
+// position lpos; the residual starts as `in` (row stride in_stride, 0 = one row
+// shared by all streams) and ends in lres_.
+void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos) {
+    const LayerW &L = *w_.local;
+    float *lk = lkv_, *lv = lkv_ + (size_t)S_ * kHeads * kLocalLen * kHeadDim;
+    const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
+    hip_check(launch_ln_rows(in, in_stride, L.ln1_w, L.ln1_b, a_, n, s), "local ln1");
+    GemmArgs q;
+    q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
+    q.bias = L.attn_b; q.q_out = q_; q.k_pool = lk; q.v_pool = lv; q.page_size = kLocalLen;
+    q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
+    hip_check(launch_gemm(q, EPI_QKV, KV_F32, s), "local qkv");
+    AttnArgs t;
+    t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen; t.stream_stride = 1;
+    t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out = o_;
+    hip_check(launch_attn(t, KV_F32, s), "local attention");
+    GemmArgs p;
+    p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
+    p.y = lres_; p.ldy = kHidden; p.resid_in = in; p.resid_stride = in_stride; p.bias = L.proj_b;
+    hip_check(launch_gemm(p, EPI_RESID, KV_F32, s), "local proj");
+    hip_check(launch_ln_rows(lres_, kHidden, L.ln2_w, L.ln2_b, a_, n, s), "local ln2");
+    GemmArgs f1;
+    f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = a_; f1.lda = kHidden; f1.M = n;
+    f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+    hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
+    GemmArgs f2;
+    f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
+    f2.y = lres_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
+    hip_check(launch_gemm(f2, EPI_RESID, KV_F32, s), "local fc_out");
+}
+
+// The local half of a frame for n streams (llm.cpp:648-698).
+void Batch::enqueue_frame_local(hipStream_t s, int n) {
+    const StreamState st = state();
+    enqueue_local_step(s, n, hidden_, kHidden, 0);
+    hip_check(launch_gate_rows(lres_, w_.llnf_w, w_.llnf_b, w_.wte, st, n, s), "gate");
+    for (int ch = 0; ch < kNVq; ++ch) {
+        if (ch == 0)
+            enqueue_local_step(s, n, w_.slot_in, 0, 1);
+        else
+            enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
+        hip_check(launch_ln_rows(lres_, kHidden, w_.llnf_w, w_.llnf_b, a_, n, s), "local ln_f");
+        GemmArgs hd;
+        hd.w = w_.aemb[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
+        hd.y = logits_; hd.ldy = kCodebook;
+        hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
+        hip_check(launch_sample_rows(logits_, ch, w_.aemb[ch], next_in_, st, n, ch == kNVq - 1, s), "sample");
+    }
+}
+
+// global_step (llm.cpp:248-255) for n streams over the paged cache.
+void Batch::enqueue_global(hipStream_t s, int n) {
+    const StreamState st = state();
+    EmbedArgs e;
+    e.wte = w_.wte;
+    for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = w_.aemb[ch];
+    hip_check(launch_embed_rows(e, row_, n, x_, s), "embed");
+    const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
+    for (int l = 0; l < kLayers; ++l) {
+        const LayerW &L = w_.global[l];
+        void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
+        void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
+        hip_check(launch_ln_rows(x_, kHidden, L.ln1_w, L.ln1_b, a_, n, s), "ln1");
+        GemmArgs q;
+        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
+        q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
+        q.page_table = table_; q.table_stride = pages_; q.page_size = kPage;
+        q.stream_stride = 1; q.row_pos = pos_d_; q.row_active = active_; q.rope_cos = rc; q.rope_sin = rs;
+        hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "qkv");
+        AttnArgs t;
+        t.q = q_; t.k_pool = kp; t.v_pool = vp; t.page_table = table_; t.table_stride = pages_; t.page_size = kPage;
+        t.stream_stride = 1; t.row_pos = pos_d_; t.rows = n; t.max_keys = cap_; t.out = o_;
+        hip_check(launch_attn(t, kvt_, s), "attention");
+        GemmArgs p;
+        p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
+        p.y = x_; p.ldy = kHidden; p.bias = L.proj_b;
+        hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "proj");
+        hip_check(launch_ln_rows(x_, kHidden, L.ln2_w, L.ln2_b, a_, n, s), "ln2");
+        GemmArgs f1;
+        f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = a_; f1.lda = kHidden; f1.M = n;
+        f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+        hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
+        GemmArgs f2;
+        f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
+        f2.y = x_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
+        hip_check(launch_gemm(f2, EPI_RESID, kvt_, s), "fc_out");
+    }
+    hip_check(launch_ln_rows(x_, kHidden, w_.lnf_w, w_.lnf_b, hidden_, n, s, active_), "ln_f");
+    hip_check(launch_advance_rows(st, n, s), "advance");
+}
+
+Batch::Graphs &Batch::graphs_for(int n) {
+    auto it = graphs_.find(n);
+    if (it != graphs_.end()) return it->second;
+    Graphs g;
+    hipGraph_t graph = nullptr;
+    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+    enqueue_frame_local(stream_, n);
+    hip_check(hipStreamEndCapture(stream_, &graph), "end capture");
+    hip_check(hipGraphInstantiate(&g.local, graph, nullptr, nullptr, 0), "instantiate");
+    (void)hipGraphDestroy(graph);
+    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+    enqueue_global(stream_, n);
+    hip_check(hipStreamEndCapture(stream_, &graph), "end capture");
+    hip_check(hipGraphInstantiate(&g.global, graph, nullptr, nullptr, 0), "instantiate");
+    (void)hipGraphDestroy(graph);
+    return graphs_[n] = g;
+}
+
+void Batch::global_step(int n, const int32_t *rows) {
+    if (n <= 0 || n > S_) throw Status(MOSS_HIP_EINVAL, "n_streams out of range");
+    for (int s = 0; s < n; ++s) {
+        if (pos_[s] >= cap_) throw Status(MOSS_HIP_ESTATE, "stream " + std::to_string(s) + " is at capacity");
+        if (rows[(size_t)s * 17] < 0 || rows[(size_t)s * 17] >= kVocab)
+            throw Status(MOSS_HIP_EINVAL, "row " + std::to_string(s) + ": text id out of [0, 16384)");
+    }
+    hip_check(hipSetDevice(model_.device()), "hipSetDevice");
+    Graphs &g = graphs_for(n);
+    std::vector<unsigned char> act(n, 1);
+    hip_check(hipMemcpyAsync(row_, rows, sizeof(int32_t) * 17 * n, hipMemcpyHostToDevice, stream_), "rows h2d");
+    hip_check(hipMemcpyAsync(active_, act.data(), n, hipMemcpyHostToDevice, stream_), "active h2d");
+    write_ctrl(0, 0, 1.0f);
+    hip_check(hipGraphLaunch(g.global, stream_), "graph launch");
+    hip_check(hipMemcpyAsync(pos_.data(), pos_d_, sizeof(int) * S_, hipMemcpyDeviceToHost, stream_), "pos d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+}
+
+double Batch::generate(int n, int frames, const moss_hip_sample_params &p, int32_t *out_rows, int *out_frames) {
+    if (n <= 0 || n > S_) throw Status(MOSS_HIP_EINVAL, "n_streams out of range");
+    if (!(p.greedy || p.top_k == 1) || !p.end_greedy)
+        throw Status(MOSS_HIP_EUNSUPPORTED, "only greedy decoding with the greedy end gate runs on the device");
+    if (frames <= 0) return 0.0;
+    if (frames > cap_ + 1) frames = cap_ + 1;
+    hip_check(hipSetDevice(model_.device()), "hipSetDevice");
+    Graphs &g = graphs_for(n);
+    std::vector<unsigned char> act(n);
+    for (int s = 0; s < n; ++s) act[s] = pos_[s] < cap_ ? 1 : 0;
+    hip_check(hipMemcpyAsync(active_, act.data(), n, hipMemcpyHostToDevice, stream_), "active h2d");
+    hip_check(hipMemsetAsync(counts_, 0, sizeof(int) * (size_t)n * kNVq * kCodebook, stream_), "counts clear");
+    write_ctrl(0, p.min_frames, p.repetition_penalty);
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    hip_check(hipEventRecord(ev_[0], stream_), "event");
+    for (int f = 0; f < frames; ++f) {
+        hip_check(hipGraphLaunch(g.local, stream_), "graph launch");
+        hip_check(hipMemcpyAsync(hist_active_ + (size_t)f * S_, active_, n, hipMemcpyDeviceToDevice, stream_), "hist");
+        hip_check(hipMemcpyAsync(hist_codes_ + (size_t)f * S_ * kNVq, codes_, sizeof(int) * n * kNVq,
+                                 hipMemcpyDeviceToDevice, stream_),
+                  "hist");
+        if (f + 1 < frames) hip_check(hipGraphLaunch(g.global, stream_), "graph launch");
+    }
+    hip_check(hipEventRecord(ev_[1], stream_), "event");
+    std::vector<unsigned char> ha((size_t)frames * S_);
+    std::vector<int> hc((size_t)frames * S_ * kNVq);
+    hip_check(hipMemcpyAsync(ha.data(), hist_active_, ha.size(), hipMemcpyDeviceToHost, stream_), "hist d2h");
+    hip_check(hipMemcpyAsync(hc.data(), hist_codes_, hc.size() * sizeof(int), hipMemcpyDeviceToHost, stream_), "hist d2h");
+    hip_check(hipMemcpyAsync(pos_.data(), pos_d_, sizeof(int) * S_, hipMemcpyDeviceToHost, stream_), "pos d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, ev_[0], ev_[1]), "elapsed");
+    for (int s = 0; s < n; ++s) {
+        int nf = 0;
+        while (nf < frames && ha[(size_t)nf * S_ + s]) ++nf;
+        if (out_frames) out_frames[s] = nf;
+        for (int f = 0; f < nf; ++f) {
+            int32_t *row = out_rows + ((size_t)f * n + s) * 17;
+            row[0] = 0;
+            for (int ch = 0; ch < kNVq; ++ch) row[ch + 1] = hc[((size_t)f * S_ + s) * kNVq + ch];
+        }
+    }
+    return ms;
+}
+
+}  // namespace mh

@@ -5,12 +5,16 @@
 #include <string>
 #include <vector>
 
-#include "llm_model.h"
+#include "batch_model.h"
 
 using mh::Status;
 
 struct moss_hip_llm {
     mh::Model *impl;
+};
+
+struct moss_hip_batch {
+    mh::Batch *impl;
 };
 
 namespace {
@@ -38,6 +42,12 @@ mh::Model &model_of(moss_hip_llm *m) {
     if (m == nullptr || m->impl == nullptr) throw Status(MOSS_HIP_EINVAL, "null model handle");
     mh::hip_check(hipSetDevice(m->impl->device()), "hipSetDevice");
     return *m->impl;
+}
+
+mh::Batch &batch_of(moss_hip_batch *b) {
+    if (b == nullptr || b->impl == nullptr) throw Status(MOSS_HIP_EINVAL, "null batch handle");
+    mh::hip_check(hipSetDevice(b->impl->device()), "hipSetDevice");
+    return *b->impl;
 }
 
 moss_hip_llm_options defaults(const moss_hip_llm_options *opt) {
@@ -164,7 +174,94 @@ int moss_hip_llm_kv_import(moss_hip_llm *m, int n_pos, const float *k, const flo
     });
 }
 
+// ------------------------------------------------------------------ batched streams
+
+int moss_hip_batch_create(moss_hip_llm *model, int max_streams, int capacity, int kv_dtype, moss_hip_batch **out) {
+    return guard([&] {
+        if (out == nullptr) throw Status(MOSS_HIP_EINVAL, "null output");
+        *out = nullptr;
+        mh::Model &m = model_of(model);
+        if (kv_dtype != 0 && kv_dtype != 1) throw Status(MOSS_HIP_EINVAL, "kv_dtype must be 0 (fp16) or 1 (fp32)");
+        auto *h = new moss_hip_batch{nullptr};
+        try {
+            h->impl = new mh::Batch(m, max_streams, capacity, kv_dtype == 1 ? mh::KV_F32 : mh::KV_F16);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+void moss_hip_batch_destroy(moss_hip_batch *b) {
+    if (!b) return;
+    delete b->impl;
+    delete b;
+}
+
+int moss_hip_batch_set_stream(moss_hip_batch *b, int stream, int n_pos, const float *k, const float *v,
+                              const float *hidden) {
+    return guard([&] {
+        if (n_pos > 0 && (!k || !v)) throw Status(MOSS_HIP_EINVAL, "null buffer");
+        batch_of(b).set_stream(stream, n_pos, k, v, hidden);
+    });
+}
+
+int moss_hip_batch_get_hidden(moss_hip_batch *b, int stream, float *out) {
+    return guard([&] {
+        if (!out) throw Status(MOSS_HIP_EINVAL, "null output");
+        batch_of(b).get_hidden(stream, out);
+    });
+}
+
+int moss_hip_batch_position(const moss_hip_batch *b, int stream) {
+    if (!b || !b->impl || stream < 0 || stream >= b->impl->max_streams()) return -1;
+    return b->impl->position(stream);
+}
+
+int moss_hip_batch_kv_export(moss_hip_batch *b, int stream, int n_pos, float *k, float *v) {
+    return guard([&] {
+        if (n_pos > 0 && (!k || !v)) throw Status(MOSS_HIP_EINVAL, "null buffer");
+        batch_of(b).kv_export(stream, n_pos, k, v);
+    });
+}
+
+int moss_hip_batch_global_step(moss_hip_batch *b, int n_streams, const int32_t *rows) {
+    return guard([&] {
+        if (!rows) throw Status(MOSS_HIP_EINVAL, "null rows");
+        batch_of(b).global_step(n_streams, rows);
+    });
+}
+
+int moss_hip_batch_generate(moss_hip_batch *b, int n_streams, int frames, const moss_hip_sample_params *p,
+                            int32_t *out_rows, int *out_frames, double *elapsed_ms) {
+    return guard([&] {
+        if (!p || !out_rows || frames < 0) throw Status(MOSS_HIP_EINVAL, "bad arguments");
+        const double ms = batch_of(b).generate(n_streams, frames, *p, out_rows, out_frames);
+        if (elapsed_ms) *elapsed_ms = ms;
+    });
+}
+
 // ------------------------------------------------------------------ operators
+
+int moss_hip_gemm_q8x4(const void *w, int rows, int cols, const float *x, int m, float *y, void *stream) {
+    return guard([&] {
+        if (!w || !x || !y) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (rows <= 0 || rows % 16 || cols <= 0 || cols % 32 || m <= 0)
+            throw Status(MOSS_HIP_EINVAL, "shape must satisfy rows % 16 == 0, cols % 32 == 0, m > 0");
+        mh::GemmArgs g;
+        g.w = static_cast<const uint8_t *>(w);
+        g.N = rows;
+        g.K = cols;
+        g.a = x;
+        g.lda = cols;
+        g.M = m;
+        g.y = y;
+        g.ldy = rows;
+        mh::hip_check(mh::launch_gemm(g, mh::EPI_F32, mh::KV_F16, static_cast<hipStream_t>(stream)), "gemm launch");
+    });
+}
+
 
 int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_dtype, void *y, int y_dtype,
                        void *stream) {
@@ -203,21 +300,22 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
         if (!q || !k_cache || !v_cache || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
         if (heads <= 0 || ctx_stride <= 0 || n_keys <= 0 || n_keys > ctx_stride)
             throw Status(MOSS_HIP_EINVAL, "need 0 < n_keys <= ctx_stride");
-        if (n_keys > mh::attn_max_keys()) throw Status(MOSS_HIP_EINVAL, "n_keys above 4096");
         if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
             throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
-        mh::AttnArgs a;
+        mh::AttnArgs a;  // the cache is one page of ctx_stride positions
         a.q = q;
-        a.k_cache = k_cache;
-        a.v_cache = v_cache;
-        a.ctx_stride = ctx_stride;
+        a.k_pool = k_cache;
+        a.v_pool = v_cache;
+        a.page_size = ctx_stride;
         a.heads = heads;
-        a.pos_const = n_keys - 1;
+        a.q_stride = heads * mh::kHeadDim;
+        a.out_stride = heads * mh::kHeadDim;
+        a.pos0 = n_keys - 1;
         a.max_keys = n_keys;
         a.out = out;
         a.out_f16 = out_dtype == MOSS_HIP_F16;
         const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
-        mh::hip_check(mh::launch_attn_decode(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
+        mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
     });
 }
 

@@ -234,18 +234,21 @@ __global__ void kv_export_kernel(const void *src, int n_pos, int ctx_stride, flo
 }  // namespace
 
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     hipLaunchKernelGGL(embed_kernel, dim3(kHidden / 64), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_layernorm(const float *x, const float *w, const float *b, float *out, DevState *state,
                             int bump_pos, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     hipLaunchKernelGGL(layernorm_kernel, dim3(1), dim3(256), 0, s, x, w, b, out, state, bump_pos);
     return hipGetLastError();
 }
 
 hipError_t launch_dequant_rows(const uint8_t *w, int mat_rows, int cols, const int *rows_dev, int n, float *out,
                                hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(dequant_rows_kernel, dim3(n), dim3(256), 0, s, w, mat_rows, cols, rows_dev, out);
     return hipGetLastError();
@@ -253,16 +256,19 @@ hipError_t launch_dequant_rows(const uint8_t *w, int mat_rows, int cols, const i
 
 hipError_t launch_gate(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
                        DevState *state, float *gate_log, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     hipLaunchKernelGGL(gate_kernel, dim3(1), dim3(256), 0, s, x_raw, lnf_w, lnf_b, wte, state, gate_log);
     return hipGetLastError();
 }
 
 hipError_t launch_sample_greedy(const SampleArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     hipLaunchKernelGGL(sample_greedy_kernel, dim3(1), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 hipError_t launch_kv_import(const float *src, int n_pos, void *dst, int ctx_stride, KvType kv, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (n_pos <= 0) return hipSuccess;
     if (n_pos > ctx_stride) return hipErrorInvalidValue;
     if (kv == KV_F16)
@@ -273,12 +279,285 @@ hipError_t launch_kv_import(const float *src, int n_pos, void *dst, int ctx_stri
 }
 
 hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType kv, float *dst, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (n_pos <= 0) return hipSuccess;
     if (n_pos > ctx_stride) return hipErrorInvalidValue;
     if (kv == KV_F16)
         hipLaunchKernelGGL(kv_export_kernel<KV_F16>, dim3(n_pos), dim3(256), 0, s, src, n_pos, ctx_stride, dst);
     else
         hipLaunchKernelGGL(kv_export_kernel<KV_F32>, dim3(n_pos), dim3(256), 0, s, src, n_pos, ctx_stride, dst);
+    return hipGetLastError();
+}
+
+}  // namespace mh
+
+// ------------------------------------------------------------------ row-batched kernels
+namespace mh {
+namespace {
+
+__global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stride, const float *w, const float *b,
+                                                      float *out, const unsigned char *mask) {
+    __shared__ float red[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    if (mask != nullptr && !mask[r]) return;
+    const float *xr = x + (size_t)r * x_stride;
+    float v[3], o[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v[i] = xr[t + 256 * i];
+    layernorm_768(v, w, b, o, red);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+}
+
+// grid (12, rows): same per-element serial sum as embed_kernel
+__global__ __launch_bounds__(64) void embed_rows_kernel(EmbedArgs a, const int *rows, float *x) {
+    const int nb = kHidden / 32;
+    const int r = blockIdx.y, c = blockIdx.x * 64 + threadIdx.x;
+    const int *row = rows + (size_t)r * (kNVq + 1);
+    float e[kNVq];
+    bool use[kNVq];
+#pragma unroll
+    for (int ch = 0; ch < kNVq; ++ch) {
+        const int code = row[ch + 1];
+        use[ch] = !(code == kAudioPad || code < 0 || code >= kCodebook);
+        e[ch] = q8x4_elem(a.aemb[ch], nb, use[ch] ? code : 0, c);
+    }
+    float v = q8x4_elem(a.wte, nb, row[0], c);
+#pragma unroll
+    for (int ch = 0; ch < kNVq; ++ch)
+        if (use[ch]) v = v + e[ch];
+    x[(size_t)r * kHidden + c] = v;
+}
+
+// gate_kernel per stream (one workgroup per stream): same arithmetic, per-stream outputs.
+__global__ __launch_bounds__(256) void gate_rows_kernel(const float *x_raw, const float *lnf_w, const float *lnf_b,
+                                                        const uint8_t *wte, StreamState st) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    __shared__ float hbuf[kHidden];
+    __shared__ int8_t qa[kHidden];
+    __shared__ float da[kHidden / 32];
+    __shared__ float lanes[2][8];
+    const int srow = blockIdx.x, t = threadIdx.x;
+    if (!st.active[srow]) return;
+    const float *xr = x_raw + (size_t)srow * kHidden;
+    float v[3], o[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v[i] = xr[t + 256 * i];
+    layernorm_768(v, lnf_w, lnf_b, o, red);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) hbuf[t + 256 * i] = o[i];
+    __syncthreads();
+    const int nb = kHidden / 32;
+    if (t < nb) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float av = fabsf(hbuf[32 * t + i]);
+            amax = amax < av ? av : amax;
+        }
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        da[t] = d;
+        for (int i = 0; i < 32; ++i) {
+            int q = (int)rintf(hbuf[32 * t + i] * id);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            qa[32 * t + i] = (int8_t)q;
+        }
+    }
+    __syncthreads();
+    if (t < 16) {
+        const int which = t >> 3, lane = t & 7;
+        const int r = which == 0 ? kEndToken : kSlotToken;
+        const uint8_t *grp = wte + (size_t)(r >> 2) * nb * kBlockBytes;
+        float acc = 0.0f;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t *blk = grp + (size_t)b * kBlockBytes;
+            const float dw = h2f(*(const uint16_t *)(blk + 2 * (r & 3)));
+            const int8_t *qs = (const int8_t *)(blk + 8 + 32 * (r & 3));
+            int32_t p = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) p += (int32_t)qs[4 * lane + u] * (int32_t)qa[32 * b + 4 * lane + u];
+            const float scale = dw * da[b];
+            acc = fmaf((float)p, scale, acc);
+        }
+        lanes[which][lane] = acc;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float g[2];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const float *a8 = lanes[w];
+            const float s0 = a8[0] + a8[4], s1 = a8[1] + a8[5], s2 = a8[2] + a8[6], s3 = a8[3] + a8[7];
+            const float t0 = s0 + s2, t1 = s1 + s3;
+            g[w] = t0 + t1;
+        }
+        st.gate[2 * srow] = g[0];
+        st.gate[2 * srow + 1] = g[1];
+        if (st.ctrl[0] >= st.ctrl[1] && g[0] > g[1]) st.active[srow] = 0;
+    }
+}
+
+// sample_greedy_kernel per stream; inactive streams keep their state.
+__global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, int ch, const uint8_t *aemb,
+                                                          float *next_in, StreamState st, int last_channel) {
+#pragma clang fp contract(off)
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ int used_s;
+    const int srow = blockIdx.x, t = threadIdx.x;
+    const float *lg = logits + (size_t)srow * kCodebook;
+    float *nxt = next_in + (size_t)srow * kHidden;
+    const int nb = kHidden / 32;
+    if (!st.active[srow]) {
+        // keep the next local input defined (row 0) so later kernels read finite values
+        for (int c = t; c < kHidden; c += 256) nxt[c] = q8x4_elem(aemb, nb, 0, c);
+        return;
+    }
+    const float p = __int_as_float(st.ctrl[2]);
+    const int *cnt = st.counts + ((size_t)srow * kNVq + ch) * kCodebook;
+    float best = -INFINITY;
+    int besti = kCodebook;
+    for (int i = t; i < kCodebook; i += 256) {
+        float v = lg[i];
+        if (p != 1.0f) {
+            const int c = cnt[i];
+            for (int k = 0; k < c; ++k) v = v < 0.0f ? v * p : v / p;
+        }
+        if (v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(besti, off);
+        if (ov > best || (ov == best && oi < besti)) {
+            best = ov;
+            besti = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = besti;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float b = bv[0];
+        int idx = bi[0];
+        for (int w = 1; w < 4; ++w)
+            if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
+                b = bv[w];
+                idx = bi[w];
+            }
+        if (idx >= kCodebook) idx = 0;
+        st.codes[srow * kNVq + ch] = idx;
+        st.row[srow * (kNVq + 1) + ch + 1] = idx;
+        st.counts[((size_t)srow * kNVq + ch) * kCodebook + idx] += 1;
+        if (last_channel) st.row[srow * (kNVq + 1)] = kSlotToken;
+        used_s = idx;
+    }
+    __syncthreads();
+    const int used = used_s;
+    for (int c = t; c < kHidden; c += 256) nxt[c] = q8x4_elem(aemb, nb, used, c);
+}
+
+__global__ void advance_rows_kernel(StreamState st, int streams) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s == 0) st.ctrl[0] += 1;
+    if (s >= streams || !st.active[s]) return;
+    const int p = st.pos[s] + 1;
+    st.pos[s] = p;
+    if (p >= st.capacity) st.active[s] = 0;
+}
+
+template <int KV>
+__global__ void kv_import_paged_kernel(const float *src, void *pool, const int *table_row, int page_size) {
+    const int p = blockIdx.x;
+    const size_t page_base = (size_t)table_row[p / page_size] * kHeads * page_size;
+    for (int e = threadIdx.x; e < kHidden; e += blockDim.x) {
+        const size_t idx = ((page_base + (size_t)(e >> 6) * page_size) + p % page_size) * kHeadDim + (e & 63);
+        const float v = src[(size_t)p * kHidden + e];
+        if constexpr (KV == KV_F16)
+            ((__half *)pool)[idx] = __float2half_rn(v);
+        else
+            ((float *)pool)[idx] = v;
+    }
+}
+
+template <int KV>
+__global__ void kv_export_paged_kernel(const void *pool, const int *table_row, int page_size, float *dst) {
+    const int p = blockIdx.x;
+    const size_t page_base = (size_t)table_row[p / page_size] * kHeads * page_size;
+    for (int e = threadIdx.x; e < kHidden; e += blockDim.x) {
+        const size_t idx = ((page_base + (size_t)(e >> 6) * page_size) + p % page_size) * kHeadDim + (e & 63);
+        float v;
+        if constexpr (KV == KV_F16)
+            v = __half2float(((const __half *)pool)[idx]);
+        else
+            v = ((const float *)pool)[idx];
+        dst[(size_t)p * kHidden + e] = v;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_kv_import_paged(const float *src, int n_pos, void *pool, const int *table_row, int page_size,
+                                  KvType kv, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (n_pos <= 0) return hipSuccess;
+    if (kv == KV_F16)
+        hipLaunchKernelGGL(kv_import_paged_kernel<KV_F16>, dim3(n_pos), dim3(256), 0, s, src, pool, table_row, page_size);
+    else
+        hipLaunchKernelGGL(kv_import_paged_kernel<KV_F32>, dim3(n_pos), dim3(256), 0, s, src, pool, table_row, page_size);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int page_size, int n_pos, KvType kv,
+                                  float *dst, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (n_pos <= 0) return hipSuccess;
+    if (kv == KV_F16)
+        hipLaunchKernelGGL(kv_export_paged_kernel<KV_F16>, dim3(n_pos), dim3(256), 0, s, pool, table_row, page_size, dst);
+    else
+        hipLaunchKernelGGL(kv_export_paged_kernel<KV_F32>, dim3(n_pos), dim3(256), 0, s, pool, table_row, page_size, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const float *b, float *out, int rows,
+                          hipStream_t s, const unsigned char *mask) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const EmbedArgs &e, const int *rows, int n, float *x, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(kHidden / 64, n), dim3(64), 0, s, e, rows, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_rows(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
+                            const StreamState &st, int streams, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    hipLaunchKernelGGL(gate_rows_kernel, dim3(streams), dim3(256), 0, s, x_raw, lnf_w, lnf_b, wte, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
+                              int streams, int last_channel, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    hipLaunchKernelGGL(sample_rows_kernel, dim3(streams), dim3(256), 0, s, logits, ch, aemb, next_in, st,
+                       last_channel);
+    return hipGetLastError();
+}
+
+hipError_t launch_advance_rows(const StreamState &st, int streams, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    hipLaunchKernelGGL(advance_rows_kernel, dim3((streams + 63) / 64), dim3(64), 0, s, st, streams);
     return hipGetLastError();
 }
 

@@ -1,0 +1,193 @@
+// gemm_mfma.hip -- W8A16 GEMM over the native Q8_0_4X4 layout on CDNA4 matrix cores.
+//
+// Replaces gemm_par (reference csrc/include/moss/gemv.h:54, csrc/src/gemv.cpp:276-309)
+// in its A16 mode -- Y[m][n] = sum_b fp32(d[n,b]) * sum_i q[n,b,i] * x[m][32b+i] --
+// for M >= 16 rows: prefill (M = prompt rows) and batched multi-stream decode
+// (M = streams).
+//
+// v_mfma_f32_16x16x32_f16: one instruction covers one 32-column scale block.
+// Lane l holds A[row l%16][k 8(l/16)..+7], B[k 8(l/16)..+7][col l%16] and gets
+// D[row 4(l/16)+i][col l%16].  B is the weight row n = col: 8 consecutive int8
+// of one row of the 4x4 block (one 8-byte load), exact in fp16.  A is the fp32
+// activation split as x = hi + lo with hi = fp16(x), lo = fp16(x - hi): two
+// MFMAs (hi, lo) give the block dot to ~2^-22 relative, then the fp32 block
+// scale d[n,b] (the same for all 4 values a lane holds) is applied with an FMA
+// into the fp32 accumulator -- the reference's per-block scale-then-accumulate
+// order.
+//
+// Workgroup tile: 64 rows (wave w: rows 16w..16w+15) x 16*NT columns; grid
+// (N / (16 NT), ceil(M / 64)).  Each wave streams its A rows and the shared B
+// columns KB blocks at a time with every load of a chunk issued before use.
+#include "mh_ops.h"
+
+namespace mh {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int KB = 4;  // scale blocks per load chunk
+
+__device__ __forceinline__ void split_hi_lo(const float (&x)[8], half8 &hi, half8 &lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const _Float16 h = (_Float16)x[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(x[i] - (float)h);
+    }
+}
+
+__device__ __forceinline__ half8 i8x8_to_h8(uint2 q) {
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = (_Float16)(int8_t)(q.x >> (8 * i));
+        r[4 + i] = (_Float16)(int8_t)(q.y >> (8 * i));
+    }
+    return r;
+}
+
+template <int EPI, int KV>
+__device__ __forceinline__ void gemm_finish(const GemmArgs &g, int m, int n, float v, float partner) {
+#pragma clang fp contract(off)
+    if constexpr (EPI == EPI_F32) {
+        g.y[(size_t)m * g.ldy + n] = v;
+    } else if constexpr (EPI == EPI_RESID) {
+        float *y = g.y + (size_t)m * g.ldy + n;
+        const float xin = g.resid_in ? g.resid_in[(size_t)m * g.resid_stride + n] : *y;
+        *y = xin + (v + g.bias[n]);
+    } else if constexpr (EPI == EPI_GELU) {
+        g.y[(size_t)m * g.ldy + n] = gelu_new(v + g.bias[n]);
+    } else {  // EPI_QKV: bias, RoPE at the row's position, q -> q_out, k/v -> KV pages
+        const float val = v + g.bias[n];
+        const int sec = n / kHidden, within = n - sec * kHidden;
+        const int h = within >> 6, d = within & 63;
+        const int s = g.row_stream ? g.row_stream[m] : m * g.stream_stride;
+        const int pos = g.row_pos ? g.row_pos[m] : g.pos0 + m * g.pos_stride;
+        float out = val;
+        if (sec < 2) {
+            const float pv = partner + g.bias[n ^ 1];
+            const float c = g.rope_cos[pos * kRopeHalf + (d >> 1)];
+            const float sn = g.rope_sin[pos * kRopeHalf + (d >> 1)];
+            const float p0 = val * c, p1 = pv * sn;
+            out = (d & 1) == 0 ? p0 - p1 : p0 + p1;
+        }
+        if (sec == 0) {
+            g.q_out[(size_t)m * kHidden + within] = out;
+        } else if (g.row_active == nullptr || g.row_active[m]) {
+            const int page = g.page_table ? g.page_table[(size_t)s * g.table_stride + pos / g.page_size] : s;
+            const size_t idx = (((size_t)page * kHeads + h) * g.page_size + pos % g.page_size) * kHeadDim + d;
+            void *pool = sec == 1 ? g.k_pool : g.v_pool;
+            if constexpr (KV == KV_F16)
+                ((__half *)pool)[idx] = __float2half_rn(out);
+            else
+                ((float *)pool)[idx] = out;
+        }
+    }
+}
+
+
+template <int EPI, int KV, int NT>
+__global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
+    const int m_base = blockIdx.y * 64 + wave * 16;
+    const int n_base = blockIdx.x * 16 * NT;
+    const int nb = g.K >> 5;
+    // A row of this lane (clamped: rows past M read row M-1 and are never stored)
+    const int arow = min(m_base + l16, g.M - 1);
+    const float *arow_p = g.a + (size_t)arow * g.lda + 8 * kq;
+    // B column (weight row) of this lane for each of the NT subtiles
+    const uint8_t *wcol[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = n_base + 16 * t + l16;
+        wcol[t] = g.w + (size_t)(n >> 2) * nb * kBlockBytes;
+    }
+    const int krow = l16 & 3;  // row inside the 4-row group (n % 4; n_base is a multiple of 16)
+
+    floatx4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int b0 = 0; b0 < nb; b0 += KB) {
+        float xa[KB][8];
+        uint2 qb[KB][NT];
+        uint16_t db[KB][NT];
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const int b = min(b0 + j, nb - 1);
+            const float4 x0 = *(const float4 *)(arow_p + 32 * b);
+            const float4 x1 = *(const float4 *)(arow_p + 32 * b + 4);
+            xa[j][0] = x0.x; xa[j][1] = x0.y; xa[j][2] = x0.z; xa[j][3] = x0.w;
+            xa[j][4] = x1.x; xa[j][5] = x1.y; xa[j][6] = x1.z; xa[j][7] = x1.w;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint8_t *blk = wcol[t] + (size_t)b * kBlockBytes;
+                const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 32 * krow + 8 * kq));
+                qb[j][t] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
+                db[j][t] = *(const uint16_t *)(blk + 2 * krow);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            if (b0 + j >= nb) break;
+            half8 hi, lo;
+            split_hi_lo(xa[j], hi, lo);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const half8 bw = i8x8_to_h8(qb[j][t]);
+                floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+                blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, bw, blk, 0, 0, 0);
+                blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, bw, blk, 0, 0, 0);
+                const float d = h2f(db[j][t]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(blk[i], d, acc[t][i]);
+            }
+        }
+    }
+
+    // epilogue: lane holds rows m_base + 4kq + i, column n_base + 16t + l16
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = n_base + 16 * t + l16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m_base + 4 * kq + i;
+            const float v = acc[t][i];
+            const float partner = __shfl_xor(v, 1);  // column n ^ 1, same row
+            if (m < g.M) gemm_finish<EPI, KV>(g, m, n, v, partner);
+        }
+    }
+}
+
+template <int EPI, int KV>
+hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    // 4 column subtiles (64 columns) per workgroup unless that leaves too few workgroups
+    const int mt = (g.M + 63) / 64;
+    const bool wide = (g.N / 64) * mt >= 128;
+    if (wide && g.N % 64 == 0) {
+        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 4>), dim3(g.N / 64, mt), dim3(256), 0, s, g);
+    } else {
+        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 1>), dim3(g.N / 16, mt), dim3(256), 0, s, g);
+    }
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (g.M <= 0 || g.N <= 0 || g.N % 16 || g.K % 32 || g.K <= 0 || g.lda < g.K || g.lda % 4) return hipErrorInvalidValue;
+    if (epi == EPI_QKV && (g.N != 3 * kHidden || g.page_size <= 0)) return hipErrorInvalidValue;
+    switch (epi) {
+        case EPI_F32: return launch_nt<EPI_F32, KV_F16>(g, s);
+        case EPI_RESID: return launch_nt<EPI_RESID, KV_F16>(g, s);
+        case EPI_GELU: return launch_nt<EPI_GELU, KV_F16>(g, s);
+        case EPI_QKV: return kv == KV_F32 ? launch_nt<EPI_QKV, KV_F32>(g, s) : launch_nt<EPI_QKV, KV_F16>(g, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mh

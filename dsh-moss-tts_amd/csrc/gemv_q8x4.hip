@@ -194,6 +194,8 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
 
 template <int PRO, int EPI, int SPLIT, int KV>
 hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int ngroups = a.rows / 4;
     constexpr int GPW = 4 / SPLIT;
     int grid = (ngroups + GPW - 1) / GPW;
@@ -210,6 +212,8 @@ hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
 
 template <int PRO, int EPI, int KV>
 hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     // blocks per wave -> batch size (iterations of 4 blocks), one of 2, 3, 6, 8
     const int per = (a.cols / 32 + split - 1) / split;
     const int its = (per + 3) / 4;
@@ -235,6 +239,7 @@ int pick_split(int rows, int cols) {
 }  // namespace
 
 hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (a.rows % 4 != 0 || a.cols % 128 != 0 || a.cols > 4096 || a.rows <= 0) return hipErrorInvalidValue;
     if (pro == PRO_LN && a.cols != kHidden) return hipErrorInvalidValue;
     if (epi == EPI_QKV && a.rows != 3 * kHidden) return hipErrorInvalidValue;

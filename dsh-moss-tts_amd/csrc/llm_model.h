@@ -60,6 +60,18 @@ public:
     void kv_import(int n_pos, const float *k, const float *v, const float *hidden);
 
     int device() const { return device_; }
+    hipStream_t stream() const { return stream_; }
+
+    // Device weights, shared with the batched engine.
+    struct Weights {
+        const LayerW *global;  // [kLayers]
+        const LayerW *local;
+        const float *lnf_w, *lnf_b, *llnf_w, *llnf_b;
+        const uint8_t *wte;
+        const uint8_t *const *aemb;  // [kNVq]
+        const float *slot_in;        // dequantised wte[kSlotToken]
+    };
+    Weights weights() const { return Weights{g_, &local_, lnf_w_, lnf_b_, llnf_w_, llnf_b_, wte_, aemb_.data(), slot_in_}; }
 
 private:
     void enqueue_global_step(hipStream_t s, const int *row_dev);
@@ -97,6 +109,7 @@ private:
     float *gate_log_ = nullptr;          // [max_ctx][2]
     int *rows_dev_ = nullptr;            // prefill rows [n][17]
     int rows_cap_ = 0;
+    float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_o_ = nullptr, *pre_h_ = nullptr;  // prefill rows
     DevState *state_ = nullptr;          // device
     DevState *hstate_ = nullptr;         // pinned host mirror
     void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]

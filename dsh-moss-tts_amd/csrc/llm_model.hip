@@ -159,7 +159,6 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     hip_check(hipMalloc(&rope_, rope.size() * 4), "hipMalloc(rope)");
     hip_check(hipMemcpy(rope_, rope.data(), rope.size() * 4, hipMemcpyHostToDevice), "upload rope");
 
-    if (max_ctx_ > attn_max_keys()) throw Status(MOSS_HIP_EINVAL, "max_ctx above the attention kernel's key capacity");
     auto fmalloc = [&](float **p, size_t n) { hip_check(hipMalloc(p, n * 4), "hipMalloc(act)"); };
     fmalloc(&x_, kHidden);
     fmalloc(&q_, kHidden);
@@ -235,10 +234,10 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         a.pos_ptr = pos; a.state = state_;
         hip_check(launch_gemv(a, PRO_LN, EPI_QKV, kvt_, s), "qkv gemv");
 
-        AttnArgs t;
-        t.q = q_; t.k_cache = a.k_cache; t.v_cache = a.v_cache; t.ctx_stride = max_ctx_;
-        t.pos_ptr = pos; t.max_keys = max_ctx_; t.out = attn_out_; t.state = state_;
-        hip_check(launch_attn_decode(t, kvt_, s), "attention");
+        AttnArgs t;  // the cache is one page of max_ctx positions
+        t.q = q_; t.k_pool = a.k_cache; t.v_pool = a.v_cache; t.page_size = max_ctx_;
+        t.row_pos = pos; t.max_keys = max_ctx_; t.out = attn_out_; t.state = state_;
+        hip_check(launch_attn(t, kvt_, s), "attention");
 
         GemvArgs p;
         p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
@@ -276,9 +275,9 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
 
     // At most 17 keys: a single split per head, normalised in place.
     AttnArgs t;
-    t.q = q_; t.k_cache = lk; t.v_cache = lv; t.ctx_stride = kLocalLen;
-    t.pos_const = lpos; t.max_keys = kLocalLen; t.out = attn_out_; t.state = state_;
-    hip_check(launch_attn_decode(t, KV_F32, s), "local attention");
+    t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen;
+    t.pos0 = lpos; t.max_keys = kLocalLen; t.out = attn_out_; t.state = state_;
+    hip_check(launch_attn(t, KV_F32, s), "local attention");
 
     GemvArgs p;
     p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
@@ -389,27 +388,73 @@ void Model::global_step(const int32_t *row) {
     ++pos_;
 }
 
-// LlmModel::prefill (llm.cpp:327-401): rows are embedded and pushed through the
-// layers one position at a time (KV for [start, start+m), hidden = ln_f of the
-// last row).  Same arithmetic as the decode step (W8A16).
+// LlmModel::prefill (llm.cpp:327-401), batched over the m rows like the
+// reference: embed all rows, then per layer LN1 -> QKV GEMM (bias, RoPE and the
+// K/V of positions [start, start+m) written in its epilogue) -> causal
+// attention of row i over keys <= start+i -> proj GEMM + residual -> LN2 ->
+// fc_in GEMM + gelu -> fc_out GEMM + residual; hidden = ln_f of the last row.
+// The GEMMs run on the matrix cores in W8A16 (the reference with MOSS_A16=1).
 void Model::prefill(const int32_t *rows, int n, int start) {
     start = start < 0 ? 0 : (start > max_ctx_ ? max_ctx_ : start);
     const int m = n < max_ctx_ - start ? n : max_ctx_ - start;
     if (m <= 0) return;
     check_rows(rows, m);
     if (m > rows_cap_) {
-        hip_check(hipFree(rows_dev_), "free rows");
+        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_};
+        for (void *p : bufs)
+            if (p) hip_check(hipFree(p), "free prefill buffers");
         rows_dev_ = nullptr;
+        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = nullptr;
+        rows_cap_ = 0;
         hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
+        hip_check(hipMalloc(&pre_x_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_a_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_q_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_o_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * (size_t)m), "hipMalloc(prefill)");
         rows_cap_ = m;
     }
     hip_check(hipMemcpyAsync(rows_dev_, rows, sizeof(int) * 17 * (size_t)m, hipMemcpyHostToDevice, stream_), "rows h2d");
-    pos_ = start;
     hstate_->stop = 0;
+    pos_ = start;
     write_state_header();
-    for (int i = 0; i < m; ++i) enqueue_global_step(stream_, rows_dev_ + 17 * (size_t)i);
-    hip_check(hipStreamSynchronize(stream_), "sync");
+    hipStream_t s = stream_;
+    EmbedArgs e;
+    e.wte = wte_;
+    for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = aemb_[ch];
+    hip_check(launch_embed_rows(e, rows_dev_, m, pre_x_, s), "prefill embed");
+    const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
+    for (int l = 0; l < kLayers; ++l) {
+        const LayerW &L = g_[l];
+        hip_check(launch_ln_rows(pre_x_, kHidden, L.ln1_w, L.ln1_b, pre_a_, m, s), "prefill ln1");
+        GemmArgs q;
+        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = pre_a_; q.lda = kHidden; q.M = m;
+        q.bias = L.attn_b; q.q_out = pre_q_;
+        q.k_pool = kv_layer(0, l); q.v_pool = kv_layer(1, l); q.page_size = max_ctx_;
+        q.pos0 = start; q.rope_cos = rc; q.rope_sin = rs;
+        hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "prefill qkv");
+        AttnArgs t;
+        t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
+        t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = pre_o_;
+        hip_check(launch_attn(t, kvt_, s), "prefill attention");
+        GemmArgs p;
+        p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
+        p.y = pre_x_; p.ldy = kHidden; p.bias = L.proj_b;
+        hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "prefill proj");
+        hip_check(launch_ln_rows(pre_x_, kHidden, L.ln2_w, L.ln2_b, pre_a_, m, s), "prefill ln2");
+        GemmArgs f1;
+        f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
+        f1.y = pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+        hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
+        GemmArgs f2;
+        f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
+        f2.y = pre_x_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
+        hip_check(launch_gemm(f2, EPI_RESID, kvt_, s), "prefill fc_out");
+    }
+    hip_check(launch_layernorm(pre_x_ + (size_t)(m - 1) * kHidden, lnf_w_, lnf_b_, hidden_, nullptr, 0, s), "ln_f");
     pos_ = start + m;
+    write_state_header();
+    hip_check(hipStreamSynchronize(s), "sync");
 }
 
 int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t seed, const int32_t *forced,

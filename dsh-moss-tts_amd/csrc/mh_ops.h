@@ -49,21 +49,56 @@ struct GemvArgs {
 // Launch y = W x with the given prologue/epilogue; kv selects the KV cache type for EPI_QKV.
 hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv, hipStream_t s);
 
+// Attention over one query row per (head, row) workgroup.  Keys of row r live in
+// stream s = row_stream[r] (0 when null); key p of stream s is at page
+// page_table[s * table_stride + p / page_size], slot p % page_size, in
+// pools laid out [page][head][page_size][64].  A null page_table means one
+// contiguous page per stream (page = stream index).  page_size must be a
+// multiple of 64 or exceed every key count.
 struct AttnArgs {
-    const float *q = nullptr;                           // [heads*64] fp32 (post-RoPE)
-    const void *k_cache = nullptr, *v_cache = nullptr;  // [heads][ctx_stride][64]
-    int ctx_stride = 0;
+    const float *q = nullptr;  // row r: q + r * q_stride, [heads*64] fp32 (post-RoPE)
+    int q_stride = kHidden;
+    const void *k_pool = nullptr, *v_pool = nullptr;
+    const int *page_table = nullptr;
+    int table_stride = 0, page_size = 0;
     int heads = kHeads;
-    const int *pos_ptr = nullptr;  // keys = *pos_ptr + 1 (or pos_const + 1)
-    int pos_const = 0;
-    int max_keys = 0;              // capacity the launch shape is sized for (<= attn_max_keys())
-    void *out = nullptr;           // [heads*64] normalised output
+    const int *row_stream = nullptr;  // stream of row r (r * stream_stride when null)
+    int stream_stride = 0;
+    const int *row_pos = nullptr;  // keys of row r = row_pos[r] + 1 (pos0 + r * pos_stride + 1 when null)
+    int pos0 = 0, pos_stride = 1;
+    int rows = 1;
+    int max_keys = 0;              // key capacity: sizes the launch and caps every row's key count
+    void *out = nullptr;           // row r: out + r * out_stride
+    int out_stride = kHidden;
     int out_f16 = 0;               // out is half (else float)
     const DevState *state = nullptr;
 };
-// Decode attention, one workgroup per head (split-KV across its waves, LDS merge).
-int attn_max_keys();
-hipError_t launch_attn_decode(const AttnArgs &a, KvType kv, hipStream_t s);
+hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s);
+
+// W8A16 GEMM on the matrix cores: Y[M][N] = A[M][K] W[N][K]^T with an epilogue.
+struct GemmArgs {
+    const uint8_t *w = nullptr;  // Q8_0_4X4, N x K
+    int N = 0, K = 0;
+    const float *a = nullptr;    // fp32 activations [M][lda]
+    int lda = 0, M = 0;
+    float *y = nullptr;          // EPI_F32 / EPI_RESID / EPI_GELU output [M][ldy]
+    int ldy = 0;
+    const float *resid_in = nullptr;  // EPI_RESID: y = resid_in[m*resid_stride + n] + (acc + bias) (y itself when null)
+    int resid_stride = 0;
+    const float *bias = nullptr;
+    // EPI_QKV: q -> q_out[M][768]; k, v -> pages (same addressing as AttnArgs)
+    float *q_out = nullptr;
+    void *k_pool = nullptr, *v_pool = nullptr;
+    const int *page_table = nullptr;
+    int table_stride = 0, page_size = 0;
+    const int *row_stream = nullptr;  // stream of row m (m * stream_stride when null)
+    int stream_stride = 0;
+    const int *row_pos = nullptr;     // position of row m (pos0 + m * pos_stride when null)
+    int pos0 = 0, pos_stride = 1;
+    const unsigned char *row_active = nullptr;  // rows with row_active[m] == 0 write no K/V
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+};
+hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
 
 // ---- frame / step kernels (frame_ops.hip)
 struct EmbedArgs {
@@ -101,9 +136,43 @@ struct SampleArgs {
 };
 hipError_t launch_sample_greedy(const SampleArgs &a, hipStream_t s);
 
+// ---- row-batched kernels (prefill rows or one row per stream)
+// out[r] = LayerNorm(x[r * x_stride]) for r < rows (x_stride 0 broadcasts one row);
+// rows with mask[r] == 0 are left untouched when mask is non-null.
+hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const float *b, float *out, int rows,
+                          hipStream_t s, const unsigned char *mask = nullptr);
+// x[r] = embedding of rows[r][17] (llm.cpp:148-157)
+hipError_t launch_embed_rows(const EmbedArgs &e, const int *rows, int n, float *x, hipStream_t s);
+
+// Per-stream decode state of the batched engine (device arrays of `streams` entries).
+struct StreamState {
+    int *pos = nullptr;            // next global position
+    unsigned char *active = nullptr;  // 1 while the stream decodes (cleared by the gate / capacity)
+    int *codes = nullptr;          // [S][16] predicted codes of the frame
+    int *row = nullptr;            // [S][17] next global-step row
+    float *gate = nullptr;         // [S][2] (l_end, l_slot)
+    int *counts = nullptr;         // [S][16][1024] used-code occurrences (repetition penalty)
+    int *ctrl = nullptr;           // [0] frame index of the current generate call, [1] min_frames,
+                                   // [2] repetition penalty (float bits) -- device-side so graphs stay valid
+    int capacity = 0;              // KV positions per stream
+};
+// End gate per stream (gate_kernel on each row); inactive streams are left alone.
+hipError_t launch_gate_rows(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
+                            const StreamState &st, int streams, hipStream_t s);
+// Greedy pick per stream for channel ch over logits[S][1024]; next_in[S][768] = aemb[ch][used].
+hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
+                              int streams, int last_channel, hipStream_t s);
+// pos[s] += 1 for active streams; streams reaching capacity become inactive.
+hipError_t launch_advance_rows(const StreamState &st, int streams, hipStream_t s);
+
 // KV import/export between the reference layout [n][768] fp32 of one layer and the
 // device layout [heads][ctx_stride][64] (fp16 or fp32).
 hipError_t launch_kv_import(const float *src, int n_pos, void *dst, int ctx_stride, KvType kv, hipStream_t s);
+// Same into pages: position p -> page table_row[p / page_size], slot p % page_size of [page][head][page_size][64].
+hipError_t launch_kv_import_paged(const float *src, int n_pos, void *pool, const int *table_row, int page_size,
+                                  KvType kv, hipStream_t s);
+hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int page_size, int n_pos, KvType kv,
+                                  float *dst, hipStream_t s);
 hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType kv, float *dst, hipStream_t s);
 
 }  // namespace mh

@@ -4,4 +4,4 @@
 ``moss_format``  .moss v1 / state-file formats and the seeded synthetic model
 """
 from . import moss_format  # noqa: F401
-from .lib import HipLLM, MossHipError, SampleParams, load  # noqa: F401
+from .lib import HipBatch, HipLLM, MossHipError, SampleParams, load  # noqa: F401

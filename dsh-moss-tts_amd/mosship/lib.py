@@ -23,7 +23,9 @@ EXPORTED = [
     "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
     "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
     "moss_hip_llm_kv_export", "moss_hip_llm_kv_import",
-    "moss_hip_gemv_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
+    "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
+    "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
+    "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
 ]
 
 
@@ -84,6 +86,16 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_llm_kv_export.argtypes = [vp, i32, vp, vp]
     L.moss_hip_llm_kv_import.argtypes = [vp, i32, vp, vp, vp]
     L.moss_hip_gemv_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp]
+    L.moss_hip_gemm_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
+    L.moss_hip_batch_create.argtypes = [vp, i32, i32, i32, C.POINTER(vp)]
+    L.moss_hip_batch_destroy.argtypes = [vp]
+    L.moss_hip_batch_destroy.restype = None
+    L.moss_hip_batch_set_stream.argtypes = [vp, i32, i32, vp, vp, vp]
+    L.moss_hip_batch_get_hidden.argtypes = [vp, i32, vp]
+    L.moss_hip_batch_position.argtypes = [vp, i32]
+    L.moss_hip_batch_kv_export.argtypes = [vp, i32, i32, vp, vp]
+    L.moss_hip_batch_global_step.argtypes = [vp, i32, vp]
+    L.moss_hip_batch_generate.argtypes = [vp, i32, i32, C.POINTER(SampleParams), vp, vp, C.POINTER(C.c_double)]
     L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
     L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
     _lib = L
@@ -114,6 +126,12 @@ def gemv_q8x4(w, rows: int, cols: int, x, y, stream=None) -> None:
     dt = {torch.float32: F32, torch.float16: F16}
     check(load().moss_hip_gemv_q8x4(C.c_void_p(w.data_ptr()), rows, cols, C.c_void_p(x.data_ptr()), dt[x.dtype],
                                     C.c_void_p(y.data_ptr()), dt[y.dtype], _stream(stream)))
+
+
+def gemm_q8x4(w, rows: int, cols: int, x, m: int, y, stream=None) -> None:
+    """Y[m][rows] = X[m][cols] W^T on the matrix cores (fp32 x / y device tensors)."""
+    check(load().moss_hip_gemm_q8x4(C.c_void_p(w.data_ptr()), rows, cols, C.c_void_p(x.data_ptr()), m,
+                                    C.c_void_p(y.data_ptr()), _stream(stream)))
 
 
 def dequant_rows_q8x4(w, mat_rows: int, cols: int, rows_idx, out, stream=None) -> None:
@@ -224,3 +242,54 @@ class HipLLM:
         v = np.ascontiguousarray(v, np.float32)
         h = np.ascontiguousarray(hidden, np.float32) if hidden is not None else None
         check(self.L.moss_hip_llm_kv_import(self._h, k.shape[1], _ptr(k), _ptr(v), _ptr(h) if h is not None else None))
+
+
+class HipBatch:
+    """Python view of a moss_hip_batch (many streams decoded in lock-step)."""
+
+    def __init__(self, model: HipLLM, max_streams: int, capacity: int, kv_fp32: bool = False):
+        self.L = load()
+        self.model = model  # keeps the weights alive
+        self._h = C.c_void_p()
+        check(self.L.moss_hip_batch_create(model._h, max_streams, capacity, 1 if kv_fp32 else 0, C.byref(self._h)))
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            self.L.moss_hip_batch_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def set_stream(self, s: int, k, v, hidden):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        h = np.ascontiguousarray(hidden, np.float32)
+        check(self.L.moss_hip_batch_set_stream(self._h, s, k.shape[1], _ptr(k), _ptr(v), _ptr(h)))
+
+    def position(self, s: int) -> int:
+        return self.L.moss_hip_batch_position(self._h, s)
+
+    def hidden(self, s: int) -> np.ndarray:
+        out = np.empty(768, np.float32)
+        check(self.L.moss_hip_batch_get_hidden(self._h, s, _ptr(out)))
+        return out
+
+    def kv_export(self, s: int, n_pos: int):
+        k = np.empty((12, n_pos, 768), np.float32)
+        v = np.empty((12, n_pos, 768), np.float32)
+        check(self.L.moss_hip_batch_kv_export(self._h, s, n_pos, _ptr(k), _ptr(v)))
+        return k, v
+
+    def global_step(self, rows):
+        rows = np.ascontiguousarray(rows, np.int32).reshape(-1, 17)
+        check(self.L.moss_hip_batch_global_step(self._h, rows.shape[0], _ptr(rows)))
+
+    def generate(self, n_streams: int, frames: int, params: SampleParams | None = None):
+        params = params or SampleParams.make()
+        out = np.zeros((max(frames, 1), n_streams, 17), np.int32)
+        nf = np.zeros(n_streams, np.int32)
+        ms = C.c_double(0.0)
+        check(self.L.moss_hip_batch_generate(self._h, n_streams, frames, C.byref(params), _ptr(out), _ptr(nf),
+                                             C.byref(ms)))
+        return {"rows": out[:frames], "frames": nf, "ms": ms.value}

@@ -122,6 +122,33 @@ int moss_hip_llm_kv_export(moss_hip_llm *m, int n_pos, float *k, float *v);
  * hidden768 != NULL, the hidden state.  fp32 values are rounded to fp16 for an fp16 cache. */
 int moss_hip_llm_kv_import(moss_hip_llm *m, int n_pos, const float *k, const float *v, const float *hidden768);
 
+/* ------------------------------------------------------------------ batched streams */
+
+/* Many independent TTS streams decoded in lock-step on one GPU.  No counterpart in the
+ * reference, which runs one LlmModel per stream (csrc/include/moss/llm.h:39-90, one
+ * generate() per job, csrc/src/runtime.cpp:336); each stream here has exactly that
+ * per-stream state and semantics (global KV, hidden, position, history, end gate).
+ * The global KV cache is paged (64-position pages behind a block table).  A batch
+ * shares `model`'s device weights and must be destroyed before it. */
+typedef struct moss_hip_batch moss_hip_batch;
+
+/* max_streams <= 1024; capacity = KV positions per stream (> 17); kv_dtype as in the options. */
+int moss_hip_batch_create(moss_hip_llm *model, int max_streams, int capacity, int kv_dtype, moss_hip_batch **out);
+void moss_hip_batch_destroy(moss_hip_batch *b);
+/* One stream's state, as load_state (csrc/src/llm.cpp:588-632): K/V [12][n_pos][768] fp32 and hidden[768]. */
+int moss_hip_batch_set_stream(moss_hip_batch *b, int stream, int n_pos, const float *k, const float *v,
+                              const float *hidden768);
+int moss_hip_batch_get_hidden(moss_hip_batch *b, int stream, float *out768);
+int moss_hip_batch_position(const moss_hip_batch *b, int stream);
+int moss_hip_batch_kv_export(moss_hip_batch *b, int stream, int n_pos, float *k, float *v);
+/* global_step (csrc/src/llm.cpp:248-255) of streams [0, n_streams): rows [n_streams][17]. */
+int moss_hip_batch_global_step(moss_hip_batch *b, int n_streams, const int32_t *rows);
+/* generate (csrc/src/llm.cpp:634-733) for streams [0, n_streams), frames in lock-step: out_rows
+ * [frames][n_streams][17]; out_frames[s] = frames stream s produced (its end gate / capacity);
+ * *elapsed_ms = device time of the whole run.  Greedy decoding with the greedy end gate. */
+int moss_hip_batch_generate(moss_hip_batch *b, int n_streams, int frames, const moss_hip_sample_params *p,
+                            int32_t *out_rows, int *out_frames, double *elapsed_ms);
+
 /* ------------------------------------------------------------------ operator layer */
 
 enum { MOSS_HIP_F32 = 0, MOSS_HIP_F16 = 1 };
@@ -132,6 +159,10 @@ enum { MOSS_HIP_F32 = 0, MOSS_HIP_F16 = 1 };
 int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_dtype, void *y, int y_dtype,
                        void *stream);
 
+/* Y[m][rows] = X[m][cols] W^T on the matrix cores -- gemm_par (csrc/include/moss/gemv.h:54,
+ * csrc/src/gemv.cpp:276-309) in its A16 mode.  x, y fp32; rows % 16 == 0, cols % 32 == 0. */
+int moss_hip_gemm_q8x4(const void *w, int rows, int cols, const float *x, int m, float *y, void *stream);
+
 /* Dequantise rows of a mat_rows x cols Q8_0_4X4 matrix to fp32 -- LlmModel::lookup_row
  * (llm.cpp:114-146) / dequantize_row_q8_0_4x4 (csrc/src/quant.cpp:56-65).  rows_dev: n device
  * int32 indices; an index outside [0, mat_rows) yields a row of NaN. */
@@ -140,7 +171,7 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
 
 /* Single-query attention over one layer's cache -- LlmModel::attention_core (llm.cpp:189-217).
  * q [heads*64] fp32 (post-RoPE); k_cache/v_cache [heads][ctx_stride][64] of kv_dtype; the
- * first n_keys (<= 4096) positions are attended.  out [heads*64] of out_dtype. */
+ * first n_keys positions are attended.  out [heads*64] of out_dtype. */
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
                          int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
 

@@ -1,0 +1,121 @@
+"""The batched multi-stream engine (moss_hip_batch_*) vs one oracle LlmModel per stream (GPU).
+
+Every stream must behave exactly like an independent LlmModel: same KV, hidden
+and greedy codes as the oracle restatement given the same state.
+"""
+import numpy as np
+import pytest
+from conftest import max_rel
+
+from mosship import HipBatch, HipLLM, SampleParams, lib
+from mosship import moss_format as mf
+from oracle import SampleParams as OSP
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _state(rng, n):
+    k = rng.standard_normal((12, n, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((12, n, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    return k, v, rng.standard_normal(768, dtype=np.float32)
+
+
+@pytest.fixture(scope="module")
+def setup(golden_model):
+    blob, _ = golden_model
+    rng = np.random.default_rng(31)
+    lens = [5, 64, 65, 130, 200]  # ragged: page boundaries on both sides
+    states = [_state(rng, n) for n in lens]
+    return blob, lens, states
+
+
+@pytest.mark.parametrize("kv32", [True, False])
+def test_batch_global_step_vs_oracle(torch_gpu, oracle, setup, kv32):
+    blob, lens, states = setup
+    print(f"batch global step kv32={kv32}", flush=True)
+    g = HipLLM(blob)
+    b = HipBatch(g, max_streams=8, capacity=256, kv_fp32=kv32)
+    for s, (k, v, h) in enumerate(states):
+        b.set_stream(s, k, v, h)
+        assert b.position(s) == lens[s]
+    rng = np.random.default_rng(5)
+    rows = np.concatenate([np.full((len(lens), 1), mf.SLOT), rng.integers(0, 1024, (len(lens), 16))], 1).astype(np.int32)
+    rows[1, 3] = mf.AUDIO_PAD
+    b.global_step(rows)
+    for s, (k, v, h) in enumerate(states):
+        m = oracle.model(blob, kv_f16=not kv32)
+        m.kv_import(k, v)
+        m.set_hidden(h)
+        m.global_step(rows[s])
+        assert b.position(s) == lens[s] + 1 == m.position
+        assert max_rel(b.hidden(s), m.hidden()) <= TOL
+        bk, bv = b.kv_export(s, lens[s] + 1)
+        ok, ov = m.kv_export(lens[s] + 1)
+        assert np.array_equal(bk[:, :lens[s]], ok[:, :lens[s]])  # imported pages untouched
+        assert max_rel(bk[:, lens[s]], ok[:, lens[s]]) <= TOL and max_rel(bv[:, lens[s]], ov[:, lens[s]]) <= TOL
+    b.close()
+    g.close()
+
+
+def test_batch_generate_vs_oracle(torch_gpu, oracle, setup):
+    """4 greedy frames (full frame: local transformer, heads, gate, global step) on 5
+    ragged streams, fp32 KV: codes and hidden per stream follow the oracle."""
+    blob, lens, states = setup
+    g = HipLLM(blob)
+    b = HipBatch(g, max_streams=8, capacity=256, kv_fp32=True)
+    for s, (k, v, h) in enumerate(states):
+        b.set_stream(s, k, v, h)
+    frames = 4
+    out = b.generate(len(lens), frames, SampleParams.make(greedy=True, min_frames=frames, repetition_penalty=1.2))
+    assert (out["frames"] == frames).all()
+    agree = []
+    for s, (k, v, h) in enumerate(states):
+        m = oracle.model(blob)
+        m.kv_import(k, v)
+        m.set_hidden(h)
+        ref = m.generate(frames, OSP.make(greedy=True, min_frames=frames, repetition_penalty=1.2))
+        agree.append(np.mean(out["rows"][:, s, 1:] == ref["rows"][:, 1:]))
+        assert b.position(s) == m.position
+        assert max_rel(b.hidden(s), m.hidden()) <= TOL
+    print("per-stream agreement", agree)
+    assert min(agree) >= 0.99
+
+
+def test_batch_end_gate_per_stream(torch_gpu, oracle, setup):
+    """min_frames = 0: each stream stops on its own end gate, like its own LlmModel."""
+    blob, lens, states = setup
+    g = HipLLM(blob)
+    b = HipBatch(g, max_streams=8, capacity=256, kv_fp32=True)
+    for s, (k, v, h) in enumerate(states):
+        b.set_stream(s, k, v, h)
+    out = b.generate(len(lens), 5, SampleParams.make(greedy=True, min_frames=0))
+    for s, (k, v, h) in enumerate(states):
+        m = oracle.model(blob)
+        m.kv_import(k, v)
+        m.set_hidden(h)
+        ref = m.generate(5, OSP.make(greedy=True, min_frames=0))
+        assert out["frames"][s] == len(ref["rows"])
+        assert np.array_equal(out["rows"][:out["frames"][s], s], ref["rows"])
+        assert b.position(s) == m.position
+
+
+def test_batch_capacity_and_errors(torch_gpu, oracle, setup):
+    blob, lens, states = setup
+    g = HipLLM(blob)
+    b = HipBatch(g, max_streams=2, capacity=66)
+    k, v, h = states[1]  # 64 positions: 2 more fit
+    b.set_stream(0, k, v, h)
+    out = b.generate(1, 10, SampleParams.make(greedy=True, min_frames=10))
+    m = oracle.model(blob, max_ctx=66)  # the reference's frame loop with kMaxCtx = 66 (llm.cpp:644,703)
+    m.kv_import(k, v)
+    m.set_hidden(h)
+    ref = m.generate(10, OSP.make(greedy=True, min_frames=10))
+    assert out["frames"][0] == len(ref["rows"]) == 2
+    assert b.position(0) == m.position == 66
+    with pytest.raises(lib.MossHipError) as e:
+        b.set_stream(1, *_state(np.random.default_rng(0), 67))
+    assert e.value.code == lib.EINVAL
+    with pytest.raises(lib.MossHipError) as e:
+        b.global_step(np.full((1, 17), 9, np.int32))  # stream 0 is at capacity
+    assert e.value.code == lib.ESTATE

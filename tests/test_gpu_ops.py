@@ -146,3 +146,22 @@ def test_operator_errors(torch_gpu):
     with pytest.raises(lib.MossHipError) as e:
         lib.gemv_q8x4(w, 6, 768, x, y)  # rows % 4 != 0
     assert e.value.code == lib.EINVAL
+
+
+@pytest.mark.parametrize("rows,cols,m", [(2304, 768, 64), (768, 3072, 64), (3072, 768, 256), (1024, 768, 1),
+                                         (768, 768, 17), (16, 128, 100), (2304, 768, 200)])
+def test_gemm_mfma_vs_oracle(torch_gpu, oracle, rows, cols, m):
+    """MFMA W8A16 GEMM (fp16 hi/lo activation split) vs the oracle's A16 gemm_par."""
+    torch = torch_gpu
+    print(f"gemm rows={rows} cols={cols} m={m}", flush=True)
+    rng = np.random.default_rng(rows + cols + m)
+    w = mf.synth_q8x4(rng, rows, cols)
+    x = (rng.standard_normal((m, cols)) * rng.choice([0.01, 1.0, 30.0], (m, 1))).astype(np.float32)
+    y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+    lib.gemm_q8x4(_dev(torch, w), rows, cols, _dev(torch, x), m, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle.gemm(w, rows, cols, x, a16=True)
+    for i in range(m):  # per row: rows of very different scale
+        assert max_rel(got[i], ref[i]) <= TOL
+    assert max_rel(got, ref) <= 1e-5
