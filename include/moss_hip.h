@@ -8,7 +8,7 @@
  *     (reference csrc/include/moss/llm.h:39-90).  Host pointers in, host
  *     pointers out; the library owns the weights, the KV cache and the decode
  *     state on the device.  A C++ class with LlmModel's public surface sits on
- *     top of these calls (dsh-moss-tts_amd/host/moss_hip_llm.hpp).
+ *     top of these calls (dsh-moss-tts_amd/host/moss/llm.h, host/llm_hip.cpp).
  *  2. Operator layer (moss_hip_gemv_q8x4, moss_hip_attn_decode, ...): the hot
  *     kernels on caller-owned device memory, for tests and benchmarks.  Every
  *     pointer argument is a device pointer; `stream` is a hipStream_t (NULL =

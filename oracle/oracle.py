@@ -451,6 +451,11 @@ class RefModel:
         if self.lib.ref_model_save_state(self.h, path.encode(), rows, rows.shape[0]) != 0:
             raise RuntimeError(self.lib.ref_last_error().decode())
 
+    def load_prefix(self, path, rows):
+        rows = np.ascontiguousarray(rows, np.int32).reshape(-1, 17)
+        if self.lib.ref_model_load_prefix(self.h, path.encode(), rows, rows.shape[0]) != 0:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+
     def generate(self, max_frames, params: SampleParams, seed=0, forced=None, timing=False, logits_path=None):
         out = np.zeros((max_frames, 17), np.int32)
         fa = np.ascontiguousarray(forced, np.int32).reshape(-1, 17) if forced is not None else None

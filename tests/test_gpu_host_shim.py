@@ -1,0 +1,122 @@
+"""The C++ drop-in moss::LlmModel (dsh-moss-tts_amd/host) driven through a
+moss_llm-style CLI, vs the oracle and the compiled reference (GPU).
+
+Covers the boundary a reference maintainer would link: load, prefill,
+generate with timing / on_frame / teacher forcing, and the .mosskv prefix and
+MOSSST1 state files (byte layout checked against the reference's loader)."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+from conftest import ROOT, max_rel
+
+from mosship import moss_format as mf
+from oracle import REF_SO
+from oracle import SampleParams as OSP
+
+pytestmark = pytest.mark.gpu
+BIN = os.path.join(ROOT, "tests", "host", "moss_llm_hip")
+
+
+def _run(*args):
+    print("moss_llm_hip", *args, flush=True)
+    out = subprocess.run([BIN, *map(str, args)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    return json.loads(out.stdout)
+
+
+@pytest.fixture(scope="module")
+def files(tmp_path_factory, golden_model):
+    blob, g = golden_model
+    d = tmp_path_factory.mktemp("shim")
+    w = d / "w.moss"
+    w.write_bytes(blob)
+    rows = g["rows"]
+    prompt = d / "rows.txt"
+    prompt.write_text("# golden prompt\n" + "\n".join(" ".join(map(str, r)) for r in rows) + "\n")
+    return blob, rows, str(w), str(prompt), d
+
+
+def test_shim_prefill_generate_state(torch_gpu, oracle, files):
+    if not os.path.exists(BIN):
+        pytest.fail("tests/host/moss_llm_hip not built (make -C dsh-moss-tts_amd)")
+    blob, rows, w, prompt, d = files
+    state = str(d / "s.state")
+    res = _run("--weights", w, "--prompt", prompt, "--frames", 4, "--min-frames", 4, "--greedy", "--rep", 1.2,
+               "--save-state", state)
+    m = oracle.model(blob)
+    m.prefill(rows, a16=True)
+    _, n_pos, rows_fp, weights_fp, k, v, hidden = mf.read_state(open(state, "rb").read())
+    assert n_pos == len(rows) and rows_fp == mf.fp_rows(rows) and weights_fp == mf.fp_weights(blob)
+    assert max_rel(hidden, m.hidden()) <= 1e-3
+    ok_, ov_ = m.kv_export(len(rows))
+    assert max_rel(k, ok_) <= 1e-3 and max_rel(v, ov_) <= 1e-3
+    ref = m.generate(4, OSP.make(greedy=True, min_frames=4, repetition_penalty=1.2))
+    codes = np.array(res["codes"])
+    assert res["frames"] == 4 == res["callbacks"] and res["position"] == m.position
+    assert np.mean(codes == ref["rows"][:, 1:]) >= 0.99
+    assert res["global_ms_per_frame"] > 0
+    if os.path.exists(REF_SO):  # the reference's own loader accepts the file (fingerprints included)
+        from oracle import RefCpu
+        r = RefCpu().model(blob, threads=2)
+        r.load_state(state, rows, ignore_fp=False)
+        assert r.position == len(rows)
+        assert np.array_equal(r.hidden(), hidden)
+
+
+def test_shim_prefix_flow(torch_gpu, oracle, files):
+    """Voice-prefix flow: prefill + save the first K rows, reload them from the file in a
+    fresh process, prefill the rest at start = K; both runs agree exactly and follow the
+    oracle; the reference's own load_prefix accepts the file."""
+    blob, rows, w, prompt, d = files
+    K = 4
+    prefix = str(d / "p.mosskv")
+    common = ["--weights", w, "--prompt", prompt, "--prefix-rows", K, "--frames", 3, "--min-frames", 3, "--greedy"]
+    a = _run(*common, "--save-prefix", prefix)
+    b = _run(*common, "--load-prefix", prefix)
+    assert a["codes"] == b["codes"] and a["hidden0"] == b["hidden0"] and a["position"] == b["position"]
+    m = oracle.model(blob)
+    m.prefill(rows[:K], a16=True)
+    m.prefill(rows[K:], start=K, a16=True)
+    ref = m.generate(3, OSP.make(greedy=True, min_frames=3))
+    assert a["position"] == m.position
+    assert np.mean(np.array(a["codes"]) == ref["rows"][:, 1:]) >= 0.99
+    with open(prefix, "rb") as f:
+        assert f.read(8) == b"MOSSPFX1"
+    if os.path.exists(REF_SO):
+        from oracle import RefCpu
+        r = RefCpu().model(blob, threads=2)
+        r.load_prefix(prefix, rows[:K])
+        assert r.position == K
+        with pytest.raises(RuntimeError):
+            r.load_prefix(prefix, rows[:K - 1])  # rows fingerprint mismatch
+
+
+def test_shim_teacher_forcing(torch_gpu, oracle, files):
+    blob, rows, w, prompt, d = files
+    m = oracle.model(blob)
+    m.prefill(rows, a16=True)
+    ref = m.generate(3, OSP.make(greedy=True, min_frames=3))
+    forced = d / "forced.txt"
+    forced.write_text("\n".join(" ".join(map(str, r[1:])) for r in ref["rows"]) + "\n")
+    res = _run("--weights", w, "--prompt", prompt, "--frames", 3, "--min-frames", 3, "--greedy",
+               "--force-codes", str(forced))
+    assert res["codes"] == ref["rows"][:, 1:].tolist() and res["frames"] == 3
+    # forcing its own greedy codes leaves the oracle where free running left it
+    mf_ = oracle.model(blob)
+    mf_.prefill(rows, a16=True)
+    mf_.generate(3, OSP.make(greedy=True, min_frames=3), forced=ref["rows"])
+    h = mf_.hidden()
+    assert res["position"] == mf_.position
+    assert abs(res["hidden0"] - h[0]) <= 1e-3 * np.abs(h).max()
+
+
+def test_shim_rejects_bad_files(torch_gpu, files):
+    blob, rows, w, prompt, d = files
+    bad = d / "bad.state"
+    bad.write_bytes(b"MOSSST1\x00" + bytes(100))
+    out = subprocess.run([BIN, "--weights", w, "--prompt", prompt, "--load-state", str(bad)], capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 2 and "bad header" in out.stderr
