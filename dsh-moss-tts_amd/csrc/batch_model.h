@@ -35,9 +35,11 @@ public:
     void kv_export(int s, int n_pos, float *k, float *v);
     // One global step for streams [0, n): rows [n][17].
     void global_step(int n, const int32_t *rows);
-    // Greedy frames for streams [0, n) (llm.cpp:634-733 per stream, in lock-step).
+    // Frames for streams [0, n) (llm.cpp:634-733 per stream, in lock-step); stream s
+    // draws from its own xoshiro stream seeded with seeds[s] (0 when seeds is null).
     // out_rows [frames][n][17]; out_frames[s] = frames stream s produced.  Returns elapsed ms.
-    double generate(int n, int frames, const moss_hip_sample_params &p, int32_t *out_rows, int *out_frames);
+    double generate(int n, int frames, const moss_hip_sample_params &p, const uint64_t *seeds, int32_t *out_rows,
+                    int *out_frames);
 
 private:
     struct Graphs {
@@ -48,7 +50,7 @@ private:
     void enqueue_global(hipStream_t s, int n);
     Graphs &graphs_for(int n);
     StreamState state() const;
-    void write_ctrl(int frame, int min_frames, float rep);
+    void write_ctrl(int min_frames, float rep, const SampleCfg &cfg);
 
     Model &model_;
     Model::Weights w_;
@@ -66,12 +68,14 @@ private:
     int rope_n_ = 0;
     float *x_ = nullptr, *a_ = nullptr, *q_ = nullptr, *o_ = nullptr, *h_ = nullptr;
     float *hidden_ = nullptr, *lres_ = nullptr, *next_in_ = nullptr, *logits_ = nullptr;
-    int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr, *ctrl_ = nullptr;
+    int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr;
+    BatchCtl *ctrl_ = nullptr;
+    uint32_t *rng_ = nullptr;                   // [S][4]
     unsigned char *active_ = nullptr;
     float *gate_ = nullptr;
     int *hist_codes_ = nullptr;                 // [cap+1][S][16] codes per frame
     unsigned char *hist_active_ = nullptr;      // [cap+1][S] active after each frame's gate
-    int *ctrl_h_ = nullptr;                     // pinned host staging for ctrl
+    BatchCtl *ctrl_h_ = nullptr;                // pinned host staging for ctrl
     std::vector<int> pos_;
     std::map<int, Graphs> graphs_;
 };

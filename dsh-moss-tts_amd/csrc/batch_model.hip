@@ -70,12 +70,14 @@ Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
     im(&codes_, (size_t)S_ * kNVq);
     im(&row_, (size_t)S_ * (kNVq + 1));
     im(&counts_, (size_t)S_ * kNVq * kCodebook);
-    im(&ctrl_, 4);
+    hip_check(hipMalloc(&ctrl_, sizeof(BatchCtl)), "hipMalloc(ctrl)");
+    hip_check(hipMalloc(&rng_, sizeof(uint32_t) * 4 * S_), "hipMalloc(rng)");
+    hip_check(hipMemset(rng_, 0, sizeof(uint32_t) * 4 * S_), "memset(rng)");
     im(&hist_codes_, (size_t)(cap_ + 1) * S_ * kNVq);
     hip_check(hipMalloc(&active_, S_), "hipMalloc(active)");
     hip_check(hipMemset(active_, 0, S_), "memset(active)");
     hip_check(hipMalloc(&hist_active_, (size_t)(cap_ + 1) * S_), "hipMalloc(history)");
-    hip_check(hipHostMalloc(&ctrl_h_, 4 * sizeof(int), hipHostMallocDefault), "hipHostMalloc(ctrl)");
+    hip_check(hipHostMalloc(&ctrl_h_, sizeof(BatchCtl), hipHostMallocDefault), "hipHostMalloc(ctrl)");
     pos_.assign(S_, 0);
 }
 
@@ -87,7 +89,7 @@ Batch::~Batch() {
         if (kv.second.global) (void)hipGraphExecDestroy(kv.second.global);
     }
     void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
-                    gate_, pos_d_, codes_, row_, counts_, ctrl_, hist_codes_, active_, hist_active_};
+                    gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (ctrl_h_) (void)hipHostFree(ctrl_h_);
@@ -105,16 +107,17 @@ StreamState Batch::state() const {
     st.gate = gate_;
     st.counts = counts_;
     st.ctrl = ctrl_;
+    st.rng = rng_;
     st.capacity = cap_;
     return st;
 }
 
-void Batch::write_ctrl(int frame, int min_frames, float rep) {
-    ctrl_h_[0] = frame;
-    ctrl_h_[1] = min_frames;
-    std::memcpy(&ctrl_h_[2], &rep, 4);
-    ctrl_h_[3] = 0;
-    hip_check(hipMemcpyAsync(ctrl_, ctrl_h_, 4 * sizeof(int), hipMemcpyHostToDevice, stream_), "ctrl h2d");
+void Batch::write_ctrl(int min_frames, float rep, const SampleCfg &cfg) {
+    ctrl_h_->frame = 0;
+    ctrl_h_->min_frames = min_frames;
+    ctrl_h_->rep_penalty = rep;
+    ctrl_h_->cfg = cfg;
+    hip_check(hipMemcpyAsync(ctrl_, ctrl_h_, sizeof(BatchCtl), hipMemcpyHostToDevice, stream_), "ctrl h2d");
 }
 
 void Batch::set_stream(int s, int n_pos, const float *k, const float *v, const float *hidden) {
@@ -302,16 +305,18 @@ void Batch::global_step(int n, const int32_t *rows) {
     std::vector<unsigned char> act(n, 1);
     hip_check(hipMemcpyAsync(row_, rows, sizeof(int32_t) * 17 * n, hipMemcpyHostToDevice, stream_), "rows h2d");
     hip_check(hipMemcpyAsync(active_, act.data(), n, hipMemcpyHostToDevice, stream_), "active h2d");
-    write_ctrl(0, 0, 1.0f);
+    moss_hip_sample_params gp{};
+    gp.greedy = 1;
+    gp.end_greedy = 1;
+    write_ctrl(0, 1.0f, sample_cfg(gp));
     hip_check(hipGraphLaunch(g.global, stream_), "graph launch");
     hip_check(hipMemcpyAsync(pos_.data(), pos_d_, sizeof(int) * S_, hipMemcpyDeviceToHost, stream_), "pos d2h");
     hip_check(hipStreamSynchronize(stream_), "sync");
 }
 
-double Batch::generate(int n, int frames, const moss_hip_sample_params &p, int32_t *out_rows, int *out_frames) {
+double Batch::generate(int n, int frames, const moss_hip_sample_params &p, const uint64_t *seeds, int32_t *out_rows,
+                       int *out_frames) {
     if (n <= 0 || n > S_) throw Status(MOSS_HIP_EINVAL, "n_streams out of range");
-    if (!(p.greedy || p.top_k == 1) || !p.end_greedy)
-        throw Status(MOSS_HIP_EUNSUPPORTED, "only greedy decoding with the greedy end gate runs on the device");
     if (frames <= 0) return 0.0;
     if (frames > cap_ + 1) frames = cap_ + 1;
     hip_check(hipSetDevice(model_.device()), "hipSetDevice");
@@ -320,7 +325,10 @@ double Batch::generate(int n, int frames, const moss_hip_sample_params &p, int32
     for (int s = 0; s < n; ++s) act[s] = pos_[s] < cap_ ? 1 : 0;
     hip_check(hipMemcpyAsync(active_, act.data(), n, hipMemcpyHostToDevice, stream_), "active h2d");
     hip_check(hipMemsetAsync(counts_, 0, sizeof(int) * (size_t)n * kNVq * kCodebook, stream_), "counts clear");
-    write_ctrl(0, p.min_frames, p.repetition_penalty);
+    write_ctrl(p.min_frames, p.repetition_penalty, sample_cfg(p));
+    std::vector<uint32_t> rs((size_t)4 * n);
+    for (int s = 0; s < n; ++s) rng_seed_host(seeds ? seeds[s] : 0, &rs[(size_t)4 * s]);
+    hip_check(hipMemcpyAsync(rng_, rs.data(), rs.size() * sizeof(uint32_t), hipMemcpyHostToDevice, stream_), "rng h2d");
     hip_check(hipStreamSynchronize(stream_), "sync");
     hip_check(hipEventRecord(ev_[0], stream_), "event");
     for (int f = 0; f < frames; ++f) {

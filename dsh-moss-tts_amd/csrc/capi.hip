@@ -234,10 +234,10 @@ int moss_hip_batch_global_step(moss_hip_batch *b, int n_streams, const int32_t *
 }
 
 int moss_hip_batch_generate(moss_hip_batch *b, int n_streams, int frames, const moss_hip_sample_params *p,
-                            int32_t *out_rows, int *out_frames, double *elapsed_ms) {
+                            const uint64_t *seeds, int32_t *out_rows, int *out_frames, double *elapsed_ms) {
     return guard([&] {
         if (!p || !out_rows || frames < 0) throw Status(MOSS_HIP_EINVAL, "bad arguments");
-        const double ms = batch_of(b).generate(n_streams, frames, *p, out_rows, out_frames);
+        const double ms = batch_of(b).generate(n_streams, frames, *p, seeds, out_rows, out_frames);
         if (elapsed_ms) *elapsed_ms = ms;
     });
 }

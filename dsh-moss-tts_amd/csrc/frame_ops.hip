@@ -53,6 +53,153 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *w, int
         out[(size_t)blockIdx.x * cols + c] = ok ? q8x4_elem(w, nb, r, c) : __int_as_float(0x7fc00000);
 }
 
+// ---- sample_token (reference csrc/src/sampler.cpp:9-79) for one 1024-entry
+// logit row, by one 256-thread workgroup.  The caller has applied the
+// repetition penalty into vals[] (LDS).
+
+struct PickLds {
+    float vals[kCodebook];     // penalised (then temperature-scaled) logits
+    uint64_t keys[kCodebook];  // sort keys: value descending, index ascending
+    float ex[kCodebook];       // exp(v - max) of the candidates, in sorted order
+    float bv[4];
+    int bi[4];
+    int pick;
+    int used;
+};
+
+// Greedy branch (sampler.cpp:23-28): argmax, the lowest index wins ties, index 0
+// when every value is NaN (the reference's scan never moves off 0).
+__device__ int pick_greedy(PickLds &L) {
+    const int t = threadIdx.x;
+    float best = -INFINITY;
+    int besti = kCodebook;
+    for (int i = t; i < kCodebook; i += 256) {  // ascending i per thread
+        const float v = L.vals[i];
+        if (v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(besti, off);
+        if (ov > best || (ov == best && oi < besti)) {
+            best = ov;
+            besti = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        L.bv[t >> 6] = best;
+        L.bi[t >> 6] = besti;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float b = L.bv[0];
+        int idx = L.bi[0];
+        for (int w = 1; w < 4; ++w)
+            if (L.bv[w] > b || (L.bv[w] == b && L.bi[w] < idx)) {
+                b = L.bv[w];
+                idx = L.bi[w];
+            }
+        L.pick = idx >= kCodebook ? 0 : idx;
+    }
+    __syncthreads();
+    return L.pick;
+}
+
+// Order-preserving map of a float to uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t float_order(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Sampling branch (sampler.cpp:30-78): temperature, top-k by a full sort
+// (value descending; equal values by index), softmax over the k candidates,
+// top-p cut, one uniform draw walked down the sorted candidates.  The
+// sequential sums run in one thread in the reference's order.
+__device__ int pick_sampled(PickLds &L, const SampleCfg &c, uint32_t *rng) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x;
+    const bool scale = c.temperature > 0.0f && c.temperature != 1.0f;
+    const float inv = scale ? 1.0f / c.temperature : 1.0f;
+    for (int i = t; i < kCodebook; i += 256) {
+        float v = L.vals[i];
+        if (scale) v = v * inv;
+        L.vals[i] = v;
+        L.keys[i] = ((uint64_t)(~float_order(v)) << 32) | (uint32_t)i;
+    }
+    __syncthreads();
+    // bitonic sort, ascending keys
+    for (int k = 2; k <= kCodebook; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = t; i < kCodebook; i += 256) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint64_t a = L.keys[i], b = L.keys[ixj];
+                    const bool up = (i & k) == 0;
+                    if ((a > b) == up) {
+                        L.keys[i] = b;
+                        L.keys[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    const int n = c.top_k > 0 ? (c.top_k < kCodebook ? c.top_k : kCodebook) : kCodebook;
+    const float maxv = L.vals[(int)(L.keys[0] & 0xffffffffu)];
+    for (int i = t; i < n; i += 256) L.ex[i] = expf(L.vals[(int)(L.keys[i] & 0xffffffffu)] - maxv);
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < n; ++i) sum += L.ex[i];
+        int cnt = n;
+        if (c.top_p < 1.0f) {
+            float cum = 0.0f;
+            int keep = 0;
+            for (; keep < n; ++keep) {
+                cum += L.ex[keep] / sum;
+                if (cum >= c.top_p) {
+                    ++keep;
+                    break;
+                }
+            }
+            cnt = keep > 1 ? keep : 1;
+            sum = 0.0f;
+            for (int i = 0; i < cnt; ++i) sum += L.ex[i];
+        }
+        float r = rng_uniform(rng) * sum;
+        int pick = (int)(L.keys[cnt - 1] & 0xffffffffu);
+        for (int i = 0; i < cnt; ++i) {
+            r -= L.ex[i];
+            if (r <= 0.0f) {
+                pick = (int)(L.keys[i] & 0xffffffffu);
+                break;
+            }
+        }
+        L.pick = pick;
+    }
+    __syncthreads();
+    return L.pick;
+}
+
+// vals[i] = logits[i] with the repetition penalty applied once per past
+// occurrence of i (sampler.cpp:13-21: v<0 ? v*p : v/p, repeated).  Each index
+// is penalised independently, so per-index counts reproduce the reference's
+// walk over the history exactly.
+__device__ void load_penalised(PickLds &L, const float *logits, const int *counts, float p) {
+#pragma clang fp contract(off)
+    for (int i = threadIdx.x; i < kCodebook; i += 256) {
+        float v = logits[i];
+        if (p != 1.0f) {
+            const int c = counts[i];
+            for (int k = 0; k < c; ++k) v = v < 0.0f ? v * p : v / p;
+        }
+        L.vals[i] = v;
+    }
+    __syncthreads();
+}
+
 // End gate (reference csrc/src/llm.cpp:274-285 + :30-35 + :678):
 //  1. h = LayerNorm(x; local lnf)                     (the local step's output)
 //  2. W8A8 quantisation of h per 32-block            (csrc/src/quant.cpp:28-43):
@@ -61,7 +208,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *w, int
 //     row_dot_q8_4x4 (csrc/src/gemv_avx2.cpp:105-121): 8 lane accumulators, lane j
 //     takes the exact int32 sum of bytes 4j..4j+3 of each block, fma'd with
 //     (d_w * d_a); then the 8 lanes are summed as _mm256 hsum does.
-//  4. stop = frame >= min_frames && l_end > l_slot   (greedy end, llm.cpp:31)
+//  4. stop = frame >= min_frames && end_reached(l_slot, l_end)  (llm.cpp:30-35,678)
 // Integer parts are exact and the fp32 operation order is the reference's, so
 // the gate values are bit-identical to the reference given the same h.
 __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const float *lnf_w, const float *lnf_b,
@@ -131,77 +278,40 @@ __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const flo
             gate_log[2 * state->frame] = g[0];
             gate_log[2 * state->frame + 1] = g[1];
         }
-        if (state->frame >= state->min_frames && g[0] > g[1]) state->stop = 1;
+        if (state->frame >= state->min_frames && end_reached(g[1], g[0], state->cfg, state->rng)) state->stop = 1;
     }
 }
 
-// Greedy pick with repetition penalty (reference csrc/src/sampler.cpp:9-28):
-// the penalty is applied once per past occurrence of a code (v<0 ? v*p : v/p,
-// repeated), then argmax with the lowest index winning ties.  Then the used code
-// (forced under teacher forcing) is appended to the history, written into the
-// next global-step row, and its aemb row becomes the next local input
-// (llm.cpp:692-697).
-__global__ __launch_bounds__(256) void sample_greedy_kernel(SampleArgs a) {
-#pragma clang fp contract(off)
-    __shared__ float bv[4];
-    __shared__ int bi[4];
-    __shared__ int used_s;
+// One pick of channel ch (reference csrc/src/sampler.cpp:9-79 as called from
+// llm.cpp:689-697): repetition penalty over this generate()'s used codes,
+// greedy (SampleParams::greedy, top_k == 1 or frame < greedy_frames) or
+// sampled with the call's xoshiro stream.  Then the used code (forced under
+// teacher forcing) is counted into the history, written into the next
+// global-step row, and its aemb row becomes the next local input.
+__global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
+    __shared__ PickLds L;
     DevState *st = a.state;
     if (st->stop) return;
     const int t = threadIdx.x;
-    const float p = st->rep_penalty;
-    const int *cnt = a.counts + a.ch * kCodebook;
-    float best = -INFINITY;
-    int besti = kCodebook;
-    for (int i = t; i < kCodebook; i += 256) {  // ascending i per thread
-        float v = a.logits[i];
-        if (p != 1.0f) {
-            const int c = cnt[i];
-            for (int k = 0; k < c; ++k) v = v < 0.0f ? v * p : v / p;
-        }
-        if (v > best) {
-            best = v;
-            besti = i;
-        }
-    }
-    // wave reduction keeping (max value, lowest index)
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(besti, off);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
-    if ((t & 63) == 0) {
-        bv[t >> 6] = best;
-        bi[t >> 6] = besti;
-    }
-    __syncthreads();
+    load_penalised(L, a.logits, a.counts + a.ch * kCodebook, st->rep_penalty);
+    const SampleCfg c = st->cfg;
+    const bool greedy = c.greedy || st->frame < c.greedy_frames;
+    const int idx = greedy ? pick_greedy(L) : pick_sampled(L, c, st->rng);
     if (t == 0) {
-        float b = bv[0];
-        int idx = bi[0];
-        for (int w = 1; w < 4; ++w)
-            if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
-                b = bv[w];
-                idx = bi[w];
-            }
-        if (idx >= kCodebook) idx = 0;  // all NaN: the reference's scan keeps index 0
         const int used = st->forced_on ? a.forced[st->frame * kNVq + a.ch] : idx;
         st->codes[a.ch] = idx;
         st->row[a.ch + 1] = used;
         a.counts[a.ch * kCodebook + used] += 1;
-        used_s = used;
+        L.used = used;
         if (a.last_channel) {
             st->row[0] = kSlotToken;
             st->frame += 1;
         }
     }
     __syncthreads();
-    const int used = used_s;
+    const int used = L.used;
     const int nb = kHidden / 32;
-    for (int c = t; c < kHidden; c += 256) a.next_input[c] = q8x4_elem(a.aemb, nb, used, c);
+    for (int c2 = t; c2 < kHidden; c2 += 256) a.next_input[c2] = q8x4_elem(a.aemb, nb, used, c2);
 }
 
 template <int KV>
@@ -261,9 +371,9 @@ hipError_t launch_gate(const float *x_raw, const float *lnf_w, const float *lnf_
     return hipGetLastError();
 }
 
-hipError_t launch_sample_greedy(const SampleArgs &a, hipStream_t s) {
+hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    hipLaunchKernelGGL(sample_greedy_kernel, dim3(1), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -394,19 +504,18 @@ __global__ __launch_bounds__(256) void gate_rows_kernel(const float *x_raw, cons
         }
         st.gate[2 * srow] = g[0];
         st.gate[2 * srow + 1] = g[1];
-        if (st.ctrl[0] >= st.ctrl[1] && g[0] > g[1]) st.active[srow] = 0;
+        if (st.ctrl->frame >= st.ctrl->min_frames && end_reached(g[1], g[0], st.ctrl->cfg, st.rng + 4 * srow))
+            st.active[srow] = 0;
     }
 }
 
-// sample_greedy_kernel per stream; inactive streams keep their state.
+// sample_kernel per stream (one workgroup each, own history and xoshiro
+// stream); inactive streams keep their state.  Teacher forcing is not offered
+// by the batched engine, so the used code is the pick.
 __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, int ch, const uint8_t *aemb,
                                                           float *next_in, StreamState st, int last_channel) {
-#pragma clang fp contract(off)
-    __shared__ float bv[4];
-    __shared__ int bi[4];
-    __shared__ int used_s;
+    __shared__ PickLds L;
     const int srow = blockIdx.x, t = threadIdx.x;
-    const float *lg = logits + (size_t)srow * kCodebook;
     float *nxt = next_in + (size_t)srow * kHidden;
     const int nb = kHidden / 32;
     if (!st.active[srow]) {
@@ -414,58 +523,23 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
         for (int c = t; c < kHidden; c += 256) nxt[c] = q8x4_elem(aemb, nb, 0, c);
         return;
     }
-    const float p = __int_as_float(st.ctrl[2]);
-    const int *cnt = st.counts + ((size_t)srow * kNVq + ch) * kCodebook;
-    float best = -INFINITY;
-    int besti = kCodebook;
-    for (int i = t; i < kCodebook; i += 256) {
-        float v = lg[i];
-        if (p != 1.0f) {
-            const int c = cnt[i];
-            for (int k = 0; k < c; ++k) v = v < 0.0f ? v * p : v / p;
-        }
-        if (v > best) {
-            best = v;
-            besti = i;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(besti, off);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
-    if ((t & 63) == 0) {
-        bv[t >> 6] = best;
-        bi[t >> 6] = besti;
-    }
-    __syncthreads();
+    int *cnt = st.counts + ((size_t)srow * kNVq + ch) * kCodebook;
+    load_penalised(L, logits + (size_t)srow * kCodebook, cnt, st.ctrl->rep_penalty);
+    const SampleCfg c = st.ctrl->cfg;
+    const bool greedy = c.greedy || st.ctrl->frame < c.greedy_frames;
+    const int idx = greedy ? pick_greedy(L) : pick_sampled(L, c, st.rng + 4 * srow);
     if (t == 0) {
-        float b = bv[0];
-        int idx = bi[0];
-        for (int w = 1; w < 4; ++w)
-            if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
-                b = bv[w];
-                idx = bi[w];
-            }
-        if (idx >= kCodebook) idx = 0;
         st.codes[srow * kNVq + ch] = idx;
         st.row[srow * (kNVq + 1) + ch + 1] = idx;
-        st.counts[((size_t)srow * kNVq + ch) * kCodebook + idx] += 1;
+        cnt[idx] += 1;
         if (last_channel) st.row[srow * (kNVq + 1)] = kSlotToken;
-        used_s = idx;
     }
-    __syncthreads();
-    const int used = used_s;
-    for (int c = t; c < kHidden; c += 256) nxt[c] = q8x4_elem(aemb, nb, used, c);
+    for (int c2 = t; c2 < kHidden; c2 += 256) nxt[c2] = q8x4_elem(aemb, nb, idx, c2);
 }
 
 __global__ void advance_rows_kernel(StreamState st, int streams) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s == 0) st.ctrl[0] += 1;
+    if (s == 0) st.ctrl->frame += 1;
     if (s >= streams || !st.active[s]) return;
     const int p = st.pos[s] + 1;
     st.pos[s] = p;

@@ -24,6 +24,19 @@ struct Status : std::runtime_error {
 
 void hip_check(hipError_t e, const char *what);
 
+// SampleParams of the C ABI -> the device copy.  Greedy as sample_token decides
+// it (sampler.cpp:23: greedy || top_k == 1).
+inline SampleCfg sample_cfg(const moss_hip_sample_params &p) {
+    SampleCfg c;
+    c.greedy = (p.greedy || p.top_k == 1) ? 1 : 0;
+    c.temperature = p.temperature;
+    c.top_k = p.top_k;
+    c.top_p = p.top_p;
+    c.end_greedy = p.end_greedy ? 1 : 0;
+    c.greedy_frames = p.greedy_frames;
+    return c;
+}
+
 struct LayerW {
     const float *ln1_w, *ln1_b, *ln2_w, *ln2_b;
     const uint8_t *attn_w;

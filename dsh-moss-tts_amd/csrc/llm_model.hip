@@ -297,7 +297,7 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
 }
 
 // The local half of a frame (llm.cpp:648-698): local step on hidden, end gate,
-// then 16 x (local step, audio head of channel ch, greedy pick + next input).
+// then 16 x (local step, audio head of channel ch, pick + next input).
 void Model::enqueue_frame_local(hipStream_t s) {
     enqueue_local_step(s, hidden_, 0);
     hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, gate_log_, s), "gate");
@@ -317,7 +317,7 @@ void Model::enqueue_frame_local(hipStream_t s) {
         sa.next_input = next_in_;
         sa.state = state_;
         sa.last_channel = ch == kNVq - 1;
-        hip_check(launch_sample_greedy(sa, s), "sample");
+        hip_check(launch_sample(sa, s), "sample");
     }
 }
 
@@ -460,10 +460,6 @@ void Model::prefill(const int32_t *rows, int n, int start) {
 int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t seed, const int32_t *forced,
                     int n_forced, int32_t *out_rows, double *timing, float *logits_dump, float *gate_dump,
                     moss_hip_frame_cb cb, void *user) {
-    (void)seed;  // greedy decoding draws no random numbers (sampler.cpp:23-28)
-    if (!(p.greedy || p.top_k == 1))
-        throw Status(MOSS_HIP_EUNSUPPORTED, "only greedy decoding runs on the device in this build");
-    if (!p.end_greedy) throw Status(MOSS_HIP_EUNSUPPORTED, "only the greedy end gate runs on the device in this build");
     if (forced && n_forced < max_frames) max_frames = n_forced;
     if (max_frames <= 0) return 0;
     const int cap = max_ctx_ + 1;  // frames beyond this cannot happen: pos reaches max_ctx first
@@ -485,6 +481,8 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     hstate_->min_frames = p.min_frames;
     hstate_->forced_on = forced ? 1 : 0;
     hstate_->rep_penalty = p.repetition_penalty;
+    hstate_->cfg = sample_cfg(p);
+    rng_seed_host(seed, hstate_->rng);  // Rng rng; rng.seed(seed) (llm.cpp:638-639)
     write_state_header();
     hip_check(hipStreamSynchronize(stream_), "sync");
 

@@ -32,6 +32,17 @@ constexpr int kWave = 64;
 
 // Device-resident decode state, read by every kernel of a captured step so the
 // same hipGraph can be replayed frame after frame.
+// Sampling controls of one generate() call (SampleParams, reference
+// csrc/include/moss/sampler.h:8-22).
+struct SampleCfg {
+    int greedy;          // SampleParams::greedy || top_k == 1 (sampler.cpp:23)
+    float temperature;
+    int top_k;
+    float top_p;
+    int end_greedy;
+    int greedy_frames;   // frames [0, greedy_frames) pick greedily (llm.cpp:686-687)
+};
+
 struct DevState {
     int pos;          // next global position (= LlmModel::pos_)
     int frame;        // frame index inside the current generate() call
@@ -39,10 +50,39 @@ struct DevState {
     int min_frames;   // SampleParams::min_frames
     int forced_on;    // teacher forcing: the used code comes from `forced`
     float rep_penalty;
+    SampleCfg cfg;
+    uint32_t rng[4];  // xoshiro128** state of this generate() call, advanced on the device
     int row[17];      // next global-step row: [slot, codes...]
     int codes[16];    // predicted codes of the current frame
     float gate[2];    // (l_end, l_slot) of the current frame
 };
+
+// xoshiro128** step and uniform draw of the reference's Rng (sampler.h:25-49).
+__device__ __forceinline__ uint32_t rng_next(uint32_t *s) {
+    const uint32_t x = s[1] * 5u;
+    const uint32_t result = ((x << 7) | (x >> 25)) * 9u;
+    const uint32_t t = s[1] << 9;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = (s[3] << 11) | (s[3] >> 21);
+    return result;
+}
+
+// 24 random bits as a float in [0, 1): exact in fp32.
+__device__ __forceinline__ float rng_uniform(uint32_t *s) { return (float)(rng_next(s) >> 8) * (1.0f / 16777216.0f); }
+
+// end_reached (llm.cpp:30-35): greedy compares the two logits; otherwise one
+// uniform draw against the slot probability of a two-way softmax, in double.
+__device__ __forceinline__ bool end_reached(float l_slot, float l_end, const SampleCfg &c, uint32_t *rng) {
+    if (c.end_greedy) return l_end > l_slot;
+    double d = (double)l_end - (double)l_slot;
+    d = d < -80.0 ? -80.0 : (d > 80.0 ? 80.0 : d);
+    const float p_slot = (float)(1.0 / (1.0 + exp(d)));
+    return rng_uniform(rng) >= p_slot;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

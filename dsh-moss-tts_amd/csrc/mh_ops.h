@@ -134,7 +134,24 @@ struct SampleArgs {
     DevState *state = nullptr;
     int last_channel = 0;           // ch == 15: advance state->frame
 };
-hipError_t launch_sample_greedy(const SampleArgs &a, hipStream_t s);
+hipError_t launch_sample(const SampleArgs &a, hipStream_t s);
+
+// Rng::seed of the reference (csrc/include/moss/sampler.h:28-35), on the host.
+inline void rng_seed_host(uint64_t v, uint32_t s[4]) {
+    s[0] = (uint32_t)v;
+    s[1] = (uint32_t)(v >> 32) ^ 0x9E3779B9u;
+    s[2] = 0x243F6A88u;
+    s[3] = 0xB7E15162u;
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t t = s[1] << 9;
+        s[2] ^= s[0];
+        s[3] ^= s[1];
+        s[1] ^= s[2];
+        s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = (s[3] << 11) | (s[3] >> 21);
+    }
+}
 
 // ---- row-batched kernels (prefill rows or one row per stream)
 // out[r] = LayerNorm(x[r * x_stride]) for r < rows (x_stride 0 broadcasts one row);
@@ -144,6 +161,15 @@ hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const fl
 // x[r] = embedding of rows[r][17] (llm.cpp:148-157)
 hipError_t launch_embed_rows(const EmbedArgs &e, const int *rows, int n, float *x, hipStream_t s);
 
+// Controls of one batched generate() call, shared by all streams; device-side
+// so the captured graphs stay valid from call to call.
+struct BatchCtl {
+    int frame;          // frame index of the current generate call
+    int min_frames;     // SampleParams::min_frames
+    float rep_penalty;  // SampleParams::repetition_penalty
+    SampleCfg cfg;
+};
+
 // Per-stream decode state of the batched engine (device arrays of `streams` entries).
 struct StreamState {
     int *pos = nullptr;            // next global position
@@ -152,14 +178,15 @@ struct StreamState {
     int *row = nullptr;            // [S][17] next global-step row
     float *gate = nullptr;         // [S][2] (l_end, l_slot)
     int *counts = nullptr;         // [S][16][1024] used-code occurrences (repetition penalty)
-    int *ctrl = nullptr;           // [0] frame index of the current generate call, [1] min_frames,
-                                   // [2] repetition penalty (float bits) -- device-side so graphs stay valid
+    uint32_t *rng = nullptr;       // [S][4] xoshiro128** state per stream
+    BatchCtl *ctrl = nullptr;
     int capacity = 0;              // KV positions per stream
 };
 // End gate per stream (gate_kernel on each row); inactive streams are left alone.
 hipError_t launch_gate_rows(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
                             const StreamState &st, int streams, hipStream_t s);
-// Greedy pick per stream for channel ch over logits[S][1024]; next_in[S][768] = aemb[ch][used].
+// Pick per stream for channel ch over logits[S][1024] (greedy or sampled, as the
+// single-stream sample kernel); next_in[S][768] = aemb[ch][used].
 hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
                               int streams, int last_channel, hipStream_t s);
 // pos[s] += 1 for active streams; streams reaching capacity become inactive.

@@ -95,7 +95,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_batch_position.argtypes = [vp, i32]
     L.moss_hip_batch_kv_export.argtypes = [vp, i32, i32, vp, vp]
     L.moss_hip_batch_global_step.argtypes = [vp, i32, vp]
-    L.moss_hip_batch_generate.argtypes = [vp, i32, i32, C.POINTER(SampleParams), vp, vp, C.POINTER(C.c_double)]
+    L.moss_hip_batch_generate.argtypes = [vp, i32, i32, C.POINTER(SampleParams), vp, vp, vp, C.POINTER(C.c_double)]
     L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
     L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
     _lib = L
@@ -285,11 +285,12 @@ class HipBatch:
         rows = np.ascontiguousarray(rows, np.int32).reshape(-1, 17)
         check(self.L.moss_hip_batch_global_step(self._h, rows.shape[0], _ptr(rows)))
 
-    def generate(self, n_streams: int, frames: int, params: SampleParams | None = None):
+    def generate(self, n_streams: int, frames: int, params: SampleParams | None = None, seeds=None):
         params = params or SampleParams.make()
         out = np.zeros((max(frames, 1), n_streams, 17), np.int32)
         nf = np.zeros(n_streams, np.int32)
         ms = C.c_double(0.0)
-        check(self.L.moss_hip_batch_generate(self._h, n_streams, frames, C.byref(params), _ptr(out), _ptr(nf),
-                                             C.byref(ms)))
+        sd = None if seeds is None else np.ascontiguousarray(seeds, np.uint64).reshape(n_streams)
+        check(self.L.moss_hip_batch_generate(self._h, n_streams, frames, C.byref(params),
+                                             None if sd is None else _ptr(sd), _ptr(out), _ptr(nf), C.byref(ms)))
         return {"rows": out[:frames], "frames": nf, "ms": ms.value}

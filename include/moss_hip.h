@@ -100,8 +100,9 @@ int moss_hip_llm_global_step(moss_hip_llm *m, const int32_t *row17);
  *   timing   [max_frames][2] (global_ms, local_ms) or NULL (FrameTiming, llm.h:34-37).
  *   logits_dump [max_frames][16][1024] or NULL (set_logits_dump, llm.h:80).
  *   gate_dump   [max_frames][2] (l_end, l_slot) or NULL (set_gate_dump, llm.h:83).
- *   cb/user: on_frame.  Greedy decoding (greedy != 0 or top_k == 1) with end_greedy != 0;
- *   other sampling modes return MOSS_HIP_EUNSUPPORTED. */
+ *   cb/user: on_frame.  Every SampleParams mode runs on the device (sampler.cpp:9-79,
+ *   llm.cpp:30-35): greedy, temperature / top-k / top-p sampling and the sampled end gate,
+ *   drawing from xoshiro128** seeded with `seed` in the reference's order. */
 int moss_hip_llm_generate(moss_hip_llm *m, int max_frames, const moss_hip_sample_params *p, uint64_t seed,
                           const int32_t *forced, int n_forced, int32_t *out_rows, int *out_frames, double *timing,
                           float *logits_dump, float *gate_dump, moss_hip_frame_cb cb, void *user);
@@ -145,9 +146,10 @@ int moss_hip_batch_kv_export(moss_hip_batch *b, int stream, int n_pos, float *k,
 int moss_hip_batch_global_step(moss_hip_batch *b, int n_streams, const int32_t *rows);
 /* generate (csrc/src/llm.cpp:634-733) for streams [0, n_streams), frames in lock-step: out_rows
  * [frames][n_streams][17]; out_frames[s] = frames stream s produced (its end gate / capacity);
- * *elapsed_ms = device time of the whole run.  Greedy decoding with the greedy end gate. */
+ * *elapsed_ms = device time of the whole run.  Stream s samples like its own LlmModel::generate
+ * with seed seeds[s] (seeds NULL = 0 for every stream). */
 int moss_hip_batch_generate(moss_hip_batch *b, int n_streams, int frames, const moss_hip_sample_params *p,
-                            int32_t *out_rows, int *out_frames, double *elapsed_ms);
+                            const uint64_t *seeds, int32_t *out_rows, int *out_frames, double *elapsed_ms);
 
 /* ------------------------------------------------------------------ operator layer */
 
