@@ -212,7 +212,7 @@ __device__ void load_penalised(PickLds &L, const float *logits, const int *count
 // Integer parts are exact and the fp32 operation order is the reference's, so
 // the gate values are bit-identical to the reference given the same h.
 __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const float *lnf_w, const float *lnf_b,
-                                                   const uint8_t *wte, DevState *state, float *gate_log) {
+                                                   const uint8_t *wte, DevState *state) {
 #pragma clang fp contract(off)
     __shared__ float red[4];
     __shared__ float hbuf[kHidden];
@@ -274,11 +274,60 @@ __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const flo
         }
         state->gate[0] = g[0];
         state->gate[1] = g[1];
-        if (gate_log != nullptr) {
-            gate_log[2 * state->frame] = g[0];
-            gate_log[2 * state->frame + 1] = g[1];
-        }
         if (state->frame >= state->min_frames && end_reached(g[1], g[0], state->cfg, state->rng)) state->stop = 1;
+    }
+}
+
+// End gate of a frame whose gate is dumped (llm.cpp:653-679): the reference then
+// computes the whole text head (text_logits = gemv over wte, the caller's GEMV)
+// and takes l_slot, l_end from it, plus the argmax over all 16384 logits (the
+// first maximum wins).  The stop rule is end_reached as in gate_kernel.
+__global__ __launch_bounds__(256) void gate_text_kernel(const float *logits, DevState *state) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    if (state->stop) return;
+    const int t = threadIdx.x;
+    float best = -INFINITY;
+    int besti = kVocab;
+    for (int i = t; i < kVocab; i += 256) {
+        const float v = logits[i];
+        if (v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(besti, off);
+        if (ov > best || (ov == best && oi < besti)) {
+            best = ov;
+            besti = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = besti;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float b = bv[0];
+        int idx = bi[0];
+        for (int w = 1; w < 4; ++w)
+            if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
+                b = bv[w];
+                idx = bi[w];
+            }
+        if (idx >= kVocab) {  // all NaN: the reference's scan keeps index 0
+            idx = 0;
+            b = logits[0];
+        }
+        const float l_end = logits[kEndToken], l_slot = logits[kSlotToken];
+        state->gate[0] = l_end;
+        state->gate[1] = l_slot;
+        state->gate_argmax = idx;
+        state->gate_argmax_v = b;
+        if (state->frame >= state->min_frames && end_reached(l_slot, l_end, state->cfg, state->rng)) state->stop = 1;
     }
 }
 
@@ -365,9 +414,15 @@ hipError_t launch_dequant_rows(const uint8_t *w, int mat_rows, int cols, const i
 }
 
 hipError_t launch_gate(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
-                       DevState *state, float *gate_log, hipStream_t s) {
+                       DevState *state, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    hipLaunchKernelGGL(gate_kernel, dim3(1), dim3(256), 0, s, x_raw, lnf_w, lnf_b, wte, state, gate_log);
+    hipLaunchKernelGGL(gate_kernel, dim3(1), dim3(256), 0, s, x_raw, lnf_w, lnf_b, wte, state);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_text(const float *logits, DevState *state, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    hipLaunchKernelGGL(gate_text_kernel, dim3(1), dim3(256), 0, s, logits, state);
     return hipGetLastError();
 }
 

@@ -89,10 +89,10 @@ public:
 private:
     void enqueue_global_step(hipStream_t s, const int *row_dev);
     void enqueue_local_step(hipStream_t s, const float *in, int lpos);
-    void enqueue_frame_local(hipStream_t s);
+    void enqueue_frame_local(hipStream_t s, bool text_gate);
     void build_graphs();
     void launch_global(hipStream_t s);
-    void launch_frame_local(hipStream_t s);
+    void launch_frame_local(hipStream_t s, bool text_gate);
     void write_state_header();
     void *kv_layer(int which, int layer) const;  // which: 0 = K, 1 = V
 
@@ -119,7 +119,7 @@ private:
     float *logits_ = nullptr;            // [16][1024]
     int *counts_ = nullptr;              // [16][1024]
     int *forced_ = nullptr;              // [max_ctx][16]
-    float *gate_log_ = nullptr;          // [max_ctx][2]
+    float *text_logits_ = nullptr;       // [16384] text head of gate-dump frames
     int *rows_dev_ = nullptr;            // prefill rows [n][17]
     int rows_cap_ = 0;
     float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_o_ = nullptr, *pre_h_ = nullptr;  // prefill rows

@@ -169,7 +169,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     fmalloc(&slot_in_, kHidden);
     fmalloc(&attn_out_, kHidden);
     fmalloc(&logits_, (size_t)kNVq * kCodebook);
-    fmalloc(&gate_log_, 2ull * (max_ctx_ + 2));
+    fmalloc(&text_logits_, kVocab);
     hip_check(hipMalloc(&counts_, sizeof(int) * kNVq * kCodebook), "hipMalloc(counts)");
     hip_check(hipMalloc(&forced_, sizeof(int) * kNVq * (max_ctx_ + 2)), "hipMalloc(forced)");
     hip_check(hipMemset(hidden_, 0, kHidden * 4), "memset(hidden)");
@@ -194,7 +194,7 @@ Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, logits_, counts_, forced_, gate_log_, rows_dev_, state_, snap_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -298,9 +298,18 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
 
 // The local half of a frame (llm.cpp:648-698): local step on hidden, end gate,
 // then 16 x (local step, audio head of channel ch, pick + next input).
-void Model::enqueue_frame_local(hipStream_t s) {
+void Model::enqueue_frame_local(hipStream_t s, bool text_gate) {
     enqueue_local_step(s, hidden_, 0);
-    hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, gate_log_, s), "gate");
+    if (text_gate) {  // gate-dump frames: the whole text head, as llm.cpp:662-667
+        GemvArgs t;
+        t.w = wte_; t.rows = kVocab; t.cols = kHidden;
+        t.x = lres_; t.ln_w = llnf_w_; t.ln_b = llnf_b_;
+        t.y = text_logits_; t.state = state_;
+        hip_check(launch_gemv(t, PRO_LN, EPI_F32, KV_F32, s), "text head");
+        hip_check(launch_gate_text(text_logits_, state_, s), "gate");
+    } else {
+        hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, s), "gate");
+    }
     for (int ch = 0; ch < kNVq; ++ch) {
         enqueue_local_step(s, ch == 0 ? slot_in_ : next_in_, ch + 1);
         GemvArgs h;
@@ -329,7 +338,7 @@ void Model::build_graphs() {
     hip_check(hipGraphInstantiate(&g_global_, g, nullptr, nullptr, 0), "instantiate global");
     (void)hipGraphDestroy(g);
     hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
-    enqueue_frame_local(stream_);
+    enqueue_frame_local(stream_, false);
     hip_check(hipStreamEndCapture(stream_, &g), "end capture");
     hip_check(hipGraphInstantiate(&g_local_, g, nullptr, nullptr, 0), "instantiate local");
     (void)hipGraphDestroy(g);
@@ -342,11 +351,11 @@ void Model::launch_global(hipStream_t s) {
         enqueue_global_step(s, reinterpret_cast<const int *>(reinterpret_cast<uint8_t *>(state_) + kStateRowOff));
 }
 
-void Model::launch_frame_local(hipStream_t s) {
-    if (g_local_)
+void Model::launch_frame_local(hipStream_t s, bool text_gate) {
+    if (g_local_ && !text_gate)
         hip_check(hipGraphLaunch(g_local_, s), "graph launch");
     else
-        enqueue_frame_local(s);
+        enqueue_frame_local(s, text_gate);
 }
 
 // Pushes the scalar header (pos .. rep_penalty) of the host mirror to the device.
@@ -491,7 +500,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
         if (pos_ >= max_ctx_) break;
         if (cancel_ != nullptr && __atomic_load_n(cancel_, __ATOMIC_RELAXED)) break;
         hip_check(hipEventRecord(ev_[0], stream_), "event");
-        launch_frame_local(stream_);
+        launch_frame_local(stream_, gate_dump != nullptr);
         hip_check(hipEventRecord(ev_[1], stream_), "event");
         const bool do_global = f + 1 < max_frames && pos_ < max_ctx_;
         if (do_global) launch_global(stream_);
@@ -503,8 +512,11 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
         hip_check(hipMemcpyAsync(hstate_, state_, sizeof(DevState), hipMemcpyDeviceToHost, stream_), "state d2h");
         hip_check(hipStreamSynchronize(stream_), "sync");
         if (gate_dump) {
-            gate_dump[2 * f] = hstate_->gate[0];
-            gate_dump[2 * f + 1] = hstate_->gate[1];
+            float *gd = gate_dump + 4 * (size_t)f;
+            gd[0] = hstate_->gate[0];
+            gd[1] = hstate_->gate[1];
+            gd[2] = (float)hstate_->gate_argmax;
+            gd[3] = hstate_->gate_argmax_v;
         }
         if (hstate_->stop) break;
         int32_t *row = out_rows + (size_t)f * 17;

@@ -55,6 +55,8 @@ struct DevState {
     int row[17];      // next global-step row: [slot, codes...]
     int codes[16];    // predicted codes of the current frame
     float gate[2];    // (l_end, l_slot) of the current frame
+    int gate_argmax;  // gate-dump frames: argmax over the full text head, and its logit
+    float gate_argmax_v;
 };
 
 // xoshiro128** step and uniform draw of the reference's Rng (sampler.h:25-49).

@@ -120,10 +120,12 @@ hipError_t launch_dequant_rows(const uint8_t *w, int mat_rows, int cols, const i
 
 // End gate: LN(x; lnf) -> W8A8 dot with wte rows 7 and 9 (reference order) -> state->gate, state->stop.
 hipError_t launch_gate(const float *x_raw, const float *lnf_w, const float *lnf_b, const uint8_t *wte,
-                       DevState *state, float *gate_log, hipStream_t s);
+                       DevState *state, hipStream_t s);
+// End gate from the full text-head logits[16384] (gate-dump frames): gate, argmax, stop.
+hipError_t launch_gate_text(const float *logits, DevState *state, hipStream_t s);
 
-// Greedy pick for channel ch: repetition penalty from counts, argmax, history update,
-// next input = dequant(aemb[ch][used]).
+// Pick for channel ch: repetition penalty from counts, greedy or sampled choice,
+// history update, next input = dequant(aemb[ch][used]).
 struct SampleArgs {
     const float *logits = nullptr;  // [1024]
     int ch = 0;

@@ -252,7 +252,7 @@ std::vector<Row> LlmModel::generate(int max_frames, const SampleParams &p, uint6
     std::vector<int32_t> out((size_t)cap * 17);
     std::vector<double> t(timing ? (size_t)cap * 2 : 0);
     std::vector<float> logits(logits_dump_path_.empty() ? 0 : (size_t)cap * kNVq * kCodebook);
-    std::vector<float> gate(gate_dump_path_.empty() ? 0 : (size_t)cap * 2);
+    std::vector<float> gate(gate_dump_path_.empty() ? 0 : (size_t)cap * 4);
     int n = 0;
     const int rc = moss_hip_llm_generate(
         h_, max_frames, &sp, seed, forced ? (*forced)[0].data() : nullptr, forced ? (int)forced->size() : 0,
@@ -270,12 +270,14 @@ std::vector<Row> LlmModel::generate(int max_frames, const SampleParams &p, uint6
             std::fclose(fp);
         }
     }
-    if (!gate_dump_path_.empty()) {  // llm.cpp:721-731 columns; argmax over the full text head is not computed
+    if (!gate_dump_path_.empty()) {  // the CSV of llm.cpp:721-731
         if (std::FILE *fp = std::fopen(gate_dump_path_.c_str(), "wb")) {
             std::fprintf(fp, "frame,argmax_id,argmax_minus_slot,slot_minus_end\n");
             const int rows = n < cap ? n + 1 : n;  // the frame that stopped also evaluated its gate
-            for (int i = 0; i < rows; ++i)
-                std::fprintf(fp, "%d,%d,%.4f,%.4f\n", i, -1, 0.0, gate[2 * i + 1] - gate[2 * i]);
+            for (int i = 0; i < rows; ++i) {
+                const float *g = gate.data() + 4 * (size_t)i;  // (l_end, l_slot, argmax_id, argmax_logit)
+                std::fprintf(fp, "%d,%d,%.4f,%.4f\n", i, (int)g[2], g[3] - g[1], g[1] - g[0]);
+            }
             std::fclose(fp);
         }
     }

@@ -202,7 +202,7 @@ class HipLLM:
         fa = np.ascontiguousarray(forced, np.int32).reshape(-1, 17) if forced is not None else None
         t = np.zeros((max(max_frames, 1), 2), np.float64) if timing else None
         ld = np.zeros((max(max_frames, 1), 16, 1024), np.float32) if logits else None
-        gd = np.zeros((max(max_frames, 1), 2), np.float32) if gate else None
+        gd = np.zeros((max(max_frames, 1), 4), np.float32) if gate else None
         n = C.c_int(0)
         cb = FRAME_CB(lambda u, f, row: on_frame(f, np.ctypeslib.as_array(row, (17,)).copy())) if on_frame \
             else FRAME_CB()

@@ -99,7 +99,9 @@ int moss_hip_llm_global_step(moss_hip_llm *m, const int32_t *row17);
  *   out_rows [max_frames][17] receives the predicted rows; *out_frames their count.
  *   timing   [max_frames][2] (global_ms, local_ms) or NULL (FrameTiming, llm.h:34-37).
  *   logits_dump [max_frames][16][1024] or NULL (set_logits_dump, llm.h:80).
- *   gate_dump   [max_frames][2] (l_end, l_slot) or NULL (set_gate_dump, llm.h:83).
+ *   gate_dump   [max_frames][4] (l_end, l_slot, argmax_id, argmax_logit) or NULL (set_gate_dump,
+ *               llm.h:83).  As in the reference (llm.cpp:653-679), a dumped frame computes the whole
+ *               16384-row text head and takes the gate logits from it instead of the 2-row W8A8 gate.
  *   cb/user: on_frame.  Every SampleParams mode runs on the device (sampler.cpp:9-79,
  *   llm.cpp:30-35): greedy, temperature / top-k / top-p sampling and the sampled end gate,
  *   drawing from xoshiro128** seeded with `seed` in the reference's order. */

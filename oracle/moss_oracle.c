@@ -695,6 +695,12 @@ void mo_model_audio_logits(mo_model *m, int ch, const float *hidden, float *logi
     mo_gemv_a16(m->aemb[ch].data, MO_CODEBOOK, MO_HIDDEN, hidden, logits);
 }
 
+/* reference csrc/src/llm.cpp:266 (text_logits: gemv_par over wte; A16 in the
+ * release decode mode) */
+void mo_model_text_logits(mo_model *m, const float *hidden, float *logits) {
+    mo_gemv_a16(m->wte.data, MO_VOCAB, MO_HIDDEN, hidden, logits);
+}
+
 /* reference csrc/src/llm.cpp:274-315 (Q8_0_4X4 branch: W8A8 AVX2 row dot on
  * rows 7 (end) and 9 (slot) of wte) */
 void mo_model_assistant_logits(mo_model *m, const float *hidden, float *pair) {
@@ -783,6 +789,7 @@ int mo_model_generate(mo_model *m, int max_frames, const mo_sample_params *p, ui
     int *hist = (int *)malloc(sizeof(int) * (size_t)MO_NVQ * (max_frames > 0 ? max_frames : 1));
     int hist_n = 0;
     void *scratch = malloc((size_t)MO_CODEBOOK * 8);
+    float *text = gate_out ? (float *)malloc(sizeof(float) * MO_VOCAB) : NULL;
     float logits[MO_CODEBOOK];
     float lx[MO_HIDDEN], input[MO_HIDDEN];
     int frames = 0;
@@ -791,12 +798,29 @@ int mo_model_generate(mo_model *m, int max_frames, const mo_sample_params *p, ui
         if (m->pos >= m->max_ctx) break;
         mo_model_local_reset(m);
         mo_model_local_step(m, m->hidden, lx);
-        float pair[2];
-        mo_model_assistant_logits(m, lx, pair);
-        float l_end = pair[0], l_slot = pair[1];
+        float l_end, l_slot;
         if (gate_out) {
-            gate_out[2 * f] = l_end;
-            gate_out[2 * f + 1] = l_slot;
+            /* gate-dump path (llm.cpp:653-679): the whole text head, its argmax
+             * (first maximum wins) and the gate logits taken from it */
+            mo_model_text_logits(m, lx, text);
+            int am = 0;
+            float av = text[0];
+            for (int v = 1; v < MO_VOCAB; ++v)
+                if (text[v] > av) {
+                    av = text[v];
+                    am = v;
+                }
+            l_slot = text[MO_SLOT];
+            l_end = text[MO_END];
+            gate_out[4 * f] = l_end;
+            gate_out[4 * f + 1] = l_slot;
+            gate_out[4 * f + 2] = (float)am;
+            gate_out[4 * f + 3] = av;
+        } else {
+            float pair[2];
+            mo_model_assistant_logits(m, lx, pair);
+            l_end = pair[0];
+            l_slot = pair[1];
         }
         if (f >= p->min_frames && end_reached(l_slot, l_end, p, &rng)) break;
         int32_t frame[17];
@@ -828,5 +852,6 @@ int mo_model_generate(mo_model *m, int max_frames, const mo_sample_params *p, ui
     }
     free(hist);
     free(scratch);
+    free(text);
     return frames;
 }

@@ -111,10 +111,13 @@ void mo_model_local_reset(mo_model *m);                                         
 void mo_model_local_step(mo_model *m, const float *in, float *out);                  /* llm.cpp:259-264 */
 void mo_model_audio_logits(mo_model *m, int ch, const float *hidden, float *logits); /* llm.cpp:268-270 */
 void mo_model_assistant_logits(mo_model *m, const float *hidden, float *pair);       /* llm.cpp:274-315 */
+void mo_model_text_logits(mo_model *m, const float *hidden, float *logits);          /* llm.cpp:266 */
 /* llm.cpp:327-401; a16 = 0 for the reference default (W8A8 prefill) */
 void mo_model_prefill(mo_model *m, const int32_t *rows17, int n_rows, int start, int a16);
 /* llm.cpp:634-733.  forced: [n_forced][17] or NULL.  out_rows: [max_frames][17].
- * logits_dump (optional): [max_frames][16][1024].  gate_out (optional): [max_frames][2] = (l_end, l_slot).
+ * logits_dump (optional): [max_frames][16][1024].  gate_out (optional): the reference's gate-dump
+ * mode (llm.cpp:653-679): [max_frames][4] = (l_end, l_slot, argmax_id, argmax_logit) from the
+ * full text head, which then also decides the end gate.
  * returns number of frames produced. */
 int mo_model_generate(mo_model *m, int max_frames, const mo_sample_params *p, uint64_t seed,
                       const int32_t *forced, int n_forced, int32_t *out_rows, float *logits_dump,

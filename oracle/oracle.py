@@ -264,7 +264,7 @@ class OracleModel:
         out = np.zeros((max_frames, 17), np.int32)
         fa = np.ascontiguousarray(forced, np.int32).reshape(-1, 17) if forced is not None else None
         ld = np.zeros((max_frames, 16, 1024), np.float32) if logits else None
-        gd = np.zeros((max_frames, 2), np.float32) if gate else None
+        gd = np.zeros((max_frames, 4), np.float32) if gate else None
         n = self.lib.mo_model_generate(self.h, max_frames, C.byref(params), seed,
                                        fa.ctypes.data if fa is not None else None, 0 if fa is None else fa.shape[0],
                                        out, ld.ctypes.data if ld is not None else None,
@@ -456,12 +456,15 @@ class RefModel:
         if self.lib.ref_model_load_prefix(self.h, path.encode(), rows, rows.shape[0]) != 0:
             raise RuntimeError(self.lib.ref_last_error().decode())
 
-    def generate(self, max_frames, params: SampleParams, seed=0, forced=None, timing=False, logits_path=None):
+    def generate(self, max_frames, params: SampleParams, seed=0, forced=None, timing=False, logits_path=None,
+                 gate_path=None):
         out = np.zeros((max_frames, 17), np.int32)
         fa = np.ascontiguousarray(forced, np.int32).reshape(-1, 17) if forced is not None else None
         t = np.zeros((max_frames, 2), np.float64) if timing else None
         if logits_path:
             self.lib.ref_model_set_logits_dump(self.h, logits_path.encode())
+        if gate_path:
+            self.lib.ref_model_set_gate_dump(self.h, gate_path.encode())
         n = self.lib.ref_model_generate(self.h, max_frames, params.ints(), params.floats(), seed,
                                         fa.ctypes.data if fa is not None else None,
                                         0 if fa is None else fa.shape[0], out,

@@ -1,9 +1,12 @@
 // moss_llm_hip -- drives the GPU moss::LlmModel (dsh-moss-tts_amd/host) the way the
 // reference's moss_llm CLI drives its CPU LlmModel (csrc/src/main.cpp:44-222):
 //   moss_llm_hip --weights x.moss --prompt rows.txt [--frames N] [--min-frames N]
-//                [--greedy] [--rep P] [--load-state s] [--ignore-state-fp]
-//                [--save-state s] [--save-prefix p] [--load-prefix p]
-//                [--force-codes codes.txt] [--dump-logits f] [--prefix-rows K]
+//                [--greedy|--sample] [--seed S] [--end-mode greedy|sample] [--rep P]
+//                [--load-state s] [--ignore-state-fp] [--save-state s]
+//                [--save-prefix p] [--load-prefix p] [--prefix-rows K]
+//                [--force-codes codes.txt] [--dump-logits f] [--dump-gate f]
+// Sampling defaults are main.cpp:133-140's (temperature 0.8, top-k 25, top-p 0.95,
+// repetition penalty 1.2).
 // Prompt rows: 17 integers per line, '#' comments (main.cpp:20-40).  Prints JSON.
 // --prefix-rows K follows the engine's voice-prefix flow (engine.cpp:200-242): the
 // first K rows are the prefix (loaded from --load-prefix, else prefilled and
@@ -36,10 +39,11 @@ static bool read_rows(const std::string &path, std::vector<Row> *rows, bool code
 }
 
 int main(int argc, char **argv) {
-    std::string weights, prompt, state_in, state_out, prefix_in, prefix_out, force, logits;
+    std::string weights, prompt, state_in, state_out, prefix_in, prefix_out, force, logits, gate, end_mode = "greedy";
+    uint64_t seed = 0;
     int frames = 8, min_frames = 0, prefix_rows = 0;
     bool greedy = false, ignore_fp = false;
-    float rep = 1.0f;
+    float rep = 1.2f;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         auto next = [&]() -> std::string { return i + 1 < argc ? argv[++i] : ""; };
@@ -48,6 +52,10 @@ int main(int argc, char **argv) {
         else if (a == "--frames") frames = std::stoi(next());
         else if (a == "--min-frames") min_frames = std::stoi(next());
         else if (a == "--greedy") greedy = true;
+        else if (a == "--sample") greedy = false;
+        else if (a == "--seed") seed = std::stoull(next());
+        else if (a == "--end-mode") end_mode = next();
+        else if (a == "--dump-gate") gate = next();
         else if (a == "--rep") rep = std::stof(next());
         else if (a == "--load-state") state_in = next();
         else if (a == "--ignore-state-fp") ignore_fp = true;
@@ -109,14 +117,19 @@ int main(int argc, char **argv) {
         return 1;
     }
     if (!logits.empty()) model.set_logits_dump(logits);
+    if (!gate.empty()) model.set_gate_dump(gate);
     SampleParams p;
     p.greedy = greedy;
+    p.end_greedy = end_mode != "sample";
     p.min_frames = min_frames;
+    p.temperature = 0.8f;
+    p.top_k = 25;
+    p.top_p = 0.95f;
     p.repetition_penalty = rep;
     std::vector<FrameTiming> timing;
     int callbacks = 0;
     const std::vector<Row> codes =
-        model.generate(frames, p, 0, &timing, forced.empty() ? nullptr : &forced, [&](int, const Row &) { ++callbacks; });
+        model.generate(frames, p, seed, &timing, forced.empty() ? nullptr : &forced, [&](int, const Row &) { ++callbacks; });
     double g = 0, l = 0;
     for (const auto &t : timing) {
         g += t.global_ms;

@@ -73,7 +73,8 @@ def test_shim_prefix_flow(torch_gpu, oracle, files):
     blob, rows, w, prompt, d = files
     K = 4
     prefix = str(d / "p.mosskv")
-    common = ["--weights", w, "--prompt", prompt, "--prefix-rows", K, "--frames", 3, "--min-frames", 3, "--greedy"]
+    common = ["--weights", w, "--prompt", prompt, "--prefix-rows", K, "--frames", 3, "--min-frames", 3, "--greedy",
+              "--rep", 1.0]
     a = _run(*common, "--save-prefix", prefix)
     b = _run(*common, "--load-prefix", prefix)
     assert a["codes"] == b["codes"] and a["hidden0"] == b["hidden0"] and a["position"] == b["position"]
@@ -101,7 +102,7 @@ def test_shim_teacher_forcing(torch_gpu, oracle, files):
     ref = m.generate(3, OSP.make(greedy=True, min_frames=3))
     forced = d / "forced.txt"
     forced.write_text("\n".join(" ".join(map(str, r[1:])) for r in ref["rows"]) + "\n")
-    res = _run("--weights", w, "--prompt", prompt, "--frames", 3, "--min-frames", 3, "--greedy",
+    res = _run("--weights", w, "--prompt", prompt, "--frames", 3, "--min-frames", 3, "--greedy", "--rep", 1.0,
                "--force-codes", str(forced))
     assert res["codes"] == ref["rows"][:, 1:].tolist() and res["frames"] == 3
     # forcing its own greedy codes leaves the oracle where free running left it
@@ -111,6 +112,29 @@ def test_shim_teacher_forcing(torch_gpu, oracle, files):
     h = mf_.hidden()
     assert res["position"] == mf_.position
     assert abs(res["hidden0"] - h[0]) <= 1e-3 * np.abs(h).max()
+
+
+def test_shim_sampling_and_gate_dump(torch_gpu, oracle, files):
+    """moss_llm's default sampling (main.cpp:133-140) with the sampled end gate and a
+    gate dump: codes, frame count and the CSV follow the oracle for the same seed."""
+    blob, rows, w, prompt, d = files
+    gate = str(d / "gate.csv")
+    res = _run("--weights", w, "--prompt", prompt, "--frames", 8, "--min-frames", 2, "--sample", "--seed", 42,
+               "--end-mode", "sample", "--dump-gate", gate)
+    m = oracle.model(blob)
+    m.prefill(rows, a16=True)
+    ref = m.generate(8, OSP.make(greedy=False, temperature=0.8, top_k=25, top_p=0.95, repetition_penalty=1.2,
+                                 end_greedy=False, min_frames=2), seed=42, gate=True)
+    assert res["frames"] == len(ref["rows"])
+    assert np.mean(np.array(res["codes"]).reshape(-1, 16) == ref["rows"][:, 1:]) >= 0.99
+    lines = open(gate).read().splitlines()
+    assert lines[0] == "frame,argmax_id,argmax_minus_slot,slot_minus_end"
+    assert len(lines) - 1 == len(ref["gate"])
+    for f, ln in enumerate(lines[1:]):
+        fr, am, am_slot, slot_end = ln.split(",")
+        l_end, l_slot, am_o, av = ref["gate"][f]
+        assert int(fr) == f and int(am) == int(am_o)
+        assert abs(float(am_slot) - (av - l_slot)) <= 2e-4 and abs(float(slot_end) - (l_slot - l_end)) <= 2e-4
 
 
 def test_shim_rejects_bad_files(torch_gpu, files):

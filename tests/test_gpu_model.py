@@ -118,17 +118,26 @@ def test_generate_free_running_fp32kv(torch_gpu, oracle, prefilled):
 
 
 def test_generate_end_gate_matches_oracle(torch_gpu, oracle, prefilled):
-    """min_frames = 0: the W8A8 end gate decides when to stop; frame count and the
-    gate logits follow the oracle."""
+    """min_frames = 0: the end gate decides when to stop.  Without a dump it is the
+    2-row W8A8 gate; with a gate dump it is taken from the full text head, whose
+    argmax is dumped too (llm.cpp:653-679).  Frame counts, gate logits and argmax
+    ids follow the oracle in both modes."""
     blob, rows, k, v, h = prefilled
-    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=False)
-    ref = m.generate(6, OSP.make(greedy=True, min_frames=0), gate=True)
-    g = HipLLM(blob, kv_fp32=True)
-    g.kv_import(k, v, h)
-    out = g.generate(6, SampleParams.make(greedy=True, min_frames=0), gate=True)
-    assert len(out["rows"]) == len(ref["rows"])
-    ng = min(len(out["gate"]), len(ref["gate"]))
-    assert max_rel(out["gate"][:ng], ref["gate"][:ng]) <= TOL
+    for dump in (False, True):
+        print(f"end gate, dump={dump}", flush=True)
+        m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=False)
+        ref = m.generate(6, OSP.make(greedy=True, min_frames=0), gate=dump)
+        g = HipLLM(blob, kv_fp32=True)
+        g.kv_import(k, v, h)
+        out = g.generate(6, SampleParams.make(greedy=True, min_frames=0), gate=dump)
+        assert len(out["rows"]) == len(ref["rows"])
+        assert np.array_equal(out["rows"], ref["rows"])
+        if dump:
+            ng = min(len(out["gate"]), len(ref["gate"]))
+            og, rg = out["gate"][:ng], ref["gate"][:ng]
+            assert np.array_equal(og[:, 2], rg[:, 2])  # argmax ids
+            assert max_rel(og[:, [0, 1, 3]], rg[:, [0, 1, 3]]) <= TOL
+        g.close()
 
 
 def test_prefill_vs_oracle(torch_gpu, oracle, golden_model):

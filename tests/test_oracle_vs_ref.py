@@ -69,3 +69,27 @@ def test_model_steps_bit_exact(oracle, ref, golden_model):
     fr = r.generate(4, p, forced=forced)
     assert np.array_equal(fo["rows"], fr["rows"])
     assert np.array_equal(o.hidden(), r.hidden())
+
+
+def test_gate_dump_mode_bit_exact(oracle, ref, golden_model, tmp_path):
+    """With a gate dump the reference takes the gate from the full text head
+    (llm.cpp:653-679, A16 in decode mode): the oracle's gate-dump mode matches its
+    CSV (argmax id exact, the printed differences to their 4 decimals) and its codes."""
+    blob, g = golden_model
+    o = oracle.model(blob)
+    r = ref.model(blob, threads=2)
+    o.prefill(g["rows"])
+    r.prefill(g["rows"])
+    p = SampleParams.make(greedy=True, min_frames=0)
+    path = str(tmp_path / "gate.csv")
+    go = o.generate(8, p, gate=True)
+    gr = r.generate(8, p, gate_path=path)
+    assert np.array_equal(go["rows"], gr["rows"])
+    lines = open(path).read().splitlines()
+    assert lines[0] == "frame,argmax_id,argmax_minus_slot,slot_minus_end"
+    rows = [ln.split(",") for ln in lines[1:]]
+    assert len(rows) == len(go["gate"])
+    for f, (fr, am, am_slot, slot_end) in enumerate(rows):
+        l_end, l_slot, am_o, av = go["gate"][f]
+        assert int(fr) == f and int(am) == int(am_o)
+        assert f"{av - l_slot:.4f}" == am_slot and f"{l_slot - l_end:.4f}" == slot_end
