@@ -137,6 +137,35 @@ def test_shim_sampling_and_gate_dump(torch_gpu, oracle, files):
         assert abs(float(am_slot) - (av - l_slot)) <= 2e-4 and abs(float(slot_end) - (l_slot - l_end)) <= 2e-4
 
 
+REF_CLI = os.path.join(ROOT, "oracle", "_ref", "moss_llm_gpu")
+
+
+@pytest.mark.parametrize("mode", ["greedy", "sample"])
+def test_reference_cli_on_the_drop_in(torch_gpu, oracle, files, mode):
+    """The reference's own moss_llm (src/main.cpp, compiled unchanged against the
+    drop-in header, oracle/Makefile) runs on the GPU and follows the oracle."""
+    if not os.path.exists(REF_CLI):
+        pytest.skip("oracle/_ref/moss_llm_gpu not built (needs the reference sources)")
+    blob, rows, w, prompt, d = files
+    args = ["--weights", w, "--prompt", prompt, "--frames", 6, "--threads", 4]
+    if mode == "greedy":
+        args += ["--greedy", "--min-frames", 6]
+        p = OSP.make(greedy=True, repetition_penalty=1.2, min_frames=6)
+    else:
+        args += ["--sample", "--seed", 9, "--end-mode", "sample", "--min-frames", 3]
+        p = OSP.make(greedy=False, temperature=0.8, top_k=25, top_p=0.95, repetition_penalty=1.2, end_greedy=False,
+                     min_frames=3)
+    print("moss_llm_gpu", *args, flush=True)
+    out = subprocess.run([REF_CLI, *map(str, args)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    res = json.loads(out.stdout)
+    m = oracle.model(blob)
+    m.prefill(rows, a16=True)
+    ref = m.generate(6, p, seed=9 if mode == "sample" else 0)
+    assert res["frames"] == len(ref["rows"]) >= 3 and res["prompt_rows"] == len(rows)
+    assert np.mean(np.array(res["codes"]).reshape(-1, 16) == ref["rows"][:, 1:]) >= 0.99
+
+
 def test_shim_rejects_bad_files(torch_gpu, files):
     blob, rows, w, prompt, d = files
     bad = d / "bad.state"
