@@ -195,7 +195,6 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
 template <int PRO, int EPI, int SPLIT, int KV>
 hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int ngroups = a.rows / 4;
     constexpr int GPW = 4 / SPLIT;
     int grid = (ngroups + GPW - 1) / GPW;
@@ -213,7 +212,6 @@ hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
 template <int PRO, int EPI, int KV>
 hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    (void)hipGetLastError();  // report only this launch's error, not a stale one
     // blocks per wave -> batch size (iterations of 4 blocks), one of 2, 3, 6, 8
     const int per = (a.cols / 32 + split - 1) / split;
     const int its = (per + 3) / 4;
@@ -223,6 +221,150 @@ hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
         case 2: return launch_nb<PRO, EPI, 2, KV>(a, nbatch, s);
         default: return launch_nb<PRO, EPI, 1, KV>(a, nbatch, s);
     }
+}
+
+// ---- large-N streaming GEMV: weights stream HBM -> LDS by direct DMA
+// (global_load_lds_dwordx4), several units in flight per wave.
+//
+// A unit is 24 consecutive blocks (3264 contiguous bytes) of one 4-row group:
+// the whole group at K = 768, one of P = nb / 24 slices at K = 1536 / 3072
+// (the wave accumulates a group's slices one after the other, so no
+// cross-wave reduction is needed).  Each wave owns a ring of kStreamStages LDS
+// slots; a unit takes 4 DMA instructions of 64 x 16 B (the 4th has 12 active
+// lanes), so a wave keeps kStreamStages - 1 units in flight without holding
+// them in registers.  The math from LDS is the register kernel's: lane
+// 16*bl + 4*k + j takes qword j of row k of block 4*it + bl.
+constexpr int kUnitBlocks = 24;
+constexpr int kUnitBytes = kUnitBlocks * kBlockBytes;  // 3264
+constexpr int kUnitChunks = kUnitBytes / 16;           // 204 = 3 x 64 + 12
+constexpr int kStreamStages = 3;  // 3 x 4 waves x 3264 B: three workgroups fit a CU's LDS
+
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+#ifndef MH_STREAM_CPOL
+#define MH_STREAM_CPOL 2  // non-temporal: the weights are read once per pass
+#endif
+__device__ __forceinline__ void issue_unit(const uint8_t *src, uint8_t *slot, int lane) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        __builtin_amdgcn_global_load_lds((const void *)(src + 16 * (64 * i + lane)), (lds_ptr)(slot + 1024 * i), 16,
+                                         0, MH_STREAM_CPOL);
+    if (lane < kUnitChunks - 192)
+        __builtin_amdgcn_global_load_lds((const void *)(src + 16 * (192 + lane)), (lds_ptr)(slot + 3072), 16, 0,
+                                         MH_STREAM_CPOL);
+}
+
+// Partial dot of one unit (24 blocks x 4 rows) from LDS.
+__device__ __forceinline__ float unit_dot(const uint8_t *slot, const float *xs, int bl, int u, int kk, int j,
+                                          float acc) {
+#pragma unroll
+    for (int it = 0; it < kUnitBlocks / 4; ++it) {
+        const int b = 4 * it + bl;
+        const uint8_t *blk = slot + b * kBlockBytes;
+        const uint2 q = *(const uint2 *)(blk + 8 + 8 * u);
+        const float d = h2f(*(const uint16_t *)(blk + 2 * kk));
+        const float4 x0 = *(const float4 *)(xs + b * 32 + 8 * j);
+        const float4 x1 = *(const float4 *)(xs + b * 32 + 8 * j + 4);
+        float sm = (float)(int8_t)(q.x) * x0.x;
+        sm = fmaf((float)(int8_t)(q.x >> 8), x0.y, sm);
+        sm = fmaf((float)(int8_t)(q.x >> 16), x0.z, sm);
+        sm = fmaf((float)(int8_t)(q.x >> 24), x0.w, sm);
+        sm = fmaf((float)(int8_t)(q.y), x1.x, sm);
+        sm = fmaf((float)(int8_t)(q.y >> 8), x1.y, sm);
+        sm = fmaf((float)(int8_t)(q.y >> 16), x1.z, sm);
+        sm = fmaf((float)(int8_t)(q.y >> 24), x1.w, sm);
+        acc = fmaf(sm, d, acc);
+    }
+    return acc;
+}
+
+// One step of a wave's stream: refill `refill` (the slot consumed last step)
+// with unit t + stages - 1, wait for unit t in `cur`, accumulate it, and on a
+// group's last slice reduce and store.  The restrict-qualified slots let the
+// compiler keep the DMA into `refill` in flight while it reads `cur`.
+template <int EPI, int KV>
+__device__ __forceinline__ void stream_step(const GemvArgs &a, const float *act, int t, int units, int P,
+                                            const uint8_t *next_src, uint8_t *__restrict__ refill,
+                                            const uint8_t *__restrict__ cur, int g, int ngroups, float &acc) {
+    const int lane = threadIdx.x & 63;
+    const int bl = lane >> 4, u = lane & 15, kk = u >> 2, j = u & 3;
+    if (t + kStreamStages - 1 < units) {
+        issue_unit(next_src, refill, lane);
+        wait_vmcnt<4 * (kStreamStages - 1)>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    const int slice = t % P;
+    acc = unit_dot(cur, act + slice * kUnitBlocks * 32, bl, u, kk, j, acc);
+    if (slice == P - 1) {
+        float yv = acc;
+        yv += __shfl_xor(yv, 1);
+        yv += __shfl_xor(yv, 2);
+        yv += __shfl_xor(yv, 16);
+        yv += __shfl_xor(yv, 32);
+        const float partner = __shfl_xor(yv, 4);
+        if (g < ngroups && lane < 16 && j == 0) finish_row<EPI, KV>(a, 4 * g + kk, yv, partner);
+        acc = 0.0f;
+    }
+}
+
+template <int PRO, int EPI, int KV>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs a) {
+    constexpr int S = kStreamStages;
+    __shared__ __attribute__((aligned(16))) uint8_t ring[S][4][kUnitBytes];
+    extern __shared__ float act[];
+    __shared__ float red[4];
+    if (a.state != nullptr && a.state->stop) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nb = a.cols >> 5;
+    const int P = nb / kUnitBlocks;
+    const int ngroups = a.rows >> 2;
+    const int gfirst = blockIdx.x * 4 + wave, gstride = gridDim.x * 4;
+    // units per wave, uniform over the workgroup (a wave past the end repeats a valid unit and stores nothing)
+    const int units = P * ((ngroups - blockIdx.x * 4 + gstride - 1) / gstride);
+    auto src = [&](int t) {
+        const int g = min(gfirst + (t / P) * gstride, ngroups - 1);
+        return a.w + ((size_t)g * nb + (t % P) * kUnitBlocks) * kBlockBytes;
+    };
+#pragma unroll
+    for (int t = 0; t < S - 1; ++t) issue_unit(src(t), ring[t][wave], lane);
+
+    stage_activation<PRO>(a, act, red);
+    __syncthreads();
+
+    float acc = 0.0f;
+    // unrolled by the ring size so every step names its two slots statically
+    for (int t = 0; t < units; t += S) {
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            if (t + r >= units) break;
+            stream_step<EPI, KV>(a, act, t + r, units, P, src(t + r + S - 1), ring[(r + S - 1) % S][wave],
+                                 ring[r][wave], gfirst + ((t + r) / P) * gstride, ngroups, acc);
+        }
+    }
+}
+
+template <int PRO, int EPI, int KV>
+hipError_t launch_stream(const GemvArgs &a, hipStream_t s) {
+    const int ngroups = a.rows / 4;
+    const size_t lds = (size_t)a.cols * sizeof(float);
+    int grid = (ngroups + 3) / 4;
+    grid = grid > 768 ? 768 : grid;  // three 4-wave workgroups per CU (LDS-bound)
+    hipLaunchKernelGGL((gemv_stream_kernel<PRO, EPI, KV>), dim3(grid), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+// The streaming kernel serves large N at K = 768, 1536 or 3072.
+bool use_stream(int rows, int cols) {
+    const int nb = cols / 32;
+    return rows / 4 >= 2048 && (nb == 24 || nb == 48 || nb == 96);
 }
 
 // Waves per 4-row group: enough workgroups to cover the 256 CUs at small N,
@@ -244,10 +386,15 @@ hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv,
     if (pro == PRO_LN && a.cols != kHidden) return hipErrorInvalidValue;
     if (epi == EPI_QKV && a.rows != 3 * kHidden) return hipErrorInvalidValue;
     const int split = pick_split(a.rows, a.cols);
-#define MH_CASE(P, E)                                                                         \
-    if (pro == P && epi == E) {                                                               \
-        if (E == EPI_QKV && kv == KV_F32) return launch_split<P, E, KV_F32>(a, split, s);  \
-        return launch_split<P, E, KV_F16>(a, split, s);                                   \
+    const bool stream = use_stream(a.rows, a.cols);
+#define MH_CASE(P, E)                                                                           \
+    if (pro == P && epi == E) {                                                                 \
+        if (stream) {                                                                           \
+            if (E == EPI_QKV && kv == KV_F32) return launch_stream<P, E, KV_F32>(a, s);        \
+            return launch_stream<P, E, KV_F16>(a, s);                                           \
+        }                                                                                       \
+        if (E == EPI_QKV && kv == KV_F32) return launch_split<P, E, KV_F32>(a, split, s);    \
+        return launch_split<P, E, KV_F16>(a, split, s);                                         \
     }
     MH_CASE(PRO_F32, EPI_F32)
     MH_CASE(PRO_F16, EPI_F16)

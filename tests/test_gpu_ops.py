@@ -18,8 +18,10 @@ def _dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+# (16384, 768), (8196, 768), (8192, 3072), (8200, 1536): the large-N LDS streaming kernel (>= 2048 groups),
+# including a ragged last round of groups and the 2- and 4-slice K = 1536 / 3072 units.
 @pytest.mark.parametrize("rows,cols", [(2304, 768), (768, 768), (3072, 768), (768, 3072), (1024, 768), (8, 768),
-                                       (4, 128), (16384, 768)])
+                                       (4, 128), (16384, 768), (8196, 768), (8192, 3072), (8200, 1536)])
 def test_gemv_f32_vs_oracle(torch_gpu, oracle, rows, cols):
     torch = torch_gpu
     print(f"gemv f32 rows={rows} cols={cols}", flush=True)
