@@ -44,7 +44,7 @@ CAL_BYTES = 256 << 20
 # HBM bytes per launch of the roofline kernel, from two hardware-counter passes over
 # `bench.py --mode gemv` (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; KiB per dispatch
 # scaled by the 256 MiB calibration copy of that same run: fetch x2.0, write x1.0).
-GEMV_TRAFFIC_BYTES = 215_934_671
+GEMV_TRAFFIC_BYTES = 215_409_357
 
 
 def log(*a):
@@ -416,7 +416,7 @@ def main():
         "gemv": {"cold_GBps": round(g["cold"]["GBps"], 1), "warm_GBps": round(g["warm"]["GBps"], 1),
                  "config0_us": round(g["config0"]["us"], 3), "config0_GBps": round(g["config0"]["GBps"], 1)},
         "roofline": {
-            "kernel": f"gemv_q8x4 (fp16 in/out), N={GEMV_N} K={GEMV_K}, weights cycled over "
+            "kernel": f"gemv_stream_kernel (fp16 in/out), N={GEMV_N} K={GEMV_K}, weights cycled over "
                       f"{g['pool_buffers']} buffers (cold)",
             "bound": "hbm",
             "achieved": round(g["cold"]["GBps"], 1),
