@@ -52,14 +52,15 @@ __device__ __forceinline__ float4 load4(const void *base, size_t idx) {
     }
 }
 
-template <int KV, int NW>
+template <int KV, int NW, bool PART>
 __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     __shared__ float qs[kHeadDim];
     __shared__ float sc[NW][64];
     __shared__ float4 po[NW][16];
     __shared__ float pm[NW], pl[NW];
     if (a.state != nullptr && a.state->stop) return;
-    const int h = blockIdx.x, r = blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // PART: one 64-key span per workgroup (blockIdx.y), one row
+    const int h = blockIdx.x, r = PART ? 0 : blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int s = a.row_stream ? a.row_stream[r] : r * a.stream_stride;
     // keys of this row, never past the capacity the caches were built for (a
     // stream parked at capacity keeps pos == capacity)
@@ -70,7 +71,11 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     float m = -INFINITY, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     const int pg = lane >> 4, dg = lane & 15;
-    for (int span = w; span * 64 < n; span += NW) {
+    // PART: exactly one span, [64 * blockIdx.y, min(n, 64 * blockIdx.y + 64))
+    const int span0 = PART ? (int)blockIdx.y : w, span_step = PART ? 1 : NW;
+    const int key_end = PART ? min(n, span0 * 64 + 64) : n;
+    if (PART && span0 * 64 >= n) return;  // a span past the live keys: the merge skips it
+    for (int span = span0; span * 64 < key_end; span += span_step) {
         const int p0 = span * 64;
         const int cnt = min(64, n - p0);
         const int page = a.page_table ? a.page_table[(size_t)s * a.table_stride + p0 / a.page_size] : s;
@@ -121,6 +126,15 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         o.z += __shfl_xor(o.z, off);
         o.w += __shfl_xor(o.w, off);
     }
+    if constexpr (PART) {
+        float *pp = a.part + ((size_t)h * gridDim.y + blockIdx.y) * kPartStride;
+        if (lane < 16) *(float4 *)(pp + 4 * dg) = o;
+        if (lane == 0) {
+            pp[64] = m;
+            pp[65] = l;
+        }
+        return;
+    }
     if (lane < 16) po[w][dg] = o;
     if (lane == 0) {
         pm[w] = m;
@@ -149,17 +163,20 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
 template <int KV>
 hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    (void)hipGetLastError();  // report only this launch's error, not a stale one
     // waves per workgroup from the key capacity the launch is sized for (fixed
     // for a captured graph): one wave per 64 keys up to 16 waves
     const int spans = (a.max_keys + 63) / 64;
+    if (a.part != nullptr) {  // split-KV: one single-wave workgroup per (head, span)
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 1, true>), dim3(a.heads, spans), dim3(64), 0, s, a);
+        return hipGetLastError();
+    }
     const dim3 grid(a.heads, a.rows);
     if (spans <= 1)
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 1>), grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 1, false>), grid, dim3(64), 0, s, a);
     else if (spans <= 4)
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 4>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false>), grid, dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 16>), grid, dim3(1024), 0, s, a);
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 16, false>), grid, dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 
@@ -167,9 +184,10 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
 
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (a.heads <= 0 || a.rows <= 0 || a.max_keys <= 0 || a.page_size <= 0 || !a.out || !a.q || !a.k_pool ||
-        !a.v_pool)
+    if (a.heads <= 0 || a.rows <= 0 || a.max_keys <= 0 || a.page_size <= 0 || (!a.out && !a.part) || !a.q ||
+        !a.k_pool || !a.v_pool)
         return hipErrorInvalidValue;
+    if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
 }
 

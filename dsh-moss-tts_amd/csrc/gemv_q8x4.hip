@@ -23,6 +23,70 @@
 namespace mh {
 namespace {
 
+// Local attention (llm.cpp:189-217 over the local cache, at most 17 keys),
+// computed by every workgroup of the consuming GEMV into its activation:
+// wave w takes heads w, w+4, w+8; lane p scores key p, then lane d sums
+// w_p v_p[d] over the keys in order, w_p = e_p * (1 / sum) as the reference.
+// All loads are unconditional (clamped to a live key, weighted 0).
+__device__ __forceinline__ void local_attention(const GemvArgs &a, float *act) {
+#pragma clang fp contract(off)
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = (a.pos_ptr ? *a.pos_ptr : a.pos_const) + 1;
+    const float *q = (const float *)a.x;
+    const float *K = (const float *)a.k_cache, *V = (const float *)a.v_cache;
+#pragma unroll
+    for (int hh = 0; hh < 3; ++hh) {
+        const int h = w + 4 * hh;
+        const float *kr = K + ((size_t)h * a.ctx_stride + min(lane, n - 1)) * kHeadDim;
+        const float *qh = q + h * kHeadDim;
+        float vv[kLocalLen];
+#pragma unroll
+        for (int p = 0; p < kLocalLen; ++p) vv[p] = V[((size_t)h * a.ctx_stride + min(p, n - 1)) * kHeadDim + lane];
+        float dot = 0.0f;  // sequential over d, unfused, as llm.cpp:196-198
+#pragma unroll
+        for (int c = 0; c < kHeadDim; c += 4) {
+            const float4 kv = *(const float4 *)(kr + c);
+            const float4 qv = *(const float4 *)(qh + c);
+            dot = dot + qv.x * kv.x;
+            dot = dot + qv.y * kv.y;
+            dot = dot + qv.z * kv.z;
+            dot = dot + qv.w * kv.w;
+        }
+        dot *= 0.125f;
+        const float mx = wave_max(lane < n ? dot : -INFINITY);
+        const float e = lane < n ? expf(dot - mx) : 0.0f;
+        const float inv = 1.0f / wave_sum(e);
+        const float wp = e * inv;
+        float o = 0.0f;
+#pragma unroll
+        for (int p = 0; p < kLocalLen; ++p) {
+            const float wq = __shfl(wp, p);  // 0 for p >= n
+            o = o + wq * vv[p];
+        }
+        act[h * kHeadDim + lane] = o;
+    }
+}
+
+// Log-sum-exp merge of split-KV partials (o, m, l per 64-key span) into the
+// attention output: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+__device__ __forceinline__ void merge_attention(const GemvArgs &a, float *act) {
+    const int n = (a.pos_ptr ? *a.pos_ptr : a.pos_const) + 1;
+    const int live = (n + 63) / 64;
+    for (int i = threadIdx.x; i < kHidden; i += 256) {
+        const int h = i >> 6, d = i & 63;
+        const float *P = a.attn_part + (size_t)h * a.attn_splits * kPartStride;
+        float M = -INFINITY;
+        for (int sp = 0; sp < live; ++sp) M = fmaxf(M, P[sp * kPartStride + 64]);
+        float L = 0.0f, O = 0.0f;
+        for (int sp = 0; sp < live; ++sp) {
+            const float sw = expf(P[sp * kPartStride + 64] - M);
+            L = fmaf(P[sp * kPartStride + 65], sw, L);
+            O = fmaf(P[sp * kPartStride + d], sw, O);
+        }
+        act[i] = O / L;
+    }
+}
+
 template <int PRO>
 __device__ __forceinline__ void stage_activation(const GemvArgs &a, float *act, float *red) {
     const int t = threadIdx.x;
@@ -45,6 +109,10 @@ __device__ __forceinline__ void stage_activation(const GemvArgs &a, float *act, 
         layernorm_768(v, a.ln_w, a.ln_b, o, red);
 #pragma unroll
         for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+    } else if constexpr (PRO == PRO_LATTN) {
+        local_attention(a, act);
+    } else if constexpr (PRO == PRO_AMERGE) {
+        merge_attention(a, act);
     }
 }
 
@@ -383,7 +451,9 @@ int pick_split(int rows, int cols) {
 hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (a.rows % 4 != 0 || a.cols % 128 != 0 || a.cols > 4096 || a.rows <= 0) return hipErrorInvalidValue;
-    if (pro == PRO_LN && a.cols != kHidden) return hipErrorInvalidValue;
+    if ((pro == PRO_LN || pro == PRO_LATTN || pro == PRO_AMERGE) && a.cols != kHidden) return hipErrorInvalidValue;
+    if (pro == PRO_LATTN && (!a.k_cache || !a.v_cache || a.ctx_stride < kLocalLen)) return hipErrorInvalidValue;
+    if (pro == PRO_AMERGE && (!a.attn_part || a.attn_splits <= 0)) return hipErrorInvalidValue;
     if (epi == EPI_QKV && a.rows != 3 * kHidden) return hipErrorInvalidValue;
     const int split = pick_split(a.rows, a.cols);
     const bool stream = use_stream(a.rows, a.cols);
@@ -404,6 +474,8 @@ hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv,
     MH_CASE(PRO_LN, EPI_GELU)
     MH_CASE(PRO_F32, EPI_RESID)
     MH_CASE(PRO_LN, EPI_F32)
+    MH_CASE(PRO_LATTN, EPI_RESID)
+    MH_CASE(PRO_AMERGE, EPI_RESID)
 #undef MH_CASE
     return hipErrorInvalidValue;
 }

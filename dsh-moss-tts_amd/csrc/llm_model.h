@@ -116,6 +116,7 @@ private:
     float *x_ = nullptr, *q_ = nullptr, *mlp_ = nullptr, *hidden_ = nullptr;
     float *lres_ = nullptr, *next_in_ = nullptr, *slot_in_ = nullptr;
     float *attn_out_ = nullptr;
+    float *attn_part_ = nullptr;         // [12][ceil(max_ctx / 64)][kPartStride] split-KV partials
     float *logits_ = nullptr;            // [16][1024]
     int *counts_ = nullptr;              // [16][1024]
     int *forced_ = nullptr;              // [max_ctx][16]

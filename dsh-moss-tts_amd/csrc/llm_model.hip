@@ -168,6 +168,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     fmalloc(&next_in_, kHidden);
     fmalloc(&slot_in_, kHidden);
     fmalloc(&attn_out_, kHidden);
+    fmalloc(&attn_part_, (size_t)kHeads * ((max_ctx_ + 63) / 64) * kPartStride);
     fmalloc(&logits_, (size_t)kNVq * kCodebook);
     fmalloc(&text_logits_, kVocab);
     hip_check(hipMalloc(&counts_, sizeof(int) * kNVq * kCodebook), "hipMalloc(counts)");
@@ -194,7 +195,7 @@ Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -210,9 +211,9 @@ void *Model::kv_layer(int which, int layer) const {
 
 // One global step: embed_row -> 12 x block_forward -> ln_f (llm.cpp:248-255).
 // block_forward (llm.cpp:230-246) is five kernels: QKV GEMV with LN1 fused in its
-// prologue and bias + RoPE + KV write in its epilogue; attention (one workgroup
-// per head, split-KV over its waves); proj GEMV adding bias and residual in its
-// epilogue; fc_in GEMV with LN2 in, bias + gelu out; fc_out GEMV with the
+// prologue and bias + RoPE + KV write in its epilogue; split-KV attention (one
+// workgroup per head and 64-key span, unnormalised partials); proj GEMV merging
+// the partials in its prologue, adding bias and residual in its epilogue; fc_in GEMV with LN2 in, bias + gelu out; fc_out GEMV with the
 // residual out.  Every position-dependent kernel reads state->pos.
 void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
     const int *pos = &state_->pos;
@@ -234,15 +235,16 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         a.pos_ptr = pos; a.state = state_;
         hip_check(launch_gemv(a, PRO_LN, EPI_QKV, kvt_, s), "qkv gemv");
 
-        AttnArgs t;  // the cache is one page of max_ctx positions
+        AttnArgs t;  // the cache is one page of max_ctx positions; split-KV partials per 64 keys
         t.q = q_; t.k_pool = a.k_cache; t.v_pool = a.v_cache; t.page_size = max_ctx_;
-        t.row_pos = pos; t.max_keys = max_ctx_; t.out = attn_out_; t.state = state_;
+        t.row_pos = pos; t.max_keys = max_ctx_; t.part = attn_part_; t.state = state_;
         hip_check(launch_attn(t, kvt_, s), "attention");
 
-        GemvArgs p;
+        GemvArgs p;  // the partials are merged in the proj prologue
         p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
-        p.x = attn_out_; p.y = x_; p.bias = L.proj_b; p.state = state_;
-        hip_check(launch_gemv(p, PRO_F32, EPI_RESID, kvt_, s), "proj gemv");
+        p.attn_part = attn_part_; p.attn_splits = (max_ctx_ + 63) / 64; p.pos_ptr = pos;
+        p.y = x_; p.bias = L.proj_b; p.state = state_;
+        hip_check(launch_gemv(p, PRO_AMERGE, EPI_RESID, kvt_, s), "proj gemv");
 
         GemvArgs f1;
         f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;
@@ -273,16 +275,12 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
     a.pos_const = lpos; a.state = state_;
     hip_check(launch_gemv(a, PRO_LN, EPI_QKV, KV_F32, s), "local qkv");
 
-    // At most 17 keys: a single split per head, normalised in place.
-    AttnArgs t;
-    t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen;
-    t.pos0 = lpos; t.max_keys = kLocalLen; t.out = attn_out_; t.state = state_;
-    hip_check(launch_attn(t, KV_F32, s), "local attention");
-
+    // At most 17 keys: the attention is computed in the proj GEMV's prologue.
     GemvArgs p;
     p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
-    p.x = attn_out_; p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_;
-    hip_check(launch_gemv(p, PRO_F32, EPI_RESID, KV_F32, s), "local proj");
+    p.x = q_; p.k_cache = lk; p.v_cache = lv; p.ctx_stride = kLocalLen; p.pos_const = lpos;
+    p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_;
+    hip_check(launch_gemv(p, PRO_LATTN, EPI_RESID, KV_F32, s), "local proj");
 
     GemvArgs f1;
     f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;

@@ -13,6 +13,10 @@ enum Prologue : int {
     PRO_F32 = 0,    // x: float[cols]
     PRO_F16 = 1,    // x: half[cols]
     PRO_LN = 2,     // x: float[768], LayerNorm(ln_w, ln_b) applied in the prologue
+    PRO_LATTN = 3,  // x: q float[768]; the prologue computes the local attention of q over
+                    // k_cache/v_cache (fp32 [12][ctx_stride][64], keys 0..pos_const)
+    PRO_AMERGE = 4, // the prologue merges split-KV attention partials attn_part
+                    // ([12][attn_splits][kPartStride]: o[64], m, l) over keys 0..*pos_ptr
 };
 
 // What happens to each output row.
@@ -40,9 +44,11 @@ struct GemvArgs {
     void *k_cache = nullptr, *v_cache = nullptr;  // [heads][ctx_stride][64]
     int ctx_stride = 0;
     const float *rope_cos = nullptr, *rope_sin = nullptr;  // [pos][32]
-    // position (EPI_QKV): *pos_ptr when non-null, else pos_const
+    // position (EPI_QKV, PRO_LATTN, PRO_AMERGE): *pos_ptr when non-null, else pos_const
     const int *pos_ptr = nullptr;
     int pos_const = 0;
+    const float *attn_part = nullptr;  // PRO_AMERGE partials
+    int attn_splits = 0;
     const DevState *state = nullptr;  // when non-null, the kernel is a no-op once state->stop is set
 };
 
@@ -71,8 +77,13 @@ struct AttnArgs {
     void *out = nullptr;           // row r: out + r * out_stride
     int out_stride = kHidden;
     int out_f16 = 0;               // out is half (else float)
+    // split-KV output (single row only): workgroup (h, s) writes the unnormalised partial of
+    // keys [64 s, 64 s + 64) to part[(h * splits + s) * kPartStride]: o[64], running max m,
+    // sum l; splits = ceil(max_keys / 64).  A consumer merges them (PRO_AMERGE).
+    float *part = nullptr;
     const DevState *state = nullptr;
 };
+constexpr int kPartStride = 68;
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s);
 
 // W8A16 GEMM on the matrix cores: Y[M][N] = A[M][K] W[N][K]^T with an epilogue.

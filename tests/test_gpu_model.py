@@ -80,6 +80,28 @@ def test_global_step_vs_oracle(torch_gpu, oracle, prefilled, kv32, graphs):
     g.close()
 
 
+@pytest.mark.parametrize("ctx", [63, 64, 65, 300, 765])
+def test_global_step_long_context(torch_gpu, oracle, golden_model, ctx):
+    """Split-KV attention (one workgroup per 64-key span, merged in the proj
+    prologue) at span boundaries and long contexts, up to the last positions."""
+    blob, _ = golden_model
+    rng = np.random.default_rng(ctx)
+    k = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    h = rng.standard_normal(768, dtype=np.float32)
+    print(f"global step at ctx {ctx}", flush=True)
+    g = HipLLM(blob)
+    g.kv_import(k, v, h)
+    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=True)
+    for step in range(2):
+        row = np.array([mf.SLOT] + list(rng.integers(0, 1024, 16)), np.int32)
+        g.global_step(row)
+        m.global_step(row)
+        assert g.position == m.position == ctx + step + 1
+        assert max_rel(g.hidden(), m.hidden()) <= TOL
+    g.close()
+
+
 @pytest.mark.parametrize("kv32", [True, False])
 def test_generate_teacher_forced(torch_gpu, oracle, prefilled, kv32):
     """Teacher forcing (the reference's own accuracy protocol, main.cpp:146-180):
