@@ -24,25 +24,32 @@ namespace mh {
 namespace {
 
 // Local attention (llm.cpp:189-217 over the local cache, at most 17 keys),
-// computed by every workgroup of the consuming GEMV into its activation:
-// wave w takes heads w, w+4, w+8; lane p scores key p, then lane d sums
-// w_p v_p[d] over the keys in order, w_p = e_p * (1 / sum) as the reference.
-// All loads are unconditional (clamped to a live key, weighted 0).
+// computed by every workgroup of the consuming GEMV into its activation, in
+// the reference's order: thread (h, p) forms score s_p = (q_h . k_p) * 0.125;
+// thread (h, p) then e_p = exp(s_p - max), the in-order sum and w_p = e_p *
+// (1 / sum); thread (h, d) finally sums w_p v_p[d] over p in order.  Every
+// global load (q, k, and the V values a thread will need) is issued up front;
+// keys past the live count are clamped to a live key and weighted 0.
 __device__ __forceinline__ void local_attention(const GemvArgs &a, float *act) {
 #pragma clang fp contract(off)
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float sc[kHeads][kLocalLen + 1];
+    const int t = threadIdx.x;
     const int n = (a.pos_ptr ? *a.pos_ptr : a.pos_const) + 1;
     const float *q = (const float *)a.x;
     const float *K = (const float *)a.k_cache, *V = (const float *)a.v_cache;
+    float vv[3][kLocalLen];
 #pragma unroll
-    for (int hh = 0; hh < 3; ++hh) {
-        const int h = w + 4 * hh;
-        const float *kr = K + ((size_t)h * a.ctx_stride + min(lane, n - 1)) * kHeadDim;
-        const float *qh = q + h * kHeadDim;
-        float vv[kLocalLen];
+    for (int k = 0; k < 3; ++k) {
+        const int i = t + 256 * k, h = i >> 6, d = i & 63;
 #pragma unroll
-        for (int p = 0; p < kLocalLen; ++p) vv[p] = V[((size_t)h * a.ctx_stride + min(p, n - 1)) * kHeadDim + lane];
-        float dot = 0.0f;  // sequential over d, unfused, as llm.cpp:196-198
+        for (int p = 0; p < kLocalLen; ++p) vv[k][p] = V[((size_t)h * a.ctx_stride + min(p, n - 1)) * kHeadDim + d];
+    }
+    const int hp = t / kLocalLen, pp = t - hp * kLocalLen;  // (head, key) of this thread's score
+    const bool scorer = t < kHeads * kLocalLen;
+    float dot = 0.0f;  // sequential over d, unfused, as llm.cpp:196-198
+    if (scorer) {
+        const float *kr = K + ((size_t)hp * a.ctx_stride + min(pp, n - 1)) * kHeadDim;
+        const float *qh = q + hp * kHeadDim;
 #pragma unroll
         for (int c = 0; c < kHeadDim; c += 4) {
             const float4 kv = *(const float4 *)(kr + c);
@@ -53,35 +60,86 @@ __device__ __forceinline__ void local_attention(const GemvArgs &a, float *act) {
             dot = dot + qv.w * kv.w;
         }
         dot *= 0.125f;
-        const float mx = wave_max(lane < n ? dot : -INFINITY);
-        const float e = lane < n ? expf(dot - mx) : 0.0f;
-        const float inv = 1.0f / wave_sum(e);
-        const float wp = e * inv;
+        sc[hp][pp] = dot;
+    }
+    __syncthreads();
+    float e = 0.0f;
+    if (scorer && pp < n) {
+        float mx = -1e30f;
+        for (int p = 0; p < n; ++p) mx = fmaxf(mx, sc[hp][p]);
+        e = expf(dot - mx);
+    }
+    __syncthreads();
+    if (scorer) sc[hp][pp] = e;
+    __syncthreads();
+    float wgt = 0.0f;  // 0 for keys past n
+    if (scorer) {
+        float sum = 0.0f;
+        for (int p = 0; p < n; ++p) sum += sc[hp][p];
+        wgt = e * (1.0f / sum);
+    }
+    __syncthreads();
+    if (scorer) sc[hp][pp] = wgt;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int i = t + 256 * k, h = i >> 6;
         float o = 0.0f;
 #pragma unroll
-        for (int p = 0; p < kLocalLen; ++p) {
-            const float wq = __shfl(wp, p);  // 0 for p >= n
-            o = o + wq * vv[p];
-        }
-        act[h * kHeadDim + lane] = o;
+        for (int p = 0; p < kLocalLen; ++p) o = o + sc[h][p] * vv[k][p];
+        act[i] = o;
     }
 }
 
 // Log-sum-exp merge of split-KV partials (o, m, l per 64-key span) into the
-// attention output: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.
+// attention output: o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s.  The
+// partial o values a thread needs are loaded up front (spans clamped to the
+// live ones and weighted 0).
+constexpr int kMaxMergeSplits = 16;  // PRO_AMERGE serves key capacities up to 1024
 __device__ __forceinline__ void merge_attention(const GemvArgs &a, float *act) {
+    __shared__ float pm[kHeads][kMaxMergeSplits], pl[kHeads][kMaxMergeSplits];
+    const int t = threadIdx.x;
     const int n = (a.pos_ptr ? *a.pos_ptr : a.pos_const) + 1;
     const int live = (n + 63) / 64;
-    for (int i = threadIdx.x; i < kHidden; i += 256) {
-        const int h = i >> 6, d = i & 63;
-        const float *P = a.attn_part + (size_t)h * a.attn_splits * kPartStride;
+    const int S = a.attn_splits;
+    float ov[3][kMaxMergeSplits];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int i = t + 256 * k, h = i >> 6, d = i & 63;
+#pragma unroll
+        for (int sp = 0; sp < kMaxMergeSplits; ++sp)
+            ov[k][sp] = a.attn_part[((size_t)h * S + min(sp, live - 1)) * kPartStride + d];
+    }
+    const int hs = t / kMaxMergeSplits, ss = t - hs * kMaxMergeSplits;
+    float m = -INFINITY, l = 0.0f;
+    if (hs < kHeads && ss < live) {
+        const float *pp = a.attn_part + ((size_t)hs * S + ss) * kPartStride;
+        m = pp[64];
+        l = pp[65];
+    }
+    if (hs < kHeads) pm[hs][ss] = m;
+    __syncthreads();
+    float sw = 0.0f;
+    if (hs < kHeads) {
         float M = -INFINITY;
-        for (int sp = 0; sp < live; ++sp) M = fmaxf(M, P[sp * kPartStride + 64]);
+#pragma unroll
+        for (int sp = 0; sp < kMaxMergeSplits; ++sp) M = fmaxf(M, pm[hs][sp]);
+        sw = ss < live ? expf(m - M) : 0.0f;
+    }
+    __syncthreads();
+    if (hs < kHeads) {
+        pm[hs][ss] = sw;
+        pl[hs][ss] = sw * l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int i = t + 256 * k, h = i >> 6;
         float L = 0.0f, O = 0.0f;
-        for (int sp = 0; sp < live; ++sp) {
-            const float sw = expf(P[sp * kPartStride + 64] - M);
-            L = fmaf(P[sp * kPartStride + 65], sw, L);
-            O = fmaf(P[sp * kPartStride + d], sw, O);
+#pragma unroll
+        for (int sp = 0; sp < kMaxMergeSplits; ++sp) {
+            L += pl[h][sp];
+            O = fmaf(ov[k][sp], pm[h][sp], O);
         }
         act[i] = O / L;
     }
@@ -453,7 +511,8 @@ hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv,
     if (a.rows % 4 != 0 || a.cols % 128 != 0 || a.cols > 4096 || a.rows <= 0) return hipErrorInvalidValue;
     if ((pro == PRO_LN || pro == PRO_LATTN || pro == PRO_AMERGE) && a.cols != kHidden) return hipErrorInvalidValue;
     if (pro == PRO_LATTN && (!a.k_cache || !a.v_cache || a.ctx_stride < kLocalLen)) return hipErrorInvalidValue;
-    if (pro == PRO_AMERGE && (!a.attn_part || a.attn_splits <= 0)) return hipErrorInvalidValue;
+    if (pro == PRO_AMERGE && (!a.attn_part || a.attn_splits <= 0 || a.attn_splits > kMaxMergeSplits))
+        return hipErrorInvalidValue;
     if (epi == EPI_QKV && a.rows != 3 * kHidden) return hipErrorInvalidValue;
     const int split = pick_split(a.rows, a.cols);
     const bool stream = use_stream(a.rows, a.cols);
