@@ -351,6 +351,8 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
         st->codes[a.ch] = idx;
         st->row[a.ch + 1] = used;
         a.counts[a.ch * kCodebook + used] += 1;
+        if (a.count_all)
+            for (int c = 0; c < a.ch; ++c) a.counts[c * kCodebook + st->row[c + 1]] += 1;
         L.used = used;
         if (a.last_channel) {
             st->row[0] = kSlotToken;

@@ -145,6 +145,71 @@ __device__ __forceinline__ void merge_attention(const GemvArgs &a, float *act) {
     }
 }
 
+// Greedy pick of the previous channel (sampler.cpp:13-28 as llm.cpp:689-697
+// calls it) done by every workgroup of the next local step's QKV GEMV:
+// penalised argmax (lowest index on ties, 0 if all NaN), the used code
+// (forced under teacher forcing), its aemb row, LayerNorm.  Workgroup 0 records
+// the pick; the count of the used code is added at the end of the frame.
+__device__ __forceinline__ void pick_input(const GemvArgs &a, float *act, float *red) {
+#pragma clang fp contract(off)
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const int t = threadIdx.x;
+    const DevState *st = a.pick_state;
+    const float pen = st->rep_penalty;
+    float best = -INFINITY;
+    int besti = kCodebook;
+#pragma unroll
+    for (int k = 0; k < kCodebook / 256; ++k) {  // ascending index per thread
+        const int i = t + 256 * k;
+        float v = a.pick_logits[i];
+        if (pen != 1.0f) {
+            const int c = a.pick_counts[i];
+            for (int r = 0; r < c; ++r) v = v < 0.0f ? v * pen : v / pen;
+        }
+        if (v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(besti, off);
+        if (ov > best || (ov == best && oi < besti)) {
+            best = ov;
+            besti = oi;
+        }
+    }
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = besti;
+    }
+    __syncthreads();
+    float b = bv[0];
+    int idx = bi[0];
+    for (int w = 1; w < 4; ++w)
+        if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
+            b = bv[w];
+            idx = bi[w];
+        }
+    if (idx >= kCodebook) idx = 0;
+    const int used = st->forced_on ? a.pick_forced[st->frame * kNVq + a.pick_ch] : idx;
+    if (blockIdx.x == 0 && t == 0) {
+        a.pick_state->codes[a.pick_ch] = idx;
+        a.pick_state->row[a.pick_ch + 1] = used;
+    }
+    float v[3], o[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v[i] = q8x4_elem(a.pick_aemb, kHidden / 32, used, t + 256 * i);
+    if (blockIdx.x == 0)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) a.pick_raw[t + 256 * i] = v[i];
+    layernorm_768(v, a.ln_w, a.ln_b, o, red);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+}
+
 template <int PRO>
 __device__ __forceinline__ void stage_activation(const GemvArgs &a, float *act, float *red) {
     const int t = threadIdx.x;
@@ -171,6 +236,8 @@ __device__ __forceinline__ void stage_activation(const GemvArgs &a, float *act, 
         local_attention(a, act);
     } else if constexpr (PRO == PRO_AMERGE) {
         merge_attention(a, act);
+    } else if constexpr (PRO == PRO_PICK) {
+        pick_input(a, act, red);
     }
 }
 
@@ -509,7 +576,11 @@ int pick_split(int rows, int cols) {
 hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (a.rows % 4 != 0 || a.cols % 128 != 0 || a.cols > 4096 || a.rows <= 0) return hipErrorInvalidValue;
-    if ((pro == PRO_LN || pro == PRO_LATTN || pro == PRO_AMERGE) && a.cols != kHidden) return hipErrorInvalidValue;
+    if ((pro == PRO_LN || pro == PRO_LATTN || pro == PRO_AMERGE || pro == PRO_PICK) && a.cols != kHidden)
+        return hipErrorInvalidValue;
+    if (pro == PRO_PICK && (!a.pick_logits || !a.pick_counts || !a.pick_aemb || !a.pick_forced || !a.pick_state ||
+                            !a.pick_raw || a.pick_ch < 0 || a.pick_ch >= kNVq))
+        return hipErrorInvalidValue;
     if (pro == PRO_LATTN && (!a.k_cache || !a.v_cache || a.ctx_stride < kLocalLen)) return hipErrorInvalidValue;
     if (pro == PRO_AMERGE && (!a.attn_part || a.attn_splits <= 0 || a.attn_splits > kMaxMergeSplits))
         return hipErrorInvalidValue;
@@ -535,6 +606,7 @@ hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv,
     MH_CASE(PRO_LN, EPI_F32)
     MH_CASE(PRO_LATTN, EPI_RESID)
     MH_CASE(PRO_AMERGE, EPI_RESID)
+    MH_CASE(PRO_PICK, EPI_QKV)
 #undef MH_CASE
     return hipErrorInvalidValue;
 }

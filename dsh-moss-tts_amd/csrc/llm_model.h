@@ -88,11 +88,11 @@ public:
 
 private:
     void enqueue_global_step(hipStream_t s, const int *row_dev);
-    void enqueue_local_step(hipStream_t s, const float *in, int lpos);
-    void enqueue_frame_local(hipStream_t s, bool text_gate);
+    void enqueue_local_step(hipStream_t s, const float *in, int lpos, int pick_ch);
+    void enqueue_frame_local(hipStream_t s, bool text_gate, bool fused);
     void build_graphs();
     void launch_global(hipStream_t s);
-    void launch_frame_local(hipStream_t s, bool text_gate);
+    void launch_frame_local(hipStream_t s, bool text_gate, bool fused);
     void write_state_header();
     void *kv_layer(int which, int layer) const;  // which: 0 = K, 1 = V
 
@@ -128,7 +128,7 @@ private:
     DevState *hstate_ = nullptr;         // pinned host mirror
     void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]
 
-    hipGraphExec_t g_global_ = nullptr, g_local_ = nullptr;
+    hipGraphExec_t g_global_ = nullptr, g_local_ = nullptr, g_local_fused_ = nullptr;
 
     int pos_ = 0, prefix_pos_ = 0;
     const volatile uint8_t *cancel_ = nullptr;

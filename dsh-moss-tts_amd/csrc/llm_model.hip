@@ -195,6 +195,7 @@ Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
+    if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
     void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
@@ -263,7 +264,9 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
 // local_step (llm.cpp:259-264) without its final ln_f: the residual stream starts
 // as `in` (read by the proj epilogue) and lives in lres_; consumers apply the
 // local ln_f in their own prologue.
-void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
+// pick_ch >= 0: the input is the greedy pick of that channel, made in the QKV
+// GEMV's prologue (which also stores the picked row in `in` for the residual).
+void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos, int pick_ch) {
     const LayerW &L = local_;
     float *lk = lkv_, *lv = lkv_ + (size_t)kHeads * kLocalLen * kHeadDim;
     GemvArgs a;
@@ -273,7 +276,16 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
     a.k_cache = lk; a.v_cache = lv; a.ctx_stride = kLocalLen;
     a.rope_cos = rope_; a.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
     a.pos_const = lpos; a.state = state_;
-    hip_check(launch_gemv(a, PRO_LN, EPI_QKV, KV_F32, s), "local qkv");
+    if (pick_ch >= 0) {
+        a.pick_logits = logits_ + (size_t)pick_ch * kCodebook;
+        a.pick_counts = counts_ + (size_t)pick_ch * kCodebook;
+        a.pick_aemb = aemb_[pick_ch];
+        a.pick_forced = forced_;
+        a.pick_ch = pick_ch;
+        a.pick_state = state_;
+        a.pick_raw = const_cast<float *>(in);
+    }
+    hip_check(launch_gemv(a, pick_ch >= 0 ? PRO_PICK : PRO_LN, EPI_QKV, KV_F32, s), "local qkv");
 
     // At most 17 keys: the attention is computed in the proj GEMV's prologue.
     GemvArgs p;
@@ -296,8 +308,12 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos) {
 
 // The local half of a frame (llm.cpp:648-698): local step on hidden, end gate,
 // then 16 x (local step, audio head of channel ch, pick + next input).
-void Model::enqueue_frame_local(hipStream_t s, bool text_gate) {
-    enqueue_local_step(s, hidden_, 0);
+//
+// fused (greedy decoding): the pick of channel ch - 1 runs in the prologue of
+// channel ch's QKV GEMV instead of a kernel of its own; only channel 15 keeps
+// its sample kernel, which also counts the frame's used codes.
+void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
+    enqueue_local_step(s, hidden_, 0, -1);
     if (text_gate) {  // gate-dump frames: the whole text head, as llm.cpp:662-667
         GemvArgs t;
         t.w = wte_; t.rows = kVocab; t.cols = kHidden;
@@ -309,7 +325,7 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate) {
         hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, s), "gate");
     }
     for (int ch = 0; ch < kNVq; ++ch) {
-        enqueue_local_step(s, ch == 0 ? slot_in_ : next_in_, ch + 1);
+        enqueue_local_step(s, ch == 0 ? slot_in_ : next_in_, ch + 1, fused && ch > 0 ? ch - 1 : -1);
         GemvArgs h;
         h.w = aemb_[ch]; h.rows = kCodebook; h.cols = kHidden;
         h.x = lres_; h.ln_w = llnf_w_; h.ln_b = llnf_b_;
@@ -324,7 +340,8 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate) {
         sa.next_input = next_in_;
         sa.state = state_;
         sa.last_channel = ch == kNVq - 1;
-        hip_check(launch_sample(sa, s), "sample");
+        sa.count_all = fused && ch == kNVq - 1;
+        if (!fused || ch == kNVq - 1) hip_check(launch_sample(sa, s), "sample");
     }
 }
 
@@ -335,11 +352,14 @@ void Model::build_graphs() {
     hip_check(hipStreamEndCapture(stream_, &g), "end capture");
     hip_check(hipGraphInstantiate(&g_global_, g, nullptr, nullptr, 0), "instantiate global");
     (void)hipGraphDestroy(g);
-    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
-    enqueue_frame_local(stream_, false);
-    hip_check(hipStreamEndCapture(stream_, &g), "end capture");
-    hip_check(hipGraphInstantiate(&g_local_, g, nullptr, nullptr, 0), "instantiate local");
-    (void)hipGraphDestroy(g);
+    for (int fused = 0; fused < 2; ++fused) {
+        hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+        enqueue_frame_local(stream_, false, fused != 0);
+        hip_check(hipStreamEndCapture(stream_, &g), "end capture");
+        hip_check(hipGraphInstantiate(fused ? &g_local_fused_ : &g_local_, g, nullptr, nullptr, 0),
+                  "instantiate local");
+        (void)hipGraphDestroy(g);
+    }
 }
 
 void Model::launch_global(hipStream_t s) {
@@ -349,11 +369,12 @@ void Model::launch_global(hipStream_t s) {
         enqueue_global_step(s, reinterpret_cast<const int *>(reinterpret_cast<uint8_t *>(state_) + kStateRowOff));
 }
 
-void Model::launch_frame_local(hipStream_t s, bool text_gate) {
-    if (g_local_ && !text_gate)
-        hip_check(hipGraphLaunch(g_local_, s), "graph launch");
+void Model::launch_frame_local(hipStream_t s, bool text_gate, bool fused) {
+    hipGraphExec_t g = fused ? g_local_fused_ : g_local_;
+    if (g && !text_gate)
+        hip_check(hipGraphLaunch(g, s), "graph launch");
     else
-        enqueue_frame_local(s, text_gate);
+        enqueue_frame_local(s, text_gate, fused);
 }
 
 // Pushes the scalar header (pos .. rep_penalty) of the host mirror to the device.
@@ -498,7 +519,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
         if (pos_ >= max_ctx_) break;
         if (cancel_ != nullptr && __atomic_load_n(cancel_, __ATOMIC_RELAXED)) break;
         hip_check(hipEventRecord(ev_[0], stream_), "event");
-        launch_frame_local(stream_, gate_dump != nullptr);
+        launch_frame_local(stream_, gate_dump != nullptr, hstate_->cfg.greedy != 0);
         hip_check(hipEventRecord(ev_[1], stream_), "event");
         const bool do_global = f + 1 < max_frames && pos_ < max_ctx_;
         if (do_global) launch_global(stream_);

@@ -17,6 +17,10 @@ enum Prologue : int {
                     // k_cache/v_cache (fp32 [12][ctx_stride][64], keys 0..pos_const)
     PRO_AMERGE = 4, // the prologue merges split-KV attention partials attn_part
                     // ([12][attn_splits][kPartStride]: o[64], m, l) over keys 0..*pos_ptr
+    PRO_PICK = 5,   // greedy pick of channel pick_ch from pick_logits (repetition penalty from
+                    // pick_counts), the used code (forced under teacher forcing) selects row
+                    // `used` of pick_aemb, then LayerNorm(ln_w, ln_b); workgroup 0 records the
+                    // pick in pick_state (codes, row)
 };
 
 // What happens to each output row.
@@ -49,6 +53,13 @@ struct GemvArgs {
     int pos_const = 0;
     const float *attn_part = nullptr;  // PRO_AMERGE partials
     int attn_splits = 0;
+    const float *pick_logits = nullptr;  // PRO_PICK: [1024] logits of channel pick_ch
+    const int *pick_counts = nullptr;    // [1024] used-code counts of that channel
+    const uint8_t *pick_aemb = nullptr;  // aemb[pick_ch]
+    const int *pick_forced = nullptr;    // [frames][16] teacher-forcing codes
+    int pick_ch = 0;
+    DevState *pick_state = nullptr;
+    float *pick_raw = nullptr;  // workgroup 0 stores the picked aemb row (the step's residual input)
     const DevState *state = nullptr;  // when non-null, the kernel is a no-op once state->stop is set
 };
 
@@ -146,6 +157,8 @@ struct SampleArgs {
     float *next_input = nullptr;    // [768]
     DevState *state = nullptr;
     int last_channel = 0;           // ch == 15: advance state->frame
+    int count_all = 0;              // also count the used codes of channels 0..14 (state->row), whose
+                                    // picks ran in GEMV prologues that deferred their counting
 };
 hipError_t launch_sample(const SampleArgs &a, hipStream_t s);
 
