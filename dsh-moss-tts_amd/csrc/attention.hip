@@ -58,7 +58,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     __shared__ float sc[NW][64];
     __shared__ float4 po[NW][16];
     __shared__ float pm[NW], pl[NW];
-    if (a.state != nullptr && a.state->stop) return;
+    const bool stopped = a.state != nullptr && a.state->stop;  // tested once q is loaded
     // PART: one 64-key span per workgroup (blockIdx.y), one row
     const int h = blockIdx.x, r = PART ? 0 : blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int s = a.row_stream ? a.row_stream[r] : r * a.stream_stride;
@@ -67,6 +67,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     const int n = min((a.row_pos ? a.row_pos[r] : a.pos0 + r * a.pos_stride) + 1, a.max_keys);
     if (threadIdx.x < kHeadDim) qs[threadIdx.x] = a.q[(size_t)r * a.q_stride + h * kHeadDim + threadIdx.x];
     __syncthreads();
+    if (stopped) return;
 
     float m = -INFINITY, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);

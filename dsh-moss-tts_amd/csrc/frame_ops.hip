@@ -11,7 +11,7 @@ namespace {
 // unconditionally (skipped channels read row 0 and are not added) so they are
 // all in flight together.
 __global__ __launch_bounds__(64) void embed_kernel(EmbedArgs a) {
-    if (a.state != nullptr && a.state->stop) return;
+    const bool stopped = a.state != nullptr && a.state->stop;  // tested before the store
     const int nb = kHidden / 32;
     const int c = blockIdx.x * 64 + threadIdx.x;
     float e[kNVq];
@@ -26,18 +26,19 @@ __global__ __launch_bounds__(64) void embed_kernel(EmbedArgs a) {
 #pragma unroll
     for (int ch = 0; ch < kNVq; ++ch)
         if (use[ch]) v = v + e[ch];
-    a.x[c] = v;
+    if (!stopped) a.x[c] = v;
 }
 
 __global__ __launch_bounds__(256) void layernorm_kernel(const float *x, const float *w, const float *b, float *out,
                                                         DevState *state, int bump_pos) {
     __shared__ float red[4];
-    if (state != nullptr && state->stop) return;
+    const bool stopped = state != nullptr && state->stop;  // tested before the stores
     const int t = threadIdx.x;
     float v[3], o[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) v[i] = x[t + 256 * i];
     layernorm_768(v, w, b, o, red);
+    if (stopped) return;
 #pragma unroll
     for (int i = 0; i < 3; ++i) out[t + 256 * i] = o[i];
     if (bump_pos && t == 0) state->pos += 1;
@@ -219,11 +220,12 @@ __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const flo
     __shared__ int8_t qa[kHidden];
     __shared__ float da[kHidden / 32];
     __shared__ float lanes[2][8];
-    if (state->stop) return;
+    const bool stopped = state->stop;  // tested once the input is loaded
     const int t = threadIdx.x;
     float v[3], o[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) v[i] = x_raw[t + 256 * i];
+    if (stopped) return;
     layernorm_768(v, lnf_w, lnf_b, o, red);
 #pragma unroll
     for (int i = 0; i < 3; ++i) hbuf[t + 256 * i] = o[i];
@@ -340,9 +342,10 @@ __global__ __launch_bounds__(256) void gate_text_kernel(const float *logits, Dev
 __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     __shared__ PickLds L;
     DevState *st = a.state;
-    if (st->stop) return;
+    const bool stopped = st->stop;  // tested once the logits are loaded
     const int t = threadIdx.x;
     load_penalised(L, a.logits, a.counts + a.ch * kCodebook, st->rep_penalty);
+    if (stopped) return;
     const SampleCfg c = st->cfg;
     const bool greedy = c.greedy || st->frame < c.greedy_frames;
     const int idx = greedy ? pick_greedy(L) : pick_sampled(L, c, st->rng);

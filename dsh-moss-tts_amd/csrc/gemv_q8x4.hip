@@ -335,7 +335,11 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     extern __shared__ float act[];
     __shared__ float red[4];
     __shared__ float part[4][4];
-    if (a.state != nullptr && a.state->stop) return;
+    // A frame that has ended (state->stop) makes this a no-op.  The flag is read
+    // here but tested after the prologue, so its load overlaps the weight and
+    // activation loads instead of delaying them (the prologue only writes
+    // per-frame scratch).
+    const bool stopped = a.state != nullptr && a.state->stop;
 
     constexpr int GPW = 4 / SPLIT;  // groups per workgroup pass
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -355,6 +359,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
 
     stage_activation<PRO>(a, act, red);
     __syncthreads();
+    if (stopped) return;
 
     for (int gb = gfirst; gb < ngroups; gb += gridDim.x * GPW) {
         const int g = gb + gslot;
