@@ -241,42 +241,67 @@ __device__ __forceinline__ void stage_activation(const GemvArgs &a, float *act, 
     }
 }
 
+// The epilogue's operands (bias, residual, RoPE factors) are loaded before the
+// dot product so their latency overlaps it: epi_load at the start of a group,
+// epi_store once the row's sum is known.
+struct EpiIn {
+    float b0 = 0.f, b1 = 0.f, res = 0.f, c = 0.f, s = 0.f;
+    int pos = 0;
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiIn epi_load(const GemvArgs &a, int r) {
+    EpiIn e;
+    if constexpr (EPI == EPI_RESID) {
+        const float *xin = a.resid_in != nullptr ? a.resid_in : (const float *)a.y;
+        e.b0 = a.bias[r];
+        e.res = xin[r];
+    } else if constexpr (EPI == EPI_GELU) {
+        e.b0 = a.bias[r];
+    } else if constexpr (EPI == EPI_QKV) {
+        e.b0 = a.bias[r];
+        e.pos = a.pos_ptr ? *a.pos_ptr : a.pos_const;
+        const int sec = r / kHidden, d = (r - sec * kHidden) & 63;
+        if (sec < 2) {
+            e.b1 = a.bias[r ^ 1];
+            e.c = a.rope_cos[e.pos * kRopeHalf + (d >> 1)];
+            e.s = a.rope_sin[e.pos * kRopeHalf + (d >> 1)];
+        }
+    }
+    return e;
+}
+
 template <int EPI, int KV>
-__device__ __forceinline__ void finish_row(const GemvArgs &a, int r, float v, float partner) {
+__device__ __forceinline__ void epi_store(const GemvArgs &a, int r, float v, float partner, const EpiIn &e) {
 #pragma clang fp contract(off)
     if constexpr (EPI == EPI_F32) {
         ((float *)a.y)[r] = v;
     } else if constexpr (EPI == EPI_F16) {
         ((__half *)a.y)[r] = __float2half_rn(v);
     } else if constexpr (EPI == EPI_RESID) {
-        float *y = (float *)a.y;
-        const float *xin = a.resid_in != nullptr ? a.resid_in : y;
-        y[r] = xin[r] + (v + a.bias[r]);
+        ((float *)a.y)[r] = e.res + (v + e.b0);
     } else if constexpr (EPI == EPI_GELU) {
-        ((float *)a.y)[r] = gelu_new(v + a.bias[r]);
+        ((float *)a.y)[r] = gelu_new(v + e.b0);
     } else {  // EPI_QKV (llm.cpp:234-236 then the KV write of llm.cpp:224-225)
-        const float val = v + a.bias[r];
+        const float val = v + e.b0;
         const int sec = r / kHidden, within = r - sec * kHidden;
         const int h = within >> 6, d = within & 63;
-        const int pos = a.pos_ptr ? *a.pos_ptr : a.pos_const;
         float out = val;
         if (sec < 2) {
-            const float pv = partner + a.bias[r ^ 1];
-            const float c = a.rope_cos[pos * kRopeHalf + (d >> 1)];
-            const float s = a.rope_sin[pos * kRopeHalf + (d >> 1)];
+            const float pv = partner + e.b1;
             // (x0, x1) -> (x0 c - x1 s, x1 c + x0 s)   (llm.cpp:181-184)
             if ((d & 1) == 0) {
-                const float p0 = val * c, p1 = pv * s;
+                const float p0 = val * e.c, p1 = pv * e.s;
                 out = p0 - p1;
             } else {
-                const float p0 = val * c, p1 = pv * s;
+                const float p0 = val * e.c, p1 = pv * e.s;
                 out = p0 + p1;
             }
         }
         if (sec == 0) {
             a.q_out[within] = out;
         } else {
-            const size_t idx = ((size_t)h * a.ctx_stride + pos) * kHeadDim + d;
+            const size_t idx = ((size_t)h * a.ctx_stride + e.pos) * kHeadDim + d;
             void *cache = sec == 1 ? a.k_cache : a.v_cache;
             if constexpr (KV == KV_F16)
                 ((__half *)cache)[idx] = __float2half_rn(out);
@@ -284,6 +309,11 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int r, float v, fl
                 ((float *)cache)[idx] = out;
         }
     }
+}
+
+template <int EPI, int KV>
+__device__ __forceinline__ void finish_row(const GemvArgs &a, int r, float v, float partner) {
+    epi_store<EPI, KV>(a, r, v, partner, epi_load<EPI>(a, r));
 }
 
 // Up to NB blocks per lane are in flight at once: all loads of a batch are
@@ -356,6 +386,9 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     uint2 qv[NB];
     uint16_t dh[NB];
     if (gfirst + gslot < ngroups) load_batch<NB>(a.w + (size_t)(gfirst + gslot) * nb * kBlockBytes, b0 + bl, b1, u, kk, qv, dh);
+    const bool storer = ks == 0 && lane < 16 && (u & 3) == 0;  // the lane that finishes row 4g + kk
+    EpiIn pre;
+    if (storer && gfirst + gslot < ngroups) pre = epi_load<EPI>(a, 4 * (gfirst + gslot) + kk);
 
     stage_activation<PRO>(a, act, red);
     __syncthreads();
@@ -364,6 +397,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     for (int gb = gfirst; gb < ngroups; gb += gridDim.x * GPW) {
         const int g = gb + gslot;
         const bool valid = g < ngroups;
+        if (gb != gfirst && storer && valid) pre = epi_load<EPI>(a, 4 * g + kk);
         float acc = 0.0f;
         if (valid) {
             const uint8_t *grp = a.w + (size_t)g * nb * kBlockBytes;
@@ -386,7 +420,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
             __syncthreads();
         }
         const float partner = __shfl_xor(yv, 4);
-        if (ks == 0 && valid && lane < 16 && j == 0) finish_row<EPI, KV>(a, 4 * g + kk, yv, partner);
+        if (storer && valid) epi_store<EPI, KV>(a, 4 * g + kk, yv, partner, pre);
     }
 }
 
