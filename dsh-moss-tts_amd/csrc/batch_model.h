@@ -45,7 +45,8 @@ private:
     struct Graphs {
         hipGraphExec_t local = nullptr, global = nullptr;
     };
-    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos);
+    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, const float *out_ln_w,
+                            const float *out_ln_b);
     void enqueue_frame_local(hipStream_t s, int n);
     void enqueue_global(hipStream_t s, int n);
     Graphs &graphs_for(int n);
@@ -71,6 +72,7 @@ private:
     int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr;
     BatchCtl *ctrl_ = nullptr;
     uint32_t *rng_ = nullptr;                   // [S][4]
+    float *part_ = nullptr;                     // [16][S][768] split-K partials
     unsigned char *active_ = nullptr;
     float *gate_ = nullptr;
     int *hist_codes_ = nullptr;                 // [cap+1][S][16] codes per frame

@@ -70,6 +70,7 @@ Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
     im(&codes_, (size_t)S_ * kNVq);
     im(&row_, (size_t)S_ * (kNVq + 1));
     im(&counts_, (size_t)S_ * kNVq * kCodebook);
+    fm(&part_, (size_t)16 * S_ * kHidden);
     hip_check(hipMalloc(&ctrl_, sizeof(BatchCtl)), "hipMalloc(ctrl)");
     hip_check(hipMalloc(&rng_, sizeof(uint32_t) * 4 * S_), "hipMalloc(rng)");
     hip_check(hipMemset(rng_, 0, sizeof(uint32_t) * 4 * S_), "memset(rng)");
@@ -89,7 +90,7 @@ Batch::~Batch() {
         if (kv.second.global) (void)hipGraphExecDestroy(kv.second.global);
     }
     void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
-                    gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_};
+                    gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_, part_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (ctrl_h_) (void)hipHostFree(ctrl_h_);
@@ -185,8 +186,12 @@ void Batch::kv_export(int s, int n_pos, float *k, float *v) {
 
 // block_forward (llm.cpp:230-246) of the local layer for n streams at local
 // position lpos; the residual starts as `in` (row stride in_stride, 0 = one row
-// shared by all streams) and ends in lres_.
-void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos) {
+// shared by all streams) and ends in lres_.  proj and fc_out are split-K GEMMs
+// whose partials are reduced, in a fixed order, by the residual + LayerNorm
+// kernel that follows each; the last one applies out_ln (the local ln_f before
+// the heads) into a_ when it is non-null.
+void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, const float *out_ln_w,
+                               const float *out_ln_b) {
     const LayerW &L = *w_.local;
     float *lk = lkv_, *lv = lkv_ + (size_t)S_ * kHeads * kLocalLen * kHeadDim;
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
@@ -202,30 +207,33 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     hip_check(launch_attn(t, KV_F32, s), "local attention");
     GemmArgs p;
     p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
-    p.y = lres_; p.ldy = kHidden; p.resid_in = in; p.resid_stride = in_stride; p.bias = L.proj_b;
-    hip_check(launch_gemm(p, EPI_RESID, KV_F32, s), "local proj");
-    hip_check(launch_ln_rows(lres_, kHidden, L.ln2_w, L.ln2_b, a_, n, s), "local ln2");
+    p.part = part_; p.ksplit = gemm_ksplit(n, kHidden, kHidden);
+    hip_check(launch_gemm(p, EPI_PART, KV_F32, s), "local proj");
+    hip_check(launch_resid_ln_rows(part_, p.ksplit, n, L.proj_b, in, in_stride, lres_, L.ln2_w, L.ln2_b, a_, nullptr, s),
+              "local proj reduce + ln2");
     GemmArgs f1;
     f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = a_; f1.lda = kHidden; f1.M = n;
     f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
     hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
     GemmArgs f2;
     f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
-    f2.y = lres_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
-    hip_check(launch_gemm(f2, EPI_RESID, KV_F32, s), "local fc_out");
+    f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
+    hip_check(launch_gemm(f2, EPI_PART, KV_F32, s), "local fc_out");
+    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, out_ln_w, out_ln_b, a_,
+                                   nullptr, s),
+              "local fc_out reduce");
 }
 
 // The local half of a frame for n streams (llm.cpp:648-698).
 void Batch::enqueue_frame_local(hipStream_t s, int n) {
     const StreamState st = state();
-    enqueue_local_step(s, n, hidden_, kHidden, 0);
+    enqueue_local_step(s, n, hidden_, kHidden, 0, nullptr, nullptr);
     hip_check(launch_gate_rows(lres_, w_.llnf_w, w_.llnf_b, w_.wte, st, n, s), "gate");
     for (int ch = 0; ch < kNVq; ++ch) {
         if (ch == 0)
-            enqueue_local_step(s, n, w_.slot_in, 0, 1);
+            enqueue_local_step(s, n, w_.slot_in, 0, 1, w_.llnf_w, w_.llnf_b);
         else
-            enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
-        hip_check(launch_ln_rows(lres_, kHidden, w_.llnf_w, w_.llnf_b, a_, n, s), "local ln_f");
+            enqueue_local_step(s, n, next_in_, kHidden, ch + 1, w_.llnf_w, w_.llnf_b);
         GemmArgs hd;
         hd.w = w_.aemb[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
@@ -241,12 +249,12 @@ void Batch::enqueue_global(hipStream_t s, int n) {
     e.wte = w_.wte;
     for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = w_.aemb[ch];
     hip_check(launch_embed_rows(e, row_, n, x_, s), "embed");
+    hip_check(launch_ln_rows(x_, kHidden, w_.global[0].ln1_w, w_.global[0].ln1_b, a_, n, s), "ln1");
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = w_.global[l];
         void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
         void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
-        hip_check(launch_ln_rows(x_, kHidden, L.ln1_w, L.ln1_b, a_, n, s), "ln1");
         GemmArgs q;
         q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
@@ -259,19 +267,26 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         hip_check(launch_attn(t, kvt_, s), "attention");
         GemmArgs p;
         p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
-        p.y = x_; p.ldy = kHidden; p.bias = L.proj_b;
-        hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "proj");
-        hip_check(launch_ln_rows(x_, kHidden, L.ln2_w, L.ln2_b, a_, n, s), "ln2");
+        p.part = part_; p.ksplit = gemm_ksplit(n, kHidden, kHidden);
+        hip_check(launch_gemm(p, EPI_PART, kvt_, s), "proj");
+        hip_check(launch_resid_ln_rows(part_, p.ksplit, n, L.proj_b, x_, kHidden, x_, L.ln2_w, L.ln2_b, a_, nullptr, s),
+                  "proj reduce + ln2");
         GemmArgs f1;
         f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = a_; f1.lda = kHidden; f1.M = n;
         f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
         GemmArgs f2;
         f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
-        f2.y = x_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
-        hip_check(launch_gemm(f2, EPI_RESID, kvt_, s), "fc_out");
+        f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
+        hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
+        // reduce + residual, then LN1 of the next layer, or ln_f into hidden (active streams only)
+        const bool last = l + 1 == kLayers;
+        hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, x_, kHidden, x_,
+                                       last ? w_.lnf_w : w_.global[l + 1].ln1_w,
+                                       last ? w_.lnf_b : w_.global[l + 1].ln1_b, last ? hidden_ : a_,
+                                       last ? active_ : nullptr, s),
+                  "fc_out reduce + ln");
     }
-    hip_check(launch_ln_rows(x_, kHidden, w_.lnf_w, w_.lnf_b, hidden_, n, s, active_), "ln_f");
     hip_check(launch_advance_rows(st, n, s), "advance");
 }
 

@@ -479,6 +479,32 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stri
     for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
 }
 
+// Split-K reduce + residual + LayerNorm of one row per workgroup (launch_resid_ln_rows).
+__global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, int ksplit, int rows,
+                                                            const float *bias, const float *resid, int resid_stride,
+                                                            float *x, const float *ln_w, const float *ln_b,
+                                                            float *out, const unsigned char *mask) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    float v[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int n = t + 256 * i;
+        float acc = part[(size_t)r * kHidden + n];
+        for (int z = 1; z < ksplit; ++z) acc += part[((size_t)z * rows + r) * kHidden + n];
+        v[i] = resid[(size_t)r * resid_stride + n] + (acc + bias[n]);
+    }
+    __syncthreads();  // every read of x (through resid) happens before any write of it
+#pragma unroll
+    for (int i = 0; i < 3; ++i) x[(size_t)r * kHidden + t + 256 * i] = v[i];
+    if (ln_w == nullptr || (mask != nullptr && !mask[r])) return;
+    float o[3];
+    layernorm_768(v, ln_w, ln_b, o, red);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+}
+
 // grid (12, rows): same per-element serial sum as embed_kernel
 __global__ __launch_bounds__(64) void embed_rows_kernel(EmbedArgs a, const int *rows, float *x) {
     const int nb = kHidden / 32;
@@ -664,6 +690,17 @@ hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const fl
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask);
+    return hipGetLastError();
+}
+
+hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
+                                int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
+                                const unsigned char *mask, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (rows <= 0) return hipSuccess;
+    if (!part || ksplit <= 0 || !bias || !resid || !x || (ln_w && (!ln_b || !out))) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(resid_ln_rows_kernel, dim3(rows), dim3(256), 0, s, part, ksplit, rows, bias, resid,
+                       resid_stride, x, ln_w, ln_b, out, mask);
     return hipGetLastError();
 }
 

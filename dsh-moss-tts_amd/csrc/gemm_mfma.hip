@@ -50,7 +50,9 @@ __device__ __forceinline__ half8 i8x8_to_h8(uint2 q) {
 template <int EPI, int KV>
 __device__ __forceinline__ void gemm_finish(const GemmArgs &g, int m, int n, float v, float partner) {
 #pragma clang fp contract(off)
-    if constexpr (EPI == EPI_F32) {
+    if constexpr (EPI == EPI_PART) {
+        g.part[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
+    } else if constexpr (EPI == EPI_F32) {
         g.y[(size_t)m * g.ldy + n] = v;
     } else if constexpr (EPI == EPI_RESID) {
         float *y = g.y + (size_t)m * g.ldy + n;
@@ -87,22 +89,76 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs &g, int m, int n, flo
 }
 
 
+// One chunk of KB scale blocks: this lane's 8 activations per block and its 8
+// weights + scale per block and column subtile.  Block indices are clamped so
+// every load is unconditional (blocks past nb are loaded but not used).
+template <int NT>
+struct Chunk {
+    float xa[KB][8];
+    uint2 qb[KB][NT];
+    uint32_t db[KB][NT];
+};
+
+template <int NT>
+__device__ __forceinline__ void load_chunk(Chunk<NT> &c, int b0, int nb, const float *arow_p,
+                                           const uint8_t *const (&wcol)[NT], int krow, int kq) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+        const int b = min(b0 + j, nb - 1);
+        const float4 x0 = *(const float4 *)(arow_p + 32 * b);
+        const float4 x1 = *(const float4 *)(arow_p + 32 * b + 4);
+        c.xa[j][0] = x0.x; c.xa[j][1] = x0.y; c.xa[j][2] = x0.z; c.xa[j][3] = x0.w;
+        c.xa[j][4] = x1.x; c.xa[j][5] = x1.y; c.xa[j][6] = x1.z; c.xa[j][7] = x1.w;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint8_t *blk = wcol[t] + (size_t)b * kBlockBytes;
+            const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 32 * krow + 8 * kq));
+            c.qb[j][t] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
+            c.db[j][t] = *(const uint16_t *)(blk + 2 * krow);
+        }
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void mfma_chunk(const Chunk<NT> &c, int b0, int nb, floatx4 (&acc)[NT]) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+        half8 hi, lo;
+        split_hi_lo(c.xa[j], hi, lo);
+        const bool live = b0 + j < nb;  // uniform; a dead block adds with a zero scale
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const half8 bw = i8x8_to_h8(c.qb[j][t]);
+            floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, bw, blk, 0, 0, 0);
+            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, bw, blk, 0, 0, 0);
+            const float d = live ? h2f((uint16_t)c.db[j][t]) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(blk[i], d, acc[t][i]);
+        }
+    }
+}
+
 template <int EPI, int KV, int NT>
 __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
     const int m_base = blockIdx.y * 64 + wave * 16;
     const int n_base = blockIdx.x * 16 * NT;
-    const int nb = g.K >> 5;
+    const int nb_all = g.K >> 5;
+    // K slice z of gridDim.z: blocks [kb0, kb0 + nb)
+    const int per = (nb_all + gridDim.z - 1) / gridDim.z;
+    const int kb0 = blockIdx.z * per;
+    const int nb = min(nb_all - kb0, per);
     // A row of this lane (clamped: rows past M read row M-1 and are never stored)
     const int arow = min(m_base + l16, g.M - 1);
-    const float *arow_p = g.a + (size_t)arow * g.lda + 8 * kq;
+    const float *arow_p = g.a + (size_t)arow * g.lda + 8 * kq + 32 * kb0;
     // B column (weight row) of this lane for each of the NT subtiles
     const uint8_t *wcol[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int n = n_base + 16 * t + l16;
-        wcol[t] = g.w + (size_t)(n >> 2) * nb * kBlockBytes;
+        wcol[t] = g.w + ((size_t)(n >> 2) * nb_all + kb0) * kBlockBytes;
     }
     const int krow = l16 & 3;  // row inside the 4-row group (n % 4; n_base is a multiple of 16)
 
@@ -110,41 +166,17 @@ __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    for (int b0 = 0; b0 < nb; b0 += KB) {
-        float xa[KB][8];
-        uint2 qb[KB][NT];
-        uint16_t db[KB][NT];
-#pragma unroll
-        for (int j = 0; j < KB; ++j) {
-            const int b = min(b0 + j, nb - 1);
-            const float4 x0 = *(const float4 *)(arow_p + 32 * b);
-            const float4 x1 = *(const float4 *)(arow_p + 32 * b + 4);
-            xa[j][0] = x0.x; xa[j][1] = x0.y; xa[j][2] = x0.z; xa[j][3] = x0.w;
-            xa[j][4] = x1.x; xa[j][5] = x1.y; xa[j][6] = x1.z; xa[j][7] = x1.w;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const uint8_t *blk = wcol[t] + (size_t)b * kBlockBytes;
-                const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 32 * krow + 8 * kq));
-                qb[j][t] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
-                db[j][t] = *(const uint16_t *)(blk + 2 * krow);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < KB; ++j) {
-            if (b0 + j >= nb) break;
-            half8 hi, lo;
-            split_hi_lo(xa[j], hi, lo);
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const half8 bw = i8x8_to_h8(qb[j][t]);
-                floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
-                blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, bw, blk, 0, 0, 0);
-                blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, bw, blk, 0, 0, 0);
-                const float d = h2f(db[j][t]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(blk[i], d, acc[t][i]);
-            }
-        }
+    // two chunks in flight: chunk c+1 is issued before chunk c is multiplied;
+    // the chunks alternate between two register sets (a copy would wait for
+    // the loads it moves)
+    Chunk<NT> ca, cb;
+    load_chunk<NT>(ca, 0, nb, arow_p, wcol, krow, kq);
+    for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
+        load_chunk<NT>(cb, b0 + KB, nb, arow_p, wcol, krow, kq);
+        mfma_chunk<NT>(ca, b0, nb, acc);
+        if (b0 + KB >= nb) break;
+        load_chunk<NT>(ca, b0 + 2 * KB, nb, arow_p, wcol, krow, kq);
+        mfma_chunk<NT>(cb, b0 + KB, nb, acc);
     }
 
     // epilogue: lane holds rows m_base + 4kq + i, column n_base + 16t + l16
@@ -164,24 +196,42 @@ __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
 template <int EPI, int KV>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    (void)hipGetLastError();  // report only this launch's error, not a stale one
     // 4 column subtiles (64 columns) per workgroup unless that leaves too few workgroups
     const int mt = (g.M + 63) / 64;
-    const bool wide = (g.N / 64) * mt >= 128;
+    const int kz = EPI == EPI_PART ? (g.ksplit > 0 ? g.ksplit : gemm_ksplit(g.M, g.N, g.K)) : 1;
+    const bool wide = (g.N / 64) * mt * kz >= 96;
     if (wide && g.N % 64 == 0) {
-        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 4>), dim3(g.N / 64, mt), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 4>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
     } else {
-        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 1>), dim3(g.N / 16, mt), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 1>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
     }
     return hipGetLastError();
 }
 }  // namespace
 
+// Split K so that a GEMM with few output tiles still spreads over the CUs:
+// about 384 workgroups of 64 x 64 tiles, at least 3 blocks per slice, at most 16.
+int gemm_ksplit(int M, int N, int K) {
+    const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
+    const int nb = K / 32;
+    int z = (384 + tiles - 1) / tiles;
+    z = z > nb / 3 ? nb / 3 : z;
+    z = z > 16 ? 16 : z;
+    z = z < 1 ? 1 : z;
+    const int per = (nb + z - 1) / z;
+    return (nb + per - 1) / per;  // no empty slice
+}
+
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (g.M <= 0 || g.N <= 0 || g.N % 16 || g.K % 32 || g.K <= 0 || g.lda < g.K || g.lda % 4) return hipErrorInvalidValue;
     if (epi == EPI_QKV && (g.N != 3 * kHidden || g.page_size <= 0)) return hipErrorInvalidValue;
+    if (epi == EPI_PART) {  // every K slice must hold at least one block
+        const int nb = g.K / 32, z = g.ksplit;
+        if (!g.part || z > 16 || z > nb || (z > 0 && (z - 1) * ((nb + z - 1) / z) >= nb)) return hipErrorInvalidValue;
+    }
     switch (epi) {
+        case EPI_PART: return launch_nt<EPI_PART, KV_F16>(g, s);
         case EPI_F32: return launch_nt<EPI_F32, KV_F16>(g, s);
         case EPI_RESID: return launch_nt<EPI_RESID, KV_F16>(g, s);
         case EPI_GELU: return launch_nt<EPI_GELU, KV_F16>(g, s);

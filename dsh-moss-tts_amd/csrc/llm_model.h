@@ -124,6 +124,7 @@ private:
     int *rows_dev_ = nullptr;            // prefill rows [n][17]
     int rows_cap_ = 0;
     float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_o_ = nullptr, *pre_h_ = nullptr;  // prefill rows
+    float *pre_part_ = nullptr;          // split-K partials of the prefill proj / fc_out GEMMs
     DevState *state_ = nullptr;          // device
     DevState *hstate_ = nullptr;         // pinned host mirror
     void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]

@@ -1,6 +1,8 @@
 // llm_model.hip -- host driver of the GPU-resident LLM (see llm_model.h).
 #include "llm_model.h"
 
+#include <algorithm>
+
 #include <chrono>
 #include <cmath>
 #include <cstddef>
@@ -196,7 +198,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -428,11 +430,11 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     if (m <= 0) return;
     check_rows(rows, m);
     if (m > rows_cap_) {
-        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_};
+        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_};
         for (void *p : bufs)
             if (p) hip_check(hipFree(p), "free prefill buffers");
         rows_dev_ = nullptr;
-        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = nullptr;
+        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = pre_part_ = nullptr;
         rows_cap_ = 0;
         hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
         hip_check(hipMalloc(&pre_x_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
@@ -440,6 +442,8 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(hipMalloc(&pre_q_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
         hip_check(hipMalloc(&pre_o_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
         hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * (size_t)m), "hipMalloc(prefill)");
+        const int kz = std::max(gemm_ksplit(m, kHidden, kHidden), gemm_ksplit(m, kHidden, kFF));
+        hip_check(hipMalloc(&pre_part_, sizeof(float) * kHidden * (size_t)m * kz), "hipMalloc(prefill)");
         rows_cap_ = m;
     }
     hip_check(hipMemcpyAsync(rows_dev_, rows, sizeof(int) * 17 * (size_t)m, hipMemcpyHostToDevice, stream_), "rows h2d");
@@ -451,10 +455,10 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     e.wte = wte_;
     for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = aemb_[ch];
     hip_check(launch_embed_rows(e, rows_dev_, m, pre_x_, s), "prefill embed");
+    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, pre_a_, m, s), "prefill ln1");
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
-        hip_check(launch_ln_rows(pre_x_, kHidden, L.ln1_w, L.ln1_b, pre_a_, m, s), "prefill ln1");
         GemmArgs q;
         q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = pre_a_; q.lda = kHidden; q.M = m;
         q.bias = L.attn_b; q.q_out = pre_q_;
@@ -465,19 +469,26 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
         t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = pre_o_;
         hip_check(launch_attn(t, kvt_, s), "prefill attention");
-        GemmArgs p;
+        GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
         p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
-        p.y = pre_x_; p.ldy = kHidden; p.bias = L.proj_b;
-        hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "prefill proj");
-        hip_check(launch_ln_rows(pre_x_, kHidden, L.ln2_w, L.ln2_b, pre_a_, m, s), "prefill ln2");
+        p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);
+        hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
+        hip_check(launch_resid_ln_rows(pre_part_, p.ksplit, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
+                                       pre_a_, nullptr, s),
+                  "prefill proj reduce + ln2");
         GemmArgs f1;
         f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
         f1.y = pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
         GemmArgs f2;
         f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
-        f2.y = pre_x_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
-        hip_check(launch_gemm(f2, EPI_RESID, kvt_, s), "prefill fc_out");
+        f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
+        hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
+        const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce
+        hip_check(launch_resid_ln_rows(pre_part_, f2.ksplit, m, L.fc_out_b, pre_x_, kHidden, pre_x_,
+                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, pre_a_,
+                                       nullptr, s),
+                  "prefill fc_out reduce");
     }
     hip_check(launch_layernorm(pre_x_ + (size_t)(m - 1) * kHidden, lnf_w_, lnf_b_, hidden_, nullptr, 0, s), "ln_f");
     pos_ = start + m;

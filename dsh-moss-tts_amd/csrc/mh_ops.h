@@ -30,6 +30,7 @@ enum Epilogue : int {
     EPI_QKV = 2,    // + bias, RoPE on q/k, q -> q_out, k/v -> KV cache at pos
     EPI_RESID = 3,  // y[r] = xin[r] + (acc + bias[r]), xin = resid_in or y (float)
     EPI_GELU = 4,   // y[r] = gelu_new(acc + bias[r])  (float)
+    EPI_PART = 5,   // GEMM only: split-K partial sums, part[z][m][n] for K slice z (no bias)
 };
 
 enum KvType : int { KV_F16 = 0, KV_F32 = 1 };
@@ -119,8 +120,22 @@ struct GemmArgs {
     int pos0 = 0, pos_stride = 1;
     const unsigned char *row_active = nullptr;  // rows with row_active[m] == 0 write no K/V
     const float *rope_cos = nullptr, *rope_sin = nullptr;
+    // EPI_PART: K is cut into ksplit slices of whole blocks (grid z); slice z writes
+    // part + z * M * N (row-major [M][N]).  ksplit <= 0 picks a split from the shape.
+    float *part = nullptr;
+    int ksplit = 0;
 };
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
+// The K split launch_gemm uses for an EPI_PART GEMM of this shape (1..16).
+int gemm_ksplit(int M, int N, int K);
+
+// Deterministic split-K reduce + residual (+ LayerNorm), one workgroup per row:
+//   x[m][n]   = resid[m * resid_stride + n] + ((sum_z part[z][m][n]) + bias[n])   (z in order)
+//   out[m][:] = LayerNorm(x[m][:]; ln_w, ln_b) when ln_w is non-null; rows with mask[m] == 0 keep
+//   their out row.  resid may alias x (in-place residual stream).  N == 768.
+hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
+                                int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
+                                const unsigned char *mask, hipStream_t s);
 
 // ---- frame / step kernels (frame_ops.hip)
 struct EmbedArgs {
