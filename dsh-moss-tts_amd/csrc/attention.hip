@@ -15,7 +15,8 @@
 // online softmax across its spans; the waves are then merged through LDS with a
 // log-sum-exp combine -- split-KV inside the workgroup, no cross-workgroup
 // traffic.  Every K/V load is unconditional (rows past the live count are
-// clamped to a live row and weighted 0) so a lane's loads are in flight together.
+// clamped to a live row and weighted 0), and a span's V values are loaded with
+// its K rows, so all of a lane's loads for the span are in flight together.
 #include "mh_ops.h"
 
 namespace mh {
@@ -81,6 +82,12 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         const int cnt = min(64, n - p0);
         const int page = a.page_table ? a.page_table[(size_t)s * a.table_stride + p0 / a.page_size] : s;
         const size_t base = (((size_t)page * a.heads + h) * a.page_size + p0 % a.page_size) * kHeadDim;
+        // V values of this lane (dims 4dg..4dg+3 of keys pg + 4t) are loaded with K,
+        // before the scores need to be ready
+        float4 vv[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            vv[t] = load4<KV>(a.v_pool, base + (size_t)min(pg + 4 * t, cnt - 1) * kHeadDim + 4 * dg);
         // scores, one key per lane
         const size_t krow = base + (size_t)min(lane, cnt - 1) * kHeadDim;
         float kf[8][8];
@@ -110,7 +117,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             const int i = pg + 4 * t;
-            const float4 v = load4<KV>(a.v_pool, base + (size_t)min(i, cnt - 1) * kHeadDim + 4 * dg);
+            const float4 v = vv[t];
             const float ei = sc[w][i];
             o.x = fmaf(ei, v.x, o.x);
             o.y = fmaf(ei, v.y, o.y);
@@ -165,7 +172,8 @@ template <int KV>
 hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     // waves per workgroup from the key capacity the launch is sized for (fixed
-    // for a captured graph): one wave per 64 keys up to 16 waves
+    // for a captured graph): one wave per 64 keys up to 4 waves, which then take
+    // several spans each (measured faster than 8 or 16 waves at 64 streams x ~540 keys)
     const int spans = (a.max_keys + 63) / 64;
     if (a.part != nullptr) {  // split-KV: one single-wave workgroup per (head, span)
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, true>), dim3(a.heads, spans), dim3(64), 0, s, a);
@@ -174,10 +182,8 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
     const dim3 grid(a.heads, a.rows);
     if (spans <= 1)
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, false>), grid, dim3(64), 0, s, a);
-    else if (spans <= 4)
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false>), grid, dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 16, false>), grid, dim3(1024), 0, s, a);
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

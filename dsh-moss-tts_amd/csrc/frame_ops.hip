@@ -487,12 +487,19 @@ __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, i
 #pragma clang fp contract(off)
     __shared__ float red[4];
     const int r = blockIdx.x, t = threadIdx.x;
-    float v[3];
+    // all partials are loaded before the in-order sum (slices past ksplit re-read the last one, unused)
+    float p[3][16], v[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int z = 0; z < 16; ++z) p[i][z] = part[((size_t)min(z, ksplit - 1) * rows + r) * kHidden + t + 256 * i];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int n = t + 256 * i;
-        float acc = part[(size_t)r * kHidden + n];
-        for (int z = 1; z < ksplit; ++z) acc += part[((size_t)z * rows + r) * kHidden + n];
+        float acc = p[i][0];
+#pragma unroll
+        for (int z = 1; z < 16; ++z)
+            if (z < ksplit) acc += p[i][z];
         v[i] = resid[(size_t)r * resid_stride + n] + (acc + bias[n]);
     }
     __syncthreads();  // every read of x (through resid) happens before any write of it
@@ -698,7 +705,8 @@ hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const f
                                 const unsigned char *mask, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    if (!part || ksplit <= 0 || !bias || !resid || !x || (ln_w && (!ln_b || !out))) return hipErrorInvalidValue;
+    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x || (ln_w && (!ln_b || !out)))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(resid_ln_rows_kernel, dim3(rows), dim3(256), 0, s, part, ksplit, rows, bias, resid,
                        resid_stride, x, ln_w, ln_b, out, mask);
     return hipGetLastError();
