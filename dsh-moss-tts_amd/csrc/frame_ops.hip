@@ -349,13 +349,12 @@ __global__ __launch_bounds__(256) void sample_kernel(SampleArgs a) {
     const SampleCfg c = st->cfg;
     const bool greedy = c.greedy || st->frame < c.greedy_frames;
     const int idx = greedy ? pick_greedy(L) : pick_sampled(L, c, st->rng);
+    if (a.count_all && t < a.ch) a.counts[t * kCodebook + st->row[t + 1]] += 1;  // one channel per thread
     if (t == 0) {
         const int used = st->forced_on ? a.forced[st->frame * kNVq + a.ch] : idx;
         st->codes[a.ch] = idx;
         st->row[a.ch + 1] = used;
         a.counts[a.ch * kCodebook + used] += 1;
-        if (a.count_all)
-            for (int c = 0; c < a.ch; ++c) a.counts[c * kCodebook + st->row[c + 1]] += 1;
         L.used = used;
         if (a.last_channel) {
             st->row[0] = kSlotToken;
