@@ -166,6 +166,12 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         ((__half *)a.out)[oi] = __float2half_rn(res);
     else
         ((float *)a.out)[oi] = res;
+    if (a.q8 != nullptr) {  // W8A8 copy for the proj GEMM: this head's 64 outputs are two blocks
+        float d;
+        const int q = quant_block32(res, &d);
+        a.q8[(size_t)r * kHidden + h * kHeadDim + lane] = (int8_t)q;
+        if ((lane & 31) == 0) a.d8[(size_t)r * (kHidden / 32) + 2 * h + (lane >> 5)] = d;
+    }
 }
 
 template <int KV>
@@ -195,6 +201,7 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
         !a.k_pool || !a.v_pool)
         return hipErrorInvalidValue;
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
+    if (a.q8 != nullptr && (!a.d8 || a.part != nullptr || a.heads != kHeads)) return hipErrorInvalidValue;
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
 }
 

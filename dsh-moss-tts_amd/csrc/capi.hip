@@ -51,7 +51,7 @@ mh::Batch &batch_of(moss_hip_batch *b) {
 }
 
 moss_hip_llm_options defaults(const moss_hip_llm_options *opt) {
-    moss_hip_llm_options o{0, 0, 0, 1};
+    moss_hip_llm_options o{0, 0, 0, 1, 0};
     if (opt) o = *opt;
     return o;
 }
@@ -262,6 +262,34 @@ int moss_hip_gemm_q8x4(const void *w, int rows, int cols, const float *x, int m,
     });
 }
 
+
+int moss_hip_quantize_rows(const float *x, int m, int cols, int8_t *q, float *d, void *stream) {
+    return guard([&] {
+        if (!x || !q || !d) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (m <= 0 || cols <= 0 || cols % 256) throw Status(MOSS_HIP_EINVAL, "shape must satisfy m > 0, cols % 256 == 0");
+        mh::hip_check(mh::launch_quant_rows(x, cols, cols, m, q, d, static_cast<hipStream_t>(stream)), "quantize launch");
+    });
+}
+
+int moss_hip_gemm_q8x4_w8a8(const void *w, int rows, int cols, const int8_t *q, const float *d, int m, float *y,
+                            void *stream) {
+    return guard([&] {
+        if (!w || !q || !d || !y) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (rows <= 0 || rows % 16 || cols <= 0 || cols % 32 || m <= 0)
+            throw Status(MOSS_HIP_EINVAL, "shape must satisfy rows % 16 == 0, cols % 32 == 0, m > 0");
+        mh::GemmArgs g;
+        g.w = static_cast<const uint8_t *>(w);
+        g.N = rows;
+        g.K = cols;
+        g.a8 = q;
+        g.d8 = d;
+        g.lda = cols;
+        g.M = m;
+        g.y = y;
+        g.ldy = rows;
+        mh::hip_check(mh::launch_gemm(g, mh::EPI_F32, mh::KV_F16, static_cast<hipStream_t>(stream)), "gemm launch");
+    });
+}
 
 int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_dtype, void *y, int y_dtype,
                        void *stream) {

@@ -464,8 +464,21 @@ hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType k
 namespace mh {
 namespace {
 
+// Row r's 768 values o (thread t holds t, t+256, t+512) to int8 blocks of 32.
+__device__ __forceinline__ void quant_row_768(const float (&o)[3], int r, int8_t *q8, float *d8) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int c = t + 256 * i;
+        float d;
+        const int q = quant_block32(o[i], &d);
+        q8[(size_t)r * kHidden + c] = (int8_t)q;
+        if ((c & 31) == 0) d8[(size_t)r * (kHidden / 32) + (c >> 5)] = d;
+    }
+}
+
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stride, const float *w, const float *b,
-                                                      float *out, const unsigned char *mask) {
+                                                      float *out, const unsigned char *mask, int8_t *q8, float *d8) {
     __shared__ float red[4];
     const int r = blockIdx.x, t = threadIdx.x;
     if (mask != nullptr && !mask[r]) return;
@@ -476,13 +489,26 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stri
     layernorm_768(v, w, b, o, red);
 #pragma unroll
     for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+    if (q8 != nullptr) quant_row_768(o, r, q8, d8);
+}
+
+// One row per workgroup, one 32-block per half-wave at a time.
+__global__ __launch_bounds__(256) void quant_rows_kernel(const float *x, int x_stride, int K, int8_t *q8, float *d8) {
+    const int r = blockIdx.x;
+    for (int c = threadIdx.x; c < K; c += 256) {
+        float d;
+        const int q = quant_block32(x[(size_t)r * x_stride + c], &d);
+        q8[(size_t)r * K + c] = (int8_t)q;
+        if ((c & 31) == 0) d8[(size_t)r * (K / 32) + (c >> 5)] = d;
+    }
 }
 
 // Split-K reduce + residual + LayerNorm of one row per workgroup (launch_resid_ln_rows).
 __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, int ksplit, int rows,
                                                             const float *bias, const float *resid, int resid_stride,
                                                             float *x, const float *ln_w, const float *ln_b,
-                                                            float *out, const unsigned char *mask) {
+                                                            float *out, const unsigned char *mask, int8_t *q8,
+                                                            float *d8) {
 #pragma clang fp contract(off)
     __shared__ float red[4];
     const int r = blockIdx.x, t = threadIdx.x;
@@ -509,6 +535,7 @@ __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, i
     layernorm_768(v, ln_w, ln_b, o, red);
 #pragma unroll
     for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+    if (q8 != nullptr) quant_row_768(o, r, q8, d8);
 }
 
 // grid (12, rows): same per-element serial sum as embed_kernel
@@ -692,22 +719,33 @@ hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int pa
 }
 
 hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const float *b, float *out, int rows,
-                          hipStream_t s, const unsigned char *mask) {
+                          hipStream_t s, const unsigned char *mask, int8_t *q8, float *d8) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask);
+    if (q8 && !d8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask, q8, d8);
     return hipGetLastError();
 }
 
 hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
                                 int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
-                                const unsigned char *mask, hipStream_t s) {
+                                const unsigned char *mask, hipStream_t s, int8_t *q8, float *d8) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x || (ln_w && (!ln_b || !out)))
+    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x || (ln_w && (!ln_b || !out)) ||
+        (q8 && (!d8 || !ln_w)))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(resid_ln_rows_kernel, dim3(rows), dim3(256), 0, s, part, ksplit, rows, bias, resid,
-                       resid_stride, x, ln_w, ln_b, out, mask);
+                       resid_stride, x, ln_w, ln_b, out, mask, q8, d8);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(const float *x, int x_stride, int K, int rows, int8_t *q8, float *d8, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (rows <= 0) return hipSuccess;
+    // every lane of a wave takes part in each block's shuffles: K a multiple of 256
+    if (!x || !q8 || !d8 || K <= 0 || K % 256 != 0 || x_stride < K) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(quant_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, K, q8, d8);
     return hipGetLastError();
 }
 

@@ -89,26 +89,35 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs &g, int m, int n, flo
 }
 
 
-// One chunk of KB scale blocks: this lane's 8 activations per block and its 8
-// weights + scale per block and column subtile.  Block indices are clamped so
-// every load is unconditional (blocks past nb are loaded but not used).
-template <int NT>
+// One chunk of KB scale blocks: this lane's 8 activations per block (fp32, or
+// int8 + the block scale of the lane's row under W8A8) and its 8 weights +
+// scale per block and column subtile.  Block indices are clamped so every load
+// is unconditional (blocks past nb are loaded but not used).
+template <int NT, bool A8>
 struct Chunk {
-    float xa[KB][8];
+    float xa[A8 ? 1 : KB][8];
+    uint64_t xq[A8 ? KB : 1];
+    float xd[A8 ? KB : 1];
     uint2 qb[KB][NT];
     uint32_t db[KB][NT];
 };
 
-template <int NT>
-__device__ __forceinline__ void load_chunk(Chunk<NT> &c, int b0, int nb, const float *arow_p,
+template <int NT, bool A8>
+__device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, int nb, const float *arow_p,
+                                           const int8_t *arow_q, const float *arow_d,
                                            const uint8_t *const (&wcol)[NT], int krow, int kq) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
         const int b = min(b0 + j, nb - 1);
-        const float4 x0 = *(const float4 *)(arow_p + 32 * b);
-        const float4 x1 = *(const float4 *)(arow_p + 32 * b + 4);
-        c.xa[j][0] = x0.x; c.xa[j][1] = x0.y; c.xa[j][2] = x0.z; c.xa[j][3] = x0.w;
-        c.xa[j][4] = x1.x; c.xa[j][5] = x1.y; c.xa[j][6] = x1.z; c.xa[j][7] = x1.w;
+        if constexpr (A8) {
+            c.xq[j] = *(const uint64_t *)(arow_q + 32 * b);
+            c.xd[j] = arow_d[b];
+        } else {
+            const float4 x0 = *(const float4 *)(arow_p + 32 * b);
+            const float4 x1 = *(const float4 *)(arow_p + 32 * b + 4);
+            c.xa[j][0] = x0.x; c.xa[j][1] = x0.y; c.xa[j][2] = x0.z; c.xa[j][3] = x0.w;
+            c.xa[j][4] = x1.x; c.xa[j][5] = x1.y; c.xa[j][6] = x1.z; c.xa[j][7] = x1.w;
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint8_t *blk = wcol[t] + (size_t)b * kBlockBytes;
@@ -119,27 +128,50 @@ __device__ __forceinline__ void load_chunk(Chunk<NT> &c, int b0, int nb, const f
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void mfma_chunk(const Chunk<NT> &c, int b0, int nb, floatx4 (&acc)[NT]) {
+typedef int intx4 __attribute__((ext_vector_type(4)));
+
+template <int NT, bool A8>
+__device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int nb, int kq, floatx4 (&acc)[NT]) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
-        half8 hi, lo;
-        split_hi_lo(c.xa[j], hi, lo);
         const bool live = b0 + j < nb;  // uniform; a dead block adds with a zero scale
+        if constexpr (A8) {
+            // W8A8 (gemv_avx2.cpp:105-121): the exact int32 block dot, times
+            // scale = d_w * d_a (fp32), accumulated with an FMA.  D row 4kq + i
+            // takes d_a from the lane that loaded that A row.
+            float da[4];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const half8 bw = i8x8_to_h8(c.qb[j][t]);
-            floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
-            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, bw, blk, 0, 0, 0);
-            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, bw, blk, 0, 0, 0);
-            const float d = live ? h2f((uint16_t)c.db[j][t]) : 0.0f;
+            for (int i = 0; i < 4; ++i) da[i] = __shfl(c.xd[j], 4 * kq + i);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(blk[i], d, acc[t][i]);
+            for (int t = 0; t < NT; ++t) {
+                const long bq = (long)(((uint64_t)c.qb[j][t].y << 32) | c.qb[j][t].x);
+                const intx4 p = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)c.xq[j], bq, intx4{0, 0, 0, 0}, 0, 0, 0);
+                const float dw = live ? h2f((uint16_t)c.db[j][t]) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float scale = dw * da[i];
+                    acc[t][i] = fmaf((float)p[i], scale, acc[t][i]);
+                }
+            }
+        } else {
+            half8 hi, lo;
+            split_hi_lo(c.xa[j], hi, lo);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const half8 bw = i8x8_to_h8(c.qb[j][t]);
+                floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+                blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, bw, blk, 0, 0, 0);
+                blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, bw, blk, 0, 0, 0);
+                const float d = live ? h2f((uint16_t)c.db[j][t]) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(blk[i], d, acc[t][i]);
+            }
         }
     }
 }
 
-template <int EPI, int KV, int NT>
+template <int EPI, int KV, int NT, bool A8>
 __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
@@ -152,7 +184,9 @@ __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
     const int nb = min(nb_all - kb0, per);
     // A row of this lane (clamped: rows past M read row M-1 and are never stored)
     const int arow = min(m_base + l16, g.M - 1);
-    const float *arow_p = g.a + (size_t)arow * g.lda + 8 * kq + 32 * kb0;
+    const float *arow_p = A8 ? nullptr : g.a + (size_t)arow * g.lda + 8 * kq + 32 * kb0;
+    const int8_t *arow_q = A8 ? g.a8 + (size_t)arow * g.lda + 8 * kq + 32 * kb0 : nullptr;
+    const float *arow_d = A8 ? g.d8 + (size_t)arow * (g.lda / 32) + kb0 : nullptr;
     // B column (weight row) of this lane for each of the NT subtiles
     const uint8_t *wcol[NT];
 #pragma unroll
@@ -169,14 +203,14 @@ __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
     // two chunks in flight: chunk c+1 is issued before chunk c is multiplied;
     // the chunks alternate between two register sets (a copy would wait for
     // the loads it moves)
-    Chunk<NT> ca, cb;
-    load_chunk<NT>(ca, 0, nb, arow_p, wcol, krow, kq);
+    Chunk<NT, A8> ca, cb;
+    load_chunk<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
     for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
-        load_chunk<NT>(cb, b0 + KB, nb, arow_p, wcol, krow, kq);
-        mfma_chunk<NT>(ca, b0, nb, acc);
+        load_chunk<NT, A8>(cb, b0 + KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+        mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
         if (b0 + KB >= nb) break;
-        load_chunk<NT>(ca, b0 + 2 * KB, nb, arow_p, wcol, krow, kq);
-        mfma_chunk<NT>(cb, b0 + KB, nb, acc);
+        load_chunk<NT, A8>(ca, b0 + 2 * KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+        mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
     }
 
     // epilogue: lane holds rows m_base + 4kq + i, column n_base + 16t + l16
@@ -193,7 +227,7 @@ __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
     }
 }
 
-template <int EPI, int KV>
+template <int EPI, int KV, bool A8>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     // 4 column subtiles (64 columns) per workgroup unless that leaves too few workgroups
@@ -201,11 +235,16 @@ hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     const int kz = EPI == EPI_PART ? (g.ksplit > 0 ? g.ksplit : gemm_ksplit(g.M, g.N, g.K)) : 1;
     const bool wide = (g.N / 64) * mt * kz >= 96;
     if (wide && g.N % 64 == 0) {
-        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 4>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 4, A8>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
     } else {
-        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 1>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 1, A8>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
     }
     return hipGetLastError();
+}
+
+template <int EPI, int KV>
+hipError_t launch_a(const GemmArgs &g, hipStream_t s) {
+    return g.a8 != nullptr ? launch_nt<EPI, KV, true>(g, s) : launch_nt<EPI, KV, false>(g, s);
 }
 }  // namespace
 
@@ -230,12 +269,13 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
         const int nb = g.K / 32, z = g.ksplit;
         if (!g.part || z > 16 || z > nb || (z > 0 && (z - 1) * ((nb + z - 1) / z) >= nb)) return hipErrorInvalidValue;
     }
+    if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
     switch (epi) {
-        case EPI_PART: return launch_nt<EPI_PART, KV_F16>(g, s);
-        case EPI_F32: return launch_nt<EPI_F32, KV_F16>(g, s);
-        case EPI_RESID: return launch_nt<EPI_RESID, KV_F16>(g, s);
-        case EPI_GELU: return launch_nt<EPI_GELU, KV_F16>(g, s);
-        case EPI_QKV: return kv == KV_F32 ? launch_nt<EPI_QKV, KV_F32>(g, s) : launch_nt<EPI_QKV, KV_F16>(g, s);
+        case EPI_PART: return launch_a<EPI_PART, KV_F16>(g, s);
+        case EPI_F32: return launch_a<EPI_F32, KV_F16>(g, s);
+        case EPI_RESID: return launch_a<EPI_RESID, KV_F16>(g, s);
+        case EPI_GELU: return launch_a<EPI_GELU, KV_F16>(g, s);
+        case EPI_QKV: return kv == KV_F32 ? launch_a<EPI_QKV, KV_F32>(g, s) : launch_a<EPI_QKV, KV_F16>(g, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -97,6 +97,7 @@ private:
     void *kv_layer(int which, int layer) const;  // which: 0 = K, 1 = V
 
     int device_ = 0, max_ctx_ = kMaxCtx, use_graphs_ = 1;
+    bool prefill_a16_ = false;  // prefill GEMMs on fp32 activations (else W8A8)
     KvType kvt_ = KV_F16;
     size_t kv_esize_ = 2;
     hipStream_t stream_ = nullptr;
@@ -125,6 +126,8 @@ private:
     int rows_cap_ = 0;
     float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_o_ = nullptr, *pre_h_ = nullptr;  // prefill rows
     float *pre_part_ = nullptr;          // split-K partials of the prefill proj / fc_out GEMMs
+    int8_t *pre_q8_ = nullptr;           // W8A8 prefill: the current GEMM's int8 activations [m][<=3072]
+    float *pre_d8_ = nullptr;            //   and their block scales [m][<=96]
     DevState *state_ = nullptr;          // device
     DevState *hstate_ = nullptr;         // pinned host mirror
     void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]

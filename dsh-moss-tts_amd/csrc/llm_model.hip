@@ -64,6 +64,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     kvt_ = opt.kv_dtype == 1 ? KV_F32 : KV_F16;
     kv_esize_ = kvt_ == KV_F32 ? 4 : 2;
     use_graphs_ = opt.use_graphs;
+    prefill_a16_ = opt.prefill_a16 != 0;
     const uint8_t *b = static_cast<const uint8_t *>(blob);
     auto idx = parse_index(b, bytes);
 
@@ -198,7 +199,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, pre_q8_, pre_d8_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -423,18 +424,21 @@ void Model::global_step(const int32_t *row) {
 // K/V of positions [start, start+m) written in its epilogue) -> causal
 // attention of row i over keys <= start+i -> proj GEMM + residual -> LN2 ->
 // fc_in GEMM + gelu -> fc_out GEMM + residual; hidden = ln_f of the last row.
-// The GEMMs run on the matrix cores in W8A16 (the reference with MOSS_A16=1).
+// The GEMMs run on the matrix cores: W8A8 by default (int8 activations per
+// 32-block, i8 MFMA, fp32 block-scale FMA -- the reference's prefill), or
+// W8A16 on fp32 activations (the reference with MOSS_A16=1) when prefill_a16.
 void Model::prefill(const int32_t *rows, int n, int start) {
     start = start < 0 ? 0 : (start > max_ctx_ ? max_ctx_ : start);
     const int m = n < max_ctx_ - start ? n : max_ctx_ - start;
     if (m <= 0) return;
     check_rows(rows, m);
     if (m > rows_cap_) {
-        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_};
+        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_};
         for (void *p : bufs)
             if (p) hip_check(hipFree(p), "free prefill buffers");
         rows_dev_ = nullptr;
-        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = pre_part_ = nullptr;
+        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = pre_part_ = pre_d8_ = nullptr;
+        pre_q8_ = nullptr;
         rows_cap_ = 0;
         hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
         hip_check(hipMalloc(&pre_x_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
@@ -444,6 +448,8 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * (size_t)m), "hipMalloc(prefill)");
         const int kz = std::max(gemm_ksplit(m, kHidden, kHidden), gemm_ksplit(m, kHidden, kFF));
         hip_check(hipMalloc(&pre_part_, sizeof(float) * kHidden * (size_t)m * kz), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_q8_, (size_t)kFF * m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_d8_, sizeof(float) * (kFF / 32) * (size_t)m), "hipMalloc(prefill)");
         rows_cap_ = m;
     }
     hip_check(hipMemcpyAsync(rows_dev_, rows, sizeof(int) * 17 * (size_t)m, hipMemcpyHostToDevice, stream_), "rows h2d");
@@ -455,7 +461,18 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     e.wte = wte_;
     for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = aemb_[ch];
     hip_check(launch_embed_rows(e, rows_dev_, m, pre_x_, s), "prefill embed");
-    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, pre_a_, m, s), "prefill ln1");
+    // W8A8 (the reference's prefill, llm.cpp:319-328): every GEMM input is also
+    // quantised per 32-block by the kernel that produces it
+    const bool a8 = !prefill_a16_;
+    int8_t *q8 = a8 ? pre_q8_ : nullptr;
+    float *d8 = a8 ? pre_d8_ : nullptr;
+    auto operand = [&](GemmArgs &g) {
+        if (a8) {
+            g.a8 = pre_q8_;
+            g.d8 = pre_d8_;
+        }
+    };
+    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, pre_a_, m, s, nullptr, q8, d8), "prefill ln1");
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
@@ -464,30 +481,36 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         q.bias = L.attn_b; q.q_out = pre_q_;
         q.k_pool = kv_layer(0, l); q.v_pool = kv_layer(1, l); q.page_size = max_ctx_;
         q.pos0 = start; q.rope_cos = rc; q.rope_sin = rs;
+        operand(q);
         hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "prefill qkv");
         AttnArgs t;
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
         t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = pre_o_;
+        t.q8 = q8; t.d8 = d8;
         hip_check(launch_attn(t, kvt_, s), "prefill attention");
         GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
         p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
         p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);
+        operand(p);
         hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
         hip_check(launch_resid_ln_rows(pre_part_, p.ksplit, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
-                                       pre_a_, nullptr, s),
+                                       pre_a_, nullptr, s, q8, d8),
                   "prefill proj reduce + ln2");
         GemmArgs f1;
         f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
         f1.y = pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+        operand(f1);
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
+        if (a8) hip_check(launch_quant_rows(pre_h_, kFF, kFF, m, pre_q8_, pre_d8_, s), "prefill quant h");
         GemmArgs f2;
         f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
         f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
+        operand(f2);
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
         const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce
         hip_check(launch_resid_ln_rows(pre_part_, f2.ksplit, m, L.fc_out_b, pre_x_, kHidden, pre_x_,
                                        last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, pre_a_,
-                                       nullptr, s),
+                                       nullptr, s, last ? nullptr : q8, last ? nullptr : d8),
                   "prefill fc_out reduce");
     }
     hip_check(launch_layernorm(pre_x_ + (size_t)(m - 1) * kHidden, lnf_w_, lnf_b_, hidden_, nullptr, 0, s), "ln_f");

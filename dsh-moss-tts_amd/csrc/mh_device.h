@@ -141,6 +141,24 @@ __device__ __forceinline__ void layernorm_768(const float (&x)[3], const float *
     }
 }
 
+// Activation quantisation of one 32-value block held by 32 consecutive lanes
+// (quantize_row_q8_0_scaled, reference csrc/src/quant.cpp:28-54): amax over the
+// block, d = amax / 127, id = 1 / d (0 when d == 0), q = clamp(rint(x * id),
+// +-127).  The max is order-independent, so this equals the serial scan.
+// Returns q; *d_out receives d in every lane of the block.
+__device__ __forceinline__ int quant_block32(float x, float *d_out) {
+#pragma clang fp contract(off)
+    float amax = fabsf(x);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float d = amax / 127.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    int q = (int)rintf(x * id);
+    q = q < -127 ? -127 : (q > 127 ? 127 : q);
+    *d_out = d;
+    return q;
+}
+
 // gelu_new (reference csrc/src/llm.cpp:22-25)
 __device__ __forceinline__ float gelu_new(float v) {
 #pragma clang fp contract(off)

@@ -93,6 +93,9 @@ struct AttnArgs {
     // keys [64 s, 64 s + 64) to part[(h * splits + s) * kPartStride]: o[64], running max m,
     // sum l; splits = ceil(max_keys / 64).  A consumer merges them (PRO_AMERGE).
     float *part = nullptr;
+    // optional W8A8 copy of the (normalised) output rows: q8[r][768] int8, d8[r][24] block scales
+    int8_t *q8 = nullptr;
+    float *d8 = nullptr;
     const DevState *state = nullptr;
 };
 constexpr int kPartStride = 68;
@@ -124,6 +127,10 @@ struct GemmArgs {
     // part + z * M * N (row-major [M][N]).  ksplit <= 0 picks a split from the shape.
     float *part = nullptr;
     int ksplit = 0;
+    // W8A8 (reference gemv_avx2.cpp:105-121 per block): when a8 is non-null the activations are
+    // int8 a8[M][lda] with fp32 block scales d8[M][lda / 32], and `a` is unused
+    const int8_t *a8 = nullptr;
+    const float *d8 = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
 // The K split launch_gemm uses for an EPI_PART GEMM of this shape (1..16).
@@ -135,7 +142,11 @@ int gemm_ksplit(int M, int N, int K);
 //   their out row.  resid may alias x (in-place residual stream).  N == 768.
 hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
                                 int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
-                                const unsigned char *mask, hipStream_t s);
+                                const unsigned char *mask, hipStream_t s, int8_t *q8 = nullptr, float *d8 = nullptr);
+
+// W8A8 activation quantisation of rows (quant.cpp:28-54): q8[r][K] int8 and d8[r][K/32]
+// fp32 block scales from x[r * x_stride + k].  K % 256 == 0.
+hipError_t launch_quant_rows(const float *x, int x_stride, int K, int rows, int8_t *q8, float *d8, hipStream_t s);
 
 // ---- frame / step kernels (frame_ops.hip)
 struct EmbedArgs {
@@ -198,7 +209,8 @@ inline void rng_seed_host(uint64_t v, uint32_t s[4]) {
 // out[r] = LayerNorm(x[r * x_stride]) for r < rows (x_stride 0 broadcasts one row);
 // rows with mask[r] == 0 are left untouched when mask is non-null.
 hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const float *b, float *out, int rows,
-                          hipStream_t s, const unsigned char *mask = nullptr);
+                          hipStream_t s, const unsigned char *mask = nullptr, int8_t *q8 = nullptr,
+                          float *d8 = nullptr);
 // x[r] = embedding of rows[r][17] (llm.cpp:148-157)
 hipError_t launch_embed_rows(const EmbedArgs &e, const int *rows, int n, float *x, hipStream_t s);
 

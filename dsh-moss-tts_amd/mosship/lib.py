@@ -26,6 +26,7 @@ EXPORTED = [
     "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
+    "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8",
 ]
 
 
@@ -36,7 +37,8 @@ class MossHipError(RuntimeError):
 
 
 class Options(C.Structure):
-    _fields_ = [("device", C.c_int), ("max_ctx", C.c_int), ("kv_dtype", C.c_int), ("use_graphs", C.c_int)]
+    _fields_ = [("device", C.c_int), ("max_ctx", C.c_int), ("kv_dtype", C.c_int), ("use_graphs", C.c_int),
+                ("prefill_a16", C.c_int)]
 
 
 class SampleParams(C.Structure):
@@ -87,6 +89,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_llm_kv_import.argtypes = [vp, i32, vp, vp, vp]
     L.moss_hip_gemv_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp]
     L.moss_hip_gemm_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
+    L.moss_hip_quantize_rows.argtypes = [vp, i32, i32, vp, vp, vp]
+    L.moss_hip_gemm_q8x4_w8a8.argtypes = [vp, i32, i32, vp, vp, i32, vp, vp]
     L.moss_hip_batch_create.argtypes = [vp, i32, i32, i32, C.POINTER(vp)]
     L.moss_hip_batch_destroy.argtypes = [vp]
     L.moss_hip_batch_destroy.restype = None
@@ -134,6 +138,18 @@ def gemm_q8x4(w, rows: int, cols: int, x, m: int, y, stream=None) -> None:
                                     C.c_void_p(y.data_ptr()), _stream(stream)))
 
 
+def quantize_rows(x, m: int, cols: int, q, d, stream=None) -> None:
+    """W8A8 activation quantisation: q[m][cols] int8, d[m][cols/32] fp32 (device tensors)."""
+    check(load().moss_hip_quantize_rows(C.c_void_p(x.data_ptr()), m, cols, C.c_void_p(q.data_ptr()),
+                                        C.c_void_p(d.data_ptr()), _stream(stream)))
+
+
+def gemm_q8x4_w8a8(w, rows: int, cols: int, q, d, m: int, y, stream=None) -> None:
+    """Y[m][rows] from int8 activations q and block scales d on the int8 matrix cores."""
+    check(load().moss_hip_gemm_q8x4_w8a8(C.c_void_p(w.data_ptr()), rows, cols, C.c_void_p(q.data_ptr()),
+                                         C.c_void_p(d.data_ptr()), m, C.c_void_p(y.data_ptr()), _stream(stream)))
+
+
 def dequant_rows_q8x4(w, mat_rows: int, cols: int, rows_idx, out, stream=None) -> None:
     check(load().moss_hip_dequant_rows_q8x4(C.c_void_p(w.data_ptr()), mat_rows, cols, C.c_void_p(rows_idx.data_ptr()),
                                             rows_idx.numel(), C.c_void_p(out.data_ptr()), _stream(stream)))
@@ -152,11 +168,12 @@ def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, o
 class HipLLM:
     """Python view of the GPU LlmModel (moss_hip_llm_*)."""
 
-    def __init__(self, blob: bytes, device: int = 0, max_ctx: int = 0, kv_fp32: bool = False, graphs: bool = True):
+    def __init__(self, blob: bytes, device: int = 0, max_ctx: int = 0, kv_fp32: bool = False, graphs: bool = True,
+                 prefill_a16: bool = False):
         L = self.L = load()
         self._h = C.c_void_p()
         buf = np.frombuffer(blob, dtype=np.uint8)
-        opt = Options(device, max_ctx, 1 if kv_fp32 else 0, 1 if graphs else 0)
+        opt = Options(device, max_ctx, 1 if kv_fp32 else 0, 1 if graphs else 0, 1 if prefill_a16 else 0)
         check(L.moss_hip_llm_create(_ptr(buf), buf.size, C.byref(opt), C.byref(self._h)))
 
     def close(self):

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 1
+#define MOSS_HIP_ABI_VERSION 2
 
 enum {
     MOSS_HIP_OK = 0,
@@ -56,6 +56,8 @@ typedef struct {
     int max_ctx;    /* KV capacity in positions; 0 = 768 (kMaxCtx, csrc/include/moss/llm.h:28) */
     int kv_dtype;   /* 0 = fp16 KV cache (default), 1 = fp32 KV cache (the reference's own precision) */
     int use_graphs; /* 1 = replay the global step and the frame as hipGraphs (default), 0 = direct launches */
+    int prefill_a16; /* prefill activations: 0 = W8A8, int8 per 32-block (the reference's prefill unless
+                        MOSS_A16 is 1/all, csrc/src/gemv.cpp:23-48, llm.cpp:319-328); 1 = W8A16 fp32 */
 } moss_hip_llm_options;
 
 /* SampleParams (csrc/include/moss/sampler.h:8-22), field for field. */
@@ -166,6 +168,16 @@ int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_d
 /* Y[m][rows] = X[m][cols] W^T on the matrix cores -- gemm_par (csrc/include/moss/gemv.h:54,
  * csrc/src/gemv.cpp:276-309) in its A16 mode.  x, y fp32; rows % 16 == 0, cols % 32 == 0. */
 int moss_hip_gemm_q8x4(const void *w, int rows, int cols, const float *x, int m, float *y, void *stream);
+
+/* W8A8 activation quantisation -- quantize_row_q8_0_scaled (csrc/src/quant.cpp:28-54) per row:
+ * q[m][cols] int8 and d[m][cols/32] fp32 block scales of x[m][cols].  cols % 256 == 0. */
+int moss_hip_quantize_rows(const float *x, int m, int cols, int8_t *q, float *d, void *stream);
+
+/* W8A8 GEMM -- gemm_par without MOSS_A16 (csrc/src/gemv.cpp:281-309; row kernel
+ * row_dot_q8_4x4, csrc/src/gemv_avx2.cpp:105-121): Y[m][rows] from int8 activations q[m][cols]
+ * with block scales d[m][cols/32] (as moss_hip_quantize_rows writes them).  rows % 16 == 0. */
+int moss_hip_gemm_q8x4_w8a8(const void *w, int rows, int cols, const int8_t *q, const float *d, int m, float *y,
+                            void *stream);
 
 /* Dequantise rows of a mat_rows x cols Q8_0_4X4 matrix to fp32 -- LlmModel::lookup_row
  * (llm.cpp:114-146) / dequantize_row_q8_0_4x4 (csrc/src/quant.cpp:56-65).  rows_dev: n device

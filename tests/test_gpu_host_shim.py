@@ -1,5 +1,7 @@
 """The C++ drop-in moss::LlmModel (dsh-moss-tts_amd/host) driven through a
-moss_llm-style CLI, vs the oracle and the compiled reference (GPU).
+moss_llm-style CLI, vs the oracle and the compiled reference (GPU).  The drop-in
+runs with its defaults (fp16 KV, W8A8 prefill as the reference's), so the oracle
+emulates the fp16 KV rounding.
 
 Covers the boundary a reference maintainer would link: load, prefill,
 generate with timing / on_frame / teacher forcing, and the .mosskv prefix and
@@ -20,9 +22,15 @@ pytestmark = pytest.mark.gpu
 BIN = os.path.join(ROOT, "tests", "host", "moss_llm_hip")
 
 
-def _run(*args):
+# The file/flow tests compare decoded codes with the oracle, so the drop-in runs
+# its prefill in the reference's MOSS_A16=1 mode (W8A16, smooth in its inputs);
+# the default W8A8 prefill is checked on its own below.
+A16_ENV = dict(os.environ, MOSS_A16="1")
+
+
+def _run(*args, env=A16_ENV):
     print("moss_llm_hip", *args, flush=True)
-    out = subprocess.run([BIN, *map(str, args)], capture_output=True, text=True, timeout=120)
+    out = subprocess.run([BIN, *map(str, args)], capture_output=True, text=True, timeout=120, env=env)
     assert out.returncode == 0, out.stderr
     return json.loads(out.stdout)
 
@@ -46,7 +54,7 @@ def test_shim_prefill_generate_state(torch_gpu, oracle, files):
     state = str(d / "s.state")
     res = _run("--weights", w, "--prompt", prompt, "--frames", 4, "--min-frames", 4, "--greedy", "--rep", 1.2,
                "--save-state", state)
-    m = oracle.model(blob)
+    m = oracle.model(blob, kv_f16=True)
     m.prefill(rows, a16=True)
     _, n_pos, rows_fp, weights_fp, k, v, hidden = mf.read_state(open(state, "rb").read())
     assert n_pos == len(rows) and rows_fp == mf.fp_rows(rows) and weights_fp == mf.fp_weights(blob)
@@ -78,7 +86,7 @@ def test_shim_prefix_flow(torch_gpu, oracle, files):
     a = _run(*common, "--save-prefix", prefix)
     b = _run(*common, "--load-prefix", prefix)
     assert a["codes"] == b["codes"] and a["hidden0"] == b["hidden0"] and a["position"] == b["position"]
-    m = oracle.model(blob)
+    m = oracle.model(blob, kv_f16=True)
     m.prefill(rows[:K], a16=True)
     m.prefill(rows[K:], start=K, a16=True)
     ref = m.generate(3, OSP.make(greedy=True, min_frames=3))
@@ -97,7 +105,7 @@ def test_shim_prefix_flow(torch_gpu, oracle, files):
 
 def test_shim_teacher_forcing(torch_gpu, oracle, files):
     blob, rows, w, prompt, d = files
-    m = oracle.model(blob)
+    m = oracle.model(blob, kv_f16=True)
     m.prefill(rows, a16=True)
     ref = m.generate(3, OSP.make(greedy=True, min_frames=3))
     forced = d / "forced.txt"
@@ -106,7 +114,7 @@ def test_shim_teacher_forcing(torch_gpu, oracle, files):
                "--force-codes", str(forced))
     assert res["codes"] == ref["rows"][:, 1:].tolist() and res["frames"] == 3
     # forcing its own greedy codes leaves the oracle where free running left it
-    mf_ = oracle.model(blob)
+    mf_ = oracle.model(blob, kv_f16=True)
     mf_.prefill(rows, a16=True)
     mf_.generate(3, OSP.make(greedy=True, min_frames=3), forced=ref["rows"])
     h = mf_.hidden()
@@ -121,7 +129,7 @@ def test_shim_sampling_and_gate_dump(torch_gpu, oracle, files):
     gate = str(d / "gate.csv")
     res = _run("--weights", w, "--prompt", prompt, "--frames", 8, "--min-frames", 2, "--sample", "--seed", 42,
                "--end-mode", "sample", "--dump-gate", gate)
-    m = oracle.model(blob)
+    m = oracle.model(blob, kv_f16=True)
     m.prefill(rows, a16=True)
     ref = m.generate(8, OSP.make(greedy=False, temperature=0.8, top_k=25, top_p=0.95, repetition_penalty=1.2,
                                  end_greedy=False, min_frames=2), seed=42, gate=True)
@@ -156,14 +164,29 @@ def test_reference_cli_on_the_drop_in(torch_gpu, oracle, files, mode):
         p = OSP.make(greedy=False, temperature=0.8, top_k=25, top_p=0.95, repetition_penalty=1.2, end_greedy=False,
                      min_frames=3)
     print("moss_llm_gpu", *args, flush=True)
-    out = subprocess.run([REF_CLI, *map(str, args)], capture_output=True, text=True, timeout=120)
+    out = subprocess.run([REF_CLI, *map(str, args)], capture_output=True, text=True, timeout=120, env=A16_ENV)
     assert out.returncode == 0, out.stderr
     res = json.loads(out.stdout)
-    m = oracle.model(blob)
+    m = oracle.model(blob, kv_f16=True)
     m.prefill(rows, a16=True)
     ref = m.generate(6, p, seed=9 if mode == "sample" else 0)
     assert res["frames"] == len(ref["rows"]) >= 3 and res["prompt_rows"] == len(rows)
     assert np.mean(np.array(res["codes"]).reshape(-1, 16) == ref["rows"][:, 1:]) >= 0.99
+
+
+def test_shim_default_w8a8_prefill(torch_gpu, oracle, files):
+    """Without MOSS_A16 the drop-in prefills in W8A8 like the reference: its state file
+    holds KV and hidden within the W8A8 end-to-end bar of the oracle's W8A8 prefill."""
+    blob, rows, w, prompt, d = files
+    state = str(d / "w8.state")
+    _run("--weights", w, "--prompt", prompt, "--frames", 1, "--greedy", "--save-state", state,
+         env={k: v for k, v in os.environ.items() if k != "MOSS_A16"})
+    m = oracle.model(blob, kv_f16=True)
+    m.prefill(rows)
+    _, n_pos, _, _, k, v, hidden = mf.read_state(open(state, "rb").read())
+    ok_, ov_ = m.kv_export(n_pos)
+    assert max_rel(hidden, m.hidden()) <= 3e-2
+    assert max_rel(k, ok_) <= 3e-2 and max_rel(v, ov_) <= 3e-2
 
 
 def test_shim_rejects_bad_files(torch_gpu, files):

@@ -162,24 +162,50 @@ def test_generate_end_gate_matches_oracle(torch_gpu, oracle, prefilled):
         g.close()
 
 
-def test_prefill_vs_oracle(torch_gpu, oracle, golden_model):
+# W8A8 prefill end to end: every GEMM input is re-quantised per 32-block, so an
+# input difference of one ulp can move a value across a rounding boundary and
+# change it by a full quantisation step (d = amax / 127).  The oracle itself,
+# run with its KV rounded to fp16 (a 5e-4 perturbation), moves its W8A8 prefill
+# hidden state by 1.5e-2 (A16: 1.7e-4).  The W8A8 operators are held to the
+# tight bars separately (quantisation bit-exact, GEMM <= 1e-5, test_gpu_ops);
+# end to end the bar is 3e-2 (A16: 1e-3).
+W8A8_E2E_TOL = 3e-2
+
+
+@pytest.mark.parametrize("a16", [False, True])
+def test_prefill_vs_oracle(torch_gpu, oracle, golden_model, a16):
+    """Prefill in the reference's W8A8 mode (the default: int8 activations per
+    32-block, i8 MFMA) and in its MOSS_A16=1 mode, against the golden hidden
+    state the compiled reference wrote and the oracle's KV."""
+    TOL = 1e-3 if a16 else W8A8_E2E_TOL
     blob, g = golden_model
     rows = g["rows"]
-    gm = HipLLM(blob, kv_fp32=True)
+    print(f"prefill a16={a16}", flush=True)
+    gm = HipLLM(blob, kv_fp32=True, prefill_a16=a16)
     gm.prefill(rows)
     assert gm.position == len(rows)
-    assert max_rel(gm.hidden(), g["hidden_prefill_a16"]) <= TOL
+    assert max_rel(gm.hidden(), g["hidden_prefill_a16" if a16 else "hidden_prefill"]) <= TOL
     m = oracle.model(blob)
-    m.prefill(rows, a16=True)
+    m.prefill(rows, a16=a16)
     gk, gv = gm.kv_export(len(rows))
     ok, ov = m.kv_export(len(rows))
     assert max_rel(gk, ok) <= TOL and max_rel(gv, ov) <= TOL
-    # continue from start = position (multi-chunk prompts, engine.cpp:463)
+    if not a16:
+        assert max_rel(gk[0], g["k_prefill_l0"]) <= TOL and max_rel(gv[11], g["v_prefill_l11"]) <= TOL
+    # continue from start = position (multi-chunk prompts, engine.cpp:463), and a longer prompt
     extra = mf.text_rows(np.arange(5))
     gm.prefill(extra, start=gm.position)
-    m.prefill(extra, start=m.position, a16=True)
+    m.prefill(extra, start=m.position, a16=a16)
     assert gm.position == m.position
     assert max_rel(gm.hidden(), m.hidden()) <= TOL
+    long_rows = mf.text_rows(np.random.default_rng(3).integers(0, mf.VOCAB, 200))
+    long_rows[50:80, 1:] = np.random.default_rng(4).integers(0, 1024, (30, 16))
+    gm.reset()
+    gm.prefill(long_rows)
+    m2 = oracle.model(blob)
+    m2.prefill(long_rows, a16=a16)
+    assert max_rel(gm.hidden(), m2.hidden()) <= TOL
+    gm.close()
 
 
 def test_snapshot_restore_prefix(torch_gpu, prefilled):

@@ -167,3 +167,48 @@ def test_gemm_mfma_vs_oracle(torch_gpu, oracle, rows, cols, m):
     for i in range(m):  # per row: rows of very different scale
         assert max_rel(got[i], ref[i]) <= TOL
     assert max_rel(got, ref) <= 1e-5
+
+
+def test_quantize_rows_bit_exact(torch_gpu, oracle):
+    """W8A8 activation quantisation (quant.cpp:28-54) on the GPU == the oracle, bit for bit:
+    int8 values and fp32 block scales, including an all-zero block, exact .5 ties and
+    values at the clamp."""
+    torch = torch_gpu
+    rng = np.random.default_rng(17)
+    m, cols = 9, 3072
+    x = (rng.standard_normal((m, cols)) * rng.choice([1e-3, 1.0, 50.0], (m, 1))).astype(np.float32)
+    x[0, :32] = 0.0                                      # d = 0 -> id = 0 -> q = 0
+    x[1, :32] = np.arange(32, dtype=np.float32) - 15.5    # ties at k + 0.5 after scaling
+    x[1, 31] = 127.0                                      # amax = 127: scale 1, ties stay ties
+    x[2, 64:96] = rng.standard_normal(32) * 1e30          # huge values
+    q = torch.empty((m, cols), dtype=torch.int8, device="cuda")
+    d = torch.empty((m, cols // 32), dtype=torch.float32, device="cuda")
+    lib.quantize_rows(_dev(torch, x), m, cols, q, d)
+    torch.cuda.synchronize()
+    for i in range(m):
+        oq, _, od = oracle.quantize_row(x[i])
+        assert np.array_equal(q[i].cpu().numpy(), oq), i
+        assert np.array_equal(d[i].cpu().numpy(), od), i
+
+
+@pytest.mark.parametrize("rows,cols,m", [(2304, 768, 64), (768, 3072, 256), (1024, 768, 1), (16, 768, 100)])
+def test_gemm_w8a8_vs_oracle(torch_gpu, oracle, rows, cols, m):
+    """W8A8 GEMM on the int8 matrix cores vs the oracle's W8A8 gemm_par (row_dot_q8_4x4
+    order) on the same quantised activations: only the fp32 accumulation order of the
+    per-block scaled integer dots differs."""
+    torch = torch_gpu
+    print(f"gemm w8a8 rows={rows} cols={cols} m={m}", flush=True)
+    rng = np.random.default_rng(rows * 3 + cols + m)
+    w = mf.synth_q8x4(rng, rows, cols)
+    x = (rng.standard_normal((m, cols)) * rng.choice([0.01, 1.0, 30.0], (m, 1))).astype(np.float32)
+    q = torch.empty((m, cols), dtype=torch.int8, device="cuda")
+    d = torch.empty((m, cols // 32), dtype=torch.float32, device="cuda")
+    y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+    xd = _dev(torch, x)
+    lib.quantize_rows(xd, m, cols, q, d)
+    lib.gemm_q8x4_w8a8(_dev(torch, w), rows, cols, q, d, m, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle.gemm(w, rows, cols, x, a16=False)
+    for i in range(m):
+        assert max_rel(got[i], ref[i]) <= 1e-5, i
