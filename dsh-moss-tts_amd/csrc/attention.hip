@@ -127,13 +127,14 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
-#pragma unroll
-    for (int off = 16; off < 64; off <<= 1) {
-        o.x += __shfl_xor(o.x, off);
-        o.y += __shfl_xor(o.y, off);
-        o.z += __shfl_xor(o.z, off);
-        o.w += __shfl_xor(o.w, off);
-    }
+    o.x += xshfl<16>(o.x);
+    o.y += xshfl<16>(o.y);
+    o.z += xshfl<16>(o.z);
+    o.w += xshfl<16>(o.w);
+    o.x += xshfl<32>(o.x);
+    o.y += xshfl<32>(o.y);
+    o.z += xshfl<32>(o.z);
+    o.w += xshfl<32>(o.w);
     if constexpr (PART) {
         float *pp = a.part + ((size_t)h * gridDim.y + blockIdx.y) * kPartStride;
         if (lane < 16) *(float4 *)(pp + 4 * dg) = o;

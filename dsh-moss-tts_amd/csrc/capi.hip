@@ -51,7 +51,7 @@ mh::Batch &batch_of(moss_hip_batch *b) {
 }
 
 moss_hip_llm_options defaults(const moss_hip_llm_options *opt) {
-    moss_hip_llm_options o{0, 0, 0, 1, 0};
+    moss_hip_llm_options o{0, 0, 0, 1, 0, 0};
     if (opt) o = *opt;
     return o;
 }

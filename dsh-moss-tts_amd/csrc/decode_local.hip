@@ -1,0 +1,333 @@
+// decode_local.hip -- one step of the local transformer of the single-stream decode in one launch (gfx950).
+//
+// Replaces local_step (reference csrc/src/llm.cpp:259-264: block_forward of the
+// one local layer at local position lpos, llm.cpp:230-246) and, for the
+// channel steps, the channel's audio head (audio_logits, llm.cpp:686-688:
+// logits = aemb[ch] . local_ln_f(x)).  The stages hand their outputs on through
+// LL words (mh_ll.h), as in decode_layer.hip:
+//   Q  lpos 0 only, b < 288: LN1 + QKV of the block input (the global hidden
+//      state), RoPE, k/v into the local cache                  -> LL q|k|v
+//   P  b < 192: the step's input -- for lpos >= 2 the code of the previous
+//      channel, picked here (greedy: penalised argmax of its logits, or the
+//      forced code) or written by the sampler -- and its q|k|v: from the
+//      QKV stage (lpos 0) or from the precomputed row of (lpos, code); the
+//      local attention over keys 0..lpos (every workgroup computes all 12
+//      heads: at most 17 keys); proj + residual                -> LL x + attn
+//   M  every b: LN2 + fc_in + gelu_new                          -> LL h
+//   F  b < 192: fc_out + residual -> x_out (memory) and, with a head, LL x_out
+//   H  b < 256, with a head: local ln_f + the audio head GEMV  -> logits (memory)
+//
+// Precomputed q|k|v rows.  For lpos >= 1 the block input is an embedding row
+// -- wte[slot] at lpos 1, aemb[lpos - 2][code] at lpos >= 2 -- and RoPE uses
+// the fixed position lpos, so q|k|v = RoPE_lpos(attn_w . LN1(row) + attn_b) is
+// a function of (lpos, code) only.  The host computes every such row once, at
+// load, with the one-GEMV kernel of the per-operator path (the same per-row
+// arithmetic), so the table holds exactly the values that path computes live.
+#include "mh_gemv.h"
+#include "mh_ll.h"
+#include "mh_ops.h"
+
+namespace mh {
+namespace {
+
+// LL regions (words); consecutive launches differ in lpos, so in tag
+constexpr int kLQ = 0;                  // q | k | v (lpos 0)
+constexpr int kLX = kLQ + 3 * kHidden;  // x after the attention sub-block
+constexpr int kLH = kLX + kHidden;      // fc_in output
+constexpr int kLO = kLH + kFF;          // block output (head input)
+static_assert(kLO + kHidden <= kLayerWords, "local LL layout fits the exchange buffer");
+
+template <bool LIVE_QKV>
+__global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float act[kFF];
+    __shared__ float xm[kHidden];
+    __shared__ float qkv[3 * kHidden];             // q | k | v of this position
+    __shared__ float sc[kHeads][kLocalLen + 1];
+    __shared__ float red[4];
+    __shared__ float part[4][4];
+    __shared__ float pbv[4];
+    __shared__ int pbi[4];
+    __shared__ int used_s;
+
+    DevState *st = a.state;
+    if (st->stop) return;  // written only between frames: the same for every workgroup
+    const int lpos = a.lpos, n = lpos + 1;
+    const uint32_t tag = ((uint32_t)(st->pos + 1) << 5) | (uint32_t)(12 + lpos);
+    const int t = threadIdx.x;
+    const int b = blockIdx.x;
+    int budget = kPollBudget;
+    uint64_t *LL = a.ll;
+
+    // ---- stage Q (lpos 0): LN1 + QKV of the block input, 2 waves per group
+    if constexpr (LIVE_QKV) {
+        if (b < 3 * kHidden / 8) {
+            GemvStage<2, 3, kHidden> gs;
+            gs.prefetch(a.attn_w, b);
+            const int r = gs.row();
+            QkvEpi e;
+            if (gs.storer()) e.load(a.attn_b, a.rope_cos, a.rope_sin, r, lpos);
+            float v[3], o[3], lw[3], lb[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                v[i] = a.x_in[t + 256 * i];
+                lw[i] = a.ln1_w[t + 256 * i];
+                lb[i] = a.ln1_b[t + 256 * i];
+            }
+            layernorm_768_reg(v, lw, lb, o, red);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+            __syncthreads();
+            const float yv = gs.dot(act, part);
+            const float partner = xshfl<4>(yv);
+            if (gs.storer()) {
+                const float out = e.apply(r, yv, partner);
+                const int sec = r / kHidden, within = r - sec * kHidden;
+                if (sec > 0) {  // llm.cpp:224-225
+                    float *cache = sec == 1 ? a.lk : a.lv;
+                    cache[((size_t)(within >> 6) * kLocalLen + lpos) * kHeadDim + (within & 63)] = out;
+                }
+                ll_put(LL + kLQ + r, out, tag);
+            }
+            __syncthreads();
+        }
+    }
+
+    // ---- stage P: input, local attention, proj + residual (4 waves per group)
+    if (b < kHidden / 4) {
+        GemvStage<4, 2, kHidden> gs;
+        gs.prefetch(a.proj_w, b);
+        const int r = gs.row();
+        const float eb = gs.storer() ? a.proj_b[r] : 0.0f;
+        // cache operands of keys 0 .. lpos-1 (written by earlier launches); the
+        // key at lpos, and the clamped ones past it, come from this step's row
+        const int kmax = max(lpos - 1, 0);
+        float vv[3][kLocalLen];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int i = t + 256 * k, h = i >> 6, d = i & 63;
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p) vv[k][p] = a.lv[((size_t)h * kLocalLen + min(p, kmax)) * kHeadDim + d];
+        }
+        const int hp = t / kLocalLen, pp = t - hp * kLocalLen;  // (head, key) of this thread's score
+        const bool scorer = t < kHeads * kLocalLen;
+        float4 kr[kHeadDim / 4];
+        {
+            const float *row = a.lk + ((size_t)min(hp, kHeads - 1) * kLocalLen + min(pp, kmax)) * kHeadDim;
+#pragma unroll
+            for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)(row + 4 * c);
+        }
+        // the step's input row and its q | k | v
+        float eres = 0.0f;
+        if constexpr (LIVE_QKV) {
+            if (gs.storer()) eres = a.x_in[r];
+            const bool ok = ll_gather<3 * kHidden / 256>(LL + kLQ, 3 * kHidden, tag, qkv, budget);
+            if (__syncthreads_or(!ok)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
+            }
+        } else {
+            const float *row;
+            if (a.ch_in < 0) {  // lpos 1: wte[slot]
+                row = a.qkv_table;
+                if (gs.storer()) eres = a.x_in[r];
+            } else {
+                int used;
+                if (a.pick) {  // greedy pick of channel ch_in (llm.cpp:689-697)
+                    int idx = greedy_pick_1024(a.logits_in, a.counts_in, st->rep_penalty, pbv, pbi);
+                    if (idx >= kCodebook) idx = 0;
+                    used = st->forced_on ? a.forced[st->frame * kNVq + a.ch_in] : idx;
+                    if (b == 0 && t == 0) {
+                        st->codes[a.ch_in] = idx;
+                        st->row[a.ch_in + 1] = used;
+                    }
+                } else {  // written by the sampler of channel ch_in
+                    if (t == 0) used_s = st->row[a.ch_in + 1];
+                    __syncthreads();
+                    used = used_s;
+                }
+                row = a.qkv_table + (size_t)used * 3 * kHidden;
+                if (gs.storer()) eres = q8x4_elem(a.aemb_in, kHidden / 32, used, r);  // lookup_row (llm.cpp:697)
+            }
+#pragma unroll
+            for (int k = 0; k < 3 * kHidden / 256; ++k) qkv[t + 256 * k] = row[t + 256 * k];
+            if (b == 0)  // this position's k, v into the local cache (llm.cpp:224-225), for later steps
+#pragma unroll
+                for (int k = 0; k < kHidden / 256; ++k) {
+                    const int i = t + 256 * k, idx = ((i >> 6) * kLocalLen + lpos) * kHeadDim + (i & 63);
+                    a.lk[idx] = row[kHidden + i];
+                    a.lv[idx] = row[2 * kHidden + i];
+                }
+            __syncthreads();
+        }
+        // local attention (llm.cpp:189-217 over the local cache), in the
+        // reference's order: s_p = (q_h . k_p) * 0.125 summed over d in order;
+        // e_p = exp(s_p - max), the in-order sum, w_p = e_p * (1 / sum);
+        // o[d] = sum_p w_p v_p[d] in order
+        float dot = 0.0f;
+        if (scorer) {
+            if (min(pp, n - 1) == lpos)
+#pragma unroll
+                for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)&qkv[kHidden + hp * kHeadDim + 4 * c];
+#pragma unroll
+            for (int c = 0; c < kHeadDim / 4; ++c) {
+                const float4 qv = *(const float4 *)&qkv[hp * kHeadDim + 4 * c];
+                dot = dot + qv.x * kr[c].x;
+                dot = dot + qv.y * kr[c].y;
+                dot = dot + qv.z * kr[c].z;
+                dot = dot + qv.w * kr[c].w;
+            }
+            dot *= 0.125f;
+            sc[hp][pp] = dot;
+        }
+        __syncthreads();
+        float e = 0.0f;
+        if (scorer && pp < n) {
+            float s[kLocalLen];
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p) s[p] = sc[hp][p];
+            float mx = -1e30f;
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p)
+                if (p < n) mx = fmaxf(mx, s[p]);
+            e = expf(dot - mx);
+        }
+        __syncthreads();
+        if (scorer) sc[hp][pp] = e;
+        __syncthreads();
+        float wgt = 0.0f;  // 0 for keys past n
+        if (scorer) {
+            float s[kLocalLen];
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p) s[p] = sc[hp][p];
+            float sum = 0.0f;
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p)
+                if (p < n) sum += s[p];
+            wgt = e * (1.0f / sum);
+        }
+        __syncthreads();
+        if (scorer) sc[hp][pp] = wgt;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int i = t + 256 * k, h = i >> 6;
+            const float vnew = qkv[2 * kHidden + i];
+            float o = 0.0f;
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p) o = o + sc[h][p] * (min(p, n - 1) == lpos ? vnew : vv[k][p]);
+            act[i] = o;
+        }
+        __syncthreads();
+        const float yv = gs.dot(act, part);
+        if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+    }
+
+    // ---- stage M: LN2 + fc_in + gelu_new, 2 waves per group, every workgroup
+    {
+        GemvStage<2, 3, kHidden> gs;
+        gs.prefetch(a.fc_in_w, b);
+        const int r = gs.row();
+        const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
+        float lw[3], lb[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            lw[i] = a.ln2_w[t + 256 * i];
+            lb[i] = a.ln2_b[t + 256 * i];
+        }
+        const bool ok = ll_gather<3>(LL + kLX, kHidden, tag, xm, budget);
+        if (__syncthreads_or(!ok)) {
+            if (t == 0) atomicOr(a.err, 1u);
+            return;
+        }
+        float v[3], o[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
+        layernorm_768_reg(v, lw, lb, o, red);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+        __syncthreads();
+        const float yv = gs.dot(act, part);
+        if (gs.storer()) ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+    }
+
+    // ---- stage F: fc_out + residual (4 waves per group)
+    if (b < kHidden / 4) {
+        GemvStage<4, 6, kFF> gs;
+        gs.prefetch(a.fc_out_w, b);
+        const int r = gs.row();
+        const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
+        const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
+        if (__syncthreads_or(!ok)) {
+            if (t == 0) atomicOr(a.err, 1u);
+            return;
+        }
+        const float yv = gs.dot(act, part);
+        if (gs.storer()) {
+            const float xo = xm[r] + (yv + eb);  // llm.cpp:245
+            a.x_out[r] = xo;
+            if (a.head_w) ll_put(LL + kLO + r, xo, tag);
+        }
+        __syncthreads();
+    }
+
+    // ---- stage H: local ln_f + audio head (4 waves per group)
+    if (a.head_w && b < kCodebook / 4) {
+        GemvStage<4, 2, kHidden> gs;
+        gs.prefetch(a.head_w, b);
+        float lw[3], lb[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            lw[i] = a.lnf_w[t + 256 * i];
+            lb[i] = a.lnf_b[t + 256 * i];
+        }
+        const bool ok = ll_gather<3>(LL + kLO, kHidden, tag, xm, budget);
+        if (__syncthreads_or(!ok)) {
+            if (t == 0) atomicOr(a.err, 1u);
+            return;
+        }
+        float v[3], o[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
+        layernorm_768_reg(v, lw, lb, o, red);  // normalize(lx, local_lnf) (llm.cpp:262)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+        __syncthreads();
+        const float yv = gs.dot(act, part);
+        if (gs.storer()) a.logits_out[gs.row()] = yv;
+    }
+}
+
+}  // namespace
+
+hipError_t decode_local_occupancy(int *per_cu) {
+    int a = 0, b = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, decode_local_kernel<true>, 256, 0);
+    if (e != hipSuccess) return e;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, decode_local_kernel<false>, 256, 0);
+    if (e != hipSuccess) return e;
+    *per_cu = a < b ? a : b;
+    return hipSuccess;
+}
+
+hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (!a.attn_w || !a.proj_w || !a.fc_in_w || !a.fc_out_w || !a.lk || !a.lv || !a.state || !a.ll || !a.err ||
+        !a.x_out || a.lpos < 0 || a.lpos >= kLocalLen)
+        return hipErrorInvalidValue;
+    if (a.lpos == 0) {
+        if (!a.x_in || !a.rope_cos || !a.rope_sin) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(decode_local_kernel<true>, dim3(kLayerGrid), dim3(256), 0, s, a);
+    } else {
+        if (!a.qkv_table) return hipErrorInvalidValue;
+        if (a.ch_in < 0 && (a.lpos != 1 || !a.x_in)) return hipErrorInvalidValue;
+        if (a.ch_in >= 0 && (a.ch_in != a.lpos - 2 || !a.aemb_in ||
+                             (a.pick && (!a.logits_in || !a.counts_in || !a.forced))))
+            return hipErrorInvalidValue;
+        if (a.head_w && (!a.logits_out || !a.lnf_w || !a.lnf_b)) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(decode_local_kernel<false>, dim3(kLayerGrid), dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mh

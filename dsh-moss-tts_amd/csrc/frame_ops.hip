@@ -81,15 +81,7 @@ __device__ int pick_greedy(PickLds &L) {
             besti = i;
         }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(besti, off);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
+    wave_argmax(best, besti);
     if ((t & 63) == 0) {
         L.bv[t >> 6] = best;
         L.bi[t >> 6] = besti;
@@ -298,15 +290,7 @@ __global__ __launch_bounds__(256) void gate_text_kernel(const float *logits, Dev
             besti = i;
         }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(besti, off);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
+    wave_argmax(best, besti);
     if ((t & 63) == 0) {
         bv[t >> 6] = best;
         bi[t >> 6] = besti;

@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
         for (int i = 0; i < 4; ++i) {
             const int m = m_base + 4 * kq + i;
             const float v = acc[t][i];
-            const float partner = __shfl_xor(v, 1);  // column n ^ 1, same row
+            const float partner = xshfl<1>(v);  // column n ^ 1, same row
             if (m < g.M) gemm_finish<EPI, KV>(g, m, n, v, partner);
         }
     }

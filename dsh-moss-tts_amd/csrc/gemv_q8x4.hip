@@ -18,6 +18,7 @@
 // epilogues fuse what block_forward
 // (llm.cpp:230-246) does next to each GEMV: bias + RoPE + KV write (QKV),
 // residual add (proj, fc_out), bias + gelu_new (fc_in).
+#include "mh_gemv.h"
 #include "mh_ops.h"
 
 namespace mh {
@@ -151,48 +152,11 @@ __device__ __forceinline__ void merge_attention(const GemvArgs &a, float *act) {
 // (forced under teacher forcing), its aemb row, LayerNorm.  Workgroup 0 records
 // the pick; the count of the used code is added at the end of the frame.
 __device__ __forceinline__ void pick_input(const GemvArgs &a, float *act, float *red) {
-#pragma clang fp contract(off)
     __shared__ float bv[4];
     __shared__ int bi[4];
     const int t = threadIdx.x;
     const DevState *st = a.pick_state;
-    const float pen = st->rep_penalty;
-    float best = -INFINITY;
-    int besti = kCodebook;
-#pragma unroll
-    for (int k = 0; k < kCodebook / 256; ++k) {  // ascending index per thread
-        const int i = t + 256 * k;
-        float v = a.pick_logits[i];
-        if (pen != 1.0f) {
-            const int c = a.pick_counts[i];
-            for (int r = 0; r < c; ++r) v = v < 0.0f ? v * pen : v / pen;
-        }
-        if (v > best) {
-            best = v;
-            besti = i;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(besti, off);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
-    if ((t & 63) == 0) {
-        bv[t >> 6] = best;
-        bi[t >> 6] = besti;
-    }
-    __syncthreads();
-    float b = bv[0];
-    int idx = bi[0];
-    for (int w = 1; w < 4; ++w)
-        if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
-            b = bv[w];
-            idx = bi[w];
-        }
+    int idx = greedy_pick_1024(a.pick_logits, a.pick_counts, st->rep_penalty, bv, bi);
     if (idx >= kCodebook) idx = 0;
     const int used = st->forced_on ? a.pick_forced[st->frame * kNVq + a.pick_ch] : idx;
     if (blockIdx.x == 0 && t == 0) {
@@ -316,50 +280,6 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int r, float v, fl
     epi_store<EPI, KV>(a, r, v, partner, epi_load<EPI>(a, r));
 }
 
-// Up to NB blocks per lane are in flight at once: all loads of a batch are
-// issued before the first is consumed.  NB is picked per shape so a wave's
-// K-slice is one batch whenever it is at most 32 blocks.
-//
-// Loads are unconditional (the block index is clamped to the wave's last block,
-// so every address is valid): guarded loads would make the compiler wait on
-// each one in turn.
-template <int NB>
-__device__ __forceinline__ void load_batch(const uint8_t *grp, int first_b, int b1, int u, int kk, uint2 (&qv)[NB],
-                                           uint16_t (&dh)[NB]) {
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-        const int b = min(first_b + 4 * it, b1 - 1);
-        const uint8_t *blk = grp + (size_t)b * kBlockBytes;
-        const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 8 * u));
-        qv[it] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
-        dh[it] = *(const uint16_t *)(blk + 2 * kk);
-    }
-}
-
-template <int NB>
-__device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1, int j, const uint2 (&qv)[NB],
-                                           const uint16_t (&dh)[NB], float acc) {
-#pragma unroll
-    for (int it = 0; it < NB; ++it) {
-        const int b = first_b + 4 * it;
-        if (b < b1) {
-            const float4 x0 = *(const float4 *)(act + b * 32 + 8 * j);
-            const float4 x1 = *(const float4 *)(act + b * 32 + 8 * j + 4);
-            const uint2 q = qv[it];
-            float s = (float)(int8_t)(q.x) * x0.x;
-            s = fmaf((float)(int8_t)(q.x >> 8), x0.y, s);
-            s = fmaf((float)(int8_t)(q.x >> 16), x0.z, s);
-            s = fmaf((float)(int8_t)(q.x >> 24), x0.w, s);
-            s = fmaf((float)(int8_t)(q.y), x1.x, s);
-            s = fmaf((float)(int8_t)(q.y >> 8), x1.y, s);
-            s = fmaf((float)(int8_t)(q.y >> 16), x1.z, s);
-            s = fmaf((float)(int8_t)(q.y >> 24), x1.w, s);
-            acc = fmaf(s, h2f(dh[it]), acc);
-        }
-    }
-    return acc;
-}
-
 template <int PRO, int EPI, int SPLIT, int KV, int NB>
 __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     extern __shared__ float act[];
@@ -406,10 +326,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
                 acc = dot_batch<NB>(act, base + bl, b1, j, qv, dh, acc);
             }
         }
-        acc += __shfl_xor(acc, 1);
-        acc += __shfl_xor(acc, 2);
-        acc += __shfl_xor(acc, 16);
-        acc += __shfl_xor(acc, 32);
+        acc = row_lane_sum(acc);
         float yv = acc;
         if constexpr (SPLIT > 1) {
             if (lane < 16 && j == 0) part[wave][kk] = acc;
@@ -419,7 +336,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
             for (int s2 = 1; s2 < SPLIT; ++s2) yv += part[gslot * SPLIT + s2][kk];
             __syncthreads();
         }
-        const float partner = __shfl_xor(yv, 4);
+        const float partner = xshfl<4>(yv);
         if (storer && valid) epi_store<EPI, KV>(a, 4 * g + kk, yv, partner, pre);
     }
 }
@@ -537,11 +454,8 @@ __device__ __forceinline__ void stream_step(const GemvArgs &a, const float *act,
     acc = unit_dot(cur, act + slice * kUnitBlocks * 32, bl, u, kk, j, acc);
     if (slice == P - 1) {
         float yv = acc;
-        yv += __shfl_xor(yv, 1);
-        yv += __shfl_xor(yv, 2);
-        yv += __shfl_xor(yv, 16);
-        yv += __shfl_xor(yv, 32);
-        const float partner = __shfl_xor(yv, 4);
+        yv = row_lane_sum(yv);
+        const float partner = xshfl<4>(yv);
         if (g < ngroups && lane < 16 && j == 0) finish_row<EPI, KV>(a, 4 * g + kk, yv, partner);
         acc = 0.0f;
     }

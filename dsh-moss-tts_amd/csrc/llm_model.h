@@ -98,6 +98,12 @@ private:
 
     int device_ = 0, max_ctx_ = kMaxCtx, use_graphs_ = 1;
     bool prefill_a16_ = false;  // prefill GEMMs on fp32 activations (else W8A8)
+    bool fused_layers_ = false; // global step as one decode_layer launch per layer, local steps as decode_local
+    float *qkv_table_ = nullptr;   // [1 + 15 * 1024][2304] local q|k|v of (lpos >= 1, input code)
+    void build_qkv_table();
+    uint64_t *ll_ = nullptr;    // kLayerWords exchange words of the fused layer launches
+    void clear_exchange();      // before a sequence of fused launches: no stale word carries a current tag
+    void check_exchange();      // throws if a fused launch ran out of its wait budget
     KvType kvt_ = KV_F16;
     size_t kv_esize_ = 2;
     hipStream_t stream_ = nullptr;

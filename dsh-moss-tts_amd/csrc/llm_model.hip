@@ -65,6 +65,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     kv_esize_ = kvt_ == KV_F32 ? 4 : 2;
     use_graphs_ = opt.use_graphs;
     prefill_a16_ = opt.prefill_a16 != 0;
+    if (opt.decode_kernels != 0 && opt.decode_kernels != 1) throw Status(MOSS_HIP_EINVAL, "decode_kernels: 0 or 1");
     const uint8_t *b = static_cast<const uint8_t *>(blob);
     auto idx = parse_index(b, bytes);
 
@@ -175,6 +176,15 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     fmalloc(&logits_, (size_t)kNVq * kCodebook);
     fmalloc(&text_logits_, kVocab);
     hip_check(hipMalloc(&counts_, sizeof(int) * kNVq * kCodebook), "hipMalloc(counts)");
+    if (opt.decode_kernels == 0 && max_ctx_ <= 64 * 4 * kLayerMaxQuarters) {
+        bool fits = false;
+        hip_check(decode_layer_fits(device_, &fits), "decode layer occupancy");
+        fused_layers_ = fits;
+    }
+    if (fused_layers_) {
+        hip_check(hipMalloc(&ll_, sizeof(uint64_t) * kLayerWords), "hipMalloc(exchange)");
+        hip_check(hipMemset(ll_, 0, sizeof(uint64_t) * kLayerWords), "memset(exchange)");
+    }
     hip_check(hipMalloc(&forced_, sizeof(int) * kNVq * (max_ctx_ + 2)), "hipMalloc(forced)");
     hip_check(hipMemset(hidden_, 0, kHidden * 4), "memset(hidden)");
     hip_check(hipMalloc(&state_, sizeof(DevState)), "hipMalloc(state)");
@@ -190,6 +200,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     hip_check(hipMemcpy(rows_dev_, &slot, sizeof(int), hipMemcpyHostToDevice), "slot row");
     hip_check(launch_dequant_rows(wte_, kVocab, kHidden, rows_dev_, 1, slot_in_, stream_), "dequant slot row");
     hip_check(hipStreamSynchronize(stream_), "sync");
+    if (fused_layers_) build_qkv_table();
     if (use_graphs_) build_graphs();
 }
 
@@ -199,7 +210,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, pre_q8_, pre_d8_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, pre_q8_, pre_d8_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -230,6 +241,17 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
     hip_check(launch_embed(e, s), "embed");
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
+        if (fused_layers_) {
+            LayerArgs d;
+            d.attn_w = L.attn_w; d.proj_w = L.proj_w; d.fc_in_w = L.fc_in_w; d.fc_out_w = L.fc_out_w;
+            d.attn_b = L.attn_b; d.proj_b = L.proj_b; d.fc_in_b = L.fc_in_b; d.fc_out_b = L.fc_out_b;
+            d.ln1_w = L.ln1_w; d.ln1_b = L.ln1_b; d.ln2_w = L.ln2_w; d.ln2_b = L.ln2_b;
+            d.x = x_; d.k_cache = kv_layer(0, l); d.v_cache = kv_layer(1, l); d.ctx_stride = max_ctx_;
+            d.rope_cos = rope_; d.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
+            d.state = state_; d.ll = ll_; d.err = &state_->ll_err; d.instance = l;
+            hip_check(launch_decode_layer(d, kvt_, s), "decode layer");
+            continue;
+        }
         GemvArgs a;
         a.w = L.attn_w; a.rows = 3 * kHidden; a.cols = kHidden;
         a.x = x_; a.ln_w = L.ln1_w; a.ln_b = L.ln1_b;
@@ -262,6 +284,50 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         hip_check(launch_gemv(f2, PRO_F32, EPI_RESID, kvt_, s), "fc_out gemv");
     }
     hip_check(launch_layernorm(x_, lnf_w_, lnf_b_, hidden_, state_, 1, s), "ln_f");
+}
+
+// q|k|v rows of the local steps at lpos >= 1, whose block input is an embedding
+// row: wte[slot] at lpos 1, aemb[lpos - 2][code] at lpos >= 2.  Each row is
+// RoPE_lpos(attn_w . LN1(row) + attn_b), computed by the per-operator QKV GEMV
+// (the kernel the per-operator path runs live on the same row), with the
+// position folded into the RoPE table pointer and the k / v "cache" pointed at
+// the row itself.
+void Model::build_qkv_table() {
+    const size_t row = 3 * kHidden;
+    hip_check(hipMalloc(&qkv_table_, sizeof(float) * row * (1 + (size_t)(kNVq - 1) * kCodebook)),
+              "hipMalloc(qkv table)");
+    float *emb = nullptr;
+    int *ids = nullptr;
+    hip_check(hipMalloc(&emb, sizeof(float) * kCodebook * kHidden), "hipMalloc(table input)");
+    hip_check(hipMalloc(&ids, sizeof(int) * kCodebook), "hipMalloc(table ids)");
+    std::vector<int> iota(kCodebook);
+    for (int i = 0; i < kCodebook; ++i) iota[i] = i;
+    auto one = [&](const float *x, float *dst, int lpos) {
+        GemvArgs a;
+        a.w = local_.attn_w; a.rows = 3 * kHidden; a.cols = kHidden;
+        a.x = x; a.ln_w = local_.ln1_w; a.ln_b = local_.ln1_b; a.bias = local_.attn_b;
+        a.q_out = dst; a.k_cache = dst + kHidden; a.v_cache = dst + 2 * kHidden; a.ctx_stride = 1;
+        a.rope_cos = rope_ + (size_t)lpos * kRopeHalf;
+        a.rope_sin = rope_ + ((size_t)rope_n_ + lpos) * kRopeHalf;
+        a.pos_const = 0;
+        hip_check(launch_gemv(a, PRO_LN, EPI_QKV, KV_F32, stream_), "qkv table row");
+    };
+    try {
+        hip_check(hipMemcpyAsync(ids, iota.data(), sizeof(int) * kCodebook, hipMemcpyHostToDevice, stream_), "ids h2d");
+        one(slot_in_, qkv_table_, 1);
+        for (int ch = 0; ch + 1 < kNVq; ++ch) {  // input channel ch feeds lpos ch + 2
+            hip_check(launch_dequant_rows(aemb_[ch], kCodebook, kHidden, ids, kCodebook, emb, stream_), "dequant aemb");
+            for (int code = 0; code < kCodebook; ++code)
+                one(emb + (size_t)code * kHidden, qkv_table_ + (1 + (size_t)ch * kCodebook + code) * row, ch + 2);
+        }
+        hip_check(hipStreamSynchronize(stream_), "sync");
+    } catch (...) {
+        (void)hipFree(emb);
+        (void)hipFree(ids);
+        throw;
+    }
+    (void)hipFree(emb);
+    (void)hipFree(ids);
 }
 
 // local_step (llm.cpp:259-264) without its final ln_f: the residual stream starts
@@ -316,6 +382,55 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos, int pic
 // channel ch's QKV GEMV instead of a kernel of its own; only channel 15 keeps
 // its sample kernel, which also counts the frame's used codes.
 void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
+    if (fused_layers_ && !text_gate) {  // one launch per local step (+ the channel's audio head)
+        LocalArgs base;
+        const LayerW &L = local_;
+        base.attn_w = L.attn_w; base.proj_w = L.proj_w; base.fc_in_w = L.fc_in_w; base.fc_out_w = L.fc_out_w;
+        base.attn_b = L.attn_b; base.proj_b = L.proj_b; base.fc_in_b = L.fc_in_b; base.fc_out_b = L.fc_out_b;
+        base.ln1_w = L.ln1_w; base.ln1_b = L.ln1_b; base.ln2_w = L.ln2_w; base.ln2_b = L.ln2_b;
+        base.lnf_w = llnf_w_; base.lnf_b = llnf_b_;
+        base.lk = lkv_; base.lv = lkv_ + (size_t)kHeads * kLocalLen * kHeadDim;
+        base.rope_cos = rope_; base.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
+        base.state = state_; base.ll = ll_; base.err = &state_->ll_err; base.x_out = lres_;
+        LocalArgs z = base;  // lpos 0 on the global hidden state, then the end gate
+        z.lpos = 0;
+        z.x_in = hidden_;
+        hip_check(launch_decode_local(z, s), "local step");
+        hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, s), "gate");
+        for (int ch = 0; ch < kNVq; ++ch) {
+            LocalArgs c = base;
+            c.lpos = ch + 1;
+            if (ch == 0) {
+                c.x_in = slot_in_;
+                c.qkv_table = qkv_table_;
+            } else {
+                c.ch_in = ch - 1;
+                c.aemb_in = aemb_[ch - 1];
+                c.qkv_table = qkv_table_ + (1 + (size_t)(ch - 1) * kCodebook) * 3 * kHidden;
+                c.pick = fused ? 1 : 0;
+                c.logits_in = logits_ + (size_t)(ch - 1) * kCodebook;
+                c.counts_in = counts_ + (size_t)(ch - 1) * kCodebook;
+                c.forced = forced_;
+            }
+            c.head_w = aemb_[ch];
+            c.logits_out = logits_ + (size_t)ch * kCodebook;
+            hip_check(launch_decode_local(c, s), "local step");
+            if (!fused || ch == kNVq - 1) {
+                SampleArgs sa;
+                sa.logits = logits_ + (size_t)ch * kCodebook;
+                sa.ch = ch;
+                sa.counts = counts_;
+                sa.forced = forced_;
+                sa.aemb = aemb_[ch];
+                sa.next_input = next_in_;
+                sa.state = state_;
+                sa.last_channel = ch == kNVq - 1;
+                sa.count_all = fused && ch == kNVq - 1;
+                hip_check(launch_sample(sa, s), "sample");
+            }
+        }
+        return;
+    }
     enqueue_local_step(s, hidden_, 0, -1);
     if (text_gate) {  // gate-dump frames: the whole text head, as llm.cpp:662-667
         GemvArgs t;
@@ -381,6 +496,19 @@ void Model::launch_frame_local(hipStream_t s, bool text_gate, bool fused) {
 }
 
 // Pushes the scalar header (pos .. rep_penalty) of the host mirror to the device.
+void Model::clear_exchange() {
+    if (!fused_layers_) return;
+    hip_check(hipMemsetAsync(ll_, 0, sizeof(uint64_t) * kLayerWords, stream_), "exchange clear");
+    hip_check(hipMemsetAsync(&state_->ll_err, 0, sizeof(unsigned), stream_), "exchange error clear");
+    hstate_->ll_err = 0;
+}
+
+void Model::check_exchange() {
+    if (hstate_->ll_err != 0)
+        throw Status(MOSS_HIP_EDEVICE, "decode layer: a stage waited past its budget for another workgroup "
+                                       "(the device did not hold all workgroups of the launch at once)");
+}
+
 void Model::write_state_header() {
     hstate_->pos = pos_;
     hip_check(hipMemcpyAsync(state_, hstate_, offsetof(DevState, row), hipMemcpyHostToDevice, stream_), "state h2d");
@@ -414,8 +542,12 @@ void Model::global_step(const int32_t *row) {
     hip_check(hipMemcpyAsync(reinterpret_cast<uint8_t *>(state_) + kStateRowOff, row, 17 * sizeof(int32_t),
                              hipMemcpyHostToDevice, stream_),
               "row h2d");
+    clear_exchange();
     launch_global(stream_);
+    hip_check(hipMemcpyAsync(&hstate_->ll_err, &state_->ll_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+              "state d2h");
     hip_check(hipStreamSynchronize(stream_), "sync");
+    check_exchange();
     ++pos_;
 }
 
@@ -546,6 +678,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     hstate_->cfg = sample_cfg(p);
     rng_seed_host(seed, hstate_->rng);  // Rng rng; rng.seed(seed) (llm.cpp:638-639)
     write_state_header();
+    clear_exchange();
     hip_check(hipStreamSynchronize(stream_), "sync");
 
     int frames = 0;
@@ -564,6 +697,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
                       "logits d2h");
         hip_check(hipMemcpyAsync(hstate_, state_, sizeof(DevState), hipMemcpyDeviceToHost, stream_), "state d2h");
         hip_check(hipStreamSynchronize(stream_), "sync");
+        check_exchange();
         if (gate_dump) {
             float *gd = gate_dump + 4 * (size_t)f;
             gd[0] = hstate_->gate[0];

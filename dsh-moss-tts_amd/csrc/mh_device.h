@@ -57,6 +57,7 @@ struct DevState {
     float gate[2];    // (l_end, l_slot) of the current frame
     int gate_argmax;  // gate-dump frames: argmax over the full text head, and its logit
     float gate_argmax_v;
+    unsigned ll_err;  // a fused decode-layer launch ran out of its wait budget
 };
 
 // xoshiro128** step and uniform draw of the reference's Rng (sampler.h:25-49).
@@ -86,15 +87,78 @@ __device__ __forceinline__ bool end_reached(float l_slot, float l_end, const Sam
     return rng_uniform(rng) >= p_slot;
 }
 
+// Value of lane (lane ^ M) for M = 1, 2, 4, 8, 16, 32, without the LDS
+// round trip of ds_bpermute: DPP quad permutes (1, 2), DPP row shifts under
+// bank masks (4), a DPP row rotation (8) and the gfx950 permlane swaps (16, 32).
+// Same values as __shfl_xor(v, M), so reductions keep their order and results.
+template <int M>
+__device__ __forceinline__ int xshfl(int v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "xshfl: power of two <= 32");
+    if constexpr (M == 1) {
+        return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+        // banks 0, 2 of each row (lanes 0-3, 8-11) read lane + 4 (row_shl:4),
+        // banks 1, 3 (lanes 4-7, 12-15) read lane - 4 (row_shr:4)
+        const int t = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xF, 0x5, false);
+        return __builtin_amdgcn_update_dpp(t, v, 0x114, 0xF, 0xA, false);
+    } else if constexpr (M == 8) {
+        return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);  // row_ror:8 within 16 lanes
+    } else if constexpr (M == 16) {
+        // swap of rows 1 <-> 0 and 3 <-> 2: r.x = rows [0,0,2,2], r.y = rows [1,1,3,3]
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)(((__lane_id() >> 4) & 1) ? r[0] : r[1]);
+    } else {
+        // r.x = lanes 0-31 in both halves, r.y = lanes 32-63 in both halves
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)(__lane_id() >= 32 ? r[0] : r[1]);
+    }
+}
+
+template <int M>
+__device__ __forceinline__ float xshfl(float v) {
+    return __int_as_float(xshfl<M>(__float_as_int(v)));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v += xshfl<32>(v);
+    v += xshfl<16>(v);
+    v += xshfl<8>(v);
+    v += xshfl<4>(v);
+    v += xshfl<2>(v);
+    v += xshfl<1>(v);
     return v;
 }
 
+// Wave-wide (max value, lowest index among ties) reduction; every lane ends
+// with the result.
+template <int M>
+__device__ __forceinline__ void argmax_step(float &best, int &besti) {
+    const float ov = xshfl<M>(best);
+    const int oi = xshfl<M>(besti);
+    if (ov > best || (ov == best && oi < besti)) {
+        best = ov;
+        besti = oi;
+    }
+}
+
+__device__ __forceinline__ void wave_argmax(float &best, int &besti) {
+    argmax_step<32>(best, besti);
+    argmax_step<16>(best, besti);
+    argmax_step<8>(best, besti);
+    argmax_step<4>(best, besti);
+    argmax_step<2>(best, besti);
+    argmax_step<1>(best, besti);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = fmaxf(v, xshfl<32>(v));
+    v = fmaxf(v, xshfl<16>(v));
+    v = fmaxf(v, xshfl<8>(v));
+    v = fmaxf(v, xshfl<4>(v));
+    v = fmaxf(v, xshfl<2>(v));
+    v = fmaxf(v, xshfl<1>(v));
     return v;
 }
 
@@ -107,6 +171,48 @@ __device__ __forceinline__ float q8x4_elem(const uint8_t *w, int nb, int r, int 
     const uint16_t d = *(const uint16_t *)(blk + 2 * (r & 3));
     const int8_t q = *(const int8_t *)(blk + 8 + 32 * (r & 3) + (c & 31));
     return h2f(d) * (float)q;  // exact in fp32
+}
+
+// Greedy pick over one 1024-entry logit row by a 256-thread workgroup
+// (sampler.cpp:13-28 as llm.cpp:689-697 calls it): logits under the
+// repetition penalty (applied count times, v < 0 ? v * p : v / p), argmax with
+// the lowest index winning ties; kCodebook when every value is NaN (the caller
+// maps that to 0, where the reference's scan stays).  bv / bi: 4 LDS slots.
+__device__ __forceinline__ int greedy_pick_1024(const float *logits, const int *counts, float pen, float *bv, int *bi) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x;
+    float vals[kCodebook / 256];
+    int cnt[kCodebook / 256];
+#pragma unroll
+    for (int k = 0; k < kCodebook / 256; ++k) {  // every load issued before the first use
+        vals[k] = logits[t + 256 * k];
+        cnt[k] = pen != 1.0f ? counts[t + 256 * k] : 0;
+    }
+    float best = -INFINITY;
+    int besti = kCodebook;
+#pragma unroll
+    for (int k = 0; k < kCodebook / 256; ++k) {  // ascending index per thread
+        float v = vals[k];
+        for (int r = 0; r < cnt[k]; ++r) v = v < 0.0f ? v * pen : v / pen;
+        if (v > best) {
+            best = v;
+            besti = t + 256 * k;
+        }
+    }
+    wave_argmax(best, besti);
+    if ((t & 63) == 0) {
+        bv[t >> 6] = best;
+        bi[t >> 6] = besti;
+    }
+    __syncthreads();
+    float b = bv[0];
+    int idx = bi[0];
+    for (int w = 1; w < 4; ++w)
+        if (bv[w] > b || (bv[w] == b && bi[w] < idx)) {
+            b = bv[w];
+            idx = bi[w];
+        }
+    return idx;
 }
 
 // Block-wide sum for a 256-thread workgroup (4 waves); `red` needs 4 floats.
@@ -122,10 +228,11 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 // LayerNorm over kHidden elements held as 3 values per thread of a 256-thread
 // workgroup (reference csrc/src/llm.cpp:159-171: two-pass mean / variance,
 // eps 1e-5, (x - mean) * inv * w + b).  Reductions are tree-ordered here.
-__device__ __forceinline__ void layernorm_768(const float (&x)[3], const float *w, const float *b, float (&out)[3],
-                                              float *red) {
+// The weights of this thread's elements (w[t + 256 i], b[t + 256 i]) come in
+// registers, so a caller can load them before its input is ready.
+__device__ __forceinline__ void layernorm_768_reg(const float (&x)[3], const float (&w)[3], const float (&b)[3],
+                                                  float (&out)[3], float *red) {
 #pragma clang fp contract(off)
-    const int t = threadIdx.x;
     float s = (x[0] + x[1]) + x[2];
     const float mean = block_sum_256(s, red) / (float)kHidden;
     float d0 = x[0] - mean, d1 = x[1] - mean, d2 = x[2] - mean;
@@ -134,11 +241,22 @@ __device__ __forceinline__ void layernorm_768(const float (&x)[3], const float *
     const float inv = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-        const int c = t + 256 * i;
         float y = (x[i] - mean) * inv;
-        y = y * w[c];
-        out[i] = y + b[c];
+        y = y * w[i];
+        out[i] = y + b[i];
     }
+}
+
+__device__ __forceinline__ void layernorm_768(const float (&x)[3], const float *w, const float *b, float (&out)[3],
+                                              float *red) {
+    const int t = threadIdx.x;
+    float wv[3], bv[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        wv[i] = w[t + 256 * i];
+        bv[i] = b[t + 256 * i];
+    }
+    layernorm_768_reg(x, wv, bv, out, red);
 }
 
 // Activation quantisation of one 32-value block held by 32 consecutive lanes
@@ -149,8 +267,11 @@ __device__ __forceinline__ void layernorm_768(const float (&x)[3], const float *
 __device__ __forceinline__ int quant_block32(float x, float *d_out) {
 #pragma clang fp contract(off)
     float amax = fabsf(x);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = fmaxf(amax, xshfl<1>(amax));
+    amax = fmaxf(amax, xshfl<2>(amax));
+    amax = fmaxf(amax, xshfl<4>(amax));
+    amax = fmaxf(amax, xshfl<8>(amax));
+    amax = fmaxf(amax, xshfl<16>(amax));
     const float d = amax / 127.0f;
     const float id = d > 0.0f ? 1.0f / d : 0.0f;
     int q = (int)rintf(x * id);

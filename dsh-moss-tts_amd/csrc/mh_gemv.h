@@ -1,0 +1,93 @@
+// mh_gemv.h -- per-wavefront building blocks of the Q8_0_4X4 GEMV (gfx950),
+// shared by the one-GEMV-per-launch kernels and the fused decode-layer kernel.
+//
+// A 4-row group is one contiguous run of nb*136 bytes, 8-byte aligned blocks of
+// 17 qwords (qword 0 = the 4 fp16 scales, qwords 1+4k+j = row k, columns
+// 8j..8j+7).  Lane = 16*bl + 4*k + j of a wave reads qword 1+4k+j of block
+// b = first + bl (+4 per batch step), plus its row's fp16 scale, and accumulates
+// acc += d * (8-term fp32 dot) in block order -- the per-row arithmetic of
+// row_dot_q8_4x4_actf32 (reference csrc/src/gemv_avx2.cpp:123-150).
+#pragma once
+#include "mh_device.h"
+
+namespace mh {
+
+// Up to NB blocks per lane are in flight at once: all loads of a batch are
+// issued before the first is consumed.  Loads are unconditional (the block
+// index is clamped to the wave's last block, so every address is valid):
+// guarded loads would make the compiler wait on each one in turn.
+template <int NB>
+__device__ __forceinline__ void load_batch(const uint8_t *grp, int first_b, int b1, int u, int kk, uint2 (&qv)[NB],
+                                           uint16_t (&dh)[NB]) {
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+        const int b = min(first_b + 4 * it, b1 - 1);
+        const uint8_t *blk = grp + (size_t)b * kBlockBytes;
+        const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 8 * u));
+        qv[it] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
+        dh[it] = *(const uint16_t *)(blk + 2 * kk);
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1, int j, const uint2 (&qv)[NB],
+                                           const uint16_t (&dh)[NB], float acc) {
+#pragma unroll
+    for (int it = 0; it < NB; ++it) {
+        const int b = first_b + 4 * it;
+        if (b < b1) {
+            const float4 x0 = *(const float4 *)(act + b * 32 + 8 * j);
+            const float4 x1 = *(const float4 *)(act + b * 32 + 8 * j + 4);
+            const uint2 q = qv[it];
+            float s = (float)(int8_t)(q.x) * x0.x;
+            s = fmaf((float)(int8_t)(q.x >> 8), x0.y, s);
+            s = fmaf((float)(int8_t)(q.x >> 16), x0.z, s);
+            s = fmaf((float)(int8_t)(q.x >> 24), x0.w, s);
+            s = fmaf((float)(int8_t)(q.y), x1.x, s);
+            s = fmaf((float)(int8_t)(q.y >> 8), x1.y, s);
+            s = fmaf((float)(int8_t)(q.y >> 16), x1.z, s);
+            s = fmaf((float)(int8_t)(q.y >> 24), x1.w, s);
+            acc = fmaf(s, h2f(dh[it]), acc);
+        }
+    }
+    return acc;
+}
+
+// Sum of a row's 16 lanes (lanes 16*bl + 4*kk + j for the row kk): every lane
+// of the row ends with the row's total.
+__device__ __forceinline__ float row_lane_sum(float acc) {
+    acc += xshfl<1>(acc);
+    acc += xshfl<2>(acc);
+    acc += xshfl<16>(acc);
+    acc += xshfl<32>(acc);
+    return acc;
+}
+
+// QKV epilogue of row r at position pos (llm.cpp:234-236): bias, then RoPE on
+// the q and k sections, which pairs row r with its neighbour r ^ 1 (the
+// partner's raw sum comes from the caller).  load() before the dot, apply()
+// after it.
+struct QkvEpi {
+    float b0 = 0.f, b1 = 0.f, c = 0.f, s = 0.f;
+    __device__ __forceinline__ void load(const float *bias, const float *cosv, const float *sinv, int r, int pos) {
+        const int sec = r / kHidden, d = (r - sec * kHidden) & 63;
+        b0 = bias[r];
+        if (sec < 2) {
+            b1 = bias[r ^ 1];
+            c = cosv[pos * kRopeHalf + (d >> 1)];
+            s = sinv[pos * kRopeHalf + (d >> 1)];
+        }
+    }
+    __device__ __forceinline__ float apply(int r, float v, float partner) const {
+#pragma clang fp contract(off)
+        const float val = v + b0;
+        const int sec = r / kHidden, d = (r - sec * kHidden) & 63;
+        if (sec == 2) return val;
+        const float pv = partner + b1;
+        // (x0, x1) -> (x0 c - x1 s, x1 c + x0 s)   (llm.cpp:181-184)
+        const float p0 = val * c, p1 = pv * s;
+        return (d & 1) == 0 ? p0 - p1 : p0 + p1;
+    }
+};
+
+}  // namespace mh

@@ -1,0 +1,113 @@
+// mh_ll.h -- LL words: the exchange between workgroups of one launch used by
+// the fused decode kernels (gfx950).
+//
+// An LL word is 8 bytes: a 32-bit value and a 32-bit tag, written with one
+// agent-scope store and read with agent-scope loads (both coherent across the
+// XCDs' L2 caches).  The tag is unique to the launch, so a consumer re-reads
+// the words it needs until every tag is current: the data is its own flag --
+// no barrier, counter or fence.  Every wait is bounded by a poll budget.
+#pragma once
+#include "mh_device.h"
+
+namespace mh {
+
+constexpr int kPollBudget = 1 << 16;  // poll rounds per thread and launch (~0.1 s)
+
+__device__ __forceinline__ void ll_put(uint64_t *w, float v, uint32_t tag) {
+    __hip_atomic_store(w, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t ll_load(const uint64_t *w) {
+    return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until words [0, n) of src carry `tag` and copies their values to dst
+// (LDS).  Thread t takes words t, t + 256, ... (at most MAXK); all of its loads
+// are in flight together.  Returns false when the thread's budget runs out.
+template <int MAXK>
+__device__ __forceinline__ bool ll_gather(const uint64_t *src, int n, uint32_t tag, float *dst, int &budget) {
+    const int t = threadIdx.x;
+    uint64_t w[MAXK];
+    uint32_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        w[k] = ll_load(src + min(t + 256 * k, n - 1));
+        if (t + 256 * k < n) pending |= 1u << k;
+    }
+    while (true) {
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k)
+            if (((pending >> k) & 1u) && (uint32_t)(w[k] >> 32) == tag) {
+                dst[t + 256 * k] = __uint_as_float((uint32_t)w[k]);
+                pending &= ~(1u << k);
+            }
+        if (pending == 0) return true;
+        if (--budget < 0) return false;
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) w[k] = ll_load(src + min(t + 256 * k, n - 1));
+    }
+}
+
+// One word per thread (threads with active == false return true at once).
+__device__ __forceinline__ bool ll_wait1(const uint64_t *src, bool active, uint32_t tag, float *dst, int &budget) {
+    if (!active) return true;
+    while (true) {
+        const uint64_t w = ll_load(src);
+        if ((uint32_t)(w >> 32) == tag) {
+            *dst = __uint_as_float((uint32_t)w);
+            return true;
+        }
+        if (--budget < 0) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+// A GEMV stage of a fused launch: workgroup b takes the 4-row groups
+// b * (4 / SPLIT) + w / SPLIT (SPLIT waves per group, each a K slice of one
+// batch of NB blocks per lane), the split of the one-GEMV kernels, so every
+// row is summed in the same order.  prefetch() issues the weight loads before
+// the activation is ready; dot() returns the row sum (valid in every lane of
+// the row, lanes 16*bl + 4*kk + j) once act[] is complete; all waves call it.
+template <int SPLIT, int NB, int K>
+struct GemvStage {
+    static constexpr int nb = K / 32, per = nb / SPLIT;
+    static_assert(per <= 4 * NB && nb % SPLIT == 0, "one batch per wave");
+    uint2 qv[NB];
+    uint16_t dh[NB];
+    int g, ks, b0;
+
+    __device__ __forceinline__ void prefetch(const uint8_t *w, int b) {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        g = b * (4 / SPLIT) + wave / SPLIT;
+        ks = wave % SPLIT;
+        b0 = ks * per;
+        load_batch<NB>(w + (size_t)g * nb * kBlockBytes, b0 + (lane >> 4), b0 + per, lane & 15, (lane & 15) >> 2, qv,
+                       dh);
+    }
+    // row of this lane's result (valid in the storer lanes: ks == 0, lane < 16, j == 0)
+    __device__ __forceinline__ int row() const { return 4 * g + ((threadIdx.x & 15) >> 2); }
+    __device__ __forceinline__ bool storer() const {
+        const int lane = threadIdx.x & 63;
+        return ks == 0 && lane < 16 && (lane & 3) == 0;
+    }
+    __device__ __forceinline__ float dot(const float *act, float (*part)[4]) const {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kk = (lane & 15) >> 2, j = lane & 3;
+        float acc = dot_batch<NB>(act, b0 + (lane >> 4), b0 + per, j, qv, dh, 0.0f);
+        acc = row_lane_sum(acc);
+        if constexpr (SPLIT == 1) {
+            return acc;
+        } else {
+            if (lane < 16 && j == 0) part[wave][kk] = acc;
+            __syncthreads();
+            const int g0 = (wave / SPLIT) * SPLIT;
+            float yv = part[g0][kk];
+#pragma unroll
+            for (int s2 = 1; s2 < SPLIT; ++s2) yv += part[g0 + s2][kk];
+            __syncthreads();
+            return yv;
+        }
+    }
+};
+
+}  // namespace mh

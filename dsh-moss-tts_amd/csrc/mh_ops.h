@@ -255,4 +255,51 @@ hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int pa
                                   float *dst, hipStream_t s);
 hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType kv, float *dst, hipStream_t s);
 
+// ---- one transformer block of the single-stream decode in one launch (decode_layer.hip)
+constexpr int kLayerGrid = 384;          // workgroups; all resident at once
+constexpr int kLayerMaxQuarters = 4;     // attention workgroups per head: keys per launch <= 1024
+constexpr int kLayerWords = 3 * kHidden + kHeads * kLayerMaxQuarters * 66 + kHidden + kFF;  // LL words
+struct LayerArgs {
+    const uint8_t *attn_w = nullptr, *proj_w = nullptr, *fc_in_w = nullptr, *fc_out_w = nullptr;
+    const float *attn_b = nullptr, *proj_b = nullptr, *fc_in_b = nullptr, *fc_out_b = nullptr;
+    const float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+    float *x = nullptr;                        // residual stream: block input, replaced by the block output
+    void *k_cache = nullptr, *v_cache = nullptr;  // this layer's [head][ctx_stride][64]
+    int ctx_stride = 0;
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    const DevState *state = nullptr;           // pos, stop
+    uint64_t *ll = nullptr;                    // kLayerWords exchange words
+    unsigned *err = nullptr;                   // set when a wait runs out
+    int instance = 0;                          // 0..31, distinct for consecutive launches at one position
+};
+// Whether kLayerGrid workgroups of every fused decode kernel fit the device at once.
+hipError_t decode_layer_fits(int device, bool *fits);
+hipError_t launch_decode_layer(const LayerArgs &a, KvType kv, hipStream_t s);
+
+// ---- one local-transformer step (+ the channel's audio head) in one launch (decode_local.hip)
+struct LocalArgs {
+    const uint8_t *attn_w = nullptr, *proj_w = nullptr, *fc_in_w = nullptr, *fc_out_w = nullptr;
+    const float *attn_b = nullptr, *proj_b = nullptr, *fc_in_b = nullptr, *fc_out_b = nullptr;
+    const float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+    const float *lnf_w = nullptr, *lnf_b = nullptr;  // local ln_f (head input)
+    float *lk = nullptr, *lv = nullptr;              // local cache [12][17][64] fp32
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    DevState *state = nullptr;
+    uint64_t *ll = nullptr;
+    unsigned *err = nullptr;
+    int lpos = 0;
+    const float *x_in = nullptr;       // lpos 0: block input (QKV computed here); lpos 1: the raw input row
+    const float *qkv_table = nullptr;  // lpos 1: its q|k|v row; lpos >= 2: [1024][2304] rows of (lpos, code)
+    int ch_in = -1;                    // lpos >= 2: channel of the input code (lpos - 2)
+    const uint8_t *aemb_in = nullptr;  // aemb[ch_in]
+    int pick = 0;                      // 1: greedy pick of ch_in here; 0: the sampler wrote state->row
+    const float *logits_in = nullptr;
+    const int *counts_in = nullptr, *forced = nullptr;
+    float *x_out = nullptr;            // block output (768)
+    const uint8_t *head_w = nullptr;   // aemb[lpos - 1] for the audio head, or null
+    float *logits_out = nullptr;       // [1024]
+};
+hipError_t decode_local_occupancy(int *per_cu);
+hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s);
+
 }  // namespace mh

@@ -84,7 +84,7 @@ bool LlmModel::load(const std::string &path, std::string *err) {
         if (err) *err = "weights file too small or unreadable: " + path;
         return false;
     }
-    moss_hip_llm_options opt{0, 0, 0, 1, 0};
+    moss_hip_llm_options opt{0, 0, 0, 1, 0, 0};
     if (const char *d = std::getenv("MOSS_HIP_DEVICE")) opt.device = std::atoi(d);
     // the reference's switch (gemv.cpp:23-48): MOSS_A16=1/all keeps fp32 activations in the prefill too
     if (const char *a16 = std::getenv("MOSS_A16")) opt.prefill_a16 = (a16[0] == '1' || std::strcmp(a16, "all") == 0);

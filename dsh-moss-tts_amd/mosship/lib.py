@@ -38,7 +38,7 @@ class MossHipError(RuntimeError):
 
 class Options(C.Structure):
     _fields_ = [("device", C.c_int), ("max_ctx", C.c_int), ("kv_dtype", C.c_int), ("use_graphs", C.c_int),
-                ("prefill_a16", C.c_int)]
+                ("prefill_a16", C.c_int), ("decode_kernels", C.c_int)]
 
 
 class SampleParams(C.Structure):
@@ -169,11 +169,12 @@ class HipLLM:
     """Python view of the GPU LlmModel (moss_hip_llm_*)."""
 
     def __init__(self, blob: bytes, device: int = 0, max_ctx: int = 0, kv_fp32: bool = False, graphs: bool = True,
-                 prefill_a16: bool = False):
+                 prefill_a16: bool = False, per_op: bool = False):
         L = self.L = load()
         self._h = C.c_void_p()
         buf = np.frombuffer(blob, dtype=np.uint8)
-        opt = Options(device, max_ctx, 1 if kv_fp32 else 0, 1 if graphs else 0, 1 if prefill_a16 else 0)
+        opt = Options(device, max_ctx, 1 if kv_fp32 else 0, 1 if graphs else 0, 1 if prefill_a16 else 0,
+                      1 if per_op else 0)
         check(L.moss_hip_llm_create(_ptr(buf), buf.size, C.byref(opt), C.byref(self._h)))
 
     def close(self):

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 2
+#define MOSS_HIP_ABI_VERSION 3
 
 enum {
     MOSS_HIP_OK = 0,
@@ -58,6 +58,9 @@ typedef struct {
     int use_graphs; /* 1 = replay the global step and the frame as hipGraphs (default), 0 = direct launches */
     int prefill_a16; /* prefill activations: 0 = W8A8, int8 per 32-block (the reference's prefill unless
                         MOSS_A16 is 1/all, csrc/src/gemv.cpp:23-48, llm.cpp:319-328); 1 = W8A16 fp32 */
+    int decode_kernels; /* global step of the decode: 0 = one kernel per transformer block (default, when
+                           max_ctx <= 1024 and the device holds its 384 workgroups at once), 1 = one kernel
+                           per operator (GEMV / attention).  Same arithmetic per GEMV row. */
 } moss_hip_llm_options;
 
 /* SampleParams (csrc/include/moss/sampler.h:8-22), field for field. */
@@ -90,7 +93,8 @@ int moss_hip_llm_get_hidden(moss_hip_llm *m, float *out768); /* LlmModel::hidden
 int moss_hip_llm_set_hidden(moss_hip_llm *m, const float *in768);
 
 /* LlmModel::prefill (llm.h:50, llm.cpp:327-401): rows [n_rows][17], from `start`.
- * Computed in W8A16 (the reference with MOSS_A16=1). */
+ * W8A8 (activations quantised per 32-block, as the reference's default prefill) unless
+ * opt->prefill_a16 (W8A16, the reference with MOSS_A16=1/all). */
 int moss_hip_llm_prefill(moss_hip_llm *m, const int32_t *rows, int n_rows, int start);
 
 /* LlmModel::global_step (llm.cpp:248-255): embed row -> 12 layers -> ln_f -> hidden; pos += 1. */

@@ -54,12 +54,15 @@ def test_kv_import_export_exact(torch_gpu, prefilled):
         g.close()
 
 
+@pytest.mark.parametrize("per_op", [False, True])
 @pytest.mark.parametrize("kv32", [True, False])
 @pytest.mark.parametrize("graphs", [True, False])
-def test_global_step_vs_oracle(torch_gpu, oracle, prefilled, kv32, graphs):
+def test_global_step_vs_oracle(torch_gpu, oracle, prefilled, kv32, graphs, per_op):
+    """One launch per transformer block (per_op False, the default) and one
+    launch per GEMV / attention (per_op True), with and without graphs."""
     blob, rows, k, v, h = prefilled
-    print(f"global step kv32={kv32} graphs={graphs}", flush=True)
-    g = HipLLM(blob, kv_fp32=kv32, graphs=graphs)
+    print(f"global step kv32={kv32} graphs={graphs} per_op={per_op}", flush=True)
+    g = HipLLM(blob, kv_fp32=kv32, graphs=graphs, per_op=per_op)
     g.kv_import(k, v, h)
     m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=not kv32)
     rng = np.random.default_rng(9)
@@ -80,19 +83,27 @@ def test_global_step_vs_oracle(torch_gpu, oracle, prefilled, kv32, graphs):
     g.close()
 
 
-@pytest.mark.parametrize("ctx", [63, 64, 65, 300, 765])
-def test_global_step_long_context(torch_gpu, oracle, golden_model, ctx):
-    """Split-KV attention (one workgroup per 64-key span, merged in the proj
-    prologue) at span boundaries and long contexts, up to the last positions."""
+@pytest.mark.parametrize("per_op", [False, True])
+@pytest.mark.parametrize("ctx", [0, 1, 63, 64, 65, 255, 256, 300, 765])
+def test_global_step_long_context(torch_gpu, oracle, golden_model, ctx, per_op):
+    """Split-KV attention at span boundaries (64 keys) and at the boundaries of
+    the fused kernel's attention workgroups (256 keys), up to the last positions:
+    per-span workgroups merged in the proj prologue (per_op) and 4-span
+    workgroups merged in the fused block launch."""
     blob, _ = golden_model
     rng = np.random.default_rng(ctx)
     k = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
     v = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
     h = rng.standard_normal(768, dtype=np.float32)
-    print(f"global step at ctx {ctx}", flush=True)
-    g = HipLLM(blob)
-    g.kv_import(k, v, h)
-    m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=True)
+    print(f"global step at ctx {ctx} per_op={per_op}", flush=True)
+    g = HipLLM(blob, per_op=per_op)
+    if ctx:
+        g.kv_import(k, v, h)
+        m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=True)
+    else:  # the first position of an empty cache
+        g.set_hidden(h)
+        m = oracle.model(blob, kv_f16=True)
+        m.set_hidden(h)
     for step in range(2):
         row = np.array([mf.SLOT] + list(rng.integers(0, 1024, 16)), np.int32)
         g.global_step(row)
@@ -236,3 +247,25 @@ def test_model_errors(torch_gpu, golden_model):
     with pytest.raises(lib.MossHipError) as e:
         g.generate(2, SampleParams.make(), forced=bad)
     assert e.value.code == lib.EINVAL
+
+
+def test_fused_blocks_match_per_op(torch_gpu, prefilled):
+    """The global step as one launch per transformer block against one launch
+    per GEMV / attention: every GEMV row is summed in the same order and only
+    the attention merge differs (4-span workgroups vs per-span partials), so
+    the two agree to fp32 rounding and pick the same codes."""
+    blob, rows, k, v, h = prefilled
+    frames = 12
+    outs = []
+    for per_op in (False, True):
+        print(f"generate per_op={per_op}", flush=True)
+        g = HipLLM(blob, per_op=per_op)
+        g.kv_import(k, v, h)
+        out = g.generate(frames, SampleParams.make(greedy=True, min_frames=frames), logits=True)
+        outs.append((out, g.hidden(), g.position))
+        g.close()
+    (a, ha, pa), (b, hb, pb) = outs
+    assert pa == pb
+    assert np.array_equal(a["rows"], b["rows"])
+    assert max_rel(a["logits"], b["logits"]) <= 1e-4
+    assert max_rel(ha, hb) <= 1e-4
