@@ -22,14 +22,14 @@
 // producers in other workgroups): the host checks the kernel's occupancy
 // before it uses this path (two workgroups per CU on 256 CUs).
 //
-// Stage layout (workgroup b, waves w = 0..3; the GEMV stages use the split of
-// the one-GEMV kernels, so every GEMV row is summed in the same order):
-//   Q  b < 288: QKV groups 2b, 2b+1 (2 waves per 4-row group)  -> LL q|k|v
-//   A  288 <= b < 288 + 12*Qs: unit u = b - 288, head u / Qs, waves take the
+// Stage layout (workgroup b of 192, one per CU: two workgroups sharing a CU
+// would halve each other's issue rate, and every stage is a chain of latencies):
+//   Q  b < 144: QKV groups 4b + w (one wave per 4-row group)    -> LL q|k|v
+//   A  144 <= b < 144 + 12*Qs: unit u = b - 144, head u / Qs, waves take the
 //                 64-key spans 4*(u % Qs) + w (their K/V loads are issued at
 //                 the start), merged in the workgroup          -> LL partial (o, m, l)
 //   P  b < 192: proj group b (4 waves), partials merged first   -> LL x + attn
-//   M  every b: fc_in groups 2b, 2b+1, LN2 first                -> LL h
+//   M  b < 192: fc_in groups 4b + w, LN2 first                  -> LL h
 //   F  b < 192: fc_out group b (4 waves)                        -> x (memory)
 #include <type_traits>
 
@@ -64,7 +64,7 @@ constexpr int kLLQ = 0;                            // q | k | v of the new posit
 constexpr int kLLA = kLLQ + 3 * kHidden;           // attention partials, 66 words per unit
 constexpr int kLLX = kLLA + kMaxUnits * 66;        // x after the attention sub-block (768)
 constexpr int kLLH = kLLX + kHidden;               // fc_in output (3072)
-constexpr int kAttnBase = 3 * kHidden / 4 / 2;     // attention workgroups follow the QKV ones (288)
+constexpr int kAttnBase = 3 * kHidden / 4 / 4;     // attention workgroups follow the QKV ones (144)
 static_assert(kAttnBase + kMaxUnits <= kLayerGrid, "attention workgroups inside the grid");
 static_assert(kLLH + kFF == kLayerWords, "LL layout");
 
@@ -136,9 +136,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     int budget = kPollBudget;
     uint64_t *LL = a.ll;
 
-    // ---- stage Q: LN1 + QKV, 2 waves per group
+    // ---- stage Q: LN1 + QKV, one wave per group
     if (b < kAttnBase) {
-        GemvStage<2, 3, kHidden> gs;
+        GemvStage<1, 6, kHidden> gs;
         gs.prefetch(a.attn_w, b);
         const int r = gs.row();
         QkvEpi e;
@@ -376,9 +376,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         STAGE_TS(8);
     }
 
-    // ---- stage M: LN2 + fc_in + gelu_new, 2 waves per group, every workgroup
+    // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
     {
-        GemvStage<2, 3, kHidden> gs;
+        GemvStage<1, 6, kHidden> gs;
         gs.prefetch(a.fc_in_w, b);
         const int r = gs.row();
         const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
@@ -405,6 +405,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const float yv = gs.dot(act, part);
         if (gs.storer()) ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
         STAGE_TS(11);
+        __syncthreads();  // every wave is done with act before stage F gathers into it
     }
 
     // ---- stage F: fc_out + residual (4 waves per group) -> x

@@ -5,7 +5,7 @@
 // channel steps, the channel's audio head (audio_logits, llm.cpp:686-688:
 // logits = aemb[ch] . local_ln_f(x)).  The stages hand their outputs on through
 // LL words (mh_ll.h), as in decode_layer.hip:
-//   Q  lpos 0 only, b < 288: LN1 + QKV of the block input (the global hidden
+//   Q  lpos 0 only, b < 144: LN1 + QKV of the block input (the global hidden
 //      state), RoPE, k/v into the local cache                  -> LL q|k|v
 //   P  b < 192: the step's input -- for lpos >= 2 the code of the previous
 //      channel, picked here (greedy: penalised argmax of its logits, or the
@@ -13,9 +13,11 @@
 //      QKV stage (lpos 0) or from the precomputed row of (lpos, code); the
 //      local attention over keys 0..lpos (every workgroup computes all 12
 //      heads: at most 17 keys); proj + residual                -> LL x + attn
-//   M  every b: LN2 + fc_in + gelu_new                          -> LL h
+//   M  b < 192: LN2 + fc_in + gelu_new                          -> LL h
 //   F  b < 192: fc_out + residual -> x_out (memory) and, with a head, LL x_out
-//   H  b < 256, with a head: local ln_f + the audio head GEMV  -> logits (memory)
+//   H  b < 64, with a head: local ln_f + the audio head GEMV   -> logits (memory)
+// (192 workgroups, one per CU; the GEMV stages take one wave per 4-row group,
+// or four for the K slices of proj and fc_out).
 //
 // Precomputed q|k|v rows.  For lpos >= 1 the block input is an embedding row
 // -- wte[slot] at lpos 1, aemb[lpos - 2][code] at lpos >= 2 -- and RoPE uses
@@ -37,6 +39,22 @@ constexpr int kLH = kLX + kHidden;      // fc_in output
 constexpr int kLO = kLH + kFF;          // block output (head input)
 static_assert(kLO + kHidden <= kLayerWords, "local LL layout fits the exchange buffer");
 
+// Stage timestamps (100 MHz device clock) of the last launch, per workgroup,
+// in builds with -DMH_STAGE_TRACE only.
+#ifdef MH_STAGE_TRACE
+}  // namespace
+__device__ unsigned long long mh_local_ts[kLayerGrid][16];
+namespace {
+#define STAGE_TS(k)                                                                              \
+    do {                                                                                         \
+        if (threadIdx.x == 0) mh_local_ts[blockIdx.x][k] = __builtin_amdgcn_s_memrealtime();     \
+    } while (0)
+#else
+#define STAGE_TS(k) \
+    do {            \
+    } while (0)
+#endif
+
 template <bool LIVE_QKV>
 __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma clang fp contract(off)
@@ -50,6 +68,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     __shared__ int pbi[4];
     __shared__ int used_s;
 
+    STAGE_TS(0);
     DevState *st = a.state;
     if (st->stop) return;  // written only between frames: the same for every workgroup
     const int lpos = a.lpos, n = lpos + 1;
@@ -59,10 +78,10 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     int budget = kPollBudget;
     uint64_t *LL = a.ll;
 
-    // ---- stage Q (lpos 0): LN1 + QKV of the block input, 2 waves per group
+    // ---- stage Q (lpos 0): LN1 + QKV of the block input, one wave per group
     if constexpr (LIVE_QKV) {
-        if (b < 3 * kHidden / 8) {
-            GemvStage<2, 3, kHidden> gs;
+        if (b < 3 * kHidden / 16) {
+            GemvStage<1, 6, kHidden> gs;
             gs.prefetch(a.attn_w, b);
             const int r = gs.row();
             QkvEpi e;
@@ -95,6 +114,10 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 
     // ---- stage P: input, local attention, proj + residual (4 waves per group)
     if (b < kHidden / 4) {
+        // the pick's logits first: loads complete in issue order
+        PickIn pin;
+        const bool picking = !LIVE_QKV && a.ch_in >= 0 && a.pick;
+        if (picking) greedy_pick_load(a.logits_in, a.counts_in, st->rep_penalty, pin);
         GemvStage<4, 2, kHidden> gs;
         gs.prefetch(a.proj_w, b);
         const int r = gs.row();
@@ -133,8 +156,8 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 if (gs.storer()) eres = a.x_in[r];
             } else {
                 int used;
-                if (a.pick) {  // greedy pick of channel ch_in (llm.cpp:689-697)
-                    int idx = greedy_pick_1024(a.logits_in, a.counts_in, st->rep_penalty, pbv, pbi);
+                if (picking) {  // greedy pick of channel ch_in (llm.cpp:689-697)
+                    int idx = greedy_pick_reduce(pin, st->rep_penalty, pbv, pbi);
                     if (idx >= kCodebook) idx = 0;
                     used = st->forced_on ? a.forced[st->frame * kNVq + a.ch_in] : idx;
                     if (b == 0 && t == 0) {
@@ -146,6 +169,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                     __syncthreads();
                     used = used_s;
                 }
+                STAGE_TS(1);
                 row = a.qkv_table + (size_t)used * 3 * kHidden;
                 if (gs.storer()) eres = q8x4_elem(a.aemb_in, kHidden / 32, used, r);  // lookup_row (llm.cpp:697)
             }
@@ -160,6 +184,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 }
             __syncthreads();
         }
+        STAGE_TS(2);
         // local attention (llm.cpp:189-217 over the local cache), in the
         // reference's order: s_p = (q_h . k_p) * 0.125 summed over d in order;
         // e_p = exp(s_p - max), the in-order sum, w_p = e_p * (1 / sum);
@@ -219,13 +244,15 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             act[i] = o;
         }
         __syncthreads();
+        STAGE_TS(3);
         const float yv = gs.dot(act, part);
         if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+        STAGE_TS(4);
     }
 
-    // ---- stage M: LN2 + fc_in + gelu_new, 2 waves per group, every workgroup
+    // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
     {
-        GemvStage<2, 3, kHidden> gs;
+        GemvStage<1, 6, kHidden> gs;
         gs.prefetch(a.fc_in_w, b);
         const int r = gs.row();
         const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
@@ -240,6 +267,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
+        STAGE_TS(5);
         float v[3], o[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
@@ -249,6 +277,8 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         __syncthreads();
         const float yv = gs.dot(act, part);
         if (gs.storer()) ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+        STAGE_TS(6);
+        __syncthreads();  // every wave is done with act before stage F gathers into it
     }
 
     // ---- stage F: fc_out + residual (4 waves per group)
@@ -262,18 +292,20 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
+        STAGE_TS(7);
         const float yv = gs.dot(act, part);
         if (gs.storer()) {
             const float xo = xm[r] + (yv + eb);  // llm.cpp:245
             a.x_out[r] = xo;
             if (a.head_w) ll_put(LL + kLO + r, xo, tag);
         }
+        STAGE_TS(8);
         __syncthreads();
     }
 
     // ---- stage H: local ln_f + audio head (4 waves per group)
-    if (a.head_w && b < kCodebook / 4) {
-        GemvStage<4, 2, kHidden> gs;
+    if (a.head_w && b < kCodebook / 16) {
+        GemvStage<1, 6, kHidden> gs;
         gs.prefetch(a.head_w, b);
         float lw[3], lb[3];
 #pragma unroll
@@ -286,6 +318,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
+        STAGE_TS(9);
         float v[3], o[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
@@ -295,10 +328,18 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         __syncthreads();
         const float yv = gs.dot(act, part);
         if (gs.storer()) a.logits_out[gs.row()] = yv;
+        STAGE_TS(10);
     }
 }
 
 }  // namespace
+
+#ifdef MH_STAGE_TRACE
+// [kLayerGrid][16] timestamps of the last launch (profiling builds only)
+extern "C" int mh_local_trace_read(unsigned long long *out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(mh_local_ts), sizeof(mh_local_ts));
+}
+#endif
 
 hipError_t decode_local_occupancy(int *per_cu) {
     int a = 0, b = 0;

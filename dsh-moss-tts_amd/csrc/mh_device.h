@@ -178,16 +178,26 @@ __device__ __forceinline__ float q8x4_elem(const uint8_t *w, int nb, int r, int 
 // repetition penalty (applied count times, v < 0 ? v * p : v / p), argmax with
 // the lowest index winning ties; kCodebook when every value is NaN (the caller
 // maps that to 0, where the reference's scan stays).  bv / bi: 4 LDS slots.
-__device__ __forceinline__ int greedy_pick_1024(const float *logits, const int *counts, float pen, float *bv, int *bi) {
-#pragma clang fp contract(off)
-    const int t = threadIdx.x;
+// The loads (issued first, so later loads do not delay them) and the reduction.
+struct PickIn {
     float vals[kCodebook / 256];
     int cnt[kCodebook / 256];
+};
+
+__device__ __forceinline__ void greedy_pick_load(const float *logits, const int *counts, float pen, PickIn &in) {
+    const int t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kCodebook / 256; ++k) {  // every load issued before the first use
-        vals[k] = logits[t + 256 * k];
-        cnt[k] = pen != 1.0f ? counts[t + 256 * k] : 0;
+    for (int k = 0; k < kCodebook / 256; ++k) {
+        in.vals[k] = logits[t + 256 * k];
+        in.cnt[k] = pen != 1.0f ? counts[t + 256 * k] : 0;
     }
+}
+
+__device__ __forceinline__ int greedy_pick_reduce(const PickIn &in, float pen, float *bv, int *bi) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x;
+    const float *vals = in.vals;
+    const int *cnt = in.cnt;
     float best = -INFINITY;
     int besti = kCodebook;
 #pragma unroll
@@ -213,6 +223,12 @@ __device__ __forceinline__ int greedy_pick_1024(const float *logits, const int *
             idx = bi[w];
         }
     return idx;
+}
+
+__device__ __forceinline__ int greedy_pick_1024(const float *logits, const int *counts, float pen, float *bv, int *bi) {
+    PickIn in;
+    greedy_pick_load(logits, counts, pen, in);
+    return greedy_pick_reduce(in, pen, bv, bi);
 }
 
 // Block-wide sum for a 256-thread workgroup (4 waves); `red` needs 4 floats.

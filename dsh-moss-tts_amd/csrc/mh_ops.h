@@ -256,7 +256,7 @@ hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int pa
 hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType kv, float *dst, hipStream_t s);
 
 // ---- one transformer block of the single-stream decode in one launch (decode_layer.hip)
-constexpr int kLayerGrid = 384;          // workgroups; all resident at once
+constexpr int kLayerGrid = 192;          // workgroups, one per CU; all resident at once
 constexpr int kLayerMaxQuarters = 4;     // attention workgroups per head: keys per launch <= 1024
 constexpr int kLayerWords = 3 * kHidden + kHeads * kLayerMaxQuarters * 66 + kHidden + kFF;  // LL words
 struct LayerArgs {
