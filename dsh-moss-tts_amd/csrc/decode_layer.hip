@@ -25,9 +25,10 @@
 // Stage layout (workgroup b of 192, one per CU: two workgroups sharing a CU
 // would halve each other's issue rate, and every stage is a chain of latencies):
 //   Q  b < 144: QKV groups 4b + w (one wave per 4-row group)    -> LL q|k|v
-//   A  144 <= b < 144 + 12*Qs: unit u = b - 144, head u / Qs, waves take the
-//                 64-key spans 4*(u % Qs) + w (their K/V loads are issued at
-//                 the start), merged in the workgroup          -> LL partial (o, m, l)
+//   A  144 <= b < 144 + 12*Qs (Qs = min(ceil(spans / 4), 4)): unit u = b - 144,
+//                 head u / Qs, wave w takes the 64-key span 4*(u % Qs) + w (its
+//                 K/V loads issued at the start; past 1024 keys also the spans
+//                 every 4*Qs further), merged in the workgroup -> LL partial (o, m, l)
 //   P  b < 192: proj group b (4 waves), partials merged first   -> LL x + attn
 //   M  b < 192: fc_in groups 4b + w, LN2 first                  -> LL h
 //   F  b < 192: fc_out group b (4 waves)                        -> x (memory)
@@ -124,7 +125,6 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     __shared__ float sc[4][64];
     __shared__ float4 po[4][16];
     __shared__ float pm[4], pl[4];
-    __shared__ float red[4];
     __shared__ float part[4][4];
 
     STAGE_TS(0);
@@ -143,14 +143,15 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int r = gs.row();
         QkvEpi e;
         if (gs.storer()) e.load(a.attn_b, a.rope_cos, a.rope_sin, r, pos);
-        float v[3], o[3], lw[3], lb[3];
+        float o[3], lw[3], lb[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            v[i] = a.x[t + 256 * i];
+            xm[t + 256 * i] = a.x[t + 256 * i];
             lw[i] = a.ln1_w[t + 256 * i];
             lb[i] = a.ln1_b[t + 256 * i];
         }
-        layernorm_768_reg(v, lw, lb, o, red);
+        __syncthreads();
+        layernorm_768_lds(xm, lw, lb, o);
 #pragma unroll
         for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
         __syncthreads();
@@ -176,39 +177,38 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         STAGE_TS(2);
     }
 
-    // ---- stage A: attention of head h over 64-key spans, one per wave
+    // ---- stage A: attention of head h over 64-key spans, one per wave (more,
+    // strided by 4 * Qs, past 1024 keys), online softmax across a wave's spans
     const int n = pos + 1;
     const int spans = (n + 63) >> 6;
-    const int Qs = (spans + 3) >> 2;
+    const int Qs = min((spans + 3) >> 2, kLayerMaxQuarters);
     if (b >= kAttnBase && b < kAttnBase + kHeads * Qs) {
         const int unit = b - kAttnBase;
-        const int h = unit / Qs, span = (unit - h * Qs) * 4 + wave;
-        const int p0 = span * 64, cnt = min(64, n - p0);
-        const bool live = cnt > 0;
+        const int h = unit / Qs, span0 = (unit - h * Qs) * 4 + wave;
         const int pg = lane >> 4, dg = lane & 15;
-        // this lane's score key and V keys; rows at pos (not yet in the cache for
-        // this launch's readers) come from the LL words; cache rows are clamped to
-        // pos - 1 (or 0) so every read is of a row written by an earlier launch
-        const int kkey = p0 + min(lane, max(cnt, 1) - 1);
         const int crow_max = max(pos - 1, 0);
         const size_t hbase = (size_t)h * a.ctx_stride;
-        SpanRaw<KV> raw;
-        {
-            const size_t krow = (hbase + min(kkey, crow_max)) * kHeadDim;
+        // K/V of a span: this lane's score key and V keys; cache rows are
+        // clamped to pos - 1 (or 0), rows written by earlier launches; the key
+        // at pos, and the clamped keys past it, take the LL values in run_span
+        auto load_span = [&](SpanRaw<KV> &r, int span) {
+            const int p0 = span * 64, cnt = max(min(64, n - p0), 1);
+            const size_t krow = (hbase + min(p0 + min(lane, cnt - 1), crow_max)) * kHeadDim;
             if constexpr (KV == KV_F16) {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) raw.k[c] = *(const uint4 *)((const __half *)a.k_cache + krow + 8 * c);
+                for (int c = 0; c < 8; ++c) r.k[c] = *(const uint4 *)((const __half *)a.k_cache + krow + 8 * c);
             } else {
 #pragma unroll
-                for (int c = 0; c < 16; ++c) raw.k[c] = *(const float4 *)((const float *)a.k_cache + krow + 4 * c);
+                for (int c = 0; c < 16; ++c) r.k[c] = *(const float4 *)((const float *)a.k_cache + krow + 4 * c);
             }
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int vkey = p0 + min(pg + 4 * q, max(cnt, 1) - 1);
-                const size_t vi = (hbase + min(vkey, crow_max)) * kHeadDim + 4 * dg;
-                raw.v[q] = *(const typename SpanRaw<KV>::VT *)((const uint8_t *)a.v_cache + vi * (KV == KV_F16 ? 2 : 4));
+                const size_t vi = (hbase + min(p0 + min(pg + 4 * q, cnt - 1), crow_max)) * kHeadDim + 4 * dg;
+                r.v[q] = *(const typename SpanRaw<KV>::VT *)((const uint8_t *)a.v_cache + vi * (KV == KV_F16 ? 2 : 4));
             }
-        }
+        };
+        SpanRaw<KV> raw;
+        load_span(raw, min(span0, spans - 1));  // before q is known
         // q, k, v of head h at pos
         {
             const int seg = t >> 6;
@@ -222,10 +222,10 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         STAGE_TS(3);
         float m = -INFINITY, l = 0.0f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (live) {
-            // the key at pos (and the clamped keys past the live count, which map
-            // to it in the last span) takes the LL values, in KV precision
-            if (kkey == pos) {
+        for (int span = span0; span < spans; span += 4 * Qs) {
+            if (span != span0) load_span(raw, span);
+            const int p0 = span * 64, cnt = min(64, n - p0);
+            if (p0 + min(lane, cnt - 1) == pos) {  // this lane's score key is the new one
                 if constexpr (KV == KV_F16) {
 #pragma unroll
                     for (int c = 0; c < 8; ++c) {
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                     for (int c = 0; c < 16; ++c) raw.k[c] = *(const float4 *)&qkn[kHeadDim + 4 * c];
                 }
             }
-            if (p0 + cnt - 1 == pos) {
+            if (p0 + cnt - 1 == pos) {  // the span holding the new key
                 const typename SpanRaw<KV>::VT nv = to_raw4<KV>(*(const float4 *)&qkn[2 * kHeadDim + 4 * dg]);
 #pragma unroll
                 for (int q = 0; q < 16; ++q)
@@ -251,39 +251,46 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 for (int e = 0; e < 8; ++e) dot = fmaf(qkn[8 * c + e], rawk<KV>(raw, 8 * c + e), dot);
             dot *= 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
             const float smax = wave_max(lane < cnt ? dot : -INFINITY);
-            m = smax;
-            const float e = lane < cnt ? expf(dot - m) : 0.0f;
-            l = wave_sum(e);
+            STAGE_TS(4);
+            const float m_new = fmaxf(m, smax);
+            const float rescale = expf(m - m_new);  // 0 on the first span (m = -inf)
+            const float e = lane < cnt ? expf(dot - m_new) : 0.0f;
+            l = l * rescale + wave_sum(e);
+            m = m_new;
+            o.x *= rescale;
+            o.y *= rescale;
+            o.z *= rescale;
+            o.w *= rescale;
             sc[wave][lane] = e;
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             __builtin_amdgcn_wave_barrier();
-            STAGE_TS(4);
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int i = pg + 4 * q;
                 const float4 v = raw4<KV>(raw.v[q]);
-                const float ei = sc[wave][i];
+                const float ei = sc[wave][pg + 4 * q];
                 o.x = fmaf(ei, v.x, o.x);
                 o.y = fmaf(ei, v.y, o.y);
                 o.z = fmaf(ei, v.z, o.z);
                 o.w = fmaf(ei, v.w, o.w);
             }
-            o.x += xshfl<16>(o.x);
-            o.y += xshfl<16>(o.y);
-            o.z += xshfl<16>(o.z);
-            o.w += xshfl<16>(o.w);
-            o.x += xshfl<32>(o.x);
-            o.y += xshfl<32>(o.y);
-            o.z += xshfl<32>(o.z);
-            o.w += xshfl<32>(o.w);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
         }
+        o.x += xshfl<16>(o.x);
+        o.y += xshfl<16>(o.y);
+        o.z += xshfl<16>(o.z);
+        o.w += xshfl<16>(o.w);
+        o.x += xshfl<32>(o.x);
+        o.y += xshfl<32>(o.y);
+        o.z += xshfl<32>(o.z);
+        o.w += xshfl<32>(o.w);
         if (lane < 16) po[wave][dg] = o;
         if (lane == 0) {
             pm[wave] = m;
             pl[wave] = l;
         }
         __syncthreads();
-        if (wave == 0) {  // log-sum-exp merge of the live waves (a prefix of the workgroup)
+        if (wave == 0) {  // log-sum-exp merge of the waves that saw keys (a prefix)
             const int nlive = min(4, spans - (unit - h * Qs) * 4);
             float wm[4], wl[4], wo[4];
 #pragma unroll
@@ -394,10 +401,8 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             return;
         }
         STAGE_TS(9);
-        float v[3], o[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
-        layernorm_768_reg(v, lw, lb, o, red);
+        float o[3];
+        layernorm_768_lds(xm, lw, lb, o);
 #pragma unroll
         for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
         __syncthreads();
@@ -459,8 +464,8 @@ hipError_t launch_decode_layer(const LayerArgs &a, KvType kv, hipStream_t s) {
     if (!a.attn_w || !a.proj_w || !a.fc_in_w || !a.fc_out_w || !a.x || !a.k_cache || !a.v_cache || !a.state ||
         !a.ll || !a.err || !a.rope_cos || !a.rope_sin)
         return hipErrorInvalidValue;
-    // keys per launch at most 64 * 4 * kLayerMaxQuarters; tag bits: instance < 32
-    if (a.ctx_stride <= 0 || a.ctx_stride > 64 * 4 * kLayerMaxQuarters || a.instance < 0 || a.instance >= 32)
+    // tag bits: instance < 32, position + 1 < 2^27
+    if (a.ctx_stride <= 0 || a.ctx_stride >= (1 << 26) || a.instance < 0 || a.instance >= 32)
         return hipErrorInvalidValue;
     if (kv == KV_F16)
         hipLaunchKernelGGL(decode_layer_kernel<KV_F16>, dim3(kLayerGrid), dim3(256), 0, s, a);

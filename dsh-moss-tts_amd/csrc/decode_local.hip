@@ -62,7 +62,6 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     __shared__ float xm[kHidden];
     __shared__ float qkv[3 * kHidden];             // q | k | v of this position
     __shared__ float sc[kHeads][kLocalLen + 1];
-    __shared__ float red[4];
     __shared__ float part[4][4];
     __shared__ float pbv[4];
     __shared__ int pbi[4];
@@ -86,14 +85,15 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             const int r = gs.row();
             QkvEpi e;
             if (gs.storer()) e.load(a.attn_b, a.rope_cos, a.rope_sin, r, lpos);
-            float v[3], o[3], lw[3], lb[3];
+            float o[3], lw[3], lb[3];
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
-                v[i] = a.x_in[t + 256 * i];
+                xm[t + 256 * i] = a.x_in[t + 256 * i];
                 lw[i] = a.ln1_w[t + 256 * i];
                 lb[i] = a.ln1_b[t + 256 * i];
             }
-            layernorm_768_reg(v, lw, lb, o, red);
+            __syncthreads();
+            layernorm_768_lds(xm, lw, lb, o);
 #pragma unroll
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
@@ -268,10 +268,8 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             return;
         }
         STAGE_TS(5);
-        float v[3], o[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
-        layernorm_768_reg(v, lw, lb, o, red);
+        float o[3];
+        layernorm_768_lds(xm, lw, lb, o);
 #pragma unroll
         for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
         __syncthreads();
@@ -319,10 +317,8 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             return;
         }
         STAGE_TS(9);
-        float v[3], o[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) v[i] = xm[t + 256 * i];
-        layernorm_768_reg(v, lw, lb, o, red);  // normalize(lx, local_lnf) (llm.cpp:262)
+        float o[3];
+        layernorm_768_lds(xm, lw, lb, o);  // normalize(lx, local_lnf) (llm.cpp:262)
 #pragma unroll
         for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
         __syncthreads();

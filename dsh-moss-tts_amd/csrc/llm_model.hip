@@ -176,11 +176,14 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     fmalloc(&logits_, (size_t)kNVq * kCodebook);
     fmalloc(&text_logits_, kVocab);
     hip_check(hipMalloc(&counts_, sizeof(int) * kNVq * kCodebook), "hipMalloc(counts)");
-    if (opt.decode_kernels == 0 && max_ctx_ <= 64 * 4 * kLayerMaxQuarters) {
+    if (opt.decode_kernels == 0) {
         bool fits = false;
         hip_check(decode_layer_fits(device_, &fits), "decode layer occupancy");
         fused_layers_ = fits;
     }
+    // the per-operator global step merges at most 16 split-KV spans in the proj prologue
+    if (!fused_layers_ && max_ctx_ > 64 * 16)
+        throw Status(MOSS_HIP_EUNSUPPORTED, "max_ctx > 1024 needs the fused decode kernels (decode_kernels = 0)");
     if (fused_layers_) {
         hip_check(hipMalloc(&ll_, sizeof(uint64_t) * kLayerWords), "hipMalloc(exchange)");
         hip_check(hipMemset(ll_, 0, sizeof(uint64_t) * kLayerWords), "memset(exchange)");

@@ -263,6 +263,36 @@ __device__ __forceinline__ void layernorm_768_reg(const float (&x)[3], const flo
     }
 }
 
+// LayerNorm of 768 values already in LDS: every wave forms both moments itself
+// (12 values per lane, then a wave sum), so no workgroup barrier is needed;
+// thread t normalises elements t + 256 i.  w, b: this thread's weights.
+__device__ __forceinline__ void layernorm_768_lds(const float *x, const float (&w)[3], const float (&b)[3],
+                                                  float (&out)[3]) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x, lane = t & 63;
+    float xv[kHidden / 64];
+#pragma unroll
+    for (int k = 0; k < kHidden / 64; ++k) xv[k] = x[lane + 64 * k];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kHidden / 64; ++k) s += xv[k];
+    const float mean = wave_sum(s) / (float)kHidden;
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kHidden / 64; ++k) {
+        const float d = xv[k] - mean;
+        v += d * d;
+    }
+    const float var = wave_sum(v) / (float)kHidden;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        float y = (x[t + 256 * i] - mean) * inv;
+        y = y * w[i];
+        out[i] = y + b[i];
+    }
+}
+
 __device__ __forceinline__ void layernorm_768(const float (&x)[3], const float *w, const float *b, float (&out)[3],
                                               float *red) {
     const int t = threadIdx.x;

@@ -257,7 +257,7 @@ hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType k
 
 // ---- one transformer block of the single-stream decode in one launch (decode_layer.hip)
 constexpr int kLayerGrid = 192;          // workgroups, one per CU; all resident at once
-constexpr int kLayerMaxQuarters = 4;     // attention workgroups per head: keys per launch <= 1024
+constexpr int kLayerMaxQuarters = 4;     // attention workgroups per head (4 spans of 64 keys each)
 constexpr int kLayerWords = 3 * kHidden + kHeads * kLayerMaxQuarters * 66 + kHidden + kFF;  // LL words
 struct LayerArgs {
     const uint8_t *attn_w = nullptr, *proj_w = nullptr, *fc_in_w = nullptr, *fc_out_w = nullptr;

@@ -58,9 +58,11 @@ typedef struct {
     int use_graphs; /* 1 = replay the global step and the frame as hipGraphs (default), 0 = direct launches */
     int prefill_a16; /* prefill activations: 0 = W8A8, int8 per 32-block (the reference's prefill unless
                         MOSS_A16 is 1/all, csrc/src/gemv.cpp:23-48, llm.cpp:319-328); 1 = W8A16 fp32 */
-    int decode_kernels; /* global step of the decode: 0 = one kernel per transformer block (default, when
-                           max_ctx <= 1024 and the device holds its 384 workgroups at once), 1 = one kernel
-                           per operator (GEMV / attention).  Same arithmetic per GEMV row. */
+    int decode_kernels; /* single-stream decode: 0 = one launch per transformer block of the global step
+                           and one per local step with its audio head (default, when the device holds the
+                           192 workgroups of a launch at once), 1 = one launch per operator (GEMV /
+                           attention / head).  Both follow the reference's arithmetic per value; they
+                           differ in fp32 summation order only. */
 } moss_hip_llm_options;
 
 /* SampleParams (csrc/include/moss/sampler.h:8-22), field for field. */

@@ -269,3 +269,31 @@ def test_fused_blocks_match_per_op(torch_gpu, prefilled):
     assert np.array_equal(a["rows"], b["rows"])
     assert max_rel(a["logits"], b["logits"]) <= 1e-4
     assert max_rel(ha, hb) <= 1e-4
+
+
+def test_global_step_past_768_keys(torch_gpu, oracle, golden_model):
+    """A cache of 1100 positions filled to 1050: the fused block's attention
+    waves take five 64-key spans each, two past the ones loaded up front.  The
+    per-operator path serves at most 1024 positions and says so at creation."""
+    blob, _ = golden_model
+    with pytest.raises(lib.MossHipError):
+        HipLLM(blob, max_ctx=1100, per_op=True)
+    per_op = False
+    ctx, cap = 1050, 1100
+    rng = np.random.default_rng(5)
+    k = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    h = rng.standard_normal(768, dtype=np.float32)
+    print(f"global step at ctx {ctx} of {cap} per_op={per_op}", flush=True)
+    g = HipLLM(blob, max_ctx=cap, per_op=per_op)
+    g.kv_import(k, v, h)
+    m = oracle.model(blob, max_ctx=cap, kv_f16=True)
+    m.kv_import(k, v)
+    m.set_hidden(h)
+    for step in range(2):
+        row = np.array([mf.SLOT] + list(rng.integers(0, 1024, 16)), np.int32)
+        g.global_step(row)
+        m.global_step(row)
+        assert g.position == m.position == ctx + step + 1
+        assert max_rel(g.hidden(), m.hidden()) <= TOL
+    g.close()
