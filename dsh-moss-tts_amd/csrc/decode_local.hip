@@ -34,7 +34,8 @@ namespace {
 
 // LL regions (words); consecutive launches differ in lpos, so in tag
 constexpr int kLQ = 0;                  // q | k | v (lpos 0)
-constexpr int kLX = kLQ + 3 * kHidden;  // x after the attention sub-block
+constexpr int kLA = kLQ + 3 * kHidden;  // attention output (768) and the step's input code (1)
+constexpr int kLX = kLA + kHidden + 1;  // x after the attention sub-block
 constexpr int kLH = kLX + kHidden;      // fc_in output
 constexpr int kLO = kLH + kFF;          // block output (head input)
 static_assert(kLO + kHidden <= kLayerWords, "local LL layout fits the exchange buffer");
@@ -58,7 +59,7 @@ namespace {
 template <bool LIVE_QKV>
 __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma clang fp contract(off)
-    __shared__ float act[kFF];
+    __shared__ float act[kFF + 1];
     __shared__ float xm[kHidden];
     __shared__ float qkv[3 * kHidden];             // q | k | v of this position
     __shared__ float sc[kHeads][kLocalLen + 1];
@@ -112,49 +113,42 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         }
     }
 
-    // ---- stage P: input, local attention, proj + residual (4 waves per group)
-    if (b < kHidden / 4) {
-        // the pick's logits first: loads complete in issue order
+    // ---- stage A (b < 12): head h = b of the local attention (llm.cpp:189-217
+    // over the local cache, keys 0..lpos) in the reference's order:
+    // s_p = (q_h . k_p) * 0.125 summed over d in order; e_p = exp(s_p - max),
+    // the in-order sum, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] in order.
+    // Wave 0 computes: lane p < 17 a score, lane d the output dimension d.
+    if (b < kHeads) {
+        const int h = b, lane = t & 63;
+        const bool w0 = t < 64;
+        const int kmax = max(lpos - 1, 0);
+        // loads complete in issue order: the pick's logits first
         PickIn pin;
         const bool picking = !LIVE_QKV && a.ch_in >= 0 && a.pick;
         if (picking) greedy_pick_load(a.logits_in, a.counts_in, st->rep_penalty, pin);
-        GemvStage<4, 2, kHidden> gs;
-        gs.prefetch(a.proj_w, b);
-        const int r = gs.row();
-        const float eb = gs.storer() ? a.proj_b[r] : 0.0f;
-        // cache operands of keys 0 .. lpos-1 (written by earlier launches); the
-        // key at lpos, and the clamped ones past it, come from this step's row
-        const int kmax = max(lpos - 1, 0);
-        float vv[3][kLocalLen];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            const int i = t + 256 * k, h = i >> 6, d = i & 63;
-#pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) vv[k][p] = a.lv[((size_t)h * kLocalLen + min(p, kmax)) * kHeadDim + d];
-        }
-        const int hp = t / kLocalLen, pp = t - hp * kLocalLen;  // (head, key) of this thread's score
-        const bool scorer = t < kHeads * kLocalLen;
+        // the cache rows (keys 0 .. lpos-1, written by earlier launches) before
+        // anything else; the key at lpos, and the clamped ones past it, take
+        // this step's row below
         float4 kr[kHeadDim / 4];
-        {
-            const float *row = a.lk + ((size_t)min(hp, kHeads - 1) * kLocalLen + min(pp, kmax)) * kHeadDim;
+        float vv[kLocalLen];
+        if (w0) {
+            const float *krow = a.lk + ((size_t)h * kLocalLen + min(lane, kmax)) * kHeadDim;
 #pragma unroll
-            for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)(row + 4 * c);
+            for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)(krow + 4 * c);
+#pragma unroll
+            for (int p = 0; p < kLocalLen; ++p) vv[p] = a.lv[((size_t)h * kLocalLen + min(p, kmax)) * kHeadDim + lane];
         }
-        // the step's input row and its q | k | v
-        float eres = 0.0f;
+        // q, k, v of head h at lpos
         if constexpr (LIVE_QKV) {
-            if (gs.storer()) eres = a.x_in[r];
-            const bool ok = ll_gather<3 * kHidden / 256>(LL + kLQ, 3 * kHidden, tag, qkv, budget);
+            const int seg = min(t >> 6, 2), i = seg * kHidden + h * kHeadDim + (t & 63);
+            const bool ok = ll_wait1(LL + kLQ + i, t < 3 * kHeadDim, tag, &qkv[i], budget);
             if (__syncthreads_or(!ok)) {
                 if (t == 0) atomicOr(a.err, 1u);
                 return;
             }
         } else {
-            const float *row;
-            if (a.ch_in < 0) {  // lpos 1: wte[slot]
-                row = a.qkv_table;
-                if (gs.storer()) eres = a.x_in[r];
-            } else {
+            const float *row = a.qkv_table;  // lpos 1: wte[slot]
+            if (a.ch_in >= 0) {
                 int used;
                 if (picking) {  // greedy pick of channel ch_in (llm.cpp:689-697)
                     int idx = greedy_pick_reduce(pin, st->rep_penalty, pbv, pbi);
@@ -169,85 +163,93 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                     __syncthreads();
                     used = used_s;
                 }
-                STAGE_TS(1);
+                if (b == 0 && t == 0) ll_put(LL + kLA + kHidden, __int_as_float(used), tag);  // for stage P
                 row = a.qkv_table + (size_t)used * 3 * kHidden;
-                if (gs.storer()) eres = q8x4_elem(a.aemb_in, kHidden / 32, used, r);  // lookup_row (llm.cpp:697)
             }
-#pragma unroll
-            for (int k = 0; k < 3 * kHidden / 256; ++k) qkv[t + 256 * k] = row[t + 256 * k];
-            if (b == 0)  // this position's k, v into the local cache (llm.cpp:224-225), for later steps
-#pragma unroll
-                for (int k = 0; k < kHidden / 256; ++k) {
-                    const int i = t + 256 * k, idx = ((i >> 6) * kLocalLen + lpos) * kHeadDim + (i & 63);
-                    a.lk[idx] = row[kHidden + i];
-                    a.lv[idx] = row[2 * kHidden + i];
-                }
+            STAGE_TS(1);
+            if (t < 3 * kHeadDim) {
+                const int seg = t >> 6, i = seg * kHidden + h * kHeadDim + (t & 63);
+                const float v = row[i];
+                qkv[i] = v;
+                if (seg > 0)  // this position's k, v into the local cache (llm.cpp:224-225), for later steps
+                    (seg == 1 ? a.lk : a.lv)[((size_t)h * kLocalLen + lpos) * kHeadDim + (t & 63)] = v;
+            }
             __syncthreads();
         }
         STAGE_TS(2);
-        // local attention (llm.cpp:189-217 over the local cache), in the
-        // reference's order: s_p = (q_h . k_p) * 0.125 summed over d in order;
-        // e_p = exp(s_p - max), the in-order sum, w_p = e_p * (1 / sum);
-        // o[d] = sum_p w_p v_p[d] in order
-        float dot = 0.0f;
-        if (scorer) {
-            if (min(pp, n - 1) == lpos)
+        if (w0) {
+            const float *qh = &qkv[h * kHeadDim];
+            if (min(lane, n - 1) == lpos)
 #pragma unroll
-                for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)&qkv[kHidden + hp * kHeadDim + 4 * c];
+                for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)&qkv[kHidden + h * kHeadDim + 4 * c];
+            float dot = 0.0f;
 #pragma unroll
             for (int c = 0; c < kHeadDim / 4; ++c) {
-                const float4 qv = *(const float4 *)&qkv[hp * kHeadDim + 4 * c];
+                const float4 qv = *(const float4 *)(qh + 4 * c);
                 dot = dot + qv.x * kr[c].x;
                 dot = dot + qv.y * kr[c].y;
                 dot = dot + qv.z * kr[c].z;
                 dot = dot + qv.w * kr[c].w;
             }
             dot *= 0.125f;
-            sc[hp][pp] = dot;
-        }
-        __syncthreads();
-        float e = 0.0f;
-        if (scorer && pp < n) {
-            float s[kLocalLen];
+            if (lane < kLocalLen) sc[0][lane] = dot;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            float sv[kLocalLen];
 #pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) s[p] = sc[hp][p];
+            for (int p = 0; p < kLocalLen; ++p) sv[p] = sc[0][p];
             float mx = -1e30f;
 #pragma unroll
             for (int p = 0; p < kLocalLen; ++p)
-                if (p < n) mx = fmaxf(mx, s[p]);
-            e = expf(dot - mx);
-        }
-        __syncthreads();
-        if (scorer) sc[hp][pp] = e;
-        __syncthreads();
-        float wgt = 0.0f;  // 0 for keys past n
-        if (scorer) {
-            float s[kLocalLen];
+                if (p < n) mx = fmaxf(mx, sv[p]);
+            const float e = lane < n ? expf(dot - mx) : 0.0f;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (lane < kLocalLen) sc[0][lane] = e;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) s[p] = sc[hp][p];
+            for (int p = 0; p < kLocalLen; ++p) sv[p] = sc[0][p];
             float sum = 0.0f;
 #pragma unroll
             for (int p = 0; p < kLocalLen; ++p)
-                if (p < n) sum += s[p];
-            wgt = e * (1.0f / sum);
-        }
-        __syncthreads();
-        if (scorer) sc[hp][pp] = wgt;
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            const int i = t + 256 * k, h = i >> 6;
-            const float vnew = qkv[2 * kHidden + i];
+                if (p < n) sum += sv[p];
+            const float wgt = e * (1.0f / sum);  // 0 for keys past n
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (lane < kLocalLen) sc[0][lane] = wgt;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            const float vnew = qkv[2 * kHidden + h * kHeadDim + lane];
             float o = 0.0f;
 #pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) o = o + sc[h][p] * (min(p, n - 1) == lpos ? vnew : vv[k][p]);
-            act[i] = o;
+            for (int p = 0; p < kLocalLen; ++p) o = o + sc[0][p] * (min(p, n - 1) == lpos ? vnew : vv[p]);
+            ll_put(LL + kLA + h * kHeadDim + lane, o, tag);
         }
-        __syncthreads();
         STAGE_TS(3);
+        __syncthreads();
+    }
+
+    // ---- stage P: proj + residual (4 waves per group)
+    if (b < kHidden / 4) {
+        GemvStage<4, 2, kHidden> gs;
+        gs.prefetch(a.proj_w, b);
+        const int r = gs.row();
+        const float eb = gs.storer() ? a.proj_b[r] : 0.0f;
+        const bool with_code = !LIVE_QKV && a.ch_in >= 0;  // the raw input row is aemb[ch_in][used]
+        float eres = 0.0f;
+        if (gs.storer() && !with_code) eres = a.x_in[r];
+        const bool ok = ll_gather<(kHidden + 1 + 255) / 256>(LL + kLA, kHidden + (with_code ? 1 : 0), tag, act, budget);
+        if (__syncthreads_or(!ok)) {
+            if (t == 0) atomicOr(a.err, 1u);
+            return;
+        }
+        if (gs.storer() && with_code)  // lookup_row (llm.cpp:697)
+            eres = q8x4_elem(a.aemb_in, kHidden / 32, __float_as_int(act[kHidden]), r);
         const float yv = gs.dot(act, part);
         if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
         STAGE_TS(4);
+        __syncthreads();  // act is reused by stage F
     }
 
     // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
