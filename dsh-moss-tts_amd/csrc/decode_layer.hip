@@ -25,11 +25,13 @@
 // Stage layout (workgroup b of 192, one per CU: two workgroups sharing a CU
 // would halve each other's issue rate, and every stage is a chain of latencies):
 //   Q  b < 144: QKV groups 4b + w (one wave per 4-row group)    -> LL q|k|v
-//   A  144 <= b < 144 + 12*Qs (Qs = min(ceil(spans / 4), 4)): unit u = b - 144,
-//                 head u / Qs, wave w takes the 64-key span 4*(u % Qs) + w (its
-//                 K/V loads issued at the start; past 1024 keys also the spans
-//                 every 4*Qs further), merged in the workgroup -> LL partial (o, m, l)
-//   P  b < 192: proj group b (4 waves), partials merged first   -> LL x + attn
+//   A  144 <= b < 144 + 12*Qs: unit u = b - 144 = (head u / Qs, quarter
+//                 u % Qs); wave w takes the 64-key spans 4*(u % Qs) + w + 4*Qs*i,
+//                 NS per round with all their K/V loads in flight (the first
+//                 round's issued at the start); Qs = 1 while the keys fit one
+//                 round of 4 waves (768 keys in fp16)        -> LL head output,
+//                 more quarters (longer contexts)            -> LL partial (o, m, l)
+//   P  b < 192: proj group b (4 waves), partials merged first  -> LL x + attn
 //   M  b < 192: fc_in groups 4b + w, LN2 first                  -> LL h
 //   F  b < 192: fc_out group b (4 waves)                        -> x (memory)
 #include <type_traits>
@@ -47,15 +49,35 @@ namespace {
 // shipped has none of it).
 #ifdef MH_STAGE_TRACE
 }  // namespace
-__device__ unsigned long long mh_stage_ts[kLayerGrid][16];
+__device__ unsigned long long mh_stage_ts[kLayerGrid][32];
 namespace {
-#define STAGE_TS(k)                                                                              \
-    do {                                                                                         \
-        if (threadIdx.x == 0) mh_stage_ts[blockIdx.x][k] = __builtin_amdgcn_s_memrealtime();     \
+// Kept in LDS by thread 0 and written out at the end of the launch: a global
+// store inside a stage would make the next barrier wait for it.
+#define STAGE_DECL                                         \
+    __shared__ unsigned long long stage_ts_lds[32];        \
+    if (threadIdx.x == 0)                                  \
+        for (int i_ = 0; i_ < 32; ++i_) stage_ts_lds[i_] = i_ == 16 ? __builtin_amdgcn_s_memtime() : 0
+#define STAGE_TS(k)                                                               \
+    do {                                                                          \
+        if (threadIdx.x == 0) stage_ts_lds[k] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define STAGE_FLUSH()                                                          \
+    do {                                                                       \
+        if (threadIdx.x == 0) {                                                \
+            stage_ts_lds[17] = __builtin_amdgcn_s_memtime();                   \
+            stage_ts_lds[18] = __builtin_amdgcn_s_memrealtime();               \
+            for (int i_ = 0; i_ < 32; ++i_) mh_stage_ts[blockIdx.x][i_] = stage_ts_lds[i_]; \
+        }                                                                      \
     } while (0)
 #else
+#define STAGE_DECL \
+    do {           \
+    } while (0)
 #define STAGE_TS(k) \
     do {            \
+    } while (0)
+#define STAGE_FLUSH() \
+    do {              \
     } while (0)
 #endif
 
@@ -67,6 +89,19 @@ constexpr int kLLX = kLLA + kMaxUnits * 66;        // x after the attention sub-
 constexpr int kLLH = kLLX + kHidden;               // fc_in output (3072)
 constexpr int kAttnBase = 3 * kHidden / 4 / 4;     // attention workgroups follow the QKV ones (144)
 static_assert(kAttnBase + kMaxUnits <= kLayerGrid, "attention workgroups inside the grid");
+
+// 64-key spans a wave holds in registers at once (K and V: 64 VGPRs per span
+// in fp16, 128 in fp32), and the attention workgroups per head for n keys:
+// one up to 4 * NS spans (768 keys in fp16), at most kLayerMaxQuarters.
+template <int KV>
+constexpr int kAttnSpansPerWave = KV == KV_F16 ? 3 : 1;
+template <int KV>
+constexpr int kLanesPerKey = KV == KV_F16 ? 8 : 16;  // 16-byte K loads per 64-dim key
+template <int KV>
+__device__ __forceinline__ int attn_quarters(int n) {
+    constexpr int per = 4 * kAttnSpansPerWave<KV>;
+    return min((((n + 63) >> 6) + per - 1) / per, kLayerMaxQuarters);
+}
 static_assert(kLLH + kFF == kLayerWords, "LL layout");
 
 // Raw K/V operands of one wave's 64-key span, loaded before the query is known.
@@ -104,13 +139,34 @@ __device__ __forceinline__ typename SpanRaw<KV>::VT to_raw4(float4 f) {
 }
 
 template <int KV>
-__device__ __forceinline__ float rawk(const SpanRaw<KV> &r, int i) {  // element i (0..63) of the K row
+__device__ __forceinline__ float rawk(const SpanRaw<KV> &r, int c, int e) {  // element e of K load c
     if constexpr (KV == KV_F16) {
-        const __half *h = (const __half *)&r.k[i >> 3];
-        return __half2float(h[i & 7]);
+        const __half *h = (const __half *)&r.k[c];
+        return __half2float(h[e]);
     } else {
-        const float *f = (const float *)&r.k[i >> 2];
-        return f[i & 3];
+        const float *f = (const float *)&r.k[c];
+        return f[e];
+    }
+}
+
+// Sum over the L lanes of a key (lanes differing in the low log2(L) bits of
+// `sub`) of L partial dots at once: each step keeps half of the values and
+// adds the partner's copy of them, so lane sub ends with the total of pd[sub].
+template <int L>
+__device__ __forceinline__ float key_reduce(float (&pd)[L], int sub) {
+    if constexpr (L == 1) {
+        return pd[0];
+    } else {
+        constexpr int H = L / 2;
+        const bool upper = (sub & H) != 0;
+        float nx[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float keep = upper ? pd[i + H] : pd[i];
+            const float give = upper ? pd[i] : pd[i + H];
+            nx[i] = keep + xshfl<H>(give);
+        }
+        return key_reduce<H>(nx, sub);
     }
 }
 
@@ -122,11 +178,15 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     __shared__ float pbuf[kMaxUnits * 66];     // gathered attention partials
     __shared__ float qkn[3 * kHeadDim];        // q, k, v of the new position for this head
     __shared__ float hw[kHeads][kLayerMaxQuarters + 1];  // per-head merge weights and denominator
-    __shared__ float sc[4][64];
+    __shared__ float sc[4][kAttnSpansPerWave<KV>][64];
     __shared__ float4 po[4][16];
     __shared__ float pm[4], pl[4];
     __shared__ float part[4][4];
 
+    __shared__ int wait_failed;  // set when a wait of this workgroup runs out
+    if (threadIdx.x == 0) wait_failed = 0;
+    __syncthreads();
+    STAGE_DECL;
     STAGE_TS(0);
     if (a.state->stop) return;  // written only between frames: the same for every workgroup
     const int pos = a.state->pos;
@@ -177,29 +237,40 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         STAGE_TS(2);
     }
 
-    // ---- stage A: attention of head h over 64-key spans, one per wave (more,
-    // strided by 4 * Qs, past 1024 keys), online softmax across a wave's spans
+    // ---- stage A: attention of head h.  Unit u = (head, quarter) of 12 * Qs;
+    // wave w of quarter qq takes the 64-key spans qq*4 + w + 4*Qs*i, NS of them
+    // per round with all their K/V loads in flight together; online softmax
+    // across the rounds.  Qs == 1 (contexts up to 4 * NS spans) hands on the
+    // normalised head output, more quarters hand on partials (o, m, l).
+    constexpr int NS = kAttnSpansPerWave<KV>;
     const int n = pos + 1;
     const int spans = (n + 63) >> 6;
-    const int Qs = min((spans + 3) >> 2, kLayerMaxQuarters);
+    const int Qs = attn_quarters<KV>(n);
     if (b >= kAttnBase && b < kAttnBase + kHeads * Qs) {
         const int unit = b - kAttnBase;
-        const int h = unit / Qs, span0 = (unit - h * Qs) * 4 + wave;
+        const int h = unit / Qs, qq = unit - h * Qs;
+        const int span0 = qq * 4 + wave, stride = 4 * Qs;
         const int pg = lane >> 4, dg = lane & 15;
+        constexpr int EPL = 64 / kLanesPerKey<KV>, RPI = 64 / kLanesPerKey<KV>;  // K dims per lane, keys per load
+        const int sub = lane & (kLanesPerKey<KV> - 1), rr = lane / kLanesPerKey<KV>;
+        const int kl = RPI * sub + rr;  // the key (within a span) whose score this lane ends with
         const int crow_max = max(pos - 1, 0);
         const size_t hbase = (size_t)h * a.ctx_stride;
         // K/V of a span: this lane's score key and V keys; cache rows are
         // clamped to pos - 1 (or 0), rows written by earlier launches; the key
-        // at pos, and the clamped keys past it, take the LL values in run_span
+        // at pos, and the clamped keys past it, take the LL values below
+        // K of a span: load c brings 16 bytes of key RPI*c + rr (dims sub*EPL ..),
+        // so one load covers RPI whole 128/256-byte rows; V: lane (pg, dg) keys
+        // pg + 4q, dims 4dg .. 4dg+3.  Cache rows are clamped to pos - 1 (or 0),
+        // rows written by earlier launches; the key at pos, and the clamped keys
+        // past it, take this launch's k and v below.
         auto load_span = [&](SpanRaw<KV> &r, int span) {
             const int p0 = span * 64, cnt = max(min(64, n - p0), 1);
-            const size_t krow = (hbase + min(p0 + min(lane, cnt - 1), crow_max)) * kHeadDim;
-            if constexpr (KV == KV_F16) {
 #pragma unroll
-                for (int c = 0; c < 8; ++c) r.k[c] = *(const uint4 *)((const __half *)a.k_cache + krow + 8 * c);
-            } else {
-#pragma unroll
-                for (int c = 0; c < 16; ++c) r.k[c] = *(const float4 *)((const float *)a.k_cache + krow + 4 * c);
+            for (int c = 0; c < kLanesPerKey<KV>; ++c) {
+                const int key = min(p0 + min(RPI * c + rr, cnt - 1), crow_max);
+                const size_t ki = (hbase + key) * kHeadDim + sub * EPL;
+                r.k[c] = *(const typename SpanRaw<KV>::KT *)((const uint8_t *)a.k_cache + ki * (KV == KV_F16 ? 2 : 4));
             }
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
@@ -207,14 +278,15 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 r.v[q] = *(const typename SpanRaw<KV>::VT *)((const uint8_t *)a.v_cache + vi * (KV == KV_F16 ? 2 : 4));
             }
         };
-        SpanRaw<KV> raw;
-        load_span(raw, min(span0, spans - 1));  // before q is known
+        SpanRaw<KV> raw[NS];
+#pragma unroll
+        for (int i = 0; i < NS; ++i) load_span(raw[i], min(span0 + stride * i, spans - 1));  // before q is known
         // q, k, v of head h at pos
         {
             const int seg = t >> 6;
             const bool ok = ll_wait1(LL + kLLQ + seg * kHidden + h * kHeadDim + (t & 63), t < 3 * kHeadDim, tag,
                                      &qkn[min(t, 3 * kHeadDim - 1)], budget);
-            if (__syncthreads_or(!ok)) {
+            if (sync_failed(!ok, &wait_failed)) {
                 if (t == 0) atomicOr(a.err, 1u);
                 return;
             }
@@ -222,60 +294,89 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         STAGE_TS(3);
         float m = -INFINITY, l = 0.0f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int span = span0; span < spans; span += 4 * Qs) {
-            if (span != span0) load_span(raw, span);
-            const int p0 = span * 64, cnt = min(64, n - p0);
-            if (p0 + min(lane, cnt - 1) == pos) {  // this lane's score key is the new one
-                if constexpr (KV == KV_F16) {
+        for (int c0 = span0; c0 < spans; c0 += NS * stride) {
+            if (c0 != span0) {
 #pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        const typename SpanRaw<KV>::VT lo = to_raw4<KV>(*(const float4 *)&qkn[kHeadDim + 8 * c]);
-                        const typename SpanRaw<KV>::VT hi = to_raw4<KV>(*(const float4 *)&qkn[kHeadDim + 8 * c + 4]);
-                        raw.k[c] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                    }
-                } else {
+                for (int i = 0; i < NS; ++i) load_span(raw[i], min(c0 + stride * i, spans - 1));
+            }
+            float qs[EPL];
 #pragma unroll
-                    for (int c = 0; c < 16; ++c) raw.k[c] = *(const float4 *)&qkn[kHeadDim + 4 * c];
+            for (int e = 0; e < EPL; ++e) qs[e] = qkn[sub * EPL + e];
+            STAGE_TS(20);
+            float dot[NS];
+            int cnt[NS];
+            float smax = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                const int span = c0 + stride * i;
+                const int p0 = span * 64;
+                cnt[i] = span < spans ? min(64, n - p0) : 0;
+                float pd[kLanesPerKey<KV>];
+#pragma unroll
+                for (int c = 0; c < kLanesPerKey<KV>; ++c) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) d = fmaf(qs[e], rawk<KV>(raw[i], c, e), d);
+                    pd[c] = d;
                 }
+                float d = key_reduce<kLanesPerKey<KV>>(pd, sub);  // q . k of key kl
+                if (span == spans - 1) {  // the span holding the new key: its k and v from this launch
+                    const float snew = wave_sum(qkn[lane] * qkn[kHeadDim + lane]);
+                    if (kl == pos - p0) d = snew;
+                    const typename SpanRaw<KV>::VT nv = to_raw4<KV>(*(const float4 *)&qkn[2 * kHeadDim + 4 * dg]);
+#pragma unroll
+                    for (int q = 0; q < 16; ++q)
+                        if (pg + 4 * q >= cnt[i] - 1) raw[i].v[q] = nv;
+                }
+                dot[i] = d * 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
+                if (kl < cnt[i]) smax = fmaxf(smax, dot[i]);
             }
-            if (p0 + cnt - 1 == pos) {  // the span holding the new key
-                const typename SpanRaw<KV>::VT nv = to_raw4<KV>(*(const float4 *)&qkn[2 * kHeadDim + 4 * dg]);
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    if (pg + 4 * q >= cnt - 1) raw.v[q] = nv;
-            }
-            float dot = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dot = fmaf(qkn[8 * c + e], rawk<KV>(raw, 8 * c + e), dot);
-            dot *= 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
-            const float smax = wave_max(lane < cnt ? dot : -INFINITY);
+            smax = wave_max(smax);
             STAGE_TS(4);
             const float m_new = fmaxf(m, smax);
-            const float rescale = expf(m - m_new);  // 0 on the first span (m = -inf)
-            const float e = lane < cnt ? expf(dot - m_new) : 0.0f;
-            l = l * rescale + wave_sum(e);
+            const float rescale = expf(m - m_new);  // 0 on the first round (m = -inf)
+            float esum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                const float e = kl < cnt[i] ? expf(dot[i] - m_new) : 0.0f;
+                esum += e;
+                sc[wave][i][kl] = e;
+            }
+            l = l * rescale + wave_sum(esum);
+            STAGE_TS(21);
             m = m_new;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            float4 os[NS];  // one accumulator per span: independent FMA chains
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                os[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (cnt[i] == 0) continue;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const float4 v = raw4<KV>(raw[i].v[q]);
+                    const float ei = sc[wave][i][pg + 4 * q];
+                    os[i].x = fmaf(ei, v.x, os[i].x);
+                    os[i].y = fmaf(ei, v.y, os[i].y);
+                    os[i].z = fmaf(ei, v.z, os[i].z);
+                    os[i].w = fmaf(ei, v.w, os[i].w);
+                }
+            }
             o.x *= rescale;
             o.y *= rescale;
             o.z *= rescale;
             o.w *= rescale;
-            sc[wave][lane] = e;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const float4 v = raw4<KV>(raw.v[q]);
-                const float ei = sc[wave][pg + 4 * q];
-                o.x = fmaf(ei, v.x, o.x);
-                o.y = fmaf(ei, v.y, o.y);
-                o.z = fmaf(ei, v.z, o.z);
-                o.w = fmaf(ei, v.w, o.w);
+            for (int i = 0; i < NS; ++i) {
+                o.x += os[i].x;
+                o.y += os[i].y;
+                o.z += os[i].z;
+                o.w += os[i].w;
             }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             __builtin_amdgcn_wave_barrier();
         }
+        STAGE_TS(22);
         o.x += xshfl<16>(o.x);
         o.y += xshfl<16>(o.y);
         o.z += xshfl<16>(o.z);
@@ -291,7 +392,8 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         }
         __syncthreads();
         if (wave == 0) {  // log-sum-exp merge of the waves that saw keys (a prefix)
-            const int nlive = min(4, spans - (unit - h * Qs) * 4);
+            STAGE_TS(23);
+            const int nlive = min(4, spans - qq * 4);
             float wm[4], wl[4], wo[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {  // every LDS read issued before the first use
@@ -311,11 +413,15 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                     L = fmaf(wl[w], sw, L);
                     O = fmaf(wo[w], sw, O);
                 }
-            uint64_t *dst = LL + kLLA + (size_t)unit * 66;
-            ll_put(dst + lane, O, tag);
-            if (lane == 0) {
-                ll_put(dst + 64, M, tag);
-                ll_put(dst + 65, L, tag);
+            if (Qs == 1) {  // the head's output
+                ll_put(LL + kLLA + h * kHeadDim + lane, O / L, tag);
+            } else {
+                uint64_t *dst = LL + kLLA + (size_t)unit * 66;
+                ll_put(dst + lane, O, tag);
+                if (lane == 0) {
+                    ll_put(dst + 64, M, tag);
+                    ll_put(dst + 65, L, tag);
+                }
             }
             STAGE_TS(5);
         }
@@ -331,52 +437,61 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             eb = a.proj_b[r];
             eres = a.x[r];
         }
-        const int units = kHeads * Qs;
-        const bool ok = ll_gather<(kMaxUnits * 66 + 255) / 256>(LL + kLLA, units * 66, tag, pbuf, budget);
-        if (__syncthreads_or(!ok)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        STAGE_TS(6);
-        // o = sum_q e^(m_q - M) o_q / sum_q e^(m_q - M) l_q: the weights e^(m_q - M)
-        // and the denominator once per head (thread h), then every output
-        if (t < kHeads) {
-            const float *pp = pbuf + (size_t)t * Qs * 66;
-            float mq[kLayerMaxQuarters], lq[kLayerMaxQuarters];
-#pragma unroll
-            for (int q = 0; q < kLayerMaxQuarters; ++q) {
-                const int qq = min(q, Qs - 1);
-                mq[q] = pp[qq * 66 + 64];
-                lq[q] = pp[qq * 66 + 65];
+        if (Qs == 1) {  // the heads' outputs, ready to use
+            const bool ok = ll_gather<3>(LL + kLLA, kHidden, tag, act, budget);
+            if (sync_failed(!ok, &wait_failed)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
             }
-            float M = mq[0];
-#pragma unroll
-            for (int q = 1; q < kLayerMaxQuarters; ++q)
-                if (q < Qs) M = fmaxf(M, mq[q]);
-            float L = 0.0f;
-#pragma unroll
-            for (int q = 0; q < kLayerMaxQuarters; ++q) {
-                const float sw = q < Qs ? expf(mq[q] - M) : 0.0f;
-                if (q < Qs) L = fmaf(lq[q], sw, L);
-                hw[t][q] = sw;
+            STAGE_TS(6);
+        } else {
+            const int units = kHeads * Qs;
+            const bool ok = ll_gather<(kMaxUnits * 66 + 255) / 256>(LL + kLLA, units * 66, tag, pbuf, budget);
+            if (sync_failed(!ok, &wait_failed)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
             }
-            hw[t][kLayerMaxQuarters] = L;
+            STAGE_TS(6);
+            // o = sum_q e^(m_q - M) o_q / sum_q e^(m_q - M) l_q: the weights e^(m_q - M)
+            // and the denominator once per head (thread h), then every output
+            if (t < kHeads) {
+                const float *pp = pbuf + (size_t)t * Qs * 66;
+                float mq[kLayerMaxQuarters], lq[kLayerMaxQuarters];
+#pragma unroll
+                for (int q = 0; q < kLayerMaxQuarters; ++q) {
+                    const int qq = min(q, Qs - 1);
+                    mq[q] = pp[qq * 66 + 64];
+                    lq[q] = pp[qq * 66 + 65];
+                }
+                float M = mq[0];
+#pragma unroll
+                for (int q = 1; q < kLayerMaxQuarters; ++q)
+                    if (q < Qs) M = fmaxf(M, mq[q]);
+                float L = 0.0f;
+#pragma unroll
+                for (int q = 0; q < kLayerMaxQuarters; ++q) {
+                    const float sw = q < Qs ? expf(mq[q] - M) : 0.0f;
+                    if (q < Qs) L = fmaf(lq[q], sw, L);
+                    hw[t][q] = sw;
+                }
+                hw[t][kLayerMaxQuarters] = L;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i3 = 0; i3 < 3; ++i3) {
+                const int i = t + 256 * i3, h = i >> 6, d = i & 63;
+                const float *pp = pbuf + (size_t)h * Qs * 66;
+                float oq[kLayerMaxQuarters];
+#pragma unroll
+                for (int q = 0; q < kLayerMaxQuarters; ++q) oq[q] = pp[min(q, Qs - 1) * 66 + d];
+                float O = 0.0f;
+#pragma unroll
+                for (int q = 0; q < kLayerMaxQuarters; ++q)
+                    if (q < Qs) O = fmaf(oq[q], hw[h][q], O);
+                act[i] = O / hw[h][kLayerMaxQuarters];
+            }
+            __syncthreads();
         }
-        __syncthreads();
-#pragma unroll
-        for (int i3 = 0; i3 < 3; ++i3) {
-            const int i = t + 256 * i3, h = i >> 6, d = i & 63;
-            const float *pp = pbuf + (size_t)h * Qs * 66;
-            float oq[kLayerMaxQuarters];
-#pragma unroll
-            for (int q = 0; q < kLayerMaxQuarters; ++q) oq[q] = pp[min(q, Qs - 1) * 66 + d];
-            float O = 0.0f;
-#pragma unroll
-            for (int q = 0; q < kLayerMaxQuarters; ++q)
-                if (q < Qs) O = fmaf(oq[q], hw[h][q], O);
-            act[i] = O / hw[h][kLayerMaxQuarters];
-        }
-        __syncthreads();
         STAGE_TS(7);
         const float yv = gs.dot(act, part);
         if (gs.storer()) ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
@@ -396,7 +511,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             lb[i] = a.ln2_b[t + 256 * i];
         }
         const bool ok = ll_gather<3>(LL + kLLX, kHidden, tag, xm, budget);
-        if (__syncthreads_or(!ok)) {
+        if (sync_failed(!ok, &wait_failed)) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
@@ -420,7 +535,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int r = gs.row();
         const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
         const bool ok = ll_gather<kFF / 256>(LL + kLLH, kFF, tag, act, budget);
-        if (__syncthreads_or(!ok)) {
+        if (sync_failed(!ok, &wait_failed)) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
@@ -429,6 +544,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         if (gs.storer()) a.x[r] = xm[r] + (yv + eb);  // llm.cpp:245
         STAGE_TS(13);
     }
+    STAGE_FLUSH();
 }
 
 }  // namespace
@@ -453,7 +569,7 @@ hipError_t decode_layer_fits(int device, bool *fits) {
 }
 
 #ifdef MH_STAGE_TRACE
-// [kLayerGrid][16] timestamps of the last launch (profiling builds only)
+// [kLayerGrid][32] timestamps of the last launch (profiling builds only)
 extern "C" int mh_stage_trace_read(unsigned long long *out) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(mh_stage_ts), sizeof(mh_stage_ts));
 }

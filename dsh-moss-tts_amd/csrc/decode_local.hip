@@ -44,15 +44,35 @@ static_assert(kLO + kHidden <= kLayerWords, "local LL layout fits the exchange b
 // in builds with -DMH_STAGE_TRACE only.
 #ifdef MH_STAGE_TRACE
 }  // namespace
-__device__ unsigned long long mh_local_ts[kLayerGrid][16];
+__device__ unsigned long long mh_local_ts[kLayerGrid][32];
 namespace {
-#define STAGE_TS(k)                                                                              \
-    do {                                                                                         \
-        if (threadIdx.x == 0) mh_local_ts[blockIdx.x][k] = __builtin_amdgcn_s_memrealtime();     \
+// Kept in LDS by thread 0 and written out at the end of the launch: a global
+// store inside a stage would make the next barrier wait for it.
+#define STAGE_DECL                                         \
+    __shared__ unsigned long long stage_ts_lds[32];        \
+    if (threadIdx.x == 0)                                  \
+        for (int i_ = 0; i_ < 32; ++i_) stage_ts_lds[i_] = i_ == 16 ? __builtin_amdgcn_s_memtime() : 0
+#define STAGE_TS(k)                                                               \
+    do {                                                                          \
+        if (threadIdx.x == 0) stage_ts_lds[k] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define STAGE_FLUSH()                                                          \
+    do {                                                                       \
+        if (threadIdx.x == 0) {                                                \
+            stage_ts_lds[17] = __builtin_amdgcn_s_memtime();                   \
+            stage_ts_lds[18] = __builtin_amdgcn_s_memrealtime();               \
+            for (int i_ = 0; i_ < 32; ++i_) mh_local_ts[blockIdx.x][i_] = stage_ts_lds[i_]; \
+        }                                                                      \
     } while (0)
 #else
+#define STAGE_DECL \
+    do {           \
+    } while (0)
 #define STAGE_TS(k) \
     do {            \
+    } while (0)
+#define STAGE_FLUSH() \
+    do {              \
     } while (0)
 #endif
 
@@ -68,6 +88,10 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     __shared__ int pbi[4];
     __shared__ int used_s;
 
+    __shared__ int wait_failed;  // set when a wait of this workgroup runs out
+    if (threadIdx.x == 0) wait_failed = 0;
+    __syncthreads();
+    STAGE_DECL;
     STAGE_TS(0);
     DevState *st = a.state;
     if (st->stop) return;  // written only between frames: the same for every workgroup
@@ -142,7 +166,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         if constexpr (LIVE_QKV) {
             const int seg = min(t >> 6, 2), i = seg * kHidden + h * kHeadDim + (t & 63);
             const bool ok = ll_wait1(LL + kLQ + i, t < 3 * kHeadDim, tag, &qkv[i], budget);
-            if (__syncthreads_or(!ok)) {
+            if (sync_failed(!ok, &wait_failed)) {
                 if (t == 0) atomicOr(a.err, 1u);
                 return;
             }
@@ -240,7 +264,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         float eres = 0.0f;
         if (gs.storer() && !with_code) eres = a.x_in[r];
         const bool ok = ll_gather<(kHidden + 1 + 255) / 256>(LL + kLA, kHidden + (with_code ? 1 : 0), tag, act, budget);
-        if (__syncthreads_or(!ok)) {
+        if (sync_failed(!ok, &wait_failed)) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
@@ -265,7 +289,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             lb[i] = a.ln2_b[t + 256 * i];
         }
         const bool ok = ll_gather<3>(LL + kLX, kHidden, tag, xm, budget);
-        if (__syncthreads_or(!ok)) {
+        if (sync_failed(!ok, &wait_failed)) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
@@ -288,7 +312,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         const int r = gs.row();
         const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
         const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
-        if (__syncthreads_or(!ok)) {
+        if (sync_failed(!ok, &wait_failed)) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
@@ -314,7 +338,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             lb[i] = a.lnf_b[t + 256 * i];
         }
         const bool ok = ll_gather<3>(LL + kLO, kHidden, tag, xm, budget);
-        if (__syncthreads_or(!ok)) {
+        if (sync_failed(!ok, &wait_failed)) {
             if (t == 0) atomicOr(a.err, 1u);
             return;
         }
@@ -328,12 +352,13 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         if (gs.storer()) a.logits_out[gs.row()] = yv;
         STAGE_TS(10);
     }
+    STAGE_FLUSH();
 }
 
 }  // namespace
 
 #ifdef MH_STAGE_TRACE
-// [kLayerGrid][16] timestamps of the last launch (profiling builds only)
+// [kLayerGrid][32] timestamps of the last launch (profiling builds only)
 extern "C" int mh_local_trace_read(unsigned long long *out) {
     return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(mh_local_ts), sizeof(mh_local_ts));
 }

@@ -49,6 +49,17 @@ __device__ __forceinline__ bool ll_gather(const uint64_t *src, int n, uint32_t t
     }
 }
 
+// Workgroup barrier that also tells every thread whether any thread failed its
+// wait: one barrier and one LDS read (__syncthreads_or costs three barriers and
+// a dispatch-packet load).  *flag is an LDS word the launch sets to 0, behind a
+// barrier, before any wait, and that is only ever set to 1 afterwards (a failed
+// wait ends the launch).
+__device__ __forceinline__ bool sync_failed(bool failed, volatile int *flag) {
+    if (failed) *flag = 1;
+    __syncthreads();
+    return *flag != 0;
+}
+
 // One word per thread (threads with active == false return true at once).
 __device__ __forceinline__ bool ll_wait1(const uint64_t *src, bool active, uint32_t tag, float *dst, int &budget) {
     if (!active) return true;
