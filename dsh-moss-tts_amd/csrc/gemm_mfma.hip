@@ -9,15 +9,15 @@
 // Lane l holds A[row l%16][k 8(l/16)..+7], B[k 8(l/16)..+7][col l%16] and gets
 // D[row 4(l/16)+i][col l%16].  B is the weight row n = col: 8 consecutive int8
 // of one row of the 4x4 block (one 8-byte load), exact in fp16.  A is the fp32
-// activation split as x = hi + lo with hi = fp16(x), lo = fp16(x - hi): two
+// activation split as x = hi + lo (hi = fp16(x) toward zero, lo = fp16(x - hi)): two
 // MFMAs (hi, lo) give the block dot to ~2^-22 relative, then the fp32 block
 // scale d[n,b] (the same for all 4 values a lane holds) is applied with an FMA
 // into the fp32 accumulator -- the reference's per-block scale-then-accumulate
 // order.
 //
-// Workgroup tile: 64 rows (wave w: rows 16w..16w+15) x 16*NT columns; grid
-// (N / (16 NT), ceil(M / 64)).  Each wave streams its A rows and the shared B
-// columns KB blocks at a time with every load of a chunk issued before use.
+// Workgroup tile: 16 rows x 16*NT columns; grid (N / (16 NT), ceil(M / 16),
+// K slices).  The 4 waves split the slice's blocks and sum in LDS; each wave
+// streams its A rows and B columns KB blocks at a time, two chunks in flight.
 #include "mh_ops.h"
 
 namespace mh {
@@ -28,21 +28,37 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int KB = 4;  // scale blocks per load chunk
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// x = hi + lo: hi rounds toward zero (v_cvt_pkrtz, two values per
+// instruction), so x - hi is exact in fp32; lo keeps the next ~10 bits.
 __device__ __forceinline__ void split_hi_lo(const float (&x)[8], half8 &hi, half8 &lo) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const _Float16 h = (_Float16)x[i];
-        hi[i] = h;
-        lo[i] = (_Float16)(x[i] - (float)h);
+    for (int i = 0; i < 4; ++i) {
+        const auto h = __builtin_amdgcn_cvt_pkrtz(x[2 * i], x[2 * i + 1]);
+        const auto l = __builtin_amdgcn_cvt_pkrtz(x[2 * i] - (float)h[0], x[2 * i + 1] - (float)h[1]);
+        hi[2 * i] = (_Float16)h[0];
+        hi[2 * i + 1] = (_Float16)h[1];
+        lo[2 * i] = (_Float16)l[0];
+        lo[2 * i + 1] = (_Float16)l[1];
     }
 }
 
+// int8 -> fp16, exactly: the half with bits 0x64 : (q ^ 0x80) is 1024 + (q + 128),
+// built two at a time with v_perm_b32; subtracting 1152 leaves q.
 __device__ __forceinline__ half8 i8x8_to_h8(uint2 q) {
+    const uint32_t a = q.x ^ 0x80808080u, b = q.y ^ 0x80808080u;
+    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
+    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
     half8 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        r[i] = (_Float16)(int8_t)(q.x >> (8 * i));
-        r[4 + i] = (_Float16)(int8_t)(q.y >> (8 * i));
+        const half2v v = __builtin_bit_cast(half2v, w[i]) - bias;
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
     }
     return r;
 }
@@ -171,73 +187,80 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
     }
 }
 
+// The 4 waves of a 16 x 16*NT tile take the 4
+// quarters of the K slice (grid z) and meet in LDS, summed in wave order
+// (w0 + w1) + w2) + w3, and each wave finishes NT of the 4*NT (subtile, row)
+// pairs.  A workgroup reads 16 activation rows instead of 64: the panel is
+// what limits a GEMM with M <= 64, read by every column tile.
 template <int EPI, int KV, int NT, bool A8>
-__global__ __launch_bounds__(256) void gemm_q8x4_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
+    __shared__ floatx4 red[4][NT][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
-    const int m_base = blockIdx.y * 64 + wave * 16;
+    const int m_base = blockIdx.y * 16;
     const int n_base = blockIdx.x * 16 * NT;
     const int nb_all = g.K >> 5;
-    // K slice z of gridDim.z: blocks [kb0, kb0 + nb)
-    const int per = (nb_all + gridDim.z - 1) / gridDim.z;
-    const int kb0 = blockIdx.z * per;
-    const int nb = min(nb_all - kb0, per);
-    // A row of this lane (clamped: rows past M read row M-1 and are never stored)
-    const int arow = min(m_base + l16, g.M - 1);
+    // K slice z: blocks [z * nb_all / Z, (z + 1) * nb_all / Z); wave w its w-th quarter
+    const int z0 = (int)(((long)blockIdx.z * nb_all) / gridDim.z);
+    const int nbz = (int)(((long)(blockIdx.z + 1) * nb_all) / gridDim.z) - z0;
+    const int kb0 = z0 + (wave * nbz) / 4;
+    const int nb = z0 + ((wave + 1) * nbz) / 4 - kb0;  // 0 when the slice has fewer than 4 blocks
+    const int arow = min(m_base + l16, g.M - 1);      // rows past M read row M-1, never stored
     const float *arow_p = A8 ? nullptr : g.a + (size_t)arow * g.lda + 8 * kq + 32 * kb0;
     const int8_t *arow_q = A8 ? g.a8 + (size_t)arow * g.lda + 8 * kq + 32 * kb0 : nullptr;
     const float *arow_d = A8 ? g.d8 + (size_t)arow * (g.lda / 32) + kb0 : nullptr;
-    // B column (weight row) of this lane for each of the NT subtiles
     const uint8_t *wcol[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int n = n_base + 16 * t + l16;
         wcol[t] = g.w + ((size_t)(n >> 2) * nb_all + kb0) * kBlockBytes;
     }
-    const int krow = l16 & 3;  // row inside the 4-row group (n % 4; n_base is a multiple of 16)
+    const int krow = l16 & 3;
 
     floatx4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    // two chunks in flight: chunk c+1 is issued before chunk c is multiplied;
-    // the chunks alternate between two register sets (a copy would wait for
-    // the loads it moves)
-    Chunk<NT, A8> ca, cb;
-    load_chunk<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
-    for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
-        load_chunk<NT, A8>(cb, b0 + KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
-        mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
-        if (b0 + KB >= nb) break;
-        load_chunk<NT, A8>(ca, b0 + 2 * KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
-        mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
-    }
-
-    // epilogue: lane holds rows m_base + 4kq + i, column n_base + 16t + l16
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int n = n_base + 16 * t + l16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m_base + 4 * kq + i;
-            const float v = acc[t][i];
-            const float partner = xshfl<1>(v);  // column n ^ 1, same row
-            if (m < g.M) gemm_finish<EPI, KV>(g, m, n, v, partner);
+    if (nb > 0) {
+        Chunk<NT, A8> ca, cb;
+        load_chunk<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+        for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
+            load_chunk<NT, A8>(cb, b0 + KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);  // clamped: valid past nb
+            mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
+            if (b0 + KB >= nb) break;
+            load_chunk<NT, A8>(ca, b0 + 2 * KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+            mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
         }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[wave][t][lane] = acc[t];
+    __syncthreads();
+    // lane holds rows m_base + 4kq + i, column n_base + 16t + l16
+#pragma unroll
+    for (int p = wave; p < 4 * NT; p += 4) {
+        const int t = p >> 2, i = p & 3;
+        float v = red[0][t][lane][i];
+        v += red[1][t][lane][i];
+        v += red[2][t][lane][i];
+        v += red[3][t][lane][i];
+        const int n = n_base + 16 * t + l16;
+        const int m = m_base + 4 * kq + i;
+        const float partner = xshfl<1>(v);  // column n ^ 1, same row
+        if (m < g.M) gemm_finish<EPI, KV>(g, m, n, v, partner);
     }
 }
 
 template <int EPI, int KV, bool A8>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    // 4 column subtiles (64 columns) per workgroup unless that leaves too few workgroups
-    const int mt = (g.M + 63) / 64;
+    const int mt = (g.M + 15) / 16;
     const int kz = EPI == EPI_PART ? (g.ksplit > 0 ? g.ksplit : gemm_ksplit(g.M, g.N, g.K)) : 1;
-    const bool wide = (g.N / 64) * mt * kz >= 96;
-    if (wide && g.N % 64 == 0) {
-        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 4, A8>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
+    // the widest column tile that still gives ~192 workgroups
+    if (g.N % 64 == 0 && (g.N / 64) * mt * kz >= 192) {
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
+    } else if (g.N % 32 == 0 && (g.N / 32) * mt * kz >= 192) {
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
     } else {
-        hipLaunchKernelGGL((gemm_q8x4_kernel<EPI, KV, 1, A8>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
     }
     return hipGetLastError();
 }
@@ -249,16 +272,15 @@ hipError_t launch_a(const GemmArgs &g, hipStream_t s) {
 }  // namespace
 
 // Split K so that a GEMM with few output tiles still spreads over the CUs:
-// about 384 workgroups of 64 x 64 tiles, at least 3 blocks per slice, at most 16.
+// about 256 workgroups of 16 x 16 tiles, at least 12 blocks (3 per wave) per
+// slice, at most 16 slices.  Slices are balanced: sizes differ by at most one block.
 int gemm_ksplit(int M, int N, int K) {
-    const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
+    const int tiles = ((M + 15) / 16) * (N / 16);
     const int nb = K / 32;
-    int z = (384 + tiles - 1) / tiles;
-    z = z > nb / 3 ? nb / 3 : z;
+    int z = (256 + tiles - 1) / tiles;
+    z = z > nb / 12 ? nb / 12 : z;
     z = z > 16 ? 16 : z;
-    z = z < 1 ? 1 : z;
-    const int per = (nb + z - 1) / z;
-    return (nb + per - 1) / per;  // no empty slice
+    return z < 1 ? 1 : z;
 }
 
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s) {
@@ -267,7 +289,7 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
     if (epi == EPI_QKV && (g.N != 3 * kHidden || g.page_size <= 0)) return hipErrorInvalidValue;
     if (epi == EPI_PART) {  // every K slice must hold at least one block
         const int nb = g.K / 32, z = g.ksplit;
-        if (!g.part || z > 16 || z > nb || (z > 0 && (z - 1) * ((nb + z - 1) / z) >= nb)) return hipErrorInvalidValue;
+        if (!g.part || z > 16 || z > nb) return hipErrorInvalidValue;
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
     switch (epi) {
