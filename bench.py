@@ -44,7 +44,7 @@ CAL_BYTES = 256 << 20
 # HBM bytes per launch of the roofline kernel, from two hardware-counter passes over
 # `bench.py --mode gemv` (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; KiB per dispatch
 # scaled by the 256 MiB calibration copy of that same run: fetch x2.0, write x1.0).
-GEMV_TRAFFIC_BYTES = 215_409_357
+GEMV_TRAFFIC_BYTES = 214_956_032
 
 
 def log(*a):

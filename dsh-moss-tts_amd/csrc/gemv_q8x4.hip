@@ -386,7 +386,16 @@ hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
 constexpr int kUnitBlocks = 24;
 constexpr int kUnitBytes = kUnitBlocks * kBlockBytes;  // 3264
 constexpr int kUnitChunks = kUnitBytes / 16;           // 204 = 3 x 64 + 12
-constexpr int kStreamStages = 3;  // 3 x 4 waves x 3264 B: three workgroups fit a CU's LDS
+#ifndef MH_STREAM_STAGES
+#define MH_STREAM_STAGES 2
+#endif
+#ifndef MH_STREAM_WG_PER_CU
+#define MH_STREAM_WG_PER_CU 4
+#endif
+// 2 slots x 4 waves x 3264 B + the activation: four workgroups per CU (16
+// waves) measured 74-75 % of 8 TB/s cold, against 70-71 % for three slots with
+// three workgroups and 68-73 % for the other ring/occupancy pairs tried
+constexpr int kStreamStages = MH_STREAM_STAGES;
 
 // s_waitcnt with only the vector-memory count constrained (gfx9 encoding).
 template <int N>
@@ -502,7 +511,7 @@ hipError_t launch_stream(const GemvArgs &a, hipStream_t s) {
     const int ngroups = a.rows / 4;
     const size_t lds = (size_t)a.cols * sizeof(float);
     int grid = (ngroups + 3) / 4;
-    grid = grid > 768 ? 768 : grid;  // three 4-wave workgroups per CU (LDS-bound)
+    grid = grid > 256 * MH_STREAM_WG_PER_CU ? 256 * MH_STREAM_WG_PER_CU : grid;  // MH_STREAM_WG_PER_CU 4-wave workgroups per CU
     hipLaunchKernelGGL((gemv_stream_kernel<PRO, EPI, KV>), dim3(grid), dim3(256), lds, s, a);
     return hipGetLastError();
 }
