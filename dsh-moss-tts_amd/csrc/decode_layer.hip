@@ -87,6 +87,7 @@ constexpr int kLLQ = 0;                            // q | k | v of the new posit
 constexpr int kLLA = kLLQ + 3 * kHidden;           // attention partials, 66 words per unit
 constexpr int kLLX = kLLA + kMaxUnits * 66;        // x after the attention sub-block (768)
 constexpr int kLLH = kLLX + kHidden;               // fc_in output (3072)
+constexpr int kLLO = kLLH + kFF;                   // block output, the next block's input (768)
 constexpr int kAttnBase = 3 * kHidden / 4 / 4;     // attention workgroups follow the QKV ones (144)
 static_assert(kAttnBase + kMaxUnits <= kLayerGrid, "attention workgroups inside the grid");
 
@@ -102,7 +103,7 @@ __device__ __forceinline__ int attn_quarters(int n) {
     constexpr int per = 4 * kAttnSpansPerWave<KV>;
     return min((((n + 63) >> 6) + per - 1) / per, kLayerMaxQuarters);
 }
-static_assert(kLLH + kFF == kLayerWords, "LL layout");
+static_assert(kLLO + kHidden == kLayerWords, "LL layout");
 
 // Raw K/V operands of one wave's 64-key span, loaded before the query is known.
 template <int KV>
@@ -171,9 +172,10 @@ __device__ __forceinline__ float key_reduce(float (&pd)[L], int sub) {
 }
 
 template <int KV>
-__global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
+__global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
 #pragma clang fp contract(off)
     __shared__ float act[kFF];                 // GEMV activation
+    __shared__ float xin[kHidden];             // block input (x), the last block's output at the end
     __shared__ float xm[kHidden];              // x after the attention sub-block (fc_out's residual)
     __shared__ float pbuf[kMaxUnits * 66];     // gathered attention partials
     __shared__ float qkn[3 * kHeadDim];        // q, k, v of the new position for this head
@@ -188,65 +190,66 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     __syncthreads();
     STAGE_DECL;
     STAGE_TS(0);
-    if (a.state->stop) return;  // written only between frames: the same for every workgroup
-    const int pos = a.state->pos;
-    const uint32_t tag = ((uint32_t)(pos + 1) << 5) | (uint32_t)a.instance;
+    if (g.state->stop) return;  // written only between frames: the same for every workgroup
+    const int pos = g.state->pos;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int b = blockIdx.x;
     int budget = kPollBudget;
-    uint64_t *LL = a.ll;
+    uint64_t *LL = g.ll;
 
-    // ---- stage Q: LN1 + QKV, one wave per group
-    if (b < kAttnBase) {
-        GemvStage<1, 6, kHidden> gs;
-        gs.prefetch(a.attn_w, b);
-        const int r = gs.row();
-        QkvEpi e;
-        if (gs.storer()) e.load(a.attn_b, a.rope_cos, a.rope_sin, r, pos);
-        float o[3], lw[3], lb[3];
+    // embed_row (llm.cpp:114-157): x = wte[row[0]] + sum over channels of
+    // aemb[ch][code] (pad 1024 skipped), in channel order; every workgroup
+    // builds all of x, which every stage below reads from LDS
+    {
+        const int nb = kHidden / 32;
+        const int w0 = g.row[0];
+        int code[kNVq];
+#pragma unroll
+        for (int ch = 0; ch < kNVq; ++ch) code[ch] = g.row[ch + 1];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            xm[t + 256 * i] = a.x[t + 256 * i];
-            lw[i] = a.ln1_w[t + 256 * i];
-            lb[i] = a.ln1_b[t + 256 * i];
-        }
-        __syncthreads();
-        layernorm_768_lds(xm, lw, lb, o);
+            const int c = t + 256 * i;
+            float e[kNVq];
 #pragma unroll
-        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
-        __syncthreads();
-        STAGE_TS(1);
-        const float yv = gs.dot(act, part);
-        const float partner = xshfl<4>(yv);
-        if (gs.storer()) {  // bias, RoPE (llm.cpp:234-236), KV write (llm.cpp:224-225)
-            float out = e.apply(r, yv, partner);
-            const int sec = r / kHidden, within = r - sec * kHidden;
-            if (sec > 0) {  // the cache holds KV-precision values: hand on the same
-                const size_t idx = ((size_t)(within >> 6) * a.ctx_stride + pos) * kHeadDim + (within & 63);
-                void *cache = sec == 1 ? a.k_cache : a.v_cache;
-                if constexpr (KV == KV_F16) {
-                    const __half hv = __float2half_rn(out);
-                    ((__half *)cache)[idx] = hv;
-                    out = __half2float(hv);
-                } else {
-                    ((float *)cache)[idx] = out;
-                }
+            for (int ch = 0; ch < kNVq; ++ch) {
+                const bool use = !(code[ch] == kAudioPad || code[ch] < 0 || code[ch] >= kCodebook);
+                e[ch] = use ? q8x4_elem(g.aemb[ch], nb, code[ch], c) : 0.0f;
             }
-            ll_put(LL + kLLQ + r, out, tag);
+            float v = q8x4_elem(g.wte, nb, w0, c);
+#pragma unroll
+            for (int ch = 0; ch < kNVq; ++ch) {
+                const bool use = !(code[ch] == kAudioPad || code[ch] < 0 || code[ch] >= kCodebook);
+                if (use) v = v + e[ch];
+            }
+            xin[c] = v;
         }
-        STAGE_TS(2);
+        __syncthreads();
     }
 
-    // ---- stage A: attention of head h.  Unit u = (head, quarter) of 12 * Qs;
-    // wave w of quarter qq takes the 64-key spans qq*4 + w + 4*Qs*i, NS of them
-    // per round with all their K/V loads in flight together; online softmax
-    // across the rounds.  Qs == 1 (contexts up to 4 * NS spans) hands on the
-    // normalised head output, more quarters hand on partials (o, m, l).
-    constexpr int NS = kAttnSpansPerWave<KV>;
-    const int n = pos + 1;
-    const int spans = (n + 63) >> 6;
-    const int Qs = attn_quarters<KV>(n);
-    if (b >= kAttnBase && b < kAttnBase + kHeads * Qs) {
+#pragma unroll 1
+    for (int layer = 0; layer < kLayers; ++layer) {
+        const LayerArgs a = g.layers[layer];
+        const uint32_t tag = ((uint32_t)(pos + 1) << 5) | (uint32_t)layer;
+        // per-block copies of the indices: nothing derived from them is held across blocks
+        const int t = tix(), wave = t >> 6, lane = t & 63;
+        const int b = bix();
+
+        // ---- loads that do not depend on this block's input, issued before
+        // waiting for it: the QKV weights (stage Q) and the first round of K/V
+        // spans (stage A)
+        GemvStage<1, 6, kHidden> gq;
+        QkvEpi eq;
+        int rq = 0;
+        if (b < kAttnBase) {
+            gq.prefetch(a.attn_w, b);
+            rq = gq.row();
+            if (gq.storer()) eq.load(a.attn_b, a.rope_cos, a.rope_sin, rq, pos);
+        }
+        constexpr int NS = kAttnSpansPerWave<KV>;
+        const int n = pos + 1;
+        const int spans = (n + 63) >> 6;
+        const int Qs = attn_quarters<KV>(n);
+        const bool attn_wg = b >= kAttnBase && b < kAttnBase + kHeads * Qs;
         const int unit = b - kAttnBase;
         const int h = unit / Qs, qq = unit - h * Qs;
         const int span0 = qq * 4 + wave, stride = 4 * Qs;
@@ -256,14 +259,11 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int kl = RPI * sub + rr;  // the key (within a span) whose score this lane ends with
         const int crow_max = max(pos - 1, 0);
         const size_t hbase = (size_t)h * a.ctx_stride;
-        // K/V of a span: this lane's score key and V keys; cache rows are
-        // clamped to pos - 1 (or 0), rows written by earlier launches; the key
-        // at pos, and the clamped keys past it, take the LL values below
         // K of a span: load c brings 16 bytes of key RPI*c + rr (dims sub*EPL ..),
         // so one load covers RPI whole 128/256-byte rows; V: lane (pg, dg) keys
         // pg + 4q, dims 4dg .. 4dg+3.  Cache rows are clamped to pos - 1 (or 0),
-        // rows written by earlier launches; the key at pos, and the clamped keys
-        // past it, take this launch's k and v below.
+        // rows written before this launch; the key at pos, and the clamped keys
+        // past it, take this block's k and v (stage Q) below.
         auto load_span = [&](SpanRaw<KV> &r, int span) {
             const int p0 = span * 64, cnt = max(min(64, n - p0), 1);
 #pragma unroll
@@ -279,270 +279,349 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             }
         };
         SpanRaw<KV> raw[NS];
+        if (attn_wg) {
 #pragma unroll
-        for (int i = 0; i < NS; ++i) load_span(raw[i], min(span0 + stride * i, spans - 1));  // before q is known
-        // q, k, v of head h at pos
-        {
-            const int seg = t >> 6;
-            const bool ok = ll_wait1(LL + kLLQ + seg * kHidden + h * kHeadDim + (t & 63), t < 3 * kHeadDim, tag,
-                                     &qkn[min(t, 3 * kHeadDim - 1)], budget);
+            for (int i = 0; i < NS; ++i) load_span(raw[i], min(span0 + stride * i, spans - 1));
+        }
+
+        // this block's input: the previous block's output (block 0: the embedding)
+        if (layer > 0) {
+            const uint32_t prev = ((uint32_t)(pos + 1) << 5) | (uint32_t)(layer - 1);
+            const bool ok = ll_gather<3>(LL + kLLO, kHidden, prev, xin, budget);
             if (sync_failed(!ok, &wait_failed)) {
-                if (t == 0) atomicOr(a.err, 1u);
+                if (t == 0) atomicOr(g.err, 1u);
                 return;
             }
         }
-        STAGE_TS(3);
-        float m = -INFINITY, l = 0.0f;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int c0 = span0; c0 < spans; c0 += NS * stride) {
-            if (c0 != span0) {
+
+        // ---- stage Q: LN1 + QKV, one wave per group
+        if (b < kAttnBase) {
+            const GemvStage<1, 6, kHidden> &gs = gq;
+            const int r = rq;
+            const QkvEpi &e = eq;
+            float o[3], lw[3], lb[3];
 #pragma unroll
-                for (int i = 0; i < NS; ++i) load_span(raw[i], min(c0 + stride * i, spans - 1));
+            for (int i = 0; i < 3; ++i) {
+                lw[i] = a.ln1_w[t + 256 * i];
+                lb[i] = a.ln1_b[t + 256 * i];
             }
-            float qs[EPL];
+            layernorm_768_lds(xin, lw, lb, o);
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) qs[e] = qkn[sub * EPL + e];
-            STAGE_TS(20);
-            float dot[NS];
-            int cnt[NS];
-            float smax = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                const int span = c0 + stride * i;
-                const int p0 = span * 64;
-                cnt[i] = span < spans ? min(64, n - p0) : 0;
-                float pd[kLanesPerKey<KV>];
-#pragma unroll
-                for (int c = 0; c < kLanesPerKey<KV>; ++c) {
-                    float d = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) d = fmaf(qs[e], rawk<KV>(raw[i], c, e), d);
-                    pd[c] = d;
+            for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+            __syncthreads();
+            STAGE_TS(1);
+            const float yv = gs.dot(act, part);
+            const float partner = xshfl<4>(yv);
+            if (gs.storer()) {  // bias, RoPE (llm.cpp:234-236), KV write (llm.cpp:224-225)
+                float out = e.apply(r, yv, partner);
+                const int sec = r / kHidden, within = r - sec * kHidden;
+                if (sec > 0) {  // the cache holds KV-precision values: hand on the same
+                    const size_t idx = ((size_t)(within >> 6) * a.ctx_stride + pos) * kHeadDim + (within & 63);
+                    void *cache = sec == 1 ? a.k_cache : a.v_cache;
+                    if constexpr (KV == KV_F16) {
+                        const __half hv = __float2half_rn(out);
+                        ((__half *)cache)[idx] = hv;
+                        out = __half2float(hv);
+                    } else {
+                        ((float *)cache)[idx] = out;
+                    }
                 }
-                float d = key_reduce<kLanesPerKey<KV>>(pd, sub);  // q . k of key kl
-                if (span == spans - 1) {  // the span holding the new key: its k and v from this launch
-                    const float snew = wave_sum(qkn[lane] * qkn[kHeadDim + lane]);
-                    if (kl == pos - p0) d = snew;
-                    const typename SpanRaw<KV>::VT nv = to_raw4<KV>(*(const float4 *)&qkn[2 * kHeadDim + 4 * dg]);
-#pragma unroll
-                    for (int q = 0; q < 16; ++q)
-                        if (pg + 4 * q >= cnt[i] - 1) raw[i].v[q] = nv;
-                }
-                dot[i] = d * 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
-                if (kl < cnt[i]) smax = fmaxf(smax, dot[i]);
+                ll_put(LL + kLLQ + r, out, tag);
             }
-            smax = wave_max(smax);
-            STAGE_TS(4);
-            const float m_new = fmaxf(m, smax);
-            const float rescale = expf(m - m_new);  // 0 on the first round (m = -inf)
-            float esum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                const float e = kl < cnt[i] ? expf(dot[i] - m_new) : 0.0f;
-                esum += e;
-                sc[wave][i][kl] = e;
-            }
-            l = l * rescale + wave_sum(esum);
-            STAGE_TS(21);
-            m = m_new;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            float4 os[NS];  // one accumulator per span: independent FMA chains
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                os[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (cnt[i] == 0) continue;
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const float4 v = raw4<KV>(raw[i].v[q]);
-                    const float ei = sc[wave][i][pg + 4 * q];
-                    os[i].x = fmaf(ei, v.x, os[i].x);
-                    os[i].y = fmaf(ei, v.y, os[i].y);
-                    os[i].z = fmaf(ei, v.z, os[i].z);
-                    os[i].w = fmaf(ei, v.w, os[i].w);
-                }
-            }
-            o.x *= rescale;
-            o.y *= rescale;
-            o.z *= rescale;
-            o.w *= rescale;
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                o.x += os[i].x;
-                o.y += os[i].y;
-                o.z += os[i].z;
-                o.w += os[i].w;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
+            STAGE_TS(2);
         }
-        STAGE_TS(22);
-        o.x += xshfl<16>(o.x);
-        o.y += xshfl<16>(o.y);
-        o.z += xshfl<16>(o.z);
-        o.w += xshfl<16>(o.w);
-        o.x += xshfl<32>(o.x);
-        o.y += xshfl<32>(o.y);
-        o.z += xshfl<32>(o.z);
-        o.w += xshfl<32>(o.w);
-        if (lane < 16) po[wave][dg] = o;
-        if (lane == 0) {
-            pm[wave] = m;
-            pl[wave] = l;
-        }
-        __syncthreads();
-        if (wave == 0) {  // log-sum-exp merge of the waves that saw keys (a prefix)
-            STAGE_TS(23);
-            const int nlive = min(4, spans - qq * 4);
-            float wm[4], wl[4], wo[4];
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {  // every LDS read issued before the first use
-                wm[w] = pm[w];
-                wl[w] = pl[w];
-                wo[w] = ((const float *)&po[w][0])[lane];
-            }
-            float M = wm[0];
-#pragma unroll
-            for (int w = 1; w < 4; ++w)
-                if (w < nlive) M = fmaxf(M, wm[w]);
-            float L = 0.0f, O = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-                if (w < nlive) {
-                    const float sw = expf(wm[w] - M);
-                    L = fmaf(wl[w], sw, L);
-                    O = fmaf(wo[w], sw, O);
+
+        // ---- stage A: attention of head h.  Unit u = (head, quarter) of 12 * Qs;
+        // wave w of quarter qq takes the 64-key spans qq*4 + w + 4*Qs*i, NS of them
+        // per round with all their K/V loads in flight together; online softmax
+        // across the rounds.  Qs == 1 (contexts up to 4 * NS spans) hands on the
+        // normalised head output, more quarters hand on partials (o, m, l).
+        if (attn_wg) {
+            // q, k, v of head h at pos
+            {
+                const int seg = t >> 6;
+                const bool ok = ll_wait1(LL + kLLQ + seg * kHidden + h * kHeadDim + (t & 63), t < 3 * kHeadDim, tag,
+                                         &qkn[min(t, 3 * kHeadDim - 1)], budget);
+                if (sync_failed(!ok, &wait_failed)) {
+                    if (t == 0) atomicOr(g.err, 1u);
+                    return;
                 }
-            if (Qs == 1) {  // the head's output
-                ll_put(LL + kLLA + h * kHeadDim + lane, O / L, tag);
+            }
+            STAGE_TS(3);
+            float m = -INFINITY, l = 0.0f;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int c0 = span0; c0 < spans; c0 += NS * stride) {
+                if (c0 != span0) {
+#pragma unroll
+                    for (int i = 0; i < NS; ++i) load_span(raw[i], min(c0 + stride * i, spans - 1));
+                }
+                float qs[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) qs[e] = qkn[sub * EPL + e];
+                STAGE_TS(20);
+                float dot[NS];
+                int cnt[NS];
+                float smax = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const int span = c0 + stride * i;
+                    const int p0 = span * 64;
+                    cnt[i] = span < spans ? min(64, n - p0) : 0;
+                    float pd[kLanesPerKey<KV>];
+#pragma unroll
+                    for (int c = 0; c < kLanesPerKey<KV>; ++c) {
+                        float d = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < EPL; ++e) d = fmaf(qs[e], rawk<KV>(raw[i], c, e), d);
+                        pd[c] = d;
+                    }
+                    float d = key_reduce<kLanesPerKey<KV>>(pd, sub);  // q . k of key kl
+                    if (span == spans - 1) {  // the span holding the new key: its k and v from this launch
+                        const float snew = wave_sum(qkn[lane] * qkn[kHeadDim + lane]);
+                        if (kl == pos - p0) d = snew;
+                        const typename SpanRaw<KV>::VT nv = to_raw4<KV>(*(const float4 *)&qkn[2 * kHeadDim + 4 * dg]);
+#pragma unroll
+                        for (int q = 0; q < 16; ++q)
+                            if (pg + 4 * q >= cnt[i] - 1) raw[i].v[q] = nv;
+                    }
+                    dot[i] = d * 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
+                    if (kl < cnt[i]) smax = fmaxf(smax, dot[i]);
+                }
+                smax = wave_max(smax);
+                STAGE_TS(4);
+                const float m_new = fmaxf(m, smax);
+                const float rescale = expf(m - m_new);  // 0 on the first round (m = -inf)
+                float esum = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const float e = kl < cnt[i] ? expf(dot[i] - m_new) : 0.0f;
+                    esum += e;
+                    sc[wave][i][kl] = e;
+                }
+                l = l * rescale + wave_sum(esum);
+                STAGE_TS(21);
+                m = m_new;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                float4 os[NS];  // one accumulator per span: independent FMA chains
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    os[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (cnt[i] == 0) continue;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        const float4 v = raw4<KV>(raw[i].v[q]);
+                        const float ei = sc[wave][i][pg + 4 * q];
+                        os[i].x = fmaf(ei, v.x, os[i].x);
+                        os[i].y = fmaf(ei, v.y, os[i].y);
+                        os[i].z = fmaf(ei, v.z, os[i].z);
+                        os[i].w = fmaf(ei, v.w, os[i].w);
+                    }
+                }
+                o.x *= rescale;
+                o.y *= rescale;
+                o.z *= rescale;
+                o.w *= rescale;
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    o.x += os[i].x;
+                    o.y += os[i].y;
+                    o.z += os[i].z;
+                    o.w += os[i].w;
+                }
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+            STAGE_TS(22);
+            o.x += xshfl<16>(o.x);
+            o.y += xshfl<16>(o.y);
+            o.z += xshfl<16>(o.z);
+            o.w += xshfl<16>(o.w);
+            o.x += xshfl<32>(o.x);
+            o.y += xshfl<32>(o.y);
+            o.z += xshfl<32>(o.z);
+            o.w += xshfl<32>(o.w);
+            if (lane < 16) po[wave][dg] = o;
+            if (lane == 0) {
+                pm[wave] = m;
+                pl[wave] = l;
+            }
+            __syncthreads();
+            if (wave == 0) {  // log-sum-exp merge of the waves that saw keys (a prefix)
+                STAGE_TS(23);
+                const int nlive = min(4, spans - qq * 4);
+                float wm[4], wl[4], wo[4];
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {  // every LDS read issued before the first use
+                    wm[w] = pm[w];
+                    wl[w] = pl[w];
+                    wo[w] = ((const float *)&po[w][0])[lane];
+                }
+                float M = wm[0];
+#pragma unroll
+                for (int w = 1; w < 4; ++w)
+                    if (w < nlive) M = fmaxf(M, wm[w]);
+                float L = 0.0f, O = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    if (w < nlive) {
+                        const float sw = expf(wm[w] - M);
+                        L = fmaf(wl[w], sw, L);
+                        O = fmaf(wo[w], sw, O);
+                    }
+                if (Qs == 1) {  // the head's output
+                    ll_put(LL + kLLA + h * kHeadDim + lane, O / L, tag);
+                } else {
+                    uint64_t *dst = LL + kLLA + (size_t)unit * 66;
+                    ll_put(dst + lane, O, tag);
+                    if (lane == 0) {
+                        ll_put(dst + 64, M, tag);
+                        ll_put(dst + 65, L, tag);
+                    }
+                }
+                STAGE_TS(5);
+            }
+        }
+
+        // ---- stage P: merge the partials, proj + residual (4 waves per group)
+        if (b < kHidden / 4) {
+            GemvStage<4, 2, kHidden> gs;
+            gs.prefetch(a.proj_w, b);
+            const int r = gs.row();
+            float eb = 0.f, eres = 0.f;
+            if (gs.storer()) {
+                eb = a.proj_b[r];
+                eres = xin[r];
+            }
+            if (Qs == 1) {  // the heads' outputs, ready to use
+                const bool ok = ll_gather<3>(LL + kLLA, kHidden, tag, act, budget);
+                if (sync_failed(!ok, &wait_failed)) {
+                    if (t == 0) atomicOr(g.err, 1u);
+                    return;
+                }
+                STAGE_TS(6);
             } else {
-                uint64_t *dst = LL + kLLA + (size_t)unit * 66;
-                ll_put(dst + lane, O, tag);
-                if (lane == 0) {
-                    ll_put(dst + 64, M, tag);
-                    ll_put(dst + 65, L, tag);
+                const int units = kHeads * Qs;
+                const bool ok = ll_gather<(kMaxUnits * 66 + 255) / 256>(LL + kLLA, units * 66, tag, pbuf, budget);
+                if (sync_failed(!ok, &wait_failed)) {
+                    if (t == 0) atomicOr(g.err, 1u);
+                    return;
                 }
+                STAGE_TS(6);
+                // o = sum_q e^(m_q - M) o_q / sum_q e^(m_q - M) l_q: the weights e^(m_q - M)
+                // and the denominator once per head (thread h), then every output
+                if (t < kHeads) {
+                    const float *pp = pbuf + (size_t)t * Qs * 66;
+                    float mq[kLayerMaxQuarters], lq[kLayerMaxQuarters];
+#pragma unroll
+                    for (int q = 0; q < kLayerMaxQuarters; ++q) {
+                        const int qq = min(q, Qs - 1);
+                        mq[q] = pp[qq * 66 + 64];
+                        lq[q] = pp[qq * 66 + 65];
+                    }
+                    float M = mq[0];
+#pragma unroll
+                    for (int q = 1; q < kLayerMaxQuarters; ++q)
+                        if (q < Qs) M = fmaxf(M, mq[q]);
+                    float L = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < kLayerMaxQuarters; ++q) {
+                        const float sw = q < Qs ? expf(mq[q] - M) : 0.0f;
+                        if (q < Qs) L = fmaf(lq[q], sw, L);
+                        hw[t][q] = sw;
+                    }
+                    hw[t][kLayerMaxQuarters] = L;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int i3 = 0; i3 < 3; ++i3) {
+                    const int i = t + 256 * i3, h = i >> 6, d = i & 63;
+                    const float *pp = pbuf + (size_t)h * Qs * 66;
+                    float oq[kLayerMaxQuarters];
+#pragma unroll
+                    for (int q = 0; q < kLayerMaxQuarters; ++q) oq[q] = pp[min(q, Qs - 1) * 66 + d];
+                    float O = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < kLayerMaxQuarters; ++q)
+                        if (q < Qs) O = fmaf(oq[q], hw[h][q], O);
+                    act[i] = O / hw[h][kLayerMaxQuarters];
+                }
+                __syncthreads();
             }
-            STAGE_TS(5);
+            STAGE_TS(7);
+            const float yv = gs.dot(act, part);
+            if (gs.storer()) ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+            STAGE_TS(8);
         }
-    }
 
-    // ---- stage P: merge the partials, proj + residual (4 waves per group)
-    if (b < kHidden / 4) {
-        GemvStage<4, 2, kHidden> gs;
-        gs.prefetch(a.proj_w, b);
-        const int r = gs.row();
-        float eb = 0.f, eres = 0.f;
-        if (gs.storer()) {
-            eb = a.proj_b[r];
-            eres = a.x[r];
-        }
-        if (Qs == 1) {  // the heads' outputs, ready to use
-            const bool ok = ll_gather<3>(LL + kLLA, kHidden, tag, act, budget);
+        // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
+        {
+            GemvStage<1, 6, kHidden> gs;
+            gs.prefetch(a.fc_in_w, b);
+            const int r = gs.row();
+            const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
+            float lw[3], lb[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                lw[i] = a.ln2_w[t + 256 * i];
+                lb[i] = a.ln2_b[t + 256 * i];
+            }
+            const bool ok = ll_gather<3>(LL + kLLX, kHidden, tag, xm, budget);
             if (sync_failed(!ok, &wait_failed)) {
-                if (t == 0) atomicOr(a.err, 1u);
+                if (t == 0) atomicOr(g.err, 1u);
                 return;
             }
-            STAGE_TS(6);
-        } else {
-            const int units = kHeads * Qs;
-            const bool ok = ll_gather<(kMaxUnits * 66 + 255) / 256>(LL + kLLA, units * 66, tag, pbuf, budget);
+            STAGE_TS(9);
+            float o[3];
+            layernorm_768_lds(xm, lw, lb, o);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+            __syncthreads();
+            STAGE_TS(10);
+            const float yv = gs.dot(act, part);
+            if (gs.storer()) ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+            STAGE_TS(11);
+            __syncthreads();  // every wave is done with act before stage F gathers into it
+        }
+
+        // ---- stage F: fc_out + residual (4 waves per group) -> x
+        if (b < kHidden / 4) {
+            GemvStage<4, 6, kFF> gs;
+            gs.prefetch(a.fc_out_w, b);
+            const int r = gs.row();
+            const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
+            const bool ok = ll_gather<kFF / 256>(LL + kLLH, kFF, tag, act, budget);
             if (sync_failed(!ok, &wait_failed)) {
-                if (t == 0) atomicOr(a.err, 1u);
+                if (t == 0) atomicOr(g.err, 1u);
                 return;
             }
-            STAGE_TS(6);
-            // o = sum_q e^(m_q - M) o_q / sum_q e^(m_q - M) l_q: the weights e^(m_q - M)
-            // and the denominator once per head (thread h), then every output
-            if (t < kHeads) {
-                const float *pp = pbuf + (size_t)t * Qs * 66;
-                float mq[kLayerMaxQuarters], lq[kLayerMaxQuarters];
-#pragma unroll
-                for (int q = 0; q < kLayerMaxQuarters; ++q) {
-                    const int qq = min(q, Qs - 1);
-                    mq[q] = pp[qq * 66 + 64];
-                    lq[q] = pp[qq * 66 + 65];
-                }
-                float M = mq[0];
-#pragma unroll
-                for (int q = 1; q < kLayerMaxQuarters; ++q)
-                    if (q < Qs) M = fmaxf(M, mq[q]);
-                float L = 0.0f;
-#pragma unroll
-                for (int q = 0; q < kLayerMaxQuarters; ++q) {
-                    const float sw = q < Qs ? expf(mq[q] - M) : 0.0f;
-                    if (q < Qs) L = fmaf(lq[q], sw, L);
-                    hw[t][q] = sw;
-                }
-                hw[t][kLayerMaxQuarters] = L;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i3 = 0; i3 < 3; ++i3) {
-                const int i = t + 256 * i3, h = i >> 6, d = i & 63;
-                const float *pp = pbuf + (size_t)h * Qs * 66;
-                float oq[kLayerMaxQuarters];
-#pragma unroll
-                for (int q = 0; q < kLayerMaxQuarters; ++q) oq[q] = pp[min(q, Qs - 1) * 66 + d];
-                float O = 0.0f;
-#pragma unroll
-                for (int q = 0; q < kLayerMaxQuarters; ++q)
-                    if (q < Qs) O = fmaf(oq[q], hw[h][q], O);
-                act[i] = O / hw[h][kLayerMaxQuarters];
-            }
-            __syncthreads();
+            STAGE_TS(12);
+            const float yv = gs.dot(act, part);
+            if (gs.storer()) ll_put(LL + kLLO + r, xm[r] + (yv + eb), tag);  // llm.cpp:245
+            STAGE_TS(13);
         }
-        STAGE_TS(7);
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
-        STAGE_TS(8);
-    }
 
-    // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
-    {
-        GemvStage<1, 6, kHidden> gs;
-        gs.prefetch(a.fc_in_w, b);
-        const int r = gs.row();
-        const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
-        float lw[3], lb[3];
+    }  // layer
+
+    // ln_f (llm.cpp:254) on the last block's output, then the position moves on
+    // (every workgroup read it before its first block: their outputs are in)
+    if (b == 0) {
+        const uint32_t last = ((uint32_t)(pos + 1) << 5) | (uint32_t)(kLayers - 1);
+        const bool ok = ll_gather<3>(LL + kLLO, kHidden, last, xin, budget);
+        if (sync_failed(!ok, &wait_failed)) {
+            if (t == 0) atomicOr(g.err, 1u);
+            return;
+        }
+        float o[3], lw[3], lb[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            lw[i] = a.ln2_w[t + 256 * i];
-            lb[i] = a.ln2_b[t + 256 * i];
+            lw[i] = g.lnf_w[t + 256 * i];
+            lb[i] = g.lnf_b[t + 256 * i];
         }
-        const bool ok = ll_gather<3>(LL + kLLX, kHidden, tag, xm, budget);
-        if (sync_failed(!ok, &wait_failed)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        STAGE_TS(9);
-        float o[3];
-        layernorm_768_lds(xm, lw, lb, o);
+        layernorm_768_lds(xin, lw, lb, o);
 #pragma unroll
-        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
-        __syncthreads();
-        STAGE_TS(10);
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
-        STAGE_TS(11);
-        __syncthreads();  // every wave is done with act before stage F gathers into it
-    }
-
-    // ---- stage F: fc_out + residual (4 waves per group) -> x
-    if (b < kHidden / 4) {
-        GemvStage<4, 6, kFF> gs;
-        gs.prefetch(a.fc_out_w, b);
-        const int r = gs.row();
-        const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
-        const bool ok = ll_gather<kFF / 256>(LL + kLLH, kFF, tag, act, budget);
-        if (sync_failed(!ok, &wait_failed)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        STAGE_TS(12);
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) a.x[r] = xm[r] + (yv + eb);  // llm.cpp:245
-        STAGE_TS(13);
+        for (int i = 0; i < 3; ++i) g.hidden[t + 256 * i] = o[i];
+        if (t == 0) g.state->pos = pos + 1;
     }
     STAGE_FLUSH();
 }
@@ -555,9 +634,9 @@ hipError_t decode_layer_fits(int device, bool *fits) {
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return e;
     int per_cu16 = 0, per_cu32 = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu16, decode_layer_kernel<KV_F16>, 256, 0);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu16, decode_global_kernel<KV_F16>, 256, 0);
     if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu32, decode_layer_kernel<KV_F32>, 256, 0);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu32, decode_global_kernel<KV_F32>, 256, 0);
     if (e != hipSuccess) return e;
     int per_cu_local = 0;
     e = decode_local_occupancy(&per_cu_local);
@@ -575,18 +654,16 @@ extern "C" int mh_stage_trace_read(unsigned long long *out) {
 }
 #endif
 
-hipError_t launch_decode_layer(const LayerArgs &a, KvType kv, hipStream_t s) {
+hipError_t launch_decode_global(const GlobalArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (!a.attn_w || !a.proj_w || !a.fc_in_w || !a.fc_out_w || !a.x || !a.k_cache || !a.v_cache || !a.state ||
-        !a.ll || !a.err || !a.rope_cos || !a.rope_sin)
+    if (!a.layers || !a.wte || !a.row || !a.lnf_w || !a.lnf_b || !a.hidden || !a.state || !a.ll || !a.err)
         return hipErrorInvalidValue;
-    // tag bits: instance < 32, position + 1 < 2^27
-    if (a.ctx_stride <= 0 || a.ctx_stride >= (1 << 26) || a.instance < 0 || a.instance >= 32)
-        return hipErrorInvalidValue;
+    for (int ch = 0; ch < kNVq; ++ch)
+        if (!a.aemb[ch]) return hipErrorInvalidValue;
     if (kv == KV_F16)
-        hipLaunchKernelGGL(decode_layer_kernel<KV_F16>, dim3(kLayerGrid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(decode_global_kernel<KV_F16>, dim3(kLayerGrid), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(decode_layer_kernel<KV_F32>, dim3(kLayerGrid), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(decode_global_kernel<KV_F32>, dim3(kLayerGrid), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

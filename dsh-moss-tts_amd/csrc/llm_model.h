@@ -102,6 +102,7 @@ private:
     float *qkv_table_ = nullptr;   // [1 + 15 * 1024][2304] local q|k|v of (lpos >= 1, input code)
     void build_qkv_table();
     uint64_t *ll_ = nullptr;    // kLayerWords exchange words of the fused layer launches
+    LayerArgs *layer_args_ = nullptr;  // [kLayers] per-block arguments of the fused global step (device)
     void clear_exchange();      // before a sequence of fused launches: no stale word carries a current tag
     void check_exchange();      // throws if a fused launch ran out of its wait budget
     KvType kvt_ = KV_F16;

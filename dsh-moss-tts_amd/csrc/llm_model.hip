@@ -8,6 +8,7 @@
 #include <cstddef>
 #include <cstring>
 #include <unordered_map>
+#include <vector>
 
 namespace mh {
 
@@ -187,6 +188,22 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     if (fused_layers_) {
         hip_check(hipMalloc(&ll_, sizeof(uint64_t) * kLayerWords), "hipMalloc(exchange)");
         hip_check(hipMemset(ll_, 0, sizeof(uint64_t) * kLayerWords), "memset(exchange)");
+        // tags carry (position + 1) << 5 | block: positions below 2^26, blocks below 32
+        if (max_ctx_ >= (1 << 26)) throw Status(MOSS_HIP_EINVAL, "max_ctx too large for the fused decode kernels");
+        std::vector<LayerArgs> la(kLayers);
+        for (int l = 0; l < kLayers; ++l) {
+            const LayerW &L = g_[l];
+            LayerArgs &d = la[l];
+            d.attn_w = L.attn_w; d.proj_w = L.proj_w; d.fc_in_w = L.fc_in_w; d.fc_out_w = L.fc_out_w;
+            d.attn_b = L.attn_b; d.proj_b = L.proj_b; d.fc_in_b = L.fc_in_b; d.fc_out_b = L.fc_out_b;
+            d.ln1_w = L.ln1_w; d.ln1_b = L.ln1_b; d.ln2_w = L.ln2_w; d.ln2_b = L.ln2_b;
+            d.k_cache = kv_layer(0, l); d.v_cache = kv_layer(1, l); d.ctx_stride = max_ctx_;
+            d.rope_cos = rope_; d.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
+            d.state = state_; d.ll = ll_; d.err = &state_->ll_err; d.instance = l;
+        }
+        hip_check(hipMalloc(&layer_args_, sizeof(LayerArgs) * kLayers), "hipMalloc(layer args)");
+        hip_check(hipMemcpy(layer_args_, la.data(), sizeof(LayerArgs) * kLayers, hipMemcpyHostToDevice),
+                  "upload layer args");
     }
     hip_check(hipMalloc(&forced_, sizeof(int) * kNVq * (max_ctx_ + 2)), "hipMalloc(forced)");
     hip_check(hipMemset(hidden_, 0, kHidden * 4), "memset(hidden)");
@@ -213,7 +230,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, pre_q8_, pre_d8_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, pre_q8_, pre_d8_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -228,6 +245,7 @@ void *Model::kv_layer(int which, int layer) const {
 }
 
 // One global step: embed_row -> 12 x block_forward -> ln_f (llm.cpp:248-255).
+// With the fused kernels it is one launch (decode_global_kernel).  Per operator,
 // block_forward (llm.cpp:230-246) is five kernels: QKV GEMV with LN1 fused in its
 // prologue and bias + RoPE + KV write in its epilogue; split-KV attention (one
 // workgroup per head and 64-key span, unnormalised partials); proj GEMV merging
@@ -235,6 +253,17 @@ void *Model::kv_layer(int which, int layer) const {
 // residual out.  Every position-dependent kernel reads state->pos.
 void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
     const int *pos = &state_->pos;
+    if (fused_layers_) {  // embed, 12 blocks and ln_f in one launch
+        GlobalArgs g;
+        g.layers = layer_args_;
+        g.wte = wte_;
+        for (int ch = 0; ch < kNVq; ++ch) g.aemb[ch] = aemb_[ch];
+        g.row = row_dev;
+        g.lnf_w = lnf_w_; g.lnf_b = lnf_b_; g.hidden = hidden_;
+        g.state = state_; g.ll = ll_; g.err = &state_->ll_err;
+        hip_check(launch_decode_global(g, kvt_, s), "decode global step");
+        return;
+    }
     EmbedArgs e;
     e.wte = wte_;
     for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = aemb_[ch];
@@ -244,17 +273,6 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
     hip_check(launch_embed(e, s), "embed");
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
-        if (fused_layers_) {
-            LayerArgs d;
-            d.attn_w = L.attn_w; d.proj_w = L.proj_w; d.fc_in_w = L.fc_in_w; d.fc_out_w = L.fc_out_w;
-            d.attn_b = L.attn_b; d.proj_b = L.proj_b; d.fc_in_b = L.fc_in_b; d.fc_out_b = L.fc_out_b;
-            d.ln1_w = L.ln1_w; d.ln1_b = L.ln1_b; d.ln2_w = L.ln2_w; d.ln2_b = L.ln2_b;
-            d.x = x_; d.k_cache = kv_layer(0, l); d.v_cache = kv_layer(1, l); d.ctx_stride = max_ctx_;
-            d.rope_cos = rope_; d.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
-            d.state = state_; d.ll = ll_; d.err = &state_->ll_err; d.instance = l;
-            hip_check(launch_decode_layer(d, kvt_, s), "decode layer");
-            continue;
-        }
         GemvArgs a;
         a.w = L.attn_w; a.rows = 3 * kHidden; a.cols = kHidden;
         a.x = x_; a.ln_w = L.ln1_w; a.ln_b = L.ln1_b;

@@ -87,6 +87,21 @@ __device__ __forceinline__ bool end_reached(float l_slot, float l_end, const Sam
     return rng_uniform(rng) >= p_slot;
 }
 
+// threadIdx.x / blockIdx.x behind an empty volatile asm.  Inside the block
+// loop of a persistent kernel, values derived from them (gather addresses,
+// masks, row indices) are then recomputed in each block instead of being
+// hoisted out of the loop and held in registers across all blocks.
+__device__ __forceinline__ int tix() {
+    int v = threadIdx.x;
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ int bix() {
+    int v = blockIdx.x;
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
 // Value of lane (lane ^ M) for M = 1, 2, 4, 8, 16, 32, without the LDS
 // round trip of ds_bpermute: DPP quad permutes (1, 2), DPP row shifts under
 // bank masks (4), a DPP row rotation (8) and the gfx950 permlane swaps (16, 32).
@@ -269,7 +284,7 @@ __device__ __forceinline__ void layernorm_768_reg(const float (&x)[3], const flo
 __device__ __forceinline__ void layernorm_768_lds(const float *x, const float (&w)[3], const float (&b)[3],
                                                   float (&out)[3]) {
 #pragma clang fp contract(off)
-    const int t = threadIdx.x, lane = t & 63;
+    const int t = tix(), lane = t & 63;
     float xv[kHidden / 64];
 #pragma unroll
     for (int k = 0; k < kHidden / 64; ++k) xv[k] = x[lane + 64 * k];

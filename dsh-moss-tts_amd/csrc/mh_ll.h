@@ -26,7 +26,7 @@ __device__ __forceinline__ uint64_t ll_load(const uint64_t *w) {
 // are in flight together.  Returns false when the thread's budget runs out.
 template <int MAXK>
 __device__ __forceinline__ bool ll_gather(const uint64_t *src, int n, uint32_t tag, float *dst, int &budget) {
-    const int t = threadIdx.x;
+    const int t = tix();
     uint64_t w[MAXK];
     uint32_t pending = 0;
 #pragma unroll
@@ -89,7 +89,7 @@ struct GemvStage {
     int g, ks, b0;
 
     __device__ __forceinline__ void prefetch(const uint8_t *w, int b) {
-        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        const int wave = tix() >> 6, lane = tix() & 63;
         g = b * (4 / SPLIT) + wave / SPLIT;
         ks = wave % SPLIT;
         b0 = ks * per;
@@ -97,13 +97,13 @@ struct GemvStage {
                        dh);
     }
     // row of this lane's result (valid in the storer lanes: ks == 0, lane < 16, j == 0)
-    __device__ __forceinline__ int row() const { return 4 * g + ((threadIdx.x & 15) >> 2); }
+    __device__ __forceinline__ int row() const { return 4 * g + ((tix() & 15) >> 2); }
     __device__ __forceinline__ bool storer() const {
-        const int lane = threadIdx.x & 63;
+        const int lane = tix() & 63;
         return ks == 0 && lane < 16 && (lane & 3) == 0;
     }
     __device__ __forceinline__ float dot(const float *act, float (*part)[4]) const {
-        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kk = (lane & 15) >> 2, j = lane & 3;
+        const int wave = tix() >> 6, lane = tix() & 63, kk = (lane & 15) >> 2, j = lane & 3;
         float acc = dot_batch<NB>(act, b0 + (lane >> 4), b0 + per, j, qv, dh, 0.0f);
         acc = row_lane_sum(acc);
         if constexpr (SPLIT == 1) {

@@ -258,7 +258,7 @@ hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType k
 // ---- one transformer block of the single-stream decode in one launch (decode_layer.hip)
 constexpr int kLayerGrid = 192;          // workgroups, one per CU; all resident at once
 constexpr int kLayerMaxQuarters = 4;     // attention workgroups per head (4 spans of 64 keys each)
-constexpr int kLayerWords = 3 * kHidden + kHeads * kLayerMaxQuarters * 66 + kHidden + kFF;  // LL words
+constexpr int kLayerWords = 3 * kHidden + kHeads * kLayerMaxQuarters * 66 + kHidden + kFF + kHidden;  // LL words
 struct LayerArgs {
     const uint8_t *attn_w = nullptr, *proj_w = nullptr, *fc_in_w = nullptr, *fc_out_w = nullptr;
     const float *attn_b = nullptr, *proj_b = nullptr, *fc_in_b = nullptr, *fc_out_b = nullptr;
@@ -274,7 +274,19 @@ struct LayerArgs {
 };
 // Whether kLayerGrid workgroups of every fused decode kernel fit the device at once.
 hipError_t decode_layer_fits(int device, bool *fits);
-hipError_t launch_decode_layer(const LayerArgs &a, KvType kv, hipStream_t s);
+// The whole global step in one launch: embedding of the row, kLayers blocks, ln_f.
+struct GlobalArgs {
+    const LayerArgs *layers = nullptr;  // kLayers entries in device memory (their x is unused)
+    const uint8_t *wte = nullptr;
+    const uint8_t *aemb[kNVq] = {};
+    const int *row = nullptr;           // [17] on device
+    const float *lnf_w = nullptr, *lnf_b = nullptr;
+    float *hidden = nullptr;            // [768] out: ln_f of the last block's output
+    DevState *state = nullptr;          // pos (read, then bumped by workgroup 0), stop
+    uint64_t *ll = nullptr;             // kLayerWords exchange words
+    unsigned *err = nullptr;            // set when a wait runs out
+};
+hipError_t launch_decode_global(const GlobalArgs &a, KvType kv, hipStream_t s);
 
 // ---- one local-transformer step (+ the channel's audio head) in one launch (decode_local.hip)
 struct LocalArgs {
