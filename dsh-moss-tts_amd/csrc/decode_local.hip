@@ -38,7 +38,8 @@ constexpr int kLA = kLQ + 3 * kHidden;  // attention output (768) and the step's
 constexpr int kLX = kLA + kHidden + 1;  // x after the attention sub-block
 constexpr int kLH = kLX + kHidden;      // fc_in output
 constexpr int kLO = kLH + kFF;          // block output (head input)
-static_assert(kLO + kHidden <= kLayerWords, "local LL layout fits the exchange buffer");
+constexpr int kLL = kLO + kHidden;      // head logits, the next step's pick input (1024)
+static_assert(kLL + kCodebook <= kLayerWords, "local LL layout fits the exchange buffer");
 
 // Stage timestamps (100 MHz device clock) of the last launch, per workgroup,
 // in builds with -DMH_STAGE_TRACE only.
@@ -87,6 +88,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     __shared__ float pbv[4];
     __shared__ int pbi[4];
     __shared__ int used_s;
+    __shared__ float lgt[kCodebook];  // the previous step's logits (chained launches)
 
     __shared__ int wait_failed;  // set when a wait of this workgroup runs out
     if (threadIdx.x == 0) wait_failed = 0;
@@ -95,263 +97,295 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     STAGE_TS(0);
     DevState *st = a.state;
     if (st->stop) return;  // written only between frames: the same for every workgroup
-    const int lpos = a.lpos, n = lpos + 1;
-    const uint32_t tag = ((uint32_t)(st->pos + 1) << 5) | (uint32_t)(12 + lpos);
-    const int t = threadIdx.x;
-    const int b = blockIdx.x;
+    const uint32_t tag_base = (uint32_t)(st->pos + 1) << 5;
     int budget = kPollBudget;
     uint64_t *LL = a.ll;
 
-    // ---- stage Q (lpos 0): LN1 + QKV of the block input, one wave per group
-    if constexpr (LIVE_QKV) {
-        if (b < 3 * kHidden / 16) {
-            GemvStage<1, 6, kHidden> gs;
-            gs.prefetch(a.attn_w, b);
+#pragma unroll 1
+    for (int lpos = a.lpos; lpos <= a.lpos_last; ++lpos) {
+        const int n = lpos + 1;
+        const uint32_t tag = tag_base | (uint32_t)(12 + lpos);
+        // per-step copies of the indices: nothing derived from them is held across steps
+        const int t = tix();
+        const int b = bix();
+        const int ch_in = lpos >= 2 ? lpos - 2 : -1;  // channel whose code is this step's input
+        const uint8_t *aemb_in = ch_in >= 0 ? a.aemb[ch_in] : nullptr;
+        const uint8_t *head_w = a.head && lpos >= 1 ? a.aemb[lpos - 1] : nullptr;
+        float *logits_out = lpos >= 1 ? a.logits + (size_t)(lpos - 1) * kCodebook : nullptr;
+        const bool picking = !LIVE_QKV && ch_in >= 0 && a.pick;
+        const bool pick_ll = picking && lpos > a.lpos;  // logits from this launch's previous step
+
+        // ---- stage Q (lpos 0): LN1 + QKV of the block input, one wave per group
+        if constexpr (LIVE_QKV) {
+            if (b < 3 * kHidden / 16) {
+                GemvStage<1, 6, kHidden> gs;
+                gs.prefetch(a.attn_w, b);
+                const int r = gs.row();
+                QkvEpi e;
+                if (gs.storer()) e.load(a.attn_b, a.rope_cos, a.rope_sin, r, lpos);
+                float o[3], lw[3], lb[3];
+#pragma unroll
+                for (int i = 0; i < 3; ++i) {
+                    xm[t + 256 * i] = a.x_in[t + 256 * i];
+                    lw[i] = a.ln1_w[t + 256 * i];
+                    lb[i] = a.ln1_b[t + 256 * i];
+                }
+                __syncthreads();
+                layernorm_768_lds(xm, lw, lb, o);
+#pragma unroll
+                for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+                __syncthreads();
+                const float yv = gs.dot(act, part);
+                const float partner = xshfl<4>(yv);
+                if (gs.storer()) {
+                    const float out = e.apply(r, yv, partner);
+                    const int sec = r / kHidden, within = r - sec * kHidden;
+                    if (sec > 0) {  // llm.cpp:224-225
+                        float *cache = sec == 1 ? a.lk : a.lv;
+                        cache[((size_t)(within >> 6) * kLocalLen + lpos) * kHeadDim + (within & 63)] = out;
+                    }
+                    ll_put(LL + kLQ + r, out, tag);
+                }
+                __syncthreads();
+            }
+        }
+
+        // ---- stage A (b < 12): head h = b of the local attention (llm.cpp:189-217
+        // over the local cache, keys 0..lpos) in the reference's order:
+        // s_p = (q_h . k_p) * 0.125 summed over d in order; e_p = exp(s_p - max),
+        // the in-order sum, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] in order.
+        // Wave 0 computes: lane p < 17 a score, lane d the output dimension d.
+        if (b < kHeads) {
+            const int h = b, lane = t & 63;
+            const bool w0 = t < 64;
+            const int kmax = max(lpos - 1, 0);
+            // loads complete in issue order: the pick's logits first
+            PickIn pin;
+            if (picking) {
+                if (pick_ll) {  // counts now, values once the previous step's head has stored them
+#pragma unroll
+                    for (int k = 0; k < kCodebook / 256; ++k)
+                        pin.cnt[k] = st->rep_penalty != 1.0f ? a.counts[(size_t)ch_in * kCodebook + t + 256 * k] : 0;
+                } else {
+                    greedy_pick_load(a.logits + (size_t)ch_in * kCodebook, a.counts + (size_t)ch_in * kCodebook,
+                                     st->rep_penalty, pin);
+                }
+            }
+            // the cache rows (keys 0 .. lpos-1, written by earlier launches) before
+            // anything else; the key at lpos, and the clamped ones past it, take
+            // this step's row below
+            float4 kr[kHeadDim / 4];
+            float vv[kLocalLen];
+            if (w0) {
+                const float *krow = a.lk + ((size_t)h * kLocalLen + min(lane, kmax)) * kHeadDim;
+#pragma unroll
+                for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)(krow + 4 * c);
+#pragma unroll
+                for (int p = 0; p < kLocalLen; ++p) vv[p] = a.lv[((size_t)h * kLocalLen + min(p, kmax)) * kHeadDim + lane];
+            }
+            // q, k, v of head h at lpos
+            if constexpr (LIVE_QKV) {
+                const int seg = min(t >> 6, 2), i = seg * kHidden + h * kHeadDim + (t & 63);
+                const bool ok = ll_wait1(LL + kLQ + i, t < 3 * kHeadDim, tag, &qkv[i], budget);
+                if (sync_failed(!ok, &wait_failed)) {
+                    if (t == 0) atomicOr(a.err, 1u);
+                    return;
+                }
+            } else {
+                const float *row = a.qkv_table;  // lpos 1: wte[slot]
+                if (ch_in >= 0) {
+                    int used;
+                    if (picking) {  // greedy pick of channel ch_in (llm.cpp:689-697)
+                        if (pick_ll) {
+                            const bool ok = ll_gather<kCodebook / 256>(LL + kLL, kCodebook, tag - 1, lgt, budget);
+                            if (sync_failed(!ok, &wait_failed)) {
+                                if (t == 0) atomicOr(a.err, 1u);
+                                return;
+                            }
+#pragma unroll
+                            for (int k = 0; k < kCodebook / 256; ++k) pin.vals[k] = lgt[t + 256 * k];
+                        }
+                        int idx = greedy_pick_reduce(pin, st->rep_penalty, pbv, pbi);
+                        if (idx >= kCodebook) idx = 0;
+                        used = st->forced_on ? a.forced[st->frame * kNVq + ch_in] : idx;
+                        if (b == 0 && t == 0) {
+                            st->codes[ch_in] = idx;
+                            st->row[ch_in + 1] = used;
+                        }
+                    } else {  // written by the sampler of channel ch_in
+                        if (t == 0) used_s = st->row[ch_in + 1];
+                        __syncthreads();
+                        used = used_s;
+                    }
+                    if (b == 0 && t == 0) ll_put(LL + kLA + kHidden, __int_as_float(used), tag);  // for stage P
+                    row = a.qkv_table + (1 + (size_t)ch_in * kCodebook + used) * 3 * kHidden;
+                }
+                STAGE_TS(1);
+                if (t < 3 * kHeadDim) {
+                    const int seg = t >> 6, i = seg * kHidden + h * kHeadDim + (t & 63);
+                    const float v = row[i];
+                    qkv[i] = v;
+                    if (seg > 0)  // this position's k, v into the local cache (llm.cpp:224-225), for later steps
+                        (seg == 1 ? a.lk : a.lv)[((size_t)h * kLocalLen + lpos) * kHeadDim + (t & 63)] = v;
+                }
+                __syncthreads();
+            }
+            STAGE_TS(2);
+            if (w0) {
+                const float *qh = &qkv[h * kHeadDim];
+                if (min(lane, n - 1) == lpos)
+#pragma unroll
+                    for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)&qkv[kHidden + h * kHeadDim + 4 * c];
+                float dot = 0.0f;
+#pragma unroll
+                for (int c = 0; c < kHeadDim / 4; ++c) {
+                    const float4 qv = *(const float4 *)(qh + 4 * c);
+                    dot = dot + qv.x * kr[c].x;
+                    dot = dot + qv.y * kr[c].y;
+                    dot = dot + qv.z * kr[c].z;
+                    dot = dot + qv.w * kr[c].w;
+                }
+                dot *= 0.125f;
+                if (lane < kLocalLen) sc[0][lane] = dot;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                float sv[kLocalLen];
+#pragma unroll
+                for (int p = 0; p < kLocalLen; ++p) sv[p] = sc[0][p];
+                float mx = -1e30f;
+#pragma unroll
+                for (int p = 0; p < kLocalLen; ++p)
+                    if (p < n) mx = fmaxf(mx, sv[p]);
+                const float e = lane < n ? expf(dot - mx) : 0.0f;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                if (lane < kLocalLen) sc[0][lane] = e;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int p = 0; p < kLocalLen; ++p) sv[p] = sc[0][p];
+                float sum = 0.0f;
+#pragma unroll
+                for (int p = 0; p < kLocalLen; ++p)
+                    if (p < n) sum += sv[p];
+                const float wgt = e * (1.0f / sum);  // 0 for keys past n
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                if (lane < kLocalLen) sc[0][lane] = wgt;
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                const float vnew = qkv[2 * kHidden + h * kHeadDim + lane];
+                float o = 0.0f;
+#pragma unroll
+                for (int p = 0; p < kLocalLen; ++p) o = o + sc[0][p] * (min(p, n - 1) == lpos ? vnew : vv[p]);
+                ll_put(LL + kLA + h * kHeadDim + lane, o, tag);
+            }
+            STAGE_TS(3);
+            __syncthreads();
+        }
+
+        // ---- stage P: proj + residual (4 waves per group)
+        if (b < kHidden / 4) {
+            GemvStage<4, 2, kHidden> gs;
+            gs.prefetch(a.proj_w, b);
             const int r = gs.row();
-            QkvEpi e;
-            if (gs.storer()) e.load(a.attn_b, a.rope_cos, a.rope_sin, r, lpos);
-            float o[3], lw[3], lb[3];
+            const float eb = gs.storer() ? a.proj_b[r] : 0.0f;
+            const bool with_code = !LIVE_QKV && ch_in >= 0;  // the raw input row is aemb[ch_in][used]
+            float eres = 0.0f;
+            if (gs.storer() && !with_code) eres = a.x_in[r];
+            const bool ok = ll_gather<(kHidden + 1 + 255) / 256>(LL + kLA, kHidden + (with_code ? 1 : 0), tag, act, budget);
+            if (sync_failed(!ok, &wait_failed)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
+            }
+            if (gs.storer() && with_code)  // lookup_row (llm.cpp:697)
+                eres = q8x4_elem(aemb_in, kHidden / 32, __float_as_int(act[kHidden]), r);
+            const float yv = gs.dot(act, part);
+            if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+            STAGE_TS(4);
+            __syncthreads();  // act is reused by stage F
+        }
+
+        // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
+        {
+            GemvStage<1, 6, kHidden> gs;
+            gs.prefetch(a.fc_in_w, b);
+            const int r = gs.row();
+            const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
+            float lw[3], lb[3];
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
-                xm[t + 256 * i] = a.x_in[t + 256 * i];
-                lw[i] = a.ln1_w[t + 256 * i];
-                lb[i] = a.ln1_b[t + 256 * i];
+                lw[i] = a.ln2_w[t + 256 * i];
+                lb[i] = a.ln2_b[t + 256 * i];
             }
-            __syncthreads();
+            const bool ok = ll_gather<3>(LL + kLX, kHidden, tag, xm, budget);
+            if (sync_failed(!ok, &wait_failed)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
+            }
+            STAGE_TS(5);
+            float o[3];
             layernorm_768_lds(xm, lw, lb, o);
 #pragma unroll
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
             const float yv = gs.dot(act, part);
-            const float partner = xshfl<4>(yv);
-            if (gs.storer()) {
-                const float out = e.apply(r, yv, partner);
-                const int sec = r / kHidden, within = r - sec * kHidden;
-                if (sec > 0) {  // llm.cpp:224-225
-                    float *cache = sec == 1 ? a.lk : a.lv;
-                    cache[((size_t)(within >> 6) * kLocalLen + lpos) * kHeadDim + (within & 63)] = out;
-                }
-                ll_put(LL + kLQ + r, out, tag);
-            }
-            __syncthreads();
+            if (gs.storer()) ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+            STAGE_TS(6);
+            __syncthreads();  // every wave is done with act before stage F gathers into it
         }
-    }
 
-    // ---- stage A (b < 12): head h = b of the local attention (llm.cpp:189-217
-    // over the local cache, keys 0..lpos) in the reference's order:
-    // s_p = (q_h . k_p) * 0.125 summed over d in order; e_p = exp(s_p - max),
-    // the in-order sum, w_p = e_p * (1 / sum); o[d] = sum_p w_p v_p[d] in order.
-    // Wave 0 computes: lane p < 17 a score, lane d the output dimension d.
-    if (b < kHeads) {
-        const int h = b, lane = t & 63;
-        const bool w0 = t < 64;
-        const int kmax = max(lpos - 1, 0);
-        // loads complete in issue order: the pick's logits first
-        PickIn pin;
-        const bool picking = !LIVE_QKV && a.ch_in >= 0 && a.pick;
-        if (picking) greedy_pick_load(a.logits_in, a.counts_in, st->rep_penalty, pin);
-        // the cache rows (keys 0 .. lpos-1, written by earlier launches) before
-        // anything else; the key at lpos, and the clamped ones past it, take
-        // this step's row below
-        float4 kr[kHeadDim / 4];
-        float vv[kLocalLen];
-        if (w0) {
-            const float *krow = a.lk + ((size_t)h * kLocalLen + min(lane, kmax)) * kHeadDim;
-#pragma unroll
-            for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)(krow + 4 * c);
-#pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) vv[p] = a.lv[((size_t)h * kLocalLen + min(p, kmax)) * kHeadDim + lane];
-        }
-        // q, k, v of head h at lpos
-        if constexpr (LIVE_QKV) {
-            const int seg = min(t >> 6, 2), i = seg * kHidden + h * kHeadDim + (t & 63);
-            const bool ok = ll_wait1(LL + kLQ + i, t < 3 * kHeadDim, tag, &qkv[i], budget);
+        // ---- stage F: fc_out + residual (4 waves per group)
+        if (b < kHidden / 4) {
+            GemvStage<4, 6, kFF> gs;
+            gs.prefetch(a.fc_out_w, b);
+            const int r = gs.row();
+            const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
+            const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
             if (sync_failed(!ok, &wait_failed)) {
                 if (t == 0) atomicOr(a.err, 1u);
                 return;
             }
-        } else {
-            const float *row = a.qkv_table;  // lpos 1: wte[slot]
-            if (a.ch_in >= 0) {
-                int used;
-                if (picking) {  // greedy pick of channel ch_in (llm.cpp:689-697)
-                    int idx = greedy_pick_reduce(pin, st->rep_penalty, pbv, pbi);
-                    if (idx >= kCodebook) idx = 0;
-                    used = st->forced_on ? a.forced[st->frame * kNVq + a.ch_in] : idx;
-                    if (b == 0 && t == 0) {
-                        st->codes[a.ch_in] = idx;
-                        st->row[a.ch_in + 1] = used;
-                    }
-                } else {  // written by the sampler of channel ch_in
-                    if (t == 0) used_s = st->row[a.ch_in + 1];
-                    __syncthreads();
-                    used = used_s;
-                }
-                if (b == 0 && t == 0) ll_put(LL + kLA + kHidden, __int_as_float(used), tag);  // for stage P
-                row = a.qkv_table + (size_t)used * 3 * kHidden;
+            STAGE_TS(7);
+            const float yv = gs.dot(act, part);
+            if (gs.storer()) {
+                const float xo = xm[r] + (yv + eb);  // llm.cpp:245
+                a.x_out[r] = xo;
+                if (head_w) ll_put(LL + kLO + r, xo, tag);
             }
-            STAGE_TS(1);
-            if (t < 3 * kHeadDim) {
-                const int seg = t >> 6, i = seg * kHidden + h * kHeadDim + (t & 63);
-                const float v = row[i];
-                qkv[i] = v;
-                if (seg > 0)  // this position's k, v into the local cache (llm.cpp:224-225), for later steps
-                    (seg == 1 ? a.lk : a.lv)[((size_t)h * kLocalLen + lpos) * kHeadDim + (t & 63)] = v;
-            }
+            STAGE_TS(8);
             __syncthreads();
         }
-        STAGE_TS(2);
-        if (w0) {
-            const float *qh = &qkv[h * kHeadDim];
-            if (min(lane, n - 1) == lpos)
+
+        // ---- stage H: local ln_f + audio head (4 waves per group)
+        if (head_w && b < kCodebook / 16) {
+            GemvStage<1, 6, kHidden> gs;
+            gs.prefetch(head_w, b);
+            float lw[3], lb[3];
 #pragma unroll
-                for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)&qkv[kHidden + h * kHeadDim + 4 * c];
-            float dot = 0.0f;
-#pragma unroll
-            for (int c = 0; c < kHeadDim / 4; ++c) {
-                const float4 qv = *(const float4 *)(qh + 4 * c);
-                dot = dot + qv.x * kr[c].x;
-                dot = dot + qv.y * kr[c].y;
-                dot = dot + qv.z * kr[c].z;
-                dot = dot + qv.w * kr[c].w;
+            for (int i = 0; i < 3; ++i) {
+                lw[i] = a.lnf_w[t + 256 * i];
+                lb[i] = a.lnf_b[t + 256 * i];
             }
-            dot *= 0.125f;
-            if (lane < kLocalLen) sc[0][lane] = dot;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            float sv[kLocalLen];
+            const bool ok = ll_gather<3>(LL + kLO, kHidden, tag, xm, budget);
+            if (sync_failed(!ok, &wait_failed)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
+            }
+            STAGE_TS(9);
+            float o[3];
+            layernorm_768_lds(xm, lw, lb, o);  // normalize(lx, local_lnf) (llm.cpp:262)
 #pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) sv[p] = sc[0][p];
-            float mx = -1e30f;
-#pragma unroll
-            for (int p = 0; p < kLocalLen; ++p)
-                if (p < n) mx = fmaxf(mx, sv[p]);
-            const float e = lane < n ? expf(dot - mx) : 0.0f;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            if (lane < kLocalLen) sc[0][lane] = e;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) sv[p] = sc[0][p];
-            float sum = 0.0f;
-#pragma unroll
-            for (int p = 0; p < kLocalLen; ++p)
-                if (p < n) sum += sv[p];
-            const float wgt = e * (1.0f / sum);  // 0 for keys past n
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            if (lane < kLocalLen) sc[0][lane] = wgt;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            const float vnew = qkv[2 * kHidden + h * kHeadDim + lane];
-            float o = 0.0f;
-#pragma unroll
-            for (int p = 0; p < kLocalLen; ++p) o = o + sc[0][p] * (min(p, n - 1) == lpos ? vnew : vv[p]);
-            ll_put(LL + kLA + h * kHeadDim + lane, o, tag);
+            for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+            __syncthreads();
+            const float yv = gs.dot(act, part);
+            if (gs.storer()) {
+                logits_out[gs.row()] = yv;
+                if (lpos < a.lpos_last) ll_put(LL + kLL + gs.row(), yv, tag);  // the next step's pick
+            }
+            STAGE_TS(10);
         }
-        STAGE_TS(3);
-        __syncthreads();
-    }
-
-    // ---- stage P: proj + residual (4 waves per group)
-    if (b < kHidden / 4) {
-        GemvStage<4, 2, kHidden> gs;
-        gs.prefetch(a.proj_w, b);
-        const int r = gs.row();
-        const float eb = gs.storer() ? a.proj_b[r] : 0.0f;
-        const bool with_code = !LIVE_QKV && a.ch_in >= 0;  // the raw input row is aemb[ch_in][used]
-        float eres = 0.0f;
-        if (gs.storer() && !with_code) eres = a.x_in[r];
-        const bool ok = ll_gather<(kHidden + 1 + 255) / 256>(LL + kLA, kHidden + (with_code ? 1 : 0), tag, act, budget);
-        if (sync_failed(!ok, &wait_failed)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        if (gs.storer() && with_code)  // lookup_row (llm.cpp:697)
-            eres = q8x4_elem(a.aemb_in, kHidden / 32, __float_as_int(act[kHidden]), r);
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
-        STAGE_TS(4);
-        __syncthreads();  // act is reused by stage F
-    }
-
-    // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
-    {
-        GemvStage<1, 6, kHidden> gs;
-        gs.prefetch(a.fc_in_w, b);
-        const int r = gs.row();
-        const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
-        float lw[3], lb[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            lw[i] = a.ln2_w[t + 256 * i];
-            lb[i] = a.ln2_b[t + 256 * i];
-        }
-        const bool ok = ll_gather<3>(LL + kLX, kHidden, tag, xm, budget);
-        if (sync_failed(!ok, &wait_failed)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        STAGE_TS(5);
-        float o[3];
-        layernorm_768_lds(xm, lw, lb, o);
-#pragma unroll
-        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
-        __syncthreads();
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
-        STAGE_TS(6);
-        __syncthreads();  // every wave is done with act before stage F gathers into it
-    }
-
-    // ---- stage F: fc_out + residual (4 waves per group)
-    if (b < kHidden / 4) {
-        GemvStage<4, 6, kFF> gs;
-        gs.prefetch(a.fc_out_w, b);
-        const int r = gs.row();
-        const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
-        const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
-        if (sync_failed(!ok, &wait_failed)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        STAGE_TS(7);
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) {
-            const float xo = xm[r] + (yv + eb);  // llm.cpp:245
-            a.x_out[r] = xo;
-            if (a.head_w) ll_put(LL + kLO + r, xo, tag);
-        }
-        STAGE_TS(8);
-        __syncthreads();
-    }
-
-    // ---- stage H: local ln_f + audio head (4 waves per group)
-    if (a.head_w && b < kCodebook / 16) {
-        GemvStage<1, 6, kHidden> gs;
-        gs.prefetch(a.head_w, b);
-        float lw[3], lb[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            lw[i] = a.lnf_w[t + 256 * i];
-            lb[i] = a.lnf_b[t + 256 * i];
-        }
-        const bool ok = ll_gather<3>(LL + kLO, kHidden, tag, xm, budget);
-        if (sync_failed(!ok, &wait_failed)) {
-            if (t == 0) atomicOr(a.err, 1u);
-            return;
-        }
-        STAGE_TS(9);
-        float o[3];
-        layernorm_768_lds(xm, lw, lb, o);  // normalize(lx, local_lnf) (llm.cpp:262)
-#pragma unroll
-        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
-        __syncthreads();
-        const float yv = gs.dot(act, part);
-        if (gs.storer()) a.logits_out[gs.row()] = yv;
-        STAGE_TS(10);
-    }
+    }  // lpos
     STAGE_FLUSH();
 }
 
@@ -377,18 +411,20 @@ hipError_t decode_local_occupancy(int *per_cu) {
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (!a.attn_w || !a.proj_w || !a.fc_in_w || !a.fc_out_w || !a.lk || !a.lv || !a.state || !a.ll || !a.err ||
-        !a.x_out || a.lpos < 0 || a.lpos >= kLocalLen)
+        !a.x_out || a.lpos < 0 || a.lpos_last < a.lpos || a.lpos_last >= kLocalLen)
         return hipErrorInvalidValue;
+    if (a.head && (!a.logits || !a.lnf_w || !a.lnf_b)) return hipErrorInvalidValue;
+    for (int p = a.lpos < 1 ? 1 : a.lpos; p <= a.lpos_last; ++p)  // aemb rows: inputs (p >= 2) and heads
+        if ((p >= 2 && !a.aemb[p - 2]) || (a.head && !a.aemb[p - 1])) return hipErrorInvalidValue;
     if (a.lpos == 0) {
-        if (!a.x_in || !a.rope_cos || !a.rope_sin) return hipErrorInvalidValue;
+        if (a.lpos_last != 0 || !a.x_in || !a.rope_cos || !a.rope_sin) return hipErrorInvalidValue;
         hipLaunchKernelGGL(decode_local_kernel<true>, dim3(kLayerGrid), dim3(256), 0, s, a);
     } else {
         if (!a.qkv_table) return hipErrorInvalidValue;
-        if (a.ch_in < 0 && (a.lpos != 1 || !a.x_in)) return hipErrorInvalidValue;
-        if (a.ch_in >= 0 && (a.ch_in != a.lpos - 2 || !a.aemb_in ||
-                             (a.pick && (!a.logits_in || !a.counts_in || !a.forced))))
-            return hipErrorInvalidValue;
-        if (a.head_w && (!a.logits_out || !a.lnf_w || !a.lnf_b)) return hipErrorInvalidValue;
+        if (a.lpos == 1 && !a.x_in) return hipErrorInvalidValue;
+        if (a.lpos_last >= 2 && a.pick && (!a.logits || !a.counts || !a.forced)) return hipErrorInvalidValue;
+        // a chained pick reads the previous step's head: every step but the last runs one
+        if (a.lpos_last > a.lpos && a.pick && !a.head) return hipErrorInvalidValue;
         hipLaunchKernelGGL(decode_local_kernel<false>, dim3(kLayerGrid), dim3(256), 0, s, a);
     }
     return hipGetLastError();

@@ -403,7 +403,7 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos, int pic
 // channel ch's QKV GEMV instead of a kernel of its own; only channel 15 keeps
 // its sample kernel, which also counts the frame's used codes.
 void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
-    if (fused_layers_ && !text_gate) {  // one launch per local step (+ the channel's audio head)
+    if (fused_layers_ && !text_gate) {  // lpos 0, the gate, then the channel steps (one chained launch when greedy)
         LocalArgs base;
         const LayerW &L = local_;
         base.attn_w = L.attn_w; base.proj_w = L.proj_w; base.fc_in_w = L.fc_in_w; base.fc_out_w = L.fc_out_w;
@@ -413,38 +413,40 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
         base.lk = lkv_; base.lv = lkv_ + (size_t)kHeads * kLocalLen * kHeadDim;
         base.rope_cos = rope_; base.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
         base.state = state_; base.ll = ll_; base.err = &state_->ll_err; base.x_out = lres_;
+        for (int ch = 0; ch < kNVq; ++ch) base.aemb[ch] = aemb_[ch];
+        base.qkv_table = qkv_table_;
+        base.logits = logits_;
+        base.counts = counts_;
+        base.forced = forced_;
         LocalArgs z = base;  // lpos 0 on the global hidden state, then the end gate
         z.lpos = 0;
+        z.lpos_last = 0;
         z.x_in = hidden_;
         hip_check(launch_decode_local(z, s), "local step");
         hip_check(launch_gate(lres_, llnf_w_, llnf_b_, wte_, state_, s), "gate");
+        LocalArgs c = base;  // the channel steps: input wte[slot] at lpos 1, then aemb[ch - 1][code]
+        c.x_in = slot_in_;
+        c.head = 1;
+        c.pick = fused ? 1 : 0;
+        SampleArgs sa;
+        sa.counts = counts_;
+        sa.forced = forced_;
+        sa.next_input = next_in_;
+        sa.state = state_;
+        if (fused) {  // greedy: lpos 1..16 in one launch, each step picking the previous channel
+            c.lpos = 1;
+            c.lpos_last = kNVq;
+            hip_check(launch_decode_local(c, s), "local steps");
+        }
         for (int ch = 0; ch < kNVq; ++ch) {
-            LocalArgs c = base;
-            c.lpos = ch + 1;
-            if (ch == 0) {
-                c.x_in = slot_in_;
-                c.qkv_table = qkv_table_;
-            } else {
-                c.ch_in = ch - 1;
-                c.aemb_in = aemb_[ch - 1];
-                c.qkv_table = qkv_table_ + (1 + (size_t)(ch - 1) * kCodebook) * 3 * kHidden;
-                c.pick = fused ? 1 : 0;
-                c.logits_in = logits_ + (size_t)(ch - 1) * kCodebook;
-                c.counts_in = counts_ + (size_t)(ch - 1) * kCodebook;
-                c.forced = forced_;
+            if (!fused) {
+                c.lpos = c.lpos_last = ch + 1;
+                hip_check(launch_decode_local(c, s), "local step");
             }
-            c.head_w = aemb_[ch];
-            c.logits_out = logits_ + (size_t)ch * kCodebook;
-            hip_check(launch_decode_local(c, s), "local step");
-            if (!fused || ch == kNVq - 1) {
-                SampleArgs sa;
+            if (!fused || ch == kNVq - 1) {  // channel 15's pick also counts the frame's codes
                 sa.logits = logits_ + (size_t)ch * kCodebook;
                 sa.ch = ch;
-                sa.counts = counts_;
-                sa.forced = forced_;
                 sa.aemb = aemb_[ch];
-                sa.next_input = next_in_;
-                sa.state = state_;
                 sa.last_channel = ch == kNVq - 1;
                 sa.count_all = fused && ch == kNVq - 1;
                 hip_check(launch_sample(sa, s), "sample");

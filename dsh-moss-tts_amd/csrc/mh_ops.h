@@ -299,17 +299,17 @@ struct LocalArgs {
     DevState *state = nullptr;
     uint64_t *ll = nullptr;
     unsigned *err = nullptr;
-    int lpos = 0;
+    int lpos = 0;                      // first local position of the launch
+    int lpos_last = 0;                 // last one (positions 1..16 may run as one chain)
     const float *x_in = nullptr;       // lpos 0: block input (QKV computed here); lpos 1: the raw input row
-    const float *qkv_table = nullptr;  // lpos 1: its q|k|v row; lpos >= 2: [1024][2304] rows of (lpos, code)
-    int ch_in = -1;                    // lpos >= 2: channel of the input code (lpos - 2)
-    const uint8_t *aemb_in = nullptr;  // aemb[ch_in]
-    int pick = 0;                      // 1: greedy pick of ch_in here; 0: the sampler wrote state->row
-    const float *logits_in = nullptr;
-    const int *counts_in = nullptr, *forced = nullptr;
+    const float *qkv_table = nullptr;  // [1 + 15 * 1024][2304]: row 0 for lpos 1, then (lpos, code) rows
+    const uint8_t *aemb[kNVq] = {};    // audio embeddings / tied heads
+    int pick = 0;                      // 1: greedy pick of the previous channel here; 0: the sampler wrote state->row
+    int head = 0;                      // 1: position lpos >= 1 also runs the audio head of channel lpos - 1
+    float *logits = nullptr;           // [16][1024] head outputs (channel ch at ch * 1024)
+    const int *counts = nullptr;       // [16][1024] repetition counts
+    const int *forced = nullptr;
     float *x_out = nullptr;            // block output (768)
-    const uint8_t *head_w = nullptr;   // aemb[lpos - 1] for the audio head, or null
-    float *logits_out = nullptr;       // [1024]
 };
 hipError_t decode_local_occupancy(int *per_cu);
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s);
