@@ -189,18 +189,22 @@ void Batch::kv_export(int s, int n_pos, float *k, float *v) {
 // shared by all streams) and ends in lres_.  proj and fc_out are split-K GEMMs
 // whose partials are reduced, in a fixed order, by the residual + LayerNorm
 // kernel that follows each; the last one applies out_ln (the local ln_f before
-// the heads) into a_ when it is non-null.
+// the heads) into a_ when it is non-null.  At lpos >= 1 the block input is an
+// embedding row, so LN1 + QKV is a row of the load-time q|k|v table, already
+// written into q_ and the local caches by the previous kernel.
 void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, const float *out_ln_w,
                                const float *out_ln_b) {
     const LayerW &L = *w_.local;
     float *lk = lkv_, *lv = lkv_ + (size_t)S_ * kHeads * kLocalLen * kHeadDim;
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
-    hip_check(launch_ln_rows(in, in_stride, L.ln1_w, L.ln1_b, a_, n, s), "local ln1");
-    GemmArgs q;
-    q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
-    q.bias = L.attn_b; q.q_out = q_; q.k_pool = lk; q.v_pool = lv; q.page_size = kLocalLen;
-    q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
-    hip_check(launch_gemm(q, EPI_QKV, KV_F32, s), "local qkv");
+    if (lpos == 0) {  // positions >= 1: q|k|v already in place from the load-time table
+        hip_check(launch_ln_rows(in, in_stride, L.ln1_w, L.ln1_b, a_, n, s), "local ln1");
+        GemmArgs q;
+        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
+        q.bias = L.attn_b; q.q_out = q_; q.k_pool = lk; q.v_pool = lv; q.page_size = kLocalLen;
+        q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
+        hip_check(launch_gemm(q, EPI_QKV, KV_F32, s), "local qkv");
+    }
     AttnArgs t;
     t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen; t.stream_stride = 1;
     t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out = o_;
@@ -229,6 +233,15 @@ void Batch::enqueue_frame_local(hipStream_t s, int n) {
     const StreamState st = state();
     enqueue_local_step(s, n, hidden_, kHidden, 0, nullptr, nullptr);
     hip_check(launch_gate_rows(lres_, w_.llnf_w, w_.llnf_b, w_.wte, st, n, s), "gate");
+    // q|k|v of local positions 1..16 come from the load-time table: the row of
+    // wte[slot] here, the row of (lpos, picked code) from each channel's sampler
+    LocalQkv qkv;
+    qkv.q_out = q_;
+    qkv.lk = lkv_;
+    qkv.lv = lkv_ + (size_t)S_ * kHeads * kLocalLen * kHeadDim;
+    qkv.rows = w_.qkv_table;
+    qkv.lpos = 1;
+    hip_check(launch_local_qkv_rows(qkv, n, s), "local qkv rows");
     for (int ch = 0; ch < kNVq; ++ch) {
         if (ch == 0)
             enqueue_local_step(s, n, w_.slot_in, 0, 1, w_.llnf_w, w_.llnf_b);
@@ -238,7 +251,10 @@ void Batch::enqueue_frame_local(hipStream_t s, int n) {
         hd.w = w_.aemb[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
         hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
-        hip_check(launch_sample_rows(logits_, ch, w_.aemb[ch], next_in_, st, n, ch == kNVq - 1, s), "sample");
+        LocalQkv next = qkv;  // the input of lpos ch + 2 is channel ch's code
+        next.rows = ch + 1 < kNVq ? w_.qkv_table + (1 + (size_t)ch * kCodebook) * 3 * kHidden : nullptr;
+        next.lpos = ch + 2;
+        hip_check(launch_sample_rows(logits_, ch, w_.aemb[ch], next_in_, st, n, ch == kNVq - 1, next, s), "sample");
     }
 }
 

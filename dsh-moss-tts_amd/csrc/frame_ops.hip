@@ -612,11 +612,29 @@ __global__ __launch_bounds__(256) void gate_rows_kernel(const float *x_raw, cons
     }
 }
 
+// One table row (q | k | v, 2304 floats) of stream srow: q into q_out, k and v
+// into the local caches at position lpos (page = stream, 17 positions).
+__device__ __forceinline__ void local_qkv_row(const LocalQkv &a, const float *row, int srow) {
+    for (int i = threadIdx.x; i < 3 * kHidden; i += 256) {
+        const float v = row[i];
+        if (i < kHidden) {
+            a.q_out[(size_t)srow * kHidden + i] = v;
+        } else {
+            const int j = i - kHidden, sec = j / kHidden, w = j - sec * kHidden;
+            float *cache = sec == 0 ? a.lk : a.lv;
+            cache[(((size_t)srow * kHeads + (w >> 6)) * kLocalLen + a.lpos) * kHeadDim + (w & 63)] = v;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void local_qkv_rows_kernel(LocalQkv a) { local_qkv_row(a, a.rows, blockIdx.x); }
+
 // sample_kernel per stream (one workgroup each, own history and xoshiro
 // stream); inactive streams keep their state.  Teacher forcing is not offered
 // by the batched engine, so the used code is the pick.
 __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, int ch, const uint8_t *aemb,
-                                                          float *next_in, StreamState st, int last_channel) {
+                                                          float *next_in, StreamState st, int last_channel,
+                                                          LocalQkv next) {
     __shared__ PickLds L;
     const int srow = blockIdx.x, t = threadIdx.x;
     float *nxt = next_in + (size_t)srow * kHidden;
@@ -624,6 +642,7 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
     if (!st.active[srow]) {
         // keep the next local input defined (row 0) so later kernels read finite values
         for (int c = t; c < kHidden; c += 256) nxt[c] = q8x4_elem(aemb, nb, 0, c);
+        if (next.rows) local_qkv_row(next, next.rows, srow);
         return;
     }
     int *cnt = st.counts + ((size_t)srow * kNVq + ch) * kCodebook;
@@ -638,6 +657,8 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
         if (last_channel) st.row[srow * (kNVq + 1)] = kSlotToken;
     }
     for (int c2 = t; c2 < kHidden; c2 += 256) nxt[c2] = q8x4_elem(aemb, nb, idx, c2);
+    // the next local position's q|k|v: the table row of (lpos, idx)
+    if (next.rows) local_qkv_row(next, next.rows + (size_t)(idx < kCodebook ? idx : 0) * 3 * kHidden, srow);
 }
 
 __global__ void advance_rows_kernel(StreamState st, int streams) {
@@ -748,10 +769,20 @@ hipError_t launch_gate_rows(const float *x_raw, const float *lnf_w, const float 
 }
 
 hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
-                              int streams, int last_channel, hipStream_t s) {
+                              int streams, int last_channel, const LocalQkv &next, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (next.rows && (!next.q_out || !next.lk || !next.lv || next.lpos < 1 || next.lpos >= kLocalLen))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(sample_rows_kernel, dim3(streams), dim3(256), 0, s, logits, ch, aemb, next_in, st,
-                       last_channel);
+                       last_channel, next);
+    return hipGetLastError();
+}
+
+hipError_t launch_local_qkv_rows(const LocalQkv &a, int streams, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (!a.rows || !a.q_out || !a.lk || !a.lv || a.lpos < 1 || a.lpos >= kLocalLen || streams <= 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(local_qkv_rows_kernel, dim3(streams), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

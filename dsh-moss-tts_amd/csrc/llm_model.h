@@ -83,8 +83,11 @@ public:
         const uint8_t *wte;
         const uint8_t *const *aemb;  // [kNVq]
         const float *slot_in;        // dequantised wte[kSlotToken]
+        const float *qkv_table;      // [1 + 15 * 1024][2304] local q|k|v of (lpos >= 1, input code)
     };
-    Weights weights() const { return Weights{g_, &local_, lnf_w_, lnf_b_, llnf_w_, llnf_b_, wte_, aemb_.data(), slot_in_}; }
+    Weights weights() const {
+        return Weights{g_, &local_, lnf_w_, lnf_b_, llnf_w_, llnf_b_, wte_, aemb_.data(), slot_in_, qkv_table_};
+    }
 
 private:
     void enqueue_global_step(hipStream_t s, const int *row_dev);

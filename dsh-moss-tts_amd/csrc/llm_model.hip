@@ -220,7 +220,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     hip_check(hipMemcpy(rows_dev_, &slot, sizeof(int), hipMemcpyHostToDevice), "slot row");
     hip_check(launch_dequant_rows(wte_, kVocab, kHidden, rows_dev_, 1, slot_in_, stream_), "dequant slot row");
     hip_check(hipStreamSynchronize(stream_), "sync");
-    if (fused_layers_) build_qkv_table();
+    build_qkv_table();  // the fused local steps and the batch engine look their q|k|v up
     if (use_graphs_) build_graphs();
 }
 

@@ -240,8 +240,19 @@ hipError_t launch_gate_rows(const float *x_raw, const float *lnf_w, const float 
                             const StreamState &st, int streams, hipStream_t s);
 // Pick per stream for channel ch over logits[S][1024] (greedy or sampled, as the
 // single-stream sample kernel); next_in[S][768] = aemb[ch][used].
+// q|k|v of the next local position taken from the load-time table (rows of
+// (position, input code)): q into q_out[S][768], k and v into the local caches
+// [S][12][17][64] at lpos.  The sampler writes them for the code it picks.
+struct LocalQkv {
+    const float *rows = nullptr;  // table rows of this position's input channel: [1024][2304] (or one row)
+    float *q_out = nullptr;
+    float *lk = nullptr, *lv = nullptr;
+    int lpos = 0;
+};
 hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
-                              int streams, int last_channel, hipStream_t s);
+                              int streams, int last_channel, const LocalQkv &next, hipStream_t s);
+// The same copy of one shared row (lpos 1: wte[slot]) for every stream.
+hipError_t launch_local_qkv_rows(const LocalQkv &a, int streams, hipStream_t s);
 // pos[s] += 1 for active streams; streams reaching capacity become inactive.
 hipError_t launch_advance_rows(const StreamState &st, int streams, hipStream_t s);
 
