@@ -45,8 +45,7 @@ private:
     struct Graphs {
         hipGraphExec_t local = nullptr, global = nullptr;
     };
-    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, const float *out_ln_w,
-                            const float *out_ln_b);
+    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos);
     void enqueue_frame_local(hipStream_t s, int n);
     void enqueue_global(hipStream_t s, int n);
     Graphs &graphs_for(int n);
@@ -70,9 +69,9 @@ private:
     float *x_ = nullptr, *a_ = nullptr, *q_ = nullptr, *o_ = nullptr, *h_ = nullptr;
     float *hidden_ = nullptr, *lres_ = nullptr, *next_in_ = nullptr, *logits_ = nullptr;
     int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr;
+    float *part_ = nullptr;                     // [16][S][768] split-K partials
     BatchCtl *ctrl_ = nullptr;
     uint32_t *rng_ = nullptr;                   // [S][4]
-    float *part_ = nullptr;                     // [16][S][768] split-K partials
     unsigned char *active_ = nullptr;
     float *gate_ = nullptr;
     int *hist_codes_ = nullptr;                 // [cap+1][S][16] codes per frame

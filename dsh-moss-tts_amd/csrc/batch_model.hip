@@ -186,21 +186,21 @@ void Batch::kv_export(int s, int n_pos, float *k, float *v) {
 
 // block_forward (llm.cpp:230-246) of the local layer for n streams at local
 // position lpos; the residual starts as `in` (row stride in_stride, 0 = one row
-// shared by all streams) and ends in lres_.  proj and fc_out are split-K GEMMs
-// whose partials are reduced, in a fixed order, by the residual + LayerNorm
-// kernel that follows each; the last one applies out_ln (the local ln_f before
-// the heads) into a_ when it is non-null.  At lpos >= 1 the block input is an
-// embedding row, so LN1 + QKV is a row of the load-time q|k|v table, already
-// written into q_ and the local caches by the previous kernel.
-void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, const float *out_ln_w,
-                               const float *out_ln_b) {
+// shared by all streams) and ends in lres_, with its local ln_f in a_ (the
+// heads' input).  LN1 and LN2 run in the prologue of the GEMM that consumes
+// them; proj adds bias and residual in its epilogue (one K slice), fc_out is
+// split in K and reduced, in a fixed order, with the residual and ln_f by the
+// kernel that follows it.  At lpos >= 1 the block input is an embedding row, so LN1 + QKV
+// is a row of the load-time q|k|v table, already written into q_ and the local
+// caches by the previous kernel.
+void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos) {
     const LayerW &L = *w_.local;
     float *lk = lkv_, *lv = lkv_ + (size_t)S_ * kHeads * kLocalLen * kHeadDim;
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
-    if (lpos == 0) {  // positions >= 1: q|k|v already in place from the load-time table
-        hip_check(launch_ln_rows(in, in_stride, L.ln1_w, L.ln1_b, a_, n, s), "local ln1");
+    if (lpos == 0) {  // `in` is the global hidden state, one row per stream
         GemmArgs q;
-        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
+        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = in; q.lda = in_stride; q.M = n;
+        q.ln_w = L.ln1_w; q.ln_b = L.ln1_b;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = lk; q.v_pool = lv; q.page_size = kLocalLen;
         q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
         hip_check(launch_gemm(q, EPI_QKV, KV_F32, s), "local qkv");
@@ -211,27 +211,26 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     hip_check(launch_attn(t, KV_F32, s), "local attention");
     GemmArgs p;
     p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
-    p.part = part_; p.ksplit = gemm_ksplit(n, kHidden, kHidden);
-    hip_check(launch_gemm(p, EPI_PART, KV_F32, s), "local proj");
-    hip_check(launch_resid_ln_rows(part_, p.ksplit, n, L.proj_b, in, in_stride, lres_, L.ln2_w, L.ln2_b, a_, nullptr, s),
-              "local proj reduce + ln2");
+    p.y = lres_; p.ldy = kHidden; p.bias = L.proj_b; p.resid_in = in; p.resid_stride = in_stride;
+    hip_check(launch_gemm(p, EPI_RESID, KV_F32, s), "local proj");
     GemmArgs f1;
-    f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = a_; f1.lda = kHidden; f1.M = n;
+    f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = lres_; f1.lda = kHidden; f1.M = n;
+    f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
     f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
     hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
-    GemmArgs f2;
+    GemmArgs f2;  // split K: the reduce adds bias and residual, then the local ln_f for the head
     f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
     f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
     hip_check(launch_gemm(f2, EPI_PART, KV_F32, s), "local fc_out");
-    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, out_ln_w, out_ln_b, a_,
+    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b, a_,
                                    nullptr, s),
-              "local fc_out reduce");
+              "local fc_out reduce + ln_f");
 }
 
 // The local half of a frame for n streams (llm.cpp:648-698).
 void Batch::enqueue_frame_local(hipStream_t s, int n) {
     const StreamState st = state();
-    enqueue_local_step(s, n, hidden_, kHidden, 0, nullptr, nullptr);
+    enqueue_local_step(s, n, hidden_, kHidden, 0);
     hip_check(launch_gate_rows(lres_, w_.llnf_w, w_.llnf_b, w_.wte, st, n, s), "gate");
     // q|k|v of local positions 1..16 come from the load-time table: the row of
     // wte[slot] here, the row of (lpos, picked code) from each channel's sampler
@@ -244,10 +243,10 @@ void Batch::enqueue_frame_local(hipStream_t s, int n) {
     hip_check(launch_local_qkv_rows(qkv, n, s), "local qkv rows");
     for (int ch = 0; ch < kNVq; ++ch) {
         if (ch == 0)
-            enqueue_local_step(s, n, w_.slot_in, 0, 1, w_.llnf_w, w_.llnf_b);
+            enqueue_local_step(s, n, w_.slot_in, 0, 1);
         else
-            enqueue_local_step(s, n, next_in_, kHidden, ch + 1, w_.llnf_w, w_.llnf_b);
-        GemmArgs hd;
+            enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
+        GemmArgs hd;  // the tied audio head on the local ln_f of the step's output
         hd.w = w_.aemb[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
         hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
@@ -271,7 +270,7 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         const LayerW &L = w_.global[l];
         void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
         void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
-        GemmArgs q;
+        GemmArgs q;  // on LN1(x) in a_
         q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
         q.page_table = table_; q.table_stride = pages_; q.page_size = kPage;
@@ -281,21 +280,20 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         t.q = q_; t.k_pool = kp; t.v_pool = vp; t.page_table = table_; t.table_stride = pages_; t.page_size = kPage;
         t.stream_stride = 1; t.row_pos = pos_d_; t.rows = n; t.max_keys = cap_; t.out = o_;
         hip_check(launch_attn(t, kvt_, s), "attention");
-        GemmArgs p;
+        GemmArgs p;  // x += proj + b
         p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
-        p.part = part_; p.ksplit = gemm_ksplit(n, kHidden, kHidden);
-        hip_check(launch_gemm(p, EPI_PART, kvt_, s), "proj");
-        hip_check(launch_resid_ln_rows(part_, p.ksplit, n, L.proj_b, x_, kHidden, x_, L.ln2_w, L.ln2_b, a_, nullptr, s),
-                  "proj reduce + ln2");
-        GemmArgs f1;
-        f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = a_; f1.lda = kHidden; f1.M = n;
+        p.y = x_; p.ldy = kHidden; p.bias = L.proj_b;
+        hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "proj");
+        GemmArgs f1;  // LN2 in the prologue
+        f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = x_; f1.lda = kHidden; f1.M = n;
+        f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
         f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
-        GemmArgs f2;
+        GemmArgs f2;  // split K; the reduce adds bias and residual
         f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
         f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
-        // reduce + residual, then LN1 of the next layer, or ln_f into hidden (active streams only)
+        // then LN1 of the next layer into a_, or ln_f into hidden (active streams only)
         const bool last = l + 1 == kLayers;
         hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, x_, kHidden, x_,
                                        last ? w_.lnf_w : w_.global[l + 1].ln1_w,

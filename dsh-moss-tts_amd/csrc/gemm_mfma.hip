@@ -119,9 +119,8 @@ struct Chunk {
 };
 
 template <int NT, bool A8>
-__device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, int nb, const float *arow_p,
-                                           const int8_t *arow_q, const float *arow_d,
-                                           const uint8_t *const (&wcol)[NT], int krow, int kq) {
+__device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, int nb, const float *arow_p,
+                                             const int8_t *arow_q, const float *arow_d) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
         const int b = min(b0 + j, nb - 1);
@@ -134,6 +133,15 @@ __device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, int nb, con
             c.xa[j][0] = x0.x; c.xa[j][1] = x0.y; c.xa[j][2] = x0.z; c.xa[j][3] = x0.w;
             c.xa[j][4] = x1.x; c.xa[j][5] = x1.y; c.xa[j][6] = x1.z; c.xa[j][7] = x1.w;
         }
+    }
+}
+
+template <int NT, bool A8>
+__device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, int nb, const uint8_t *const (&wcol)[NT],
+                                             int krow, int kq) {
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+        const int b = min(b0 + j, nb - 1);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const uint8_t *blk = wcol[t] + (size_t)b * kBlockBytes;
@@ -142,6 +150,14 @@ __device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, int nb, con
             c.db[j][t] = *(const uint16_t *)(blk + 2 * krow);
         }
     }
+}
+
+template <int NT, bool A8>
+__device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, int nb, const float *arow_p,
+                                           const int8_t *arow_q, const float *arow_d,
+                                           const uint8_t *const (&wcol)[NT], int krow, int kq) {
+    load_chunk_a<NT, A8>(c, b0, nb, arow_p, arow_q, arow_d);
+    load_chunk_b<NT, A8>(c, b0, nb, wcol, krow, kq);
 }
 
 typedef int intx4 __attribute__((ext_vector_type(4)));
@@ -192,8 +208,14 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
 // (w0 + w1) + w2) + w3, and each wave finishes NT of the 4*NT (subtile, row)
 // pairs.  A workgroup reads 16 activation rows instead of 64: the panel is
 // what limits a GEMM with M <= 64, read by every column tile.
-template <int EPI, int KV, int NT, bool A8>
+//
+// LN: the activation rows are LayerNormed on the way in.  The wave's whole K
+// quarter (at most 8 blocks: K <= 1024) is loaded first, the row sums of the
+// 4 waves meet in LDS (two passes: mean, then the squared deviations), and the
+// values are normalised in registers with ln_w / ln_b staged in LDS.
+template <int EPI, int KV, int NT, bool A8, bool LN>
 __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
+#pragma clang fp contract(off)
     __shared__ floatx4 red[4][NT][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
@@ -220,7 +242,77 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     floatx4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    if (nb > 0) {
+    if constexpr (LN) {
+        static_assert(!A8, "the LayerNorm prologue takes fp32 activations");
+        __shared__ float lnw[4 * 2 * KB * 32], lnb[4 * 2 * KB * 32];
+        __shared__ float lsum[4][16], lsq[4][16];
+        // loads in completion order: the activations, ln_w / ln_b (staged in LDS),
+        // then the weights, which stay in flight while the statistics are formed
+        Chunk<NT, A8> ca, cb;
+        load_chunk_a<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d);
+        load_chunk_a<NT, A8>(cb, KB, nb, arow_p, arow_q, arow_d);  // clamped: valid past nb
+        for (int c = threadIdx.x; c < g.K; c += 256) {
+            lnw[c] = g.ln_w[c];
+            lnb[c] = g.ln_b[c];
+        }
+        load_chunk_b<NT, A8>(ca, 0, nb, wcol, krow, kq);
+        load_chunk_b<NT, A8>(cb, KB, nb, wcol, krow, kq);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KB; ++j)
+            if (j < nb)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s += ca.xa[j][i];
+#pragma unroll
+        for (int j = 0; j < KB; ++j)
+            if (KB + j < nb)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s += cb.xa[j][i];
+        s += xshfl<16>(s);
+        s += xshfl<32>(s);
+        if (lane < 16) lsum[wave][lane] = s;
+        __syncthreads();
+        const float mean = (((lsum[0][l16] + lsum[1][l16]) + lsum[2][l16]) + lsum[3][l16]) / (float)g.K;
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KB; ++j)
+            if (j < nb)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float d = ca.xa[j][i] - mean;
+                    v += d * d;
+                }
+#pragma unroll
+        for (int j = 0; j < KB; ++j)
+            if (KB + j < nb)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float d = cb.xa[j][i] - mean;
+                    v += d * d;
+                }
+        v += xshfl<16>(v);
+        v += xshfl<32>(v);
+        if (lane < 16) lsq[wave][lane] = v;
+        __syncthreads();
+        const float var = (((lsq[0][l16] + lsq[1][l16]) + lsq[2][l16]) + lsq[3][l16]) / (float)g.K;
+        const float inv = 1.0f / sqrtf(var + 1e-5f);
+        auto norm = [&](float (&x)[8], int blk) {  // columns 32 blk + 8 kq + i
+            const int c = 32 * blk + 8 * kq;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float y = (x[i] - mean) * inv;
+                y = y * lnw[c + i];
+                x[i] = y + lnb[c + i];
+            }
+        };
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            if (j < nb) norm(ca.xa[j], kb0 + j);
+            if (KB + j < nb) norm(cb.xa[j], kb0 + KB + j);
+        }
+        mfma_chunk<NT, A8>(ca, 0, nb, kq, acc);
+        if (KB < nb) mfma_chunk<NT, A8>(cb, KB, nb, kq, acc);
+    } else if (nb > 0) {
         Chunk<NT, A8> ca, cb;
         load_chunk<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
         for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
@@ -249,25 +341,29 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     }
 }
 
-template <int EPI, int KV, bool A8>
+template <int EPI, int KV, bool A8, bool LN>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int mt = (g.M + 15) / 16;
     const int kz = EPI == EPI_PART ? (g.ksplit > 0 ? g.ksplit : gemm_ksplit(g.M, g.N, g.K)) : 1;
     // the widest column tile that still gives ~192 workgroups
     if (g.N % 64 == 0 && (g.N / 64) * mt * kz >= 192) {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8, LN>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
     } else if (g.N % 32 == 0 && (g.N / 32) * mt * kz >= 192) {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8, LN>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
     } else {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
     }
     return hipGetLastError();
 }
 
 template <int EPI, int KV>
 hipError_t launch_a(const GemmArgs &g, hipStream_t s) {
-    return g.a8 != nullptr ? launch_nt<EPI, KV, true>(g, s) : launch_nt<EPI, KV, false>(g, s);
+    if (g.a8 != nullptr) return launch_nt<EPI, KV, true, false>(g, s);
+    if constexpr (EPI != EPI_PART) {
+        if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true>(g, s);
+    }
+    return launch_nt<EPI, KV, false, false>(g, s);
 }
 }  // namespace
 
@@ -292,6 +388,9 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
         if (!g.part || z > 16 || z > nb) return hipErrorInvalidValue;
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
+    // LayerNorm prologue: fp32 rows of at most 4 waves x 2 chunks of blocks, whole K in the workgroup
+    if (g.ln_w != nullptr && (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))
+        return hipErrorInvalidValue;
     switch (epi) {
         case EPI_PART: return launch_a<EPI_PART, KV_F16>(g, s);
         case EPI_F32: return launch_a<EPI_F32, KV_F16>(g, s);

@@ -131,6 +131,9 @@ struct GemmArgs {
     // int8 a8[M][lda] with fp32 block scales d8[M][lda / 32], and `a` is unused
     const int8_t *a8 = nullptr;
     const float *d8 = nullptr;
+    // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
+    // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
+    const float *ln_w = nullptr, *ln_b = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
 // The K split launch_gemm uses for an EPI_PART GEMM of this shape (1..16).
