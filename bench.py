@@ -4,7 +4,7 @@ Workload (one "step" = one decoded frame): batch 1, a seeded random-init model
 with the reference's dims (12 layers, d 768, 12x64 heads, FF 3072, vocab 16384,
 W8A16 Q8_0_4X4 weights), KV cache prefilled to context 512 with N(0,1) values
 (fp16 cache), greedy decoding (min_frames = steps, so the end gate never stops
-it) replayed as hipGraphs.  A frame is what the reference's "ms/frame" counts:
+it), two fused kernel launches per frame.  A frame is what the reference's "ms/frame" counts:
 local 1-layer transformer x 17, 16 audio heads + greedy picks, the W8A8 end
 gate, and the 12-layer global step.  The global step alone is also reported.
 
@@ -411,8 +411,8 @@ def main():
         "vs_baseline": None,
         "dtype": "w8a16 (int8 weights, fp32 activations/accumulation, fp16 KV)",
         "data": "synthetic (seeded random-init weights with the reference's dims; N(0,1) fp16 KV at ctx 512)",
-        "config": {"workload": "LLM decode, batch 1, ctx 512 -> 767, 256 greedy frames under hipGraph "
-                               "(full frame = 17 local steps + 16 heads + end gate + 12-layer global step)",
+        "config": {"workload": "LLM decode, batch 1, ctx 512 -> 767, 256 greedy frames, two fused launches per "
+                               "frame (full frame = 17 local steps + 16 heads + end gate + 12-layer global step)",
                    "global_batch": 1, "seq_len": CTX, "parallelism": "none (1 GPU)"},
         "frames_per_s": round(1e3 / d["ms_per_frame"], 1),
         "global_step_ms": round(d["global_ms_event"], 4),

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
     STAGE_TS(0);
     if (g.state->stop) return;  // written only between frames: the same for every workgroup
     const int pos = g.state->pos;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int t = threadIdx.x;
     const int b = blockIdx.x;
     int budget = kPollBudget;
     uint64_t *LL = g.ll;
@@ -643,7 +643,7 @@ hipError_t decode_layer_fits(int device, bool *fits) {
     if (e != hipSuccess) return e;
     int per_cu = per_cu16 < per_cu32 ? per_cu16 : per_cu32;
     per_cu = per_cu < per_cu_local ? per_cu : per_cu_local;
-    *fits = (long)per_cu * prop.multiProcessorCount >= kLayerGrid;
+    *fits = (long)per_cu * prop.multiProcessorCount >= kLayerGrid + 1;  // the local launch adds a gate workgroup
     return hipSuccess;
 }
 

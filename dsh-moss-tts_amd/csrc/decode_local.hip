@@ -39,7 +39,8 @@ constexpr int kLX = kLA + kHidden + 1;  // x after the attention sub-block
 constexpr int kLH = kLX + kHidden;      // fc_in output
 constexpr int kLO = kLH + kFF;          // block output (head input)
 constexpr int kLL = kLO + kHidden;      // head logits, the next step's pick input (1024)
-static_assert(kLL + kCodebook <= kLayerWords, "local LL layout fits the exchange buffer");
+constexpr int kLG = kLL + kCodebook;    // position 0's block output, the end gate's input (768)
+static_assert(kLG + kHidden <= kLayerWords, "local LL layout fits the exchange buffer");
 
 // Stage timestamps (100 MHz device clock) of the last launch, per workgroup,
 // in builds with -DMH_STAGE_TRACE only.
@@ -77,7 +78,6 @@ namespace {
     } while (0)
 #endif
 
-template <bool LIVE_QKV>
 __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma clang fp contract(off)
     __shared__ float act[kFF + 1];
@@ -89,6 +89,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     __shared__ int pbi[4];
     __shared__ int used_s;
     __shared__ float lgt[kCodebook];  // the previous step's logits (chained launches)
+    __shared__ GateLds gl;
 
     __shared__ int wait_failed;  // set when a wait of this workgroup runs out
     if (threadIdx.x == 0) wait_failed = 0;
@@ -101,6 +102,32 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     int budget = kPollBudget;
     uint64_t *LL = a.ll;
 
+    // ---- the end gate (llm.cpp:653-679) in a workgroup of its own (the last):
+    // ln_f of position 0's block output, the 2-row W8A8 gate, the stop rule.  The
+    // channel steps do not wait for it: a frame the gate ends is dropped by the
+    // host, and every state it touches is rewritten before it is read again.
+    if (a.gate && (int)blockIdx.x == kLayerGrid) {
+        const int t = threadIdx.x;
+        float lw[3], lb[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            lw[i] = a.lnf_w[t + 256 * i];
+            lb[i] = a.lnf_b[t + 256 * i];
+        }
+        const bool ok = ll_gather<3>(LL + kLG, kHidden, tag_base | 12u, xm, budget);
+        if (sync_failed(!ok, &wait_failed)) {
+            if (t == 0) atomicOr(a.err, 1u);
+            return;
+        }
+        float o[3];
+        layernorm_768_lds(xm, lw, lb, o);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
+        __syncthreads();
+        gate_block(act, a.wte, st, gl);
+        return;
+    }
+
 #pragma unroll 1
     for (int lpos = a.lpos; lpos <= a.lpos_last; ++lpos) {
         const int n = lpos + 1;
@@ -112,11 +139,12 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         const uint8_t *aemb_in = ch_in >= 0 ? a.aemb[ch_in] : nullptr;
         const uint8_t *head_w = a.head && lpos >= 1 ? a.aemb[lpos - 1] : nullptr;
         float *logits_out = lpos >= 1 ? a.logits + (size_t)(lpos - 1) * kCodebook : nullptr;
-        const bool picking = !LIVE_QKV && ch_in >= 0 && a.pick;
+        const bool live = lpos == 0;  // the block input is the global hidden state: QKV computed here
+        const bool picking = !live && ch_in >= 0 && a.pick;
         const bool pick_ll = picking && lpos > a.lpos;  // logits from this launch's previous step
 
         // ---- stage Q (lpos 0): LN1 + QKV of the block input, one wave per group
-        if constexpr (LIVE_QKV) {
+        if (live) {
             if (b < 3 * kHidden / 16) {
                 GemvStage<1, 6, kHidden> gs;
                 gs.prefetch(a.attn_w, b);
@@ -137,15 +165,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 __syncthreads();
                 const float yv = gs.dot(act, part);
                 const float partner = xshfl<4>(yv);
-                if (gs.storer()) {
-                    const float out = e.apply(r, yv, partner);
-                    const int sec = r / kHidden, within = r - sec * kHidden;
-                    if (sec > 0) {  // llm.cpp:224-225
-                        float *cache = sec == 1 ? a.lk : a.lv;
-                        cache[((size_t)(within >> 6) * kLocalLen + lpos) * kHeadDim + (within & 63)] = out;
-                    }
-                    ll_put(LL + kLQ + r, out, tag);
-                }
+                if (gs.storer()) ll_put(LL + kLQ + r, e.apply(r, yv, partner), tag);  // k, v cached by stage A
                 __syncthreads();
             }
         }
@@ -184,9 +204,13 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 for (int p = 0; p < kLocalLen; ++p) vv[p] = a.lv[((size_t)h * kLocalLen + min(p, kmax)) * kHeadDim + lane];
             }
             // q, k, v of head h at lpos
-            if constexpr (LIVE_QKV) {
+            if (live) {
                 const int seg = min(t >> 6, 2), i = seg * kHidden + h * kHeadDim + (t & 63);
                 const bool ok = ll_wait1(LL + kLQ + i, t < 3 * kHeadDim, tag, &qkv[i], budget);
+                // this position's k, v into the local cache (llm.cpp:224-225) by the workgroup
+                // that reads them at the later positions: same-workgroup ordering, no fence
+                if (ok && t < 3 * kHeadDim && seg > 0)
+                    (seg == 1 ? a.lk : a.lv)[((size_t)h * kLocalLen + lpos) * kHeadDim + (t & 63)] = qkv[i];
                 if (sync_failed(!ok, &wait_failed)) {
                     if (t == 0) atomicOr(a.err, 1u);
                     return;
@@ -290,9 +314,9 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             gs.prefetch(a.proj_w, b);
             const int r = gs.row();
             const float eb = gs.storer() ? a.proj_b[r] : 0.0f;
-            const bool with_code = !LIVE_QKV && ch_in >= 0;  // the raw input row is aemb[ch_in][used]
+            const bool with_code = !live && ch_in >= 0;  // the raw input row is aemb[ch_in][used]
             float eres = 0.0f;
-            if (gs.storer() && !with_code) eres = a.x_in[r];
+            if (gs.storer() && !with_code) eres = (live ? a.x_in : a.x_slot)[r];
             const bool ok = ll_gather<(kHidden + 1 + 255) / 256>(LL + kLA, kHidden + (with_code ? 1 : 0), tag, act, budget);
             if (sync_failed(!ok, &wait_failed)) {
                 if (t == 0) atomicOr(a.err, 1u);
@@ -352,6 +376,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 const float xo = xm[r] + (yv + eb);  // llm.cpp:245
                 a.x_out[r] = xo;
                 if (head_w) ll_put(LL + kLO + r, xo, tag);
+                if (live && a.gate) ll_put(LL + kLG + r, xo, tag);  // the gate workgroup's input
             }
             STAGE_TS(8);
             __syncthreads();
@@ -381,9 +406,37 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             const float yv = gs.dot(act, part);
             if (gs.storer()) {
                 logits_out[gs.row()] = yv;
-                if (lpos < a.lpos_last) ll_put(LL + kLL + gs.row(), yv, tag);  // the next step's pick
+                if (lpos < a.lpos_last || a.final_pick) ll_put(LL + kLL + gs.row(), yv, tag);  // the next pick
             }
             STAGE_TS(10);
+        }
+
+        // ---- after the last position: the greedy pick of its channel, as
+        // sample_kernel does for the last channel (workgroup 0)
+        if (a.final_pick && lpos == a.lpos_last && b == 0) {
+            const int ch = lpos - 1;
+            PickIn pin;
+#pragma unroll
+            for (int k = 0; k < kCodebook / 256; ++k)
+                pin.cnt[k] = st->rep_penalty != 1.0f ? a.counts[(size_t)ch * kCodebook + t + 256 * k] : 0;
+            const bool ok = ll_gather<kCodebook / 256>(LL + kLL, kCodebook, tag, lgt, budget);
+            if (sync_failed(!ok, &wait_failed)) {
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
+            }
+#pragma unroll
+            for (int k = 0; k < kCodebook / 256; ++k) pin.vals[k] = lgt[t + 256 * k];
+            int idx = greedy_pick_reduce(pin, st->rep_penalty, pbv, pbi);
+            if (idx >= kCodebook) idx = 0;
+            const int used = st->forced_on ? a.forced[st->frame * kNVq + ch] : idx;
+            if (t < ch) a.counts[(size_t)t * kCodebook + st->row[t + 1]] += 1;  // the frame's earlier channels
+            if (t == 0) {
+                st->codes[ch] = idx;
+                st->row[ch + 1] = used;
+                a.counts[(size_t)ch * kCodebook + used] += 1;
+                st->row[0] = kSlotToken;
+                st->frame += 1;
+            }
         }
     }  // lpos
     STAGE_FLUSH();
@@ -399,13 +452,7 @@ extern "C" int mh_local_trace_read(unsigned long long *out) {
 #endif
 
 hipError_t decode_local_occupancy(int *per_cu) {
-    int a = 0, b = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, decode_local_kernel<true>, 256, 0);
-    if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, decode_local_kernel<false>, 256, 0);
-    if (e != hipSuccess) return e;
-    *per_cu = a < b ? a : b;
-    return hipSuccess;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_local_kernel, 256, 0);
 }
 
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s) {
@@ -416,17 +463,16 @@ hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s) {
     if (a.head && (!a.logits || !a.lnf_w || !a.lnf_b)) return hipErrorInvalidValue;
     for (int p = a.lpos < 1 ? 1 : a.lpos; p <= a.lpos_last; ++p)  // aemb rows: inputs (p >= 2) and heads
         if ((p >= 2 && !a.aemb[p - 2]) || (a.head && !a.aemb[p - 1])) return hipErrorInvalidValue;
-    if (a.lpos == 0) {
-        if (a.lpos_last != 0 || !a.x_in || !a.rope_cos || !a.rope_sin) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(decode_local_kernel<true>, dim3(kLayerGrid), dim3(256), 0, s, a);
-    } else {
-        if (!a.qkv_table) return hipErrorInvalidValue;
-        if (a.lpos == 1 && !a.x_in) return hipErrorInvalidValue;
-        if (a.lpos_last >= 2 && a.pick && (!a.logits || !a.counts || !a.forced)) return hipErrorInvalidValue;
-        // a chained pick reads the previous step's head: every step but the last runs one
-        if (a.lpos_last > a.lpos && a.pick && !a.head) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(decode_local_kernel<false>, dim3(kLayerGrid), dim3(256), 0, s, a);
-    }
+    if (a.lpos == 0 && (!a.x_in || !a.rope_cos || !a.rope_sin)) return hipErrorInvalidValue;
+    if (a.gate && (a.lpos != 0 || !a.wte || !a.lnf_w || !a.lnf_b)) return hipErrorInvalidValue;
+    if (a.lpos_last >= 1 && !a.qkv_table) return hipErrorInvalidValue;
+    if (a.lpos <= 1 && a.lpos_last >= 1 && !a.x_slot) return hipErrorInvalidValue;
+    if (a.lpos_last >= 2 && a.pick && (!a.logits || !a.counts || !a.forced)) return hipErrorInvalidValue;
+    // a chained pick reads the previous step's head: every step but the last runs one
+    if (a.lpos_last > a.lpos && a.lpos_last >= 2 && a.pick && !a.head) return hipErrorInvalidValue;
+    if (a.final_pick && (!a.pick || !a.head || a.lpos_last < 1 || !a.counts || !a.forced)) return hipErrorInvalidValue;
+    // one more workgroup for the end gate
+    hipLaunchKernelGGL(decode_local_kernel, dim3(kLayerGrid + (a.gate ? 1 : 0)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

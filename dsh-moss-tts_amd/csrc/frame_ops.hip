@@ -209,9 +209,7 @@ __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const flo
 #pragma clang fp contract(off)
     __shared__ float red[4];
     __shared__ float hbuf[kHidden];
-    __shared__ int8_t qa[kHidden];
-    __shared__ float da[kHidden / 32];
-    __shared__ float lanes[2][8];
+    __shared__ GateLds g;
     const bool stopped = state->stop;  // tested once the input is loaded
     const int t = threadIdx.x;
     float v[3], o[3];
@@ -222,54 +220,7 @@ __global__ __launch_bounds__(256) void gate_kernel(const float *x_raw, const flo
 #pragma unroll
     for (int i = 0; i < 3; ++i) hbuf[t + 256 * i] = o[i];
     __syncthreads();
-    const int nb = kHidden / 32;
-    if (t < nb) {
-        float amax = 0.0f;
-        for (int i = 0; i < 32; ++i) {
-            const float av = fabsf(hbuf[32 * t + i]);
-            amax = amax < av ? av : amax;
-        }
-        const float d = amax / 127.0f;
-        const float id = d > 0.0f ? 1.0f / d : 0.0f;
-        da[t] = d;
-        for (int i = 0; i < 32; ++i) {
-            int q = (int)rintf(hbuf[32 * t + i] * id);
-            q = q < -127 ? -127 : (q > 127 ? 127 : q);
-            qa[32 * t + i] = (int8_t)q;
-        }
-    }
-    __syncthreads();
-    if (t < 16) {
-        const int which = t >> 3, lane = t & 7;
-        const int r = which == 0 ? kEndToken : kSlotToken;
-        const uint8_t *grp = wte + (size_t)(r >> 2) * nb * kBlockBytes;
-        float acc = 0.0f;
-        for (int b = 0; b < nb; ++b) {
-            const uint8_t *blk = grp + (size_t)b * kBlockBytes;
-            const float dw = h2f(*(const uint16_t *)(blk + 2 * (r & 3)));
-            const int8_t *qs = (const int8_t *)(blk + 8 + 32 * (r & 3));
-            int32_t p = 0;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) p += (int32_t)qs[4 * lane + u] * (int32_t)qa[32 * b + 4 * lane + u];
-            const float scale = dw * da[b];
-            acc = fmaf((float)p, scale, acc);
-        }
-        lanes[which][lane] = acc;
-    }
-    __syncthreads();
-    if (t == 0) {
-        float g[2];
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const float *a8 = lanes[w];
-            const float s0 = a8[0] + a8[4], s1 = a8[1] + a8[5], s2 = a8[2] + a8[6], s3 = a8[3] + a8[7];
-            const float t0 = s0 + s2, t1 = s1 + s3;
-            g[w] = t0 + t1;
-        }
-        state->gate[0] = g[0];
-        state->gate[1] = g[1];
-        if (state->frame >= state->min_frames && end_reached(g[1], g[0], state->cfg, state->rng)) state->stop = 1;
-    }
+    gate_block(hbuf, wte, state, g);
 }
 
 // End gate of a frame whose gate is dumped (llm.cpp:653-679): the reference then

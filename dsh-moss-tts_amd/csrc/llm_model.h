@@ -111,7 +111,7 @@ private:
     KvType kvt_ = KV_F16;
     size_t kv_esize_ = 2;
     hipStream_t stream_ = nullptr;
-    hipEvent_t ev_[3] = {};
+    hipEvent_t ev_[8] = {};             // per frame slot (2): local start, local end, global end, state copied
 
     uint8_t *blob_ = nullptr;
     LayerW g_[kLayers] = {}, local_ = {};
@@ -140,6 +140,7 @@ private:
     float *pre_d8_ = nullptr;            //   and their block scales [m][<=96]
     DevState *state_ = nullptr;          // device
     DevState *hstate_ = nullptr;         // pinned host mirror
+    DevState *hread_ = nullptr;          // [2] pinned per-frame state readback (frames alternate)
     void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]
 
     hipGraphExec_t g_global_ = nullptr, g_local_ = nullptr, g_local_fused_ = nullptr;

@@ -349,4 +349,70 @@ __device__ __forceinline__ float gelu_new(float v) {
     return 0.5f * v * (1.0f + tanhf(k * (v + v3)));
 }
 
+// The 2-row W8A8 end gate on h = ln_f(x) (llm.cpp:272-315, as gate_kernel):
+// per-32-block activation quantisation (quant.cpp:28-54), the int32 block dots
+// of wte rows 7 (end) and 9 (slot) in the reference's lane order, the stop
+// rule.  Called by all 256 threads of a workgroup with h in LDS; thread 0
+// writes state->gate and, when the frame ends, state->stop.
+struct GateLds {
+    int8_t qa[kHidden];
+    float da[kHidden / 32];
+    float lanes[2][8];
+};
+__device__ __forceinline__ void gate_block(const float *hbuf, const uint8_t *wte, DevState *state, GateLds &G) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x;
+    int8_t *qa = G.qa;
+    float *da = G.da;
+    float (*lanes)[8] = G.lanes;
+    const int nb = kHidden / 32;
+    if (t < nb) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float av = fabsf(hbuf[32 * t + i]);
+            amax = amax < av ? av : amax;
+        }
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        da[t] = d;
+        for (int i = 0; i < 32; ++i) {
+            int q = (int)rintf(hbuf[32 * t + i] * id);
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            qa[32 * t + i] = (int8_t)q;
+        }
+    }
+    __syncthreads();
+    if (t < 16) {
+        const int which = t >> 3, lane = t & 7;
+        const int r = which == 0 ? kEndToken : kSlotToken;
+        const uint8_t *grp = wte + (size_t)(r >> 2) * nb * kBlockBytes;
+        float acc = 0.0f;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t *blk = grp + (size_t)b * kBlockBytes;
+            const float dw = h2f(*(const uint16_t *)(blk + 2 * (r & 3)));
+            const int8_t *qs = (const int8_t *)(blk + 8 + 32 * (r & 3));
+            int32_t p = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) p += (int32_t)qs[4 * lane + u] * (int32_t)qa[32 * b + 4 * lane + u];
+            const float scale = dw * da[b];
+            acc = fmaf((float)p, scale, acc);
+        }
+        lanes[which][lane] = acc;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float g[2];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const float *a8 = lanes[w];
+            const float s0 = a8[0] + a8[4], s1 = a8[1] + a8[5], s2 = a8[2] + a8[6], s3 = a8[3] + a8[7];
+            const float t0 = s0 + s2, t1 = s1 + s3;
+            g[w] = t0 + t1;
+        }
+        state->gate[0] = g[0];
+        state->gate[1] = g[1];
+        if (state->frame >= state->min_frames && end_reached(g[1], g[0], state->cfg, state->rng)) state->stop = 1;
+    }
+}
+
 }  // namespace mh

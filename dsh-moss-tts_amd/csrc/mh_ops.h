@@ -315,15 +315,20 @@ struct LocalArgs {
     unsigned *err = nullptr;
     int lpos = 0;                      // first local position of the launch
     int lpos_last = 0;                 // last one (positions 1..16 may run as one chain)
-    const float *x_in = nullptr;       // lpos 0: block input (QKV computed here); lpos 1: the raw input row
+    const float *x_in = nullptr;       // lpos 0: block input (the global hidden state; QKV computed here)
+    const float *x_slot = nullptr;     // lpos 1: the raw input row (dequantised wte[slot])
     const float *qkv_table = nullptr;  // [1 + 15 * 1024][2304]: row 0 for lpos 1, then (lpos, code) rows
     const uint8_t *aemb[kNVq] = {};    // audio embeddings / tied heads
     int pick = 0;                      // 1: greedy pick of the previous channel here; 0: the sampler wrote state->row
     int head = 0;                      // 1: position lpos >= 1 also runs the audio head of channel lpos - 1
     float *logits = nullptr;           // [16][1024] head outputs (channel ch at ch * 1024)
-    const int *counts = nullptr;       // [16][1024] repetition counts
+    int *counts = nullptr;             // [16][1024] repetition counts (the final pick adds the frame's codes)
     const int *forced = nullptr;
     float *x_out = nullptr;            // block output (768)
+    int gate = 0;                      // 1: after position 0, the W8A8 end gate (wte rows 7, 9); a stop ends the launch
+    const uint8_t *wte = nullptr;
+    int final_pick = 0;                // 1: after the last position, the greedy pick of its channel, the
+                                       // frame's code counts, row[0] = slot and frame + 1 (sample_kernel's work)
 };
 hipError_t decode_local_occupancy(int *per_cu);
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s);
