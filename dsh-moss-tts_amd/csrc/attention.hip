@@ -11,7 +11,9 @@
 // one page of max_ctx positions.
 //
 // One workgroup per (head, row) with NW wavefronts.  Keys are taken in spans of
-// 64 (one key per lane for the scores); wave w takes spans w, w+NW, ... with an
+// 64; each K load instruction brings 8 whole 128-byte rows (8 lanes per key),
+// and the 8 lanes of a key combine their partial dots, so every lane ends with
+// one key's score.  Wave w takes spans w, w+NW, ... with an
 // online softmax across its spans; the waves are then merged through LDS with a
 // log-sum-exp combine -- split-KV inside the workgroup, no cross-workgroup
 // traffic.  Every K/V load is unconditional (rows past the live count are
@@ -73,6 +75,14 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     float m = -INFINITY, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     const int pg = lane >> 4, dg = lane & 15;
+    // K: load c brings 16 bytes of key RPI*c + rr (dims sub*EPL ..), so one load
+    // instruction covers RPI whole rows; the LPR lanes of a key then combine
+    // their partial dots, and lane ends with the score of key kl of the span
+    constexpr int LPR = KV == KV_F16 ? 8 : 16, EPL = 64 / LPR, RPI = 64 / LPR;
+    const int sub = lane & (LPR - 1), rr = lane / LPR, kl = RPI * sub + rr;
+    float qsub[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qsub[e] = qs[sub * EPL + e];
     // PART: exactly one span, [64 * blockIdx.y, min(n, 64 * blockIdx.y + 64))
     const int span0 = PART ? (int)blockIdx.y : w, span_step = PART ? 1 : NW;
     const int key_end = PART ? min(n, span0 * 64 + 64) : n;
@@ -88,28 +98,38 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
 #pragma unroll
         for (int t = 0; t < 16; ++t)
             vv[t] = load4<KV>(a.v_pool, base + (size_t)min(pg + 4 * t, cnt - 1) * kHeadDim + 4 * dg);
-        // scores, one key per lane
-        const size_t krow = base + (size_t)min(lane, cnt - 1) * kHeadDim;
-        float kf[8][8];
+        float pd[LPR];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) load_row8<KV>(a.k_pool, krow + 8 * c, kf[c]);
-        float dot = 0.0f;
+        for (int c = 0; c < LPR; ++c) {
+            const size_t ki = base + (size_t)min(RPI * c + rr, cnt - 1) * kHeadDim + sub * EPL;
+            float kf[EPL];
+            if constexpr (KV == KV_F16) {
+                float tmp[8];
+                load_row8<KV>(a.k_pool, ki, tmp);
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
+                for (int e = 0; e < EPL; ++e) kf[e] = tmp[e];
+            } else {
+                const float4 v4 = *(const float4 *)((const float *)a.k_pool + ki);
+                kf[0] = v4.x; kf[1] = v4.y; kf[2] = v4.z; kf[3] = v4.w;
+            }
+            float d = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) dot = fmaf(qs[8 * c + e], kf[c][e], dot);
+            for (int e = 0; e < EPL; ++e) d = fmaf(qsub[e], kf[e], d);
+            pd[c] = d;
+        }
+        float dot = key_reduce<LPR>(pd, sub);  // q . k of key kl
         dot *= 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
-        const float smax = wave_max(lane < cnt ? dot : -INFINITY);
+        const float smax = wave_max(kl < cnt ? dot : -INFINITY);
         const float m_new = fmaxf(m, smax);
         const float rescale = expf(m - m_new);  // 0 on the first span (m = -inf)
-        const float e = lane < cnt ? expf(dot - m_new) : 0.0f;
+        const float e = kl < cnt ? expf(dot - m_new) : 0.0f;
         l = l * rescale + wave_sum(e);
         m = m_new;
         o.x *= rescale;
         o.y *= rescale;
         o.z *= rescale;
         o.w *= rescale;
-        sc[w][lane] = e;
+        sc[w][kl] = e;
         // sc[w][*] is written and read by different lanes of this one wave
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();

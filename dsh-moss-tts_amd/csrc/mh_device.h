@@ -136,6 +136,27 @@ __device__ __forceinline__ float xshfl(float v) {
     return __int_as_float(xshfl<M>(__float_as_int(v)));
 }
 
+// Sum over the L lanes of a key (lanes differing in the low log2(L) bits of
+// `sub`) of L partial dots at once: each step keeps half of the values and
+// adds the partner's copy of them, so lane sub ends with the total of pd[sub].
+template <int L>
+__device__ __forceinline__ float key_reduce(float (&pd)[L], int sub) {
+    if constexpr (L == 1) {
+        return pd[0];
+    } else {
+        constexpr int H = L / 2;
+        const bool upper = (sub & H) != 0;
+        float nx[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float keep = upper ? pd[i + H] : pd[i];
+            const float give = upper ? pd[i] : pd[i + H];
+            nx[i] = keep + xshfl<H>(give);
+        }
+        return key_reduce<H>(nx, sub);
+    }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += xshfl<32>(v);
     v += xshfl<16>(v);
