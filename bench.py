@@ -16,12 +16,14 @@ launch over its average duration from HIP events on its stream.
 cpu_baseline: the reference's own AVX2 CPU path (oracle/_ref, compiled from the
 reference sources) decoding from the same context-512 state on this host.
 
-Also reported: the 256-row prefill (ms; W8A8 as the reference's prefill, against
+Also reported: single-query decode attention (12 x 64 heads, fp16 K/V) at
+contexts 128, 512, 1024 and 2048, warm and cold, beside the reference's AVX2
+attention on one host core; the 256-row prefill (ms; W8A8 as the reference's prefill, against
 the 5.0 POP/s int8 MFMA peak, and W8A16 against the 2.5 PFLOP/s fp16 peak) and 64 streams with contexts ~ U[64, 1024] decoded 128 frames in
 lock-step (aggregate frames/s), each next to the reference on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
-                       [--mode full|gemv|decode|prefill|streams]
+                       [--mode full|gemv|attn|decode|prefill|streams]
 """
 from __future__ import annotations
 
@@ -184,6 +186,75 @@ def bench_prefill(blob, reps: int = 5, a16: bool = False):
     # against the dense matrix-core peak of the arithmetic used: int8 (W8A8) or fp16 (W8A16)
     peak = MFMA_F16_PEAK_TFLOPS if a16 else MFMA_I8_PEAK_TOPS
     return {"ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / peak}
+
+
+ATTN_CTX = (128, 512, 1024, 2048)
+
+
+def bench_attention(reps: int = 100):
+    """Single-query decode attention (12 heads x 64, fp16 K/V [12][ctx][64], fp32 q and
+    output) at each context length: warm (one cache, Infinity-Cache resident) and cold
+    (caches cycled through a pool of more than 512 MB), `reps` calls replayed from a graph.  Algorithmic bytes per call:
+    K and V (2 * 2 * 768 * ctx) + q and output (2 * 4 * 768 / 2 = 3072)."""
+    import torch
+
+    from mosship import lib
+    res = {}
+    cap = torch.cuda.Stream()
+    for ctx in ATTN_CTX:
+        per = 2 * 12 * ctx * 64 * 2  # bytes of one K + V pair
+        pool_n = max(2, -(-(512 << 20) // per))
+        g = torch.Generator(device="cuda").manual_seed(ctx)
+        kv = torch.randn((pool_n, 2, 12, ctx, 64), generator=g, device="cuda").to(torch.float16)
+        q = torch.randn(768, generator=g, device="cuda")
+        out = torch.empty(768, device="cuda")
+        algo = 3072 * ctx + 3072
+        r = {"algo_bytes": algo}
+        with torch.cuda.stream(cap):  # warm-up on the capture stream (its split-KV scratch is made here)
+            for i in range(min(pool_n, 16)):
+                lib.attn_decode(q, kv[i, 0], kv[i, 1], 12, ctx, ctx, out)
+        torch.cuda.synchronize()
+        # the calls are captured in a graph and replayed, so the time is the kernels', not the host's
+        for mode in ("cold", "warm"):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=cap):
+                for i in range(reps):
+                    j = i % pool_n if mode == "cold" else 0
+                    lib.attn_decode(q, kv[j, 0], kv[j, 1], 12, ctx, ctx, out)
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            r[f"us_{mode}"] = round(us, 3)
+            r[f"GBps_{mode}"] = round(algo / us / 1e3, 1)
+        r["frac_cold"] = round(r["GBps_cold"] / HBM_PEAK_GBS, 4)
+        res[str(ctx)] = r
+        del kv
+    return res
+
+
+def cpu_attention(reps: int = 20):
+    """The reference's AVX2 single-query attention (attn_avx2.cpp:93, one thread) at the
+    same context lengths: ctx - 1 cached keys plus the query row's own k/v."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import RefCpu
+    r = RefCpu(a16_mode="decode")
+    rng = np.random.default_rng(5)
+    out = {}
+    for ctx in ATTN_CTX:
+        qkv = rng.standard_normal(3 * 768).astype(np.float32)
+        kc = rng.standard_normal((ctx - 1, 768)).astype(np.float16).astype(np.float32)
+        vc = rng.standard_normal((ctx - 1, 768)).astype(np.float16).astype(np.float32)
+        r.attention_window(qkv, kc, vc)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            r.attention_window(qkv, kc, vc)
+        out[str(ctx)] = round((time.perf_counter() - t0) / reps * 1e6, 2)
+    return {"us": out, "threads": 1}
 
 
 def stream_contexts(seed: int = 64, lo: int = 64, hi: int = 1024):
@@ -351,7 +422,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "decode", "prefill", "streams"], default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams"], default="full")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -367,6 +438,9 @@ def main():
     if args.mode == "gemv":
         g = bench_gemv()
         print(json.dumps({"gemv": g}), flush=True)
+        return
+    if args.mode == "attn":
+        print(json.dumps({"attention_decode": bench_attention()}), flush=True)
         return
 
     log("generating synthetic model + ctx-512 state")
@@ -385,15 +459,18 @@ def main():
         return
     log("gemv roofline")
     g = bench_gemv()
+    log("decode attention")
+    at = bench_attention()
     log("prefill (256 rows)")
     pf = bench_prefill(blob)
     pf16 = bench_prefill(blob, a16=True)
     log("64 streams")
     st = bench_streams(blob)
-    cpu = cpu_pf = cpu_st = None
+    cpu = cpu_pf = cpu_st = cpu_at = None
     if not args.no_cpu:
         log("cpu baseline (reference)")
         cpu = cpu_baseline(blob, state)
+        cpu_at = cpu_attention()
         cpu_pf = cpu_prefill(blob)
         cpu_st = cpu_streams(blob)
     # global step at position 512: weights + vectors + embed + fp16 KV read/write
@@ -432,6 +509,7 @@ def main():
             "traffic_note": "bytes/launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated), "
                             f"{GEMV_TRAFFIC_BYTES / g['algo_bytes']:.3f}x the algorithmic bytes",
         },
+        "attention_decode": {"ctx": at, "cpu_ref": cpu_at},
         "prefill_256": {"mode": "w8a8 (the reference's prefill)", "ms": round(pf["ms"], 3),
                         "TOP/s": round(pf["TFLOPs"], 2), "mfma_frac": round(pf["mfma_frac"], 4),
                         "a16_ms": round(pf16["ms"], 3), "a16_mfma_frac": round(pf16["mfma_frac"], 4),

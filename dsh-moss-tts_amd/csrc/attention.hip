@@ -19,6 +19,7 @@
 // traffic.  Every K/V load is unconditional (rows past the live count are
 // clamped to a live row and weighted 0), and a span's V values are loaded with
 // its K rows, so all of a lane's loads for the span are in flight together.
+#include "mh_ll.h"
 #include "mh_ops.h"
 
 namespace mh {
@@ -55,7 +56,7 @@ __device__ __forceinline__ float4 load4(const void *base, size_t idx) {
     }
 }
 
-template <int KV, int NW, bool PART>
+template <int KV, int NW, bool PART, bool CHUNK = false>
 __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     __shared__ float qs[kHeadDim];
     __shared__ float sc[NW][64];
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     __shared__ float pm[NW], pl[NW];
     const bool stopped = a.state != nullptr && a.state->stop;  // tested once q is loaded
     // PART: one 64-key span per workgroup (blockIdx.y), one row
-    const int h = blockIdx.x, r = PART ? 0 : blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = blockIdx.x, r = (PART || CHUNK) ? 0 : blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int s = a.row_stream ? a.row_stream[r] : r * a.stream_stride;
     // keys of this row, never past the capacity the caches were built for (a
     // stream parked at capacity keeps pos == capacity)
@@ -83,8 +84,10 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     float qsub[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) qsub[e] = qs[sub * EPL + e];
-    // PART: exactly one span, [64 * blockIdx.y, min(n, 64 * blockIdx.y + 64))
-    const int span0 = PART ? (int)blockIdx.y : w, span_step = PART ? 1 : NW;
+    // PART: exactly one span, [64 * blockIdx.y, min(n, 64 * blockIdx.y + 64));
+    // CHUNK: workgroup y takes spans NW*y + w, then every NW*chunks further
+    const int span0 = PART ? (int)blockIdx.y : (CHUNK ? NW * (int)blockIdx.y + w : w);
+    const int span_step = PART ? 1 : (CHUNK ? NW * (int)gridDim.y : NW);
     const int key_end = PART ? min(n, span0 * 64 + 64) : n;
     if (PART && span0 * 64 >= n) return;  // a span past the live keys: the merge skips it
     for (int span = span0; span * 64 < key_end; span += span_step) {
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     __syncthreads();
     if (w != 0) return;
     // log-sum-exp merge of the waves that saw keys; lane = output dimension
-    const int live = min(NW, (n + 63) / 64);
+    const int live = CHUNK ? min(NW, (n + 63) / 64 - NW * (int)blockIdx.y) : min(NW, (n + 63) / 64);
     float M = -INFINITY;
     for (int t = 0; t < live; ++t) M = fmaxf(M, pm[t]);
     float L = 0.0f, O = 0.0f;
@@ -180,6 +183,46 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         const float sw = expf(pm[t] - M);
         L = fmaf(pl[t], sw, L);
         O = fmaf(((const float *)&po[t][0])[lane], sw, O);
+    }
+    if constexpr (CHUNK) {
+        // this slice's partial as LL words, then the last slice of the head to
+        // arrive collects every partial (each word carries its own flag) and merges
+        uint64_t *pp = a.chunk_part + ((size_t)h * gridDim.y + blockIdx.y) * kPartStride;
+        ll_put(pp + lane, O, a.chunk_tag);
+        if (lane == 0) {
+            ll_put(pp + 64, M, a.chunk_tag);
+            ll_put(pp + 65, L, a.chunk_tag);
+        }
+        unsigned prev = 0;
+        if (lane == 0) prev = atomicAdd(a.chunk_count + h, 1u);
+        prev = __shfl(prev, 0);
+        if (prev + 1 != gridDim.y) return;
+        const uint64_t *hp = a.chunk_part + (size_t)h * gridDim.y * kPartStride;
+        int budget = kPollBudget;
+        bool ok = true;
+        auto word = [&](size_t i) {  // waits for the word's tag (bounded)
+            uint64_t v = ll_load(hp + i);
+            while ((uint32_t)(v >> 32) != a.chunk_tag) {
+                if (--budget < 0) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                v = ll_load(hp + i);
+            }
+            return __uint_as_float((uint32_t)v);
+        };
+        M = -INFINITY;
+        for (unsigned c = 0; c < gridDim.y; ++c) M = fmaxf(M, word(c * kPartStride + 64));
+        L = 0.0f;
+        O = 0.0f;
+        for (unsigned c = 0; c < gridDim.y; ++c) {
+            const float sw = expf(word(c * kPartStride + 64) - M);
+            L = fmaf(word(c * kPartStride + 65), sw, L);
+            O = fmaf(word(c * kPartStride + lane), sw, O);
+        }
+        if (!ok) O = __int_as_float(0x7fc00000);  // a slice never arrived: NaN, not a stale value
+        if (lane == 0) a.chunk_count[h] = 0;       // ready for the next launch on this stream
     }
     const float res = O / L;
     const size_t oi = (size_t)r * a.out_stride + h * kHeadDim + lane;
@@ -206,6 +249,10 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, true>), dim3(a.heads, spans), dim3(64), 0, s, a);
         return hipGetLastError();
     }
+    if (a.chunks > 0) {  // one row, slices of 4 spans merged by the last slice of each head
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false, true>), dim3(a.heads, a.chunks), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     const dim3 grid(a.heads, a.rows);
     if (spans <= 1)
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, false>), grid, dim3(64), 0, s, a);
@@ -223,6 +270,10 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
         return hipErrorInvalidValue;
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
     if (a.q8 != nullptr && (!a.d8 || a.part != nullptr || a.heads != kHeads)) return hipErrorInvalidValue;
+    if (a.chunks != 0 && (a.chunks < 0 || a.chunks > kMaxChunks || a.rows != 1 || a.part != nullptr ||
+                          a.page_table != nullptr || a.q8 != nullptr || !a.chunk_part || !a.chunk_count ||
+                          4 * 64 * (a.chunks - 1) >= a.max_keys))
+        return hipErrorInvalidValue;  // every slice holds at least one live span
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
 }
 

@@ -2,7 +2,10 @@
 // No exception crosses this boundary: failures become status codes plus a
 // thread-local message (moss_hip_last_error).
 #include <cstdio>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "batch_model.h"
@@ -20,6 +23,43 @@ struct moss_hip_batch {
 namespace {
 
 thread_local std::string g_err;
+
+// Split-KV partials and per-head arrival counts of moss_hip_attn_decode, one set
+// per (device, stream): launches on one stream run in order, so each finds the
+// counts its predecessor reset.  Allocated on first use, grown with the head
+// count, kept until the process ends.
+struct AttnScratch {
+    uint64_t *part = nullptr;
+    unsigned *count = nullptr;
+    int heads = 0;
+    uint32_t tag = 0;  // LL tag of the last launch (0 is never used)
+};
+std::mutex g_scratch_mu;
+std::map<std::pair<int, hipStream_t>, AttnScratch> g_scratch;
+
+AttnScratch attn_scratch(hipStream_t s, int heads) {  // returns the entry with the tag of this launch
+    int dev = 0;
+    mh::hip_check(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    AttnScratch &e = g_scratch[{dev, s}];
+    if (e.heads < heads) {
+        if (e.part) {
+            mh::hip_check(hipStreamSynchronize(s), "sync");  // launches still using the old buffers
+            (void)hipFree(e.part);
+            (void)hipFree(e.count);
+            e = AttnScratch{};
+        }
+        mh::hip_check(hipMalloc(&e.part, sizeof(uint64_t) * heads * mh::kMaxChunks * mh::kPartStride),
+                      "hipMalloc(attention partials)");
+        mh::hip_check(hipMemset(e.part, 0, sizeof(uint64_t) * heads * mh::kMaxChunks * mh::kPartStride),
+                      "memset(attention partials)");
+        mh::hip_check(hipMalloc(&e.count, sizeof(unsigned) * heads), "hipMalloc(attention counts)");
+        mh::hip_check(hipMemset(e.count, 0, sizeof(unsigned) * heads), "memset(attention counts)");
+        e.heads = heads;
+    }
+    if (++e.tag == 0) e.tag = 1;
+    return e;
+}
 
 template <class F>
 int guard(F &&f) {
@@ -343,6 +383,15 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
         a.out = out;
         a.out_f16 = out_dtype == MOSS_HIP_F16;
         const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
+        const int spans = (n_keys + 63) / 64;
+        if (spans > 4) {  // past one workgroup's 4 spans: slices of 256 keys across workgroups
+            const AttnScratch sc = attn_scratch(static_cast<hipStream_t>(stream), heads);
+            const int chunks = (spans + 3) / 4;
+            a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;
+            a.chunk_part = sc.part;
+            a.chunk_count = sc.count;
+            a.chunk_tag = sc.tag;
+        }
         mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
     });
 }

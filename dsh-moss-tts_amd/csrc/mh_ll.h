@@ -8,6 +8,7 @@
 // no barrier, counter or fence.  Every wait is bounded by a poll budget.
 #pragma once
 #include "mh_device.h"
+#include "mh_gemv.h"
 
 namespace mh {
 

@@ -97,8 +97,18 @@ struct AttnArgs {
     int8_t *q8 = nullptr;
     float *d8 = nullptr;
     const DevState *state = nullptr;
+    // single row, long context: the keys are cut into `chunks` slices of 256 (one workgroup of
+    // 4 waves each, more spans per wave past kMaxChunks), each writes its partial (o[64], m, l)
+    // as LL words tagged chunk_tag to chunk_part[(h * chunks + c) * kPartStride] and adds one to
+    // chunk_count[h]; the last one of a head collects the partials (waiting on their tags),
+    // merges them in chunk order, writes the output and resets the count to 0
+    int chunks = 0;
+    uint64_t *chunk_part = nullptr;
+    unsigned *chunk_count = nullptr;
+    uint32_t chunk_tag = 0;          // distinct for consecutive launches on one stream
 };
 constexpr int kPartStride = 68;
+constexpr int kMaxChunks = 64;
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s);
 
 // W8A16 GEMM on the matrix cores: Y[M][N] = A[M][K] W[N][K]^T with an epilogue.

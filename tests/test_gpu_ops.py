@@ -107,7 +107,7 @@ def _to_cache(rows_768, ctx_stride, dtype):
     return c
 
 
-@pytest.mark.parametrize("ctx", [1, 17, 33, 64, 65, 128, 512, 767, 1024, 1025, 2048, 4096])
+@pytest.mark.parametrize("ctx", [1, 17, 33, 64, 65, 128, 256, 257, 512, 767, 1024, 1025, 2048, 4096, 16641])
 @pytest.mark.parametrize("kv", ["f16", "f32"])
 def test_attention_decode_vs_oracle(torch_gpu, oracle, ctx, kv):
     torch = torch_gpu
@@ -124,6 +124,22 @@ def test_attention_decode_vs_oracle(torch_gpu, oracle, ctx, kv):
     ref = oracle.attention(k.astype(npdt).astype(np.float32), v.astype(npdt).astype(np.float32), q)
     assert max_rel(out.cpu().numpy(), ref) <= TOL
     assert max_rel(out16.cpu().numpy().astype(np.float32), ref) <= TOL
+
+
+def test_attention_decode_back_to_back(torch_gpu, oracle):
+    """Past 256 keys the heads are cut into slices whose partials the last slice of
+    each head merges, resetting its arrival count: consecutive calls with different
+    slice counts on one stream each see a clean count."""
+    torch = torch_gpu
+    for ctx in (2048, 300, 257, 5000, 1300):
+        print(f"attention back-to-back ctx={ctx}", flush=True)
+        q, k, v = _attn_case(oracle, ctx, ctx + 11)
+        kc, vc = _to_cache(k, ctx, np.float16), _to_cache(v, ctx, np.float16)
+        out = torch.empty(768, dtype=torch.float32, device="cuda")
+        lib.attn_decode(_dev(torch, q), _dev(torch, kc), _dev(torch, vc), 12, ctx, ctx, out)
+        torch.cuda.synchronize()
+        ref = oracle.attention(k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32), q)
+        assert max_rel(out.cpu().numpy(), ref) <= TOL
 
 
 def test_attention_single_key_returns_v(torch_gpu):
