@@ -18,108 +18,131 @@
 // log-sum-exp combine -- split-KV inside the workgroup, no cross-workgroup
 // traffic.  Every K/V load is unconditional (rows past the live count are
 // clamped to a live row and weighted 0), and a span's V values are loaded with
-// its K rows, so all of a lane's loads for the span are in flight together.
+// its K rows, so all of a lane's loads for the span are in flight together; the
+// first span is requested before q.
+#include <type_traits>
+
 #include "mh_ll.h"
 #include "mh_ops.h"
 
 namespace mh {
 namespace {
 
+// The raw K and V of one 64-key span as one lane holds them: K load c brings 16
+// bytes (dims sub*EPL..) of key RPI*c + rr, V load t the dims 4dg..4dg+3 of key
+// pg + 4t.  Rows past the span's live count are clamped to its last live row.
 template <int KV>
-__device__ __forceinline__ void load_row8(const void *base, size_t idx, float (&f)[8]) {
-    if constexpr (KV == KV_F16) {
-        const uint4 raw = *(const uint4 *)((const __half *)base + idx);
-        const __half2 *h = (const __half2 *)&raw;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float2 t = __half22float2(h[i]);
-            f[2 * i] = t.x;
-            f[2 * i + 1] = t.y;
-        }
-    } else {
-        const float4 a = *(const float4 *)((const float *)base + idx);
-        const float4 b = *(const float4 *)((const float *)base + idx + 4);
-        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    }
-}
+struct SpanRaw {
+    static constexpr int LPR = KV == KV_F16 ? 8 : 16, EPL = 64 / LPR, RPI = 64 / LPR;
+    using VT = typename std::conditional<KV == KV_F16, uint2, uint4>::type;
+    uint4 k[LPR];
+    VT v[16];
 
-template <int KV>
-__device__ __forceinline__ float4 load4(const void *base, size_t idx) {
-    if constexpr (KV == KV_F16) {
-        const uint2 raw = *(const uint2 *)((const __half *)base + idx);
-        const __half2 *h = (const __half2 *)&raw;
-        const float2 a = __half22float2(h[0]), b = __half22float2(h[1]);
-        return make_float4(a.x, a.y, b.x, b.y);
-    } else {
-        return *(const float4 *)((const float *)base + idx);
+    __device__ __forceinline__ void load(const void *k_pool, const void *v_pool, size_t base, int cnt, int sub,
+                                         int rr, int pg, int dg) {
+        // base and cnt are wave-uniform: a scalar base plus 32-bit lane offsets
+        constexpr unsigned esz = KV == KV_F16 ? 2 : 4;
+        const char *kb = (const char *)k_pool + base * esz, *vb = (const char *)v_pool + base * esz;
+#pragma unroll
+        for (int c = 0; c < LPR; ++c)
+            k[c] = *(const uint4 *)(kb + (unsigned)(min(RPI * c + rr, cnt - 1) * kHeadDim + sub * EPL) * esz);
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            v[t] = *(const VT *)(vb + (unsigned)(min(pg + 4 * t, cnt - 1) * kHeadDim + 4 * dg) * esz);
     }
-}
+    __device__ __forceinline__ float4 vf(int t) const {
+        if constexpr (KV == KV_F16) {
+            const __half2 *hh = (const __half2 *)&v[t];
+            const float2 x = __half22float2(hh[0]), y = __half22float2(hh[1]);
+            return make_float4(x.x, x.y, y.x, y.y);
+        } else {
+            return make_float4(__uint_as_float(v[t].x), __uint_as_float(v[t].y), __uint_as_float(v[t].z),
+                               __uint_as_float(v[t].w));
+        }
+    }
+    // this lane's part of q . k for K load c
+    __device__ __forceinline__ float kdot(int c, const float (&qsub)[EPL]) const {
+        float kf[EPL];
+        if constexpr (KV == KV_F16) {
+            const __half2 *hh = (const __half2 *)&k[c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 t = __half22float2(hh[i]);
+                kf[2 * i] = t.x;
+                kf[2 * i + 1] = t.y;
+            }
+        } else {
+            kf[0] = __uint_as_float(k[c].x);
+            kf[1] = __uint_as_float(k[c].y);
+            kf[2] = __uint_as_float(k[c].z);
+            kf[3] = __uint_as_float(k[c].w);
+        }
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) d = fmaf(qsub[e], kf[e], d);
+        return d;
+    }
+};
 
 template <int KV, int NW, bool PART, bool CHUNK = false>
 __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
-    __shared__ float qs[kHeadDim];
     __shared__ float sc[NW][64];
     __shared__ float4 po[NW][16];
     __shared__ float pm[NW], pl[NW];
-    const bool stopped = a.state != nullptr && a.state->stop;  // tested once q is loaded
     // PART: one 64-key span per workgroup (blockIdx.y), one row
-    const int h = blockIdx.x, r = (PART || CHUNK) ? 0 : blockIdx.y, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int s = a.row_stream ? a.row_stream[r] : r * a.stream_stride;
+    // w is wave-uniform; saying so keeps span bases in SGPRs (loads then take a
+    // scalar base and a 32-bit lane offset)
+    const int h = blockIdx.x, r = (PART || CHUNK) ? 0 : blockIdx.y, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int s = __builtin_amdgcn_readfirstlane(a.row_stream ? a.row_stream[r] : r * a.stream_stride);
     // keys of this row, never past the capacity the caches were built for (a
     // stream parked at capacity keeps pos == capacity)
-    const int n = min((a.row_pos ? a.row_pos[r] : a.pos0 + r * a.pos_stride) + 1, a.max_keys);
-    if (threadIdx.x < kHeadDim) qs[threadIdx.x] = a.q[(size_t)r * a.q_stride + h * kHeadDim + threadIdx.x];
-    __syncthreads();
-    if (stopped) return;
+    const int n = __builtin_amdgcn_readfirstlane(
+        min((a.row_pos ? a.row_pos[r] : a.pos0 + r * a.pos_stride) + 1, a.max_keys));
 
-    float m = -INFINITY, l = 0.0f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    using Raw = SpanRaw<KV>;
+    constexpr int LPR = Raw::LPR, EPL = Raw::EPL, RPI = Raw::RPI;
     const int pg = lane >> 4, dg = lane & 15;
-    // K: load c brings 16 bytes of key RPI*c + rr (dims sub*EPL ..), so one load
-    // instruction covers RPI whole rows; the LPR lanes of a key then combine
-    // their partial dots, and lane ends with the score of key kl of the span
-    constexpr int LPR = KV == KV_F16 ? 8 : 16, EPL = 64 / LPR, RPI = 64 / LPR;
     const int sub = lane & (LPR - 1), rr = lane / LPR, kl = RPI * sub + rr;
-    float qsub[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) qsub[e] = qs[sub * EPL + e];
     // PART: exactly one span, [64 * blockIdx.y, min(n, 64 * blockIdx.y + 64));
     // CHUNK: workgroup y takes spans NW*y + w, then every NW*chunks further
     const int span0 = PART ? (int)blockIdx.y : (CHUNK ? NW * (int)blockIdx.y + w : w);
     const int span_step = PART ? 1 : (CHUNK ? NW * (int)gridDim.y : NW);
     const int key_end = PART ? min(n, span0 * 64 + 64) : n;
     if (PART && span0 * 64 >= n) return;  // a span past the live keys: the merge skips it
-    for (int span = span0; span * 64 < key_end; span += span_step) {
+    auto span_base = [&](int span) -> size_t {
         const int p0 = span * 64;
-        const int cnt = min(64, n - p0);
-        const int page = a.page_table ? a.page_table[(size_t)s * a.table_stride + p0 / a.page_size] : s;
-        const size_t base = (((size_t)page * a.heads + h) * a.page_size + p0 % a.page_size) * kHeadDim;
-        // V values of this lane (dims 4dg..4dg+3 of keys pg + 4t) are loaded with K,
-        // before the scores need to be ready
-        float4 vv[16];
+        const int page = __builtin_amdgcn_readfirstlane(
+            a.page_table ? a.page_table[(size_t)s * a.table_stride + p0 / a.page_size] : s);
+        return (((size_t)page * a.heads + h) * a.page_size + p0 % a.page_size) * kHeadDim;
+    };
+    float m = -INFINITY, l = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    // q goes straight into registers (no LDS, no barrier), requested right after
+    // the first span's K and V so that the two latencies overlap (a wave without
+    // a span never needs it)
+    float qsub[EPL];
+    bool need_q = true;
+#pragma unroll 1
+    for (int span = span0; span * 64 < key_end; span += span_step) {
+        const int cnt = min(64, n - span * 64);
+        Raw raw;
+        raw.load(a.k_pool, a.v_pool, span_base(span), cnt, sub, rr, pg, dg);
+        if (need_q) {
+            const float4 *qp = (const float4 *)(a.q + (size_t)r * a.q_stride + h * kHeadDim + sub * EPL);
 #pragma unroll
-        for (int t = 0; t < 16; ++t)
-            vv[t] = load4<KV>(a.v_pool, base + (size_t)min(pg + 4 * t, cnt - 1) * kHeadDim + 4 * dg);
+            for (int e = 0; e < EPL / 4; ++e) {
+                const float4 t = qp[e];
+                qsub[4 * e] = t.x;
+                qsub[4 * e + 1] = t.y;
+                qsub[4 * e + 2] = t.z;
+                qsub[4 * e + 3] = t.w;
+            }
+            need_q = false;
+        }
         float pd[LPR];
 #pragma unroll
-        for (int c = 0; c < LPR; ++c) {
-            const size_t ki = base + (size_t)min(RPI * c + rr, cnt - 1) * kHeadDim + sub * EPL;
-            float kf[EPL];
-            if constexpr (KV == KV_F16) {
-                float tmp[8];
-                load_row8<KV>(a.k_pool, ki, tmp);
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) kf[e] = tmp[e];
-            } else {
-                const float4 v4 = *(const float4 *)((const float *)a.k_pool + ki);
-                kf[0] = v4.x; kf[1] = v4.y; kf[2] = v4.z; kf[3] = v4.w;
-            }
-            float d = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) d = fmaf(qsub[e], kf[e], d);
-            pd[c] = d;
-        }
+        for (int c = 0; c < LPR; ++c) pd[c] = raw.kdot(c, qsub);
         float dot = key_reduce<LPR>(pd, sub);  // q . k of key kl
         dot *= 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
         const float smax = wave_max(kl < cnt ? dot : -INFINITY);
@@ -139,9 +162,8 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         // o[d] += sum_p e_p v_p[d]: lane = 16*pg + dg covers dims 4dg..4dg+3 of every 4th key
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const int i = pg + 4 * t;
-            const float4 v = vv[t];
-            const float ei = sc[w][i];
+            const float4 v = raw.vf(t);
+            const float ei = sc[w][pg + 4 * t];
             o.x = fmaf(ei, v.x, o.x);
             o.y = fmaf(ei, v.y, o.y);
             o.z = fmaf(ei, v.z, o.z);
@@ -150,6 +172,9 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }
+    // a stopped stream writes nothing (the flag is the same for every wave of
+    // the launch; it is tested here, off the path of the loads)
+    if (a.state != nullptr && a.state->stop) return;
     o.x += xshfl<16>(o.x);
     o.y += xshfl<16>(o.y);
     o.z += xshfl<16>(o.z);
@@ -185,44 +210,87 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         O = fmaf(((const float *)&po[t][0])[lane], sw, O);
     }
     if constexpr (CHUNK) {
-        // this slice's partial as LL words, then the last slice of the head to
-        // arrive collects every partial (each word carries its own flag) and merges
-        uint64_t *pp = a.chunk_part + ((size_t)h * gridDim.y + blockIdx.y) * kPartStride;
-        ll_put(pp + lane, O, a.chunk_tag);
-        if (lane == 0) {
-            ll_put(pp + 64, M, a.chunk_tag);
-            ll_put(pp + 65, L, a.chunk_tag);
+        // slices 1.. hand their partial on as LL words; slice 0 of the head (the
+        // first dispatched) keeps its own in registers and merges the others as
+        // their words arrive (each word carries the launch's tag: no counter)
+        if (blockIdx.y != 0) {
+            uint64_t *pp = a.chunk_part + ((size_t)h * gridDim.y + blockIdx.y) * kPartStride;
+            ll_put(pp + lane, O, a.chunk_tag);
+            if (lane == 0) {
+                ll_put(pp + 64, M, a.chunk_tag);
+                ll_put(pp + 65, L, a.chunk_tag);
+            }
+            return;
         }
-        unsigned prev = 0;
-        if (lane == 0) prev = atomicAdd(a.chunk_count + h, 1u);
-        prev = __shfl(prev, 0);
-        if (prev + 1 != gridDim.y) return;
+        // every load of the merge is issued before any is waited on: lane c holds
+        // slice c's (m, l) (lane 0 its own); each lane then sums its output
+        // dimension over the slices in slice order, 16 slices' words in flight
+        // (polling (m, l) alone first measured faster than polling every word)
         const uint64_t *hp = a.chunk_part + (size_t)h * gridDim.y * kPartStride;
+        const int nc = (int)gridDim.y;  // <= kMaxChunks = 64
         int budget = kPollBudget;
         bool ok = true;
-        auto word = [&](size_t i) {  // waits for the word's tag (bounded)
-            uint64_t v = ll_load(hp + i);
-            while ((uint32_t)(v >> 32) != a.chunk_tag) {
+        float mc = M, lc = L;
+        if (lane > 0 && lane < nc) {
+            uint64_t wm = ll_load(hp + (size_t)lane * kPartStride + 64);
+            uint64_t wl = ll_load(hp + (size_t)lane * kPartStride + 65);
+            while ((uint32_t)(wm >> 32) != a.chunk_tag || (uint32_t)(wl >> 32) != a.chunk_tag) {
                 if (--budget < 0) {
                     ok = false;
                     break;
                 }
                 __builtin_amdgcn_s_sleep(2);
-                v = ll_load(hp + i);
+                wm = ll_load(hp + (size_t)lane * kPartStride + 64);
+                wl = ll_load(hp + (size_t)lane * kPartStride + 65);
             }
-            return __uint_as_float((uint32_t)v);
-        };
-        M = -INFINITY;
-        for (unsigned c = 0; c < gridDim.y; ++c) M = fmaxf(M, word(c * kPartStride + 64));
-        L = 0.0f;
-        O = 0.0f;
-        for (unsigned c = 0; c < gridDim.y; ++c) {
-            const float sw = expf(word(c * kPartStride + 64) - M);
-            L = fmaf(word(c * kPartStride + 65), sw, L);
-            O = fmaf(word(c * kPartStride + lane), sw, O);
+            mc = __uint_as_float((uint32_t)wm);
+            lc = __uint_as_float((uint32_t)wl);
+        } else if (lane >= nc) {
+            mc = -INFINITY;
+            lc = 0.0f;
         }
+        M = wave_max(mc);
+        const float sw = lane < nc ? expf(mc - M) : 0.0f;
+        L = 0.0f;
+        for (int c = 0; c < nc; ++c) L = fmaf(__shfl(lc, c), __shfl(sw, c), L);
+        O *= __shfl(sw, 0);  // slice 0's own
+        for (int c0 = 1; c0 < nc; c0 += 16) {
+            uint64_t v[16];
+            uint32_t pending = 0;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)  // only slices that exist (uniform test)
+                if (c0 + k < nc) {
+                    v[k] = ll_load(hp + (size_t)(c0 + k) * kPartStride + lane);
+                    pending |= 1u << k;
+                }
+            while (true) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if (((pending >> k) & 1u) && (uint32_t)(v[k] >> 32) == a.chunk_tag) pending &= ~(1u << k);
+                if (pending == 0) break;
+                if (--budget < 0) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if ((pending >> k) & 1u) v[k] = ll_load(hp + (size_t)(c0 + k) * kPartStride + lane);
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (c0 + k < nc) O = fmaf(__uint_as_float((uint32_t)v[k]), __shfl(sw, c0 + k), O);
+        }
+        // clear every word read (tag 0 is never current): the next launch on this
+        // scratch cannot take one of them for its own, even when it carries the
+        // same tag (a captured graph replays the tag it was captured with)
+        for (int c = 1; c < nc; ++c) ll_put((uint64_t *)hp + (size_t)c * kPartStride + lane, 0.0f, 0);
+        if (lane > 0 && lane < nc) {
+            ll_put((uint64_t *)hp + (size_t)lane * kPartStride + 64, 0.0f, 0);
+            ll_put((uint64_t *)hp + (size_t)lane * kPartStride + 65, 0.0f, 0);
+        }
+        ok = __all(ok);
         if (!ok) O = __int_as_float(0x7fc00000);  // a slice never arrived: NaN, not a stale value
-        if (lane == 0) a.chunk_count[h] = 0;       // ready for the next launch on this stream
     }
     const float res = O / L;
     const size_t oi = (size_t)r * a.out_stride + h * kHeadDim + lane;
@@ -250,7 +318,8 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
         return hipGetLastError();
     }
     if (a.chunks > 0) {  // one row, slices of 4 spans merged by the last slice of each head
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false, true>), dim3(a.heads, a.chunks), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((attn_rows_kernel<KV, kSliceWaves, false, true>), dim3(a.heads, a.chunks),
+                           dim3(64 * kSliceWaves), 0, s, a);
         return hipGetLastError();
     }
     const dim3 grid(a.heads, a.rows);
@@ -271,8 +340,8 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
     if (a.q8 != nullptr && (!a.d8 || a.part != nullptr || a.heads != kHeads)) return hipErrorInvalidValue;
     if (a.chunks != 0 && (a.chunks < 0 || a.chunks > kMaxChunks || a.rows != 1 || a.part != nullptr ||
-                          a.page_table != nullptr || a.q8 != nullptr || !a.chunk_part || !a.chunk_count ||
-                          4 * 64 * (a.chunks - 1) >= a.max_keys))
+                          a.page_table != nullptr || a.q8 != nullptr || !a.chunk_part ||
+                          kSliceWaves * 64 * (a.chunks - 1) >= a.max_keys))
         return hipErrorInvalidValue;  // every slice holds at least one live span
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
 }

@@ -24,13 +24,14 @@ namespace {
 
 thread_local std::string g_err;
 
-// Split-KV partials and per-head arrival counts of moss_hip_attn_decode, one set
-// per (device, stream): launches on one stream run in order, so each finds the
-// counts its predecessor reset.  Allocated on first use, grown with the head
-// count, kept until the process ends.
+// Split-KV partials of moss_hip_attn_decode (LL words), one block per (device,
+// stream).  Each launch tags its words with the next value of `tag`, and the
+// merging workgroup clears every word it read, so a launch never takes an
+// earlier launch's partial for its own.  Allocated (and zeroed) on the first
+// call on a stream, which must not be under graph capture; grown with the head
+// count; kept until the process ends.
 struct AttnScratch {
     uint64_t *part = nullptr;
-    unsigned *count = nullptr;
     int heads = 0;
     uint32_t tag = 0;  // LL tag of the last launch (0 is never used)
 };
@@ -44,17 +45,14 @@ AttnScratch attn_scratch(hipStream_t s, int heads) {  // returns the entry with 
     AttnScratch &e = g_scratch[{dev, s}];
     if (e.heads < heads) {
         if (e.part) {
-            mh::hip_check(hipStreamSynchronize(s), "sync");  // launches still using the old buffers
+            mh::hip_check(hipStreamSynchronize(s), "sync");  // launches still using the old block
             (void)hipFree(e.part);
-            (void)hipFree(e.count);
             e = AttnScratch{};
         }
-        mh::hip_check(hipMalloc(&e.part, sizeof(uint64_t) * heads * mh::kMaxChunks * mh::kPartStride),
-                      "hipMalloc(attention partials)");
-        mh::hip_check(hipMemset(e.part, 0, sizeof(uint64_t) * heads * mh::kMaxChunks * mh::kPartStride),
-                      "memset(attention partials)");
-        mh::hip_check(hipMalloc(&e.count, sizeof(unsigned) * heads), "hipMalloc(attention counts)");
-        mh::hip_check(hipMemset(e.count, 0, sizeof(unsigned) * heads), "memset(attention counts)");
+        const size_t bytes = sizeof(uint64_t) * heads * mh::kMaxChunks * mh::kPartStride;
+        mh::hip_check(hipMalloc(&e.part, bytes), "hipMalloc(attention partials)");
+        mh::hip_check(hipMemsetAsync(e.part, 0, bytes, s), "memset(attention partials)");
+        mh::hip_check(hipStreamSynchronize(s), "sync");
         e.heads = heads;
     }
     if (++e.tag == 0) e.tag = 1;
@@ -384,12 +382,11 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
         a.out_f16 = out_dtype == MOSS_HIP_F16;
         const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
         const int spans = (n_keys + 63) / 64;
-        if (spans > 4) {  // past one workgroup's 4 spans: slices of 256 keys across workgroups
+        if (spans > mh::kOneWgSpans) {  // slices of kSliceWaves spans across workgroups
             const AttnScratch sc = attn_scratch(static_cast<hipStream_t>(stream), heads);
-            const int chunks = (spans + 3) / 4;
+            const int chunks = (spans + mh::kSliceWaves - 1) / mh::kSliceWaves;
             a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;
             a.chunk_part = sc.part;
-            a.chunk_count = sc.count;
             a.chunk_tag = sc.tag;
         }
         mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");

@@ -98,17 +98,25 @@ struct AttnArgs {
     float *d8 = nullptr;
     const DevState *state = nullptr;
     // single row, long context: the keys are cut into `chunks` slices of 256 (one workgroup of
-    // 4 waves each, more spans per wave past kMaxChunks), each writes its partial (o[64], m, l)
-    // as LL words tagged chunk_tag to chunk_part[(h * chunks + c) * kPartStride] and adds one to
-    // chunk_count[h]; the last one of a head collects the partials (waiting on their tags),
-    // merges them in chunk order, writes the output and resets the count to 0
+    // 4 waves each, more spans per wave past kMaxChunks); slices 1.. write their partial
+    // (o[64], m, l) as LL words tagged chunk_tag to chunk_part[(h * chunks + c) * kPartStride],
+    // and slice 0 of each head waits for them, merges all in slice order and writes the output
     int chunks = 0;
     uint64_t *chunk_part = nullptr;
-    unsigned *chunk_count = nullptr;
     uint32_t chunk_tag = 0;          // distinct for consecutive launches on one stream
 };
 constexpr int kPartStride = 68;
 constexpr int kMaxChunks = 64;
+#ifndef MH_SLICE_WAVES
+#define MH_SLICE_WAVES 4
+#endif
+#ifndef MH_ONE_WG_SPANS
+#define MH_ONE_WG_SPANS 4
+#endif
+// single-row slices: waves per slice workgroup (one 64-key span each); the keys
+// stay in one workgroup up to kOneWgSpans spans
+constexpr int kSliceWaves = MH_SLICE_WAVES;
+constexpr int kOneWgSpans = MH_ONE_WG_SPANS;
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s);
 
 // W8A16 GEMM on the matrix cores: Y[M][N] = A[M][K] W[N][K]^T with an epilogue.

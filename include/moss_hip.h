@@ -195,9 +195,10 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
  * q [heads*64] fp32 (post-RoPE); k_cache/v_cache [heads][ctx_stride][64] of kv_dtype; the
  * first n_keys positions are attended.  out [heads*64] of out_dtype.  Past 256 keys the keys are
  * cut into slices of 256 (at most 64 per head) attended by separate workgroups and merged by
- * the last slice of each head (log-sum-exp, slice order); the partials live in a scratch block
- * the library allocates once per (device, stream) on first use, so calls on one stream are
- * ordered and calls on different streams do not share it. */
+ * the first slice of each head (log-sum-exp, slice order); the partials live in a scratch block
+ * the library allocates once per (device, stream) on the first call on that stream (which must
+ * not be under graph capture), so calls on one stream are ordered and calls on different
+ * streams do not share it. */
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
                          int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
 

@@ -127,9 +127,9 @@ def test_attention_decode_vs_oracle(torch_gpu, oracle, ctx, kv):
 
 
 def test_attention_decode_back_to_back(torch_gpu, oracle):
-    """Past 256 keys the heads are cut into slices whose partials the last slice of
-    each head merges, resetting its arrival count: consecutive calls with different
-    slice counts on one stream each see a clean count."""
+    """Past 256 keys the heads are cut into slices whose partials the first slice of
+    each head merges: consecutive calls with different slice counts on one stream
+    never take a partial of an earlier call (some of whose slots they reuse)."""
     torch = torch_gpu
     for ctx in (2048, 300, 257, 5000, 1300):
         print(f"attention back-to-back ctx={ctx}", flush=True)
@@ -140,6 +140,43 @@ def test_attention_decode_back_to_back(torch_gpu, oracle):
         torch.cuda.synchronize()
         ref = oracle.attention(k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32), q)
         assert max_rel(out.cpu().numpy(), ref) <= TOL
+
+
+def test_attention_decode_graph_replays(torch_gpu, oracle):
+    """One split-KV call captured in a graph replays with the tag it was captured
+    with; the merging slice clears every partial word it read, so no replay takes
+    the previous replay's partials.  New q, K and V go in before each replay (with
+    eager calls of other sizes on the same stream between replays), and every
+    replay is checked against the oracle."""
+    torch = torch_gpu
+    ctx = 1500
+    s = torch.cuda.Stream()
+    q_d = torch.zeros(768, dtype=torch.float32, device="cuda")
+    k_d = torch.zeros((12, ctx, 64), dtype=torch.float16, device="cuda")
+    v_d = torch.zeros_like(k_d)
+    out = torch.zeros(768, dtype=torch.float32, device="cuda")
+    side = torch.empty(768, dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(s):  # first call on the stream: its scratch is made here
+        lib.attn_decode(q_d, k_d, v_d, 12, ctx, ctx, out)
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        lib.attn_decode(q_d, k_d, v_d, 12, ctx, ctx, out)
+    for rep in range(4):
+        print(f"attention graph replay {rep}", flush=True)
+        q, k, v = _attn_case(oracle, ctx, 100 + rep)
+        q_d.copy_(_dev(torch, q))
+        k_d.copy_(_dev(torch, _to_cache(k, ctx, np.float16)))
+        v_d.copy_(_dev(torch, _to_cache(v, ctx, np.float16)))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = oracle.attention(k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32), q)
+        assert max_rel(out.cpu().numpy(), ref) <= TOL, rep
+        with torch.cuda.stream(s):  # eager calls of other slice counts between replays
+            n = 300 + 400 * rep  # 300 .. 1500 keys of the ctx-1500 cache
+            lib.attn_decode(q_d, k_d, v_d, 12, ctx, n, side)
+        s.synchronize()
 
 
 def test_attention_single_key_returns_v(torch_gpu):
