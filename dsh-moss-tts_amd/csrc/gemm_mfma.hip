@@ -26,7 +26,12 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int KB = 4;  // scale blocks per load chunk
+#ifndef MH_GEMM_KB
+#define MH_GEMM_KB 3
+#endif
+// scale blocks per load chunk: 3 divides every per-wave block count of the model's
+// GEMMs (K = 768: 6 per wave, or 3 per wave in two K slices; K = 3072: 24 or 12)
+constexpr int KB = MH_GEMM_KB;
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
@@ -167,7 +172,8 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
 #pragma clang fp contract(off)
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
-        const bool live = b0 + j < nb;  // uniform; a dead block adds with a zero scale
+        const bool live = b0 + j < nb;  // uniform
+        if (!live) break;               // blocks past the wave's last one (loaded, clamped) are skipped
         if constexpr (A8) {
             // W8A8 (gemv_avx2.cpp:105-121): the exact int32 block dot, times
             // scale = d_w * d_a (fp32), accumulated with an FMA.  D row 4kq + i
@@ -179,7 +185,7 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
             for (int t = 0; t < NT; ++t) {
                 const long bq = (long)(((uint64_t)c.qb[j][t].y << 32) | c.qb[j][t].x);
                 const intx4 p = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)c.xq[j], bq, intx4{0, 0, 0, 0}, 0, 0, 0);
-                const float dw = live ? h2f((uint16_t)c.db[j][t]) : 0.0f;
+                const float dw = h2f((uint16_t)c.db[j][t]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float scale = dw * da[i];
@@ -195,7 +201,7 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
                 floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
                 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, bw, blk, 0, 0, 0);
                 blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, bw, blk, 0, 0, 0);
-                const float d = live ? h2f((uint16_t)c.db[j][t]) : 0.0f;
+                const float d = h2f((uint16_t)c.db[j][t]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(blk[i], d, acc[t][i]);
             }
@@ -319,7 +325,8 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             load_chunk<NT, A8>(cb, b0 + KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);  // clamped: valid past nb
             mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
             if (b0 + KB >= nb) break;
-            load_chunk<NT, A8>(ca, b0 + 2 * KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+            if (b0 + 2 * KB < nb)  // (uniform) a chunk past the wave's blocks is not requested
+                load_chunk<NT, A8>(ca, b0 + 2 * KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
             mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
         }
     }
