@@ -252,17 +252,31 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         static_assert(!A8, "the LayerNorm prologue takes fp32 activations");
         __shared__ float lnw[4 * 2 * KB * 32], lnb[4 * 2 * KB * 32];
         __shared__ float lsum[4][16], lsq[4][16];
-        // loads in completion order: the activations, ln_w / ln_b (staged in LDS),
-        // then the weights, which stay in flight while the statistics are formed
+        // loads in completion order: the activations, ln_w / ln_b (into registers),
+        // then the weights, which stay in flight while the statistics are formed;
+        // ln_w / ln_b go to LDS only after every load is issued (an LDS store of a
+        // loaded value waits for that load, and loads complete in order)
+        constexpr int LNR = (4 * 2 * KB * 32 + 255) / 256;
         Chunk<NT, A8> ca, cb;
         load_chunk_a<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d);
         load_chunk_a<NT, A8>(cb, KB, nb, arow_p, arow_q, arow_d);  // clamped: valid past nb
-        for (int c = threadIdx.x; c < g.K; c += 256) {
-            lnw[c] = g.ln_w[c];
-            lnb[c] = g.ln_b[c];
+        float lw[LNR], lb[LNR];
+#pragma unroll
+        for (int i = 0; i < LNR; ++i) {
+            const int c = min((int)threadIdx.x + 256 * i, g.K - 1);
+            lw[i] = g.ln_w[c];
+            lb[i] = g.ln_b[c];
         }
         load_chunk_b<NT, A8>(ca, 0, nb, wcol, krow, kq);
         load_chunk_b<NT, A8>(cb, KB, nb, wcol, krow, kq);
+#pragma unroll
+        for (int i = 0; i < LNR; ++i) {
+            const int c = (int)threadIdx.x + 256 * i;
+            if (c < g.K) {
+                lnw[c] = lw[i];
+                lnb[c] = lb[i];
+            }
+        }
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < KB; ++j)
@@ -376,7 +390,8 @@ hipError_t launch_a(const GemmArgs &g, hipStream_t s) {
 
 // Split K so that a GEMM with few output tiles still spreads over the CUs:
 // about 256 workgroups of 16 x 16 tiles, at least 12 blocks (3 per wave) per
-// slice, at most 16 slices.  Slices are balanced: sizes differ by at most one block.
+// slice, at most 16 slices (targets of 512-1024 workgroups, or 6 blocks per
+// slice, measured slower at 64 streams).  Slices are balanced: sizes differ by at most one block.
 int gemm_ksplit(int M, int N, int K) {
     const int tiles = ((M + 15) / 16) * (N / 16);
     const int nb = K / 32;
