@@ -590,26 +590,64 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
     const int srow = blockIdx.x, t = threadIdx.x;
     float *nxt = next_in + (size_t)srow * kHidden;
     const int nb = kHidden / 32;
-    if (!st.active[srow]) {
-        // keep the next local input defined (row 0) so later kernels read finite values
-        for (int c = t; c < kHidden; c += 256) nxt[c] = q8x4_elem(aemb, nb, 0, c);
-        if (next.rows) local_qkv_row(next, next.rows, srow);
-        return;
-    }
+    // every load that does not depend on the pick is issued first, together: the
+    // row's logits and code counts, its active flag, the control block
+    const float *lg = logits + (size_t)srow * kCodebook;
     int *cnt = st.counts + ((size_t)srow * kNVq + ch) * kCodebook;
-    load_penalised(L, logits + (size_t)srow * kCodebook, cnt, st.ctrl->rep_penalty);
+    PickIn in;
+#pragma unroll
+    for (int k = 0; k < kCodebook / 256; ++k) {
+        in.vals[k] = lg[t + 256 * k];
+        in.cnt[k] = cnt[t + 256 * k];
+    }
+    const bool active = st.active[srow] != 0;
+    const float pen = st.ctrl->rep_penalty;
     const SampleCfg c = st.ctrl->cfg;
     const bool greedy = c.greedy || st.ctrl->frame < c.greedy_frames;
-    const int idx = greedy ? pick_greedy(L) : pick_sampled(L, c, st.rng + 4 * srow);
-    if (t == 0) {
-        st.codes[srow * kNVq + ch] = idx;
-        st.row[srow * (kNVq + 1) + ch + 1] = idx;
-        cnt[idx] += 1;
-        if (last_channel) st.row[srow * (kNVq + 1)] = kSlotToken;
+    int idx = 0;  // inactive: keep the next local input defined (row 0) so later kernels read finite values
+    if (active) {
+        if (greedy) {  // the single-stream greedy pick, reduced from registers
+            if (pen == 1.0f)
+#pragma unroll
+                for (int k = 0; k < kCodebook / 256; ++k) in.cnt[k] = 0;
+            idx = greedy_pick_reduce(in, pen, L.bv, L.bi);
+            idx = idx >= kCodebook ? 0 : idx;  // every value NaN: the reference's scan stays at 0
+        } else {
+            load_penalised(L, lg, cnt, pen);
+            idx = pick_sampled(L, c, st.rng + 4 * srow);
+        }
+        if (t == 0) {
+            st.codes[srow * kNVq + ch] = idx;
+            st.row[srow * (kNVq + 1) + ch + 1] = idx;
+            cnt[idx] += 1;
+            if (last_channel) st.row[srow * (kNVq + 1)] = kSlotToken;
+        }
     }
-    for (int c2 = t; c2 < kHidden; c2 += 256) nxt[c2] = q8x4_elem(aemb, nb, idx, c2);
-    // the next local position's q|k|v: the table row of (lpos, idx)
-    if (next.rows) local_qkv_row(next, next.rows + (size_t)(idx < kCodebook ? idx : 0) * 3 * kHidden, srow);
+    // the picked code's embedding row and (next local position) q|k|v table row:
+    // both requested before either is stored
+    float ev[kHidden / 256], qv[3 * kHidden / 256];
+#pragma unroll
+    for (int j = 0; j < kHidden / 256; ++j) ev[j] = q8x4_elem(aemb, nb, idx, t + 256 * j);
+    if (next.rows) {
+        const float *row = next.rows + (size_t)idx * 3 * kHidden;
+#pragma unroll
+        for (int j = 0; j < 3 * kHidden / 256; ++j) qv[j] = row[t + 256 * j];
+    }
+#pragma unroll
+    for (int j = 0; j < kHidden / 256; ++j) nxt[t + 256 * j] = ev[j];
+    if (next.rows) {
+#pragma unroll
+        for (int j = 0; j < 3 * kHidden / 256; ++j) {
+            const int i = t + 256 * j;
+            if (i < kHidden) {
+                next.q_out[(size_t)srow * kHidden + i] = qv[j];
+            } else {
+                const int jj = i - kHidden, sec = jj / kHidden, w = jj - sec * kHidden;
+                float *cache = sec == 0 ? next.lk : next.lv;
+                cache[(((size_t)srow * kHeads + (w >> 6)) * kLocalLen + next.lpos) * kHeadDim + (w & 63)] = qv[j];
+            }
+        }
+    }
 }
 
 __global__ void advance_rows_kernel(StreamState st, int streams) {
