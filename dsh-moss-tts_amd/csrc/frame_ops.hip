@@ -447,12 +447,15 @@ __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, i
 #pragma clang fp contract(off)
     __shared__ float red[4];
     const int r = blockIdx.x, t = threadIdx.x;
-    // all partials are loaded before the in-order sum (slices past ksplit re-read the last one, unused)
+    // all partials are loaded before the in-order sum (only the ksplit live
+    // slices: the test is uniform, and clamped re-reads of the last slice cost
+    // a load instruction each)
     float p[3][16], v[3];
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
+    for (int z = 0; z < 16; ++z)
+        if (z < ksplit)
 #pragma unroll
-        for (int z = 0; z < 16; ++z) p[i][z] = part[((size_t)min(z, ksplit - 1) * rows + r) * kHidden + t + 256 * i];
+            for (int i = 0; i < 3; ++i) p[i][z] = part[((size_t)z * rows + r) * kHidden + t + 256 * i];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int n = t + 256 * i;
