@@ -4,6 +4,7 @@
 * ``RefCpu``  -- oracle/_ref/libmossref.so, the reference's own LLM-path sources
   compiled from the reference checkout by oracle/Makefile (present wherever it
   was built; it travels with the tree).
+* ``RefDecoder`` -- the reference's audio codec decoder from the same library.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this.
 """
@@ -473,3 +474,62 @@ class RefModel:
         if timing:
             res["timing"] = t[:n]
         return res
+
+
+class RefDecoder:
+    """The reference AudioDecoder (decoder.h:15-36) from oracle/_ref/libmossref.so,
+    loaded from a blob (written to a temp file: load() takes a path)."""
+
+    def __init__(self, r: RefCpu, blob: bytes, threads: int = 1):
+        L = self.lib = r.lib
+        L.ref_dec_create.restype = C.c_void_p
+        L.ref_dec_create.argtypes = [C.c_int]
+        L.ref_dec_destroy.argtypes = [C.c_void_p]
+        L.ref_dec_load.argtypes = [C.c_void_p, C.c_char_p]
+        L.ref_dec_decode.argtypes = [C.c_void_p, _i32p, C.c_int, _f32p, C.c_int, C.POINTER(C.c_double)]
+        L.ref_dec_reset_stream.argtypes = [C.c_void_p]
+        L.ref_dec_decode_chunk.argtypes = [C.c_void_p, _i32p, C.c_int, _f32p, C.c_int]
+        self.h = L.ref_dec_create(threads)
+        self.tmpdir = tempfile.mkdtemp(prefix="mossdec_")
+        self.path = os.path.join(self.tmpdir, "d.moss")
+        with open(self.path, "wb") as f:
+            f.write(blob)
+        if L.ref_dec_load(self.h, self.path.encode()) != 0:
+            raise RuntimeError(L.ref_last_error().decode())
+        self.last_ms = 0.0
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.ref_dec_destroy(self.h)
+            self.h = None
+        if getattr(self, "path", None) and os.path.exists(self.path):
+            os.remove(self.path)
+            os.rmdir(self.tmpdir)
+            self.path = None
+
+    def __del__(self):
+        self.close()
+
+    def decode(self, codes):
+        """codes [16][frames] int32 -> samples [frames * 7680] (decoder.cpp:247)."""
+        codes = np.ascontiguousarray(codes, np.int32)
+        frames = codes.shape[1]
+        out = np.empty(frames * 7680, np.float32)
+        ms = C.c_double()
+        n = self.lib.ref_dec_decode(self.h, codes, frames, out, out.size, C.byref(ms))
+        if n < 0:
+            raise RuntimeError("output buffer too small")
+        self.last_ms = ms.value
+        return out[:n]
+
+    def reset_stream(self):
+        self.lib.ref_dec_reset_stream(self.h)
+
+    def decode_chunk(self, codes):
+        """One streaming chunk (decoder.cpp:203), in order after reset_stream()."""
+        codes = np.ascontiguousarray(codes, np.int32)
+        out = np.empty(codes.shape[1] * 7680, np.float32)
+        n = self.lib.ref_dec_decode_chunk(self.h, codes, codes.shape[1], out, out.size)
+        if n < 0:
+            raise RuntimeError("output buffer too small")
+        return out[:n]

@@ -1,7 +1,8 @@
 // ref_harness.cpp -- extern "C" wrapper around the reference CPU path.
 //
 // TEST INFRASTRUCTURE ONLY (checker and CPU baseline).  Compiled by
-// oracle/Makefile together with the reference's own LLM-path sources, which
+// oracle/Makefile together with the reference's own LLM-path and audio-decoder
+// sources, which
 // stay where they are under the reference checkout; the result lands in
 // oracle/_ref/libmossref.so.  Nothing in the product links it.
 //
@@ -13,6 +14,7 @@
 #include <vector>
 
 #include "moss/attn.h"
+#include "moss/decoder.h"
 #include "moss/fp16.h"
 #include "moss/gemv.h"
 #include "moss/llm.h"
@@ -225,6 +227,36 @@ int ref_model_generate(void *m, int max_frames, const int32_t *ip, const float *
         }
     }
     return static_cast<int>(out.size());
+}
+
+// ---- audio codec decoder (decoder.h:15-36) ----
+void *ref_dec_create(int threads) { return new AudioDecoder(threads); }
+void ref_dec_destroy(void *d) { delete static_cast<AudioDecoder *>(d); }
+int ref_dec_load(void *d, const char *path) {  // decoder.cpp:26
+    std::string err;
+    if (!static_cast<AudioDecoder *>(d)->load(path, &err)) {
+        g_err = err;
+        return 1;
+    }
+    return 0;
+}
+// decoder.cpp:247 (whole utterance).  codes [16][frames]; returns the sample
+// count written to out (at most cap), -1 when cap is too small.
+int ref_dec_decode(void *d, const int32_t *codes, int frames, float *out, int cap, double *ms) {
+    auto *dec = static_cast<AudioDecoder *>(d);
+    const std::vector<float> y = dec->decode(codes, frames);
+    if (ms) *ms = dec->last_ms();
+    if (static_cast<int>(y.size()) > cap) return -1;
+    std::memcpy(out, y.data(), sizeof(float) * y.size());
+    return static_cast<int>(y.size());
+}
+void ref_dec_reset_stream(void *d) { static_cast<AudioDecoder *>(d)->reset_stream(); }  // decoder.cpp:100
+// decoder.cpp:203 (one streaming chunk, in order after reset_stream)
+int ref_dec_decode_chunk(void *d, const int32_t *codes, int frames, float *out, int cap) {
+    const std::vector<float> y = static_cast<AudioDecoder *>(d)->decode_chunk(codes, frames);
+    if (static_cast<int>(y.size()) > cap) return -1;
+    std::memcpy(out, y.data(), sizeof(float) * y.size());
+    return static_cast<int>(y.size());
 }
 
 }  // extern "C"
