@@ -192,10 +192,11 @@ ATTN_CTX = (128, 512, 1024, 2048)
 
 
 def bench_attention(reps: int = 100):
-    """Single-query decode attention (12 heads x 64, fp16 K/V [12][ctx][64], fp32 q and
-    output) at each context length: warm (one cache, Infinity-Cache resident) and cold
-    (caches cycled through a pool of more than 512 MB), `reps` calls replayed from a graph.  Algorithmic bytes per call:
-    K and V (2 * 2 * 768 * ctx) + q and output (2 * 4 * 768 / 2 = 3072)."""
+    """Single-query decode attention (12 heads x 64, fp16 K/V [12][ctx][64], fp32 q,
+    fp16 output) at each context length: warm (one cache, Infinity-Cache resident) and
+    cold (caches cycled through a pool of more than 512 MB), `reps` calls replayed from
+    a graph.  Algorithmic bytes per call: K and V (2 * 2 * 768 * ctx) + q (4 * 768) +
+    output (2 * 768)."""
     import torch
 
     from mosship import lib
@@ -207,8 +208,8 @@ def bench_attention(reps: int = 100):
         g = torch.Generator(device="cuda").manual_seed(ctx)
         kv = torch.randn((pool_n, 2, 12, ctx, 64), generator=g, device="cuda").to(torch.float16)
         q = torch.randn(768, generator=g, device="cuda")
-        out = torch.empty(768, device="cuda")
-        algo = 3072 * ctx + 3072
+        out = torch.empty(768, dtype=torch.float16, device="cuda")
+        algo = 3072 * ctx + 4608
         r = {"algo_bytes": algo}
         with torch.cuda.stream(cap):  # warm-up on the capture stream (its split-KV scratch is made here)
             for i in range(min(pool_n, 16)):
