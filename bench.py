@@ -78,12 +78,15 @@ def bench_decode(blob, state, steps, warmup):
     m.set_hidden(hidden)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    out = m.generate(steps, p, timing=True)
+    out = m.generate(steps, p)  # as a caller runs it: no per-launch timing events
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     frames = len(out["rows"])
     assert frames == steps, f"decoded {frames} of {steps} frames"
-    t = out["timing"]
+    # the global / local split from a second run of the same frames with events
+    m.restore_prefix()
+    m.set_hidden(hidden)
+    t = m.generate(steps, p, timing=True)["timing"]
     res = {
         "ms_per_frame": (t1 - t0) * 1e3 / frames,
         "global_ms_event": float(np.mean(t[:-1, 0])) if frames > 1 else 0.0,

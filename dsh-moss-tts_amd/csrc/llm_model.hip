@@ -115,7 +115,11 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
 
     hip_check(hipSetDevice(device_), "hipSetDevice");
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
-    for (auto &e : ev_) hip_check(hipEventCreate(&e), "hipEventCreate");
+    // per readback slot: three timing events around the launches (recorded only
+    // when the caller asks for timing) and one completion event (no timestamp)
+    for (int i = 0; i < 8; ++i)
+        hip_check((i & 3) == 3 ? hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming) : hipEventCreate(&ev_[i]),
+                  "hipEventCreate");
     hip_check(hipMalloc(&blob_, bytes), "hipMalloc(weights)");
     hip_check(hipMemcpy(blob_, blob, bytes, hipMemcpyHostToDevice), "upload weights");
 
@@ -730,15 +734,15 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     auto enqueue = [&](int f) {
         const int slot = f & 1;
         hipEvent_t *ev = ev_ + 4 * slot;
-        hip_check(hipEventRecord(ev[0], stream_), "event");
+        if (timing) hip_check(hipEventRecord(ev[0], stream_), "event");
         launch_frame_local(stream_, gate_dump != nullptr, hstate_->cfg.greedy != 0);
-        hip_check(hipEventRecord(ev[1], stream_), "event");
+        if (timing) hip_check(hipEventRecord(ev[1], stream_), "event");
         enq[slot].global = f + 1 < max_frames && pos_next < max_ctx_;
         if (enq[slot].global) {
             launch_global(stream_);
             ++pos_next;
         }
-        hip_check(hipEventRecord(ev[2], stream_), "event");
+        if (timing) hip_check(hipEventRecord(ev[2], stream_), "event");
         if (logits_dump)
             hip_check(hipMemcpyAsync(logits_dump + (size_t)f * kNVq * kCodebook, logits_,
                                      sizeof(float) * kNVq * kCodebook, hipMemcpyDeviceToHost, stream_),
