@@ -239,7 +239,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
                     ok = false;
                     break;
                 }
-                __builtin_amdgcn_s_sleep(2);
+                __builtin_amdgcn_s_sleep(kPollSleep);
                 wm = ll_load(hp + (size_t)lane * kPartStride + 64);
                 wl = ll_load(hp + (size_t)lane * kPartStride + 65);
             }
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
                     ok = false;
                     break;
                 }
-                __builtin_amdgcn_s_sleep(2);
+                __builtin_amdgcn_s_sleep(kPollSleep);
 #pragma unroll
                 for (int k = 0; k < 16; ++k)
                     if ((pending >> k) & 1u) v[k] = ll_load(hp + (size_t)(c0 + k) * kPartStride + lane);
