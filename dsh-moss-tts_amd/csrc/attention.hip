@@ -116,6 +116,9 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
             a.page_table ? a.page_table[(size_t)s * a.table_stride + p0 / a.page_size] : s);
         return (((size_t)page * a.heads + h) * a.page_size + p0 % a.page_size) * kHeadDim;
     };
+    // the launch's LL tag (sliced single-row launches): odd, so never the 0 of a cleared word
+    uint32_t tag = 0;
+    if constexpr (CHUNK) tag = (ll_gen_load(a.chunk_gen) << 1) | 1u;
     float m = -INFINITY, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     // q goes straight into registers (no LDS, no barrier), requested right after
@@ -215,10 +218,11 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         // their words arrive (each word carries the launch's tag: no counter)
         if (blockIdx.y != 0) {
             uint64_t *pp = a.chunk_part + ((size_t)h * gridDim.y + blockIdx.y) * kPartStride;
-            ll_put(pp + lane, O, a.chunk_tag);
+            ll_put(pp + lane, O, tag);
             if (lane == 0) {
-                ll_put(pp + 64, M, a.chunk_tag);
-                ll_put(pp + 65, L, a.chunk_tag);
+                ll_put(pp + 64, M, tag);
+                ll_put(pp + 65, L, tag);
+                ll_gen_arrive(a.chunk_gen, gridDim.x * gridDim.y);
             }
             return;
         }
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         if (lane > 0 && lane < nc) {
             uint64_t wm = ll_load(hp + (size_t)lane * kPartStride + 64);
             uint64_t wl = ll_load(hp + (size_t)lane * kPartStride + 65);
-            while ((uint32_t)(wm >> 32) != a.chunk_tag || (uint32_t)(wl >> 32) != a.chunk_tag) {
+            while ((uint32_t)(wm >> 32) != tag || (uint32_t)(wl >> 32) != tag) {
                 if (--budget < 0) {
                     ok = false;
                     break;
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
             while (true) {
 #pragma unroll
                 for (int k = 0; k < 16; ++k)
-                    if (((pending >> k) & 1u) && (uint32_t)(v[k] >> 32) == a.chunk_tag) pending &= ~(1u << k);
+                    if (((pending >> k) & 1u) && (uint32_t)(v[k] >> 32) == tag) pending &= ~(1u << k);
                 if (pending == 0) break;
                 if (--budget < 0) {
                     ok = false;
@@ -281,14 +285,14 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
             for (int k = 0; k < 16; ++k)
                 if (c0 + k < nc) O = fmaf(__uint_as_float((uint32_t)v[k]), __shfl(sw, c0 + k), O);
         }
-        // clear every word read (tag 0 is never current): the next launch on this
-        // scratch cannot take one of them for its own, even when it carries the
-        // same tag (a captured graph replays the tag it was captured with)
+        // clear every word read (tag 0 is never current), so that no word keeps a
+        // tag for the 2^31 launches after which the generation's tags repeat
         for (int c = 1; c < nc; ++c) ll_put((uint64_t *)hp + (size_t)c * kPartStride + lane, 0.0f, 0);
         if (lane > 0 && lane < nc) {
             ll_put((uint64_t *)hp + (size_t)lane * kPartStride + 64, 0.0f, 0);
             ll_put((uint64_t *)hp + (size_t)lane * kPartStride + 65, 0.0f, 0);
         }
+        if (lane == 0) ll_gen_arrive(a.chunk_gen, gridDim.x * gridDim.y);
         ok = __all(ok);
         if (!ok) O = __int_as_float(0x7fc00000);  // a slice never arrived: NaN, not a stale value
     }
@@ -339,10 +343,13 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
         return hipErrorInvalidValue;
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
     if (a.q8 != nullptr && (!a.d8 || a.part != nullptr || a.heads != kHeads)) return hipErrorInvalidValue;
+    // every slice holds at least one live span and reaches the end of the kernel (no stop
+    // flag), so every workgroup of a sliced launch arrives at the generation counter
     if (a.chunks != 0 && (a.chunks < 0 || a.chunks > kMaxChunks || a.rows != 1 || a.part != nullptr ||
-                          a.page_table != nullptr || a.q8 != nullptr || !a.chunk_part ||
+                          a.page_table != nullptr || a.row_pos != nullptr || a.q8 != nullptr ||
+                          a.state != nullptr || !a.chunk_part || !a.chunk_gen ||
                           kSliceWaves * 64 * (a.chunks - 1) >= a.max_keys))
-        return hipErrorInvalidValue;  // every slice holds at least one live span
+        return hipErrorInvalidValue;
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
 }
 

@@ -24,39 +24,46 @@ namespace {
 
 thread_local std::string g_err;
 
-// Split-KV partials of moss_hip_attn_decode (LL words), one block per (device,
-// stream).  Each launch tags its words with the next value of `tag`, and the
-// merging workgroup clears every word it read, so a launch never takes an
-// earlier launch's partial for its own.  Allocated (and zeroed) on the first
-// call on a stream, which must not be under graph capture; grown with the head
-// count; kept until the process ends.
+// Sliced-attention scratch of moss_hip_attn_decode (the generation header and
+// the LL-word partials, chunk_scratch_bytes), one block per (device, stream),
+// allocated and zeroed on the first sliced call on a stream and grown with the
+// head count; kept until the process ends.  Launches on one stream are ordered,
+// so they never share the block at once; the kernel's launch generation keeps
+// consecutive launches' words apart.  A call that would allocate is refused
+// while its stream is being captured into a graph.  A captured launch keeps the
+// block of its capture stream: its replays must not overlap other calls on that
+// stream.
 struct AttnScratch {
-    uint64_t *part = nullptr;
+    uint8_t *base = nullptr;
     int heads = 0;
-    uint32_t tag = 0;  // LL tag of the last launch (0 is never used)
 };
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, AttnScratch> g_scratch;
 
-AttnScratch attn_scratch(hipStream_t s, int heads) {  // returns the entry with the tag of this launch
+uint8_t *attn_scratch(hipStream_t s, int heads) {
     int dev = 0;
     mh::hip_check(hipGetDevice(&dev), "hipGetDevice");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     AttnScratch &e = g_scratch[{dev, s}];
     if (e.heads < heads) {
-        if (e.part) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        mh::hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            throw Status(MOSS_HIP_ESTATE, "moss_hip_attn_decode: the first call on a stream with this head count "
+                                          "allocates its scratch and cannot be captured; make one uncaptured call "
+                                          "on the stream first");
+        if (e.base) {
             mh::hip_check(hipStreamSynchronize(s), "sync");  // launches still using the old block
-            (void)hipFree(e.part);
+            (void)hipFree(e.base);
             e = AttnScratch{};
         }
-        const size_t bytes = sizeof(uint64_t) * heads * mh::kMaxChunks * mh::kPartStride;
-        mh::hip_check(hipMalloc(&e.part, bytes), "hipMalloc(attention partials)");
-        mh::hip_check(hipMemsetAsync(e.part, 0, bytes, s), "memset(attention partials)");
+        const size_t bytes = mh::chunk_scratch_bytes(heads);
+        mh::hip_check(hipMalloc(&e.base, bytes), "hipMalloc(attention scratch)");
+        mh::hip_check(hipMemsetAsync(e.base, 0, bytes, s), "memset(attention scratch)");
         mh::hip_check(hipStreamSynchronize(s), "sync");
         e.heads = heads;
     }
-    if (++e.tag == 0) e.tag = 1;
-    return e;
+    return e.base;
 }
 
 template <class F>
@@ -197,6 +204,8 @@ int moss_hip_llm_restore_prefix(moss_hip_llm *m) {
 }
 
 int moss_hip_llm_prefix_pos(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->prefix_pos() : -1; }
+
+int moss_hip_llm_gate_rows(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->gate_rows() : -1; }
 
 int moss_hip_llm_kv_export(moss_hip_llm *m, int n_pos, float *k, float *v) {
     return guard([&] {
@@ -383,11 +392,11 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
         const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
         const int spans = (n_keys + 63) / 64;
         if (spans > mh::kOneWgSpans) {  // slices of kSliceWaves spans across workgroups
-            const AttnScratch sc = attn_scratch(static_cast<hipStream_t>(stream), heads);
+            uint8_t *sc = attn_scratch(static_cast<hipStream_t>(stream), heads);
             const int chunks = (spans + mh::kSliceWaves - 1) / mh::kSliceWaves;
             a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;
-            a.chunk_part = sc.part;
-            a.chunk_tag = sc.tag;
+            a.chunk_gen = reinterpret_cast<uint32_t *>(sc);
+            a.chunk_part = reinterpret_cast<uint64_t *>(sc + mh::kChunkHeader);
         }
         mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
     });

@@ -69,6 +69,7 @@ public:
     void snapshot_prefix();
     void restore_prefix();
     int prefix_pos() const { return prefix_pos_; }
+    int gate_rows() const { return gate_rows_; }
     void kv_export(int n_pos, float *k, float *v);
     void kv_import(int n_pos, const float *k, const float *v, const float *hidden);
 
@@ -111,7 +112,10 @@ private:
     KvType kvt_ = KV_F16;
     size_t kv_esize_ = 2;
     hipStream_t stream_ = nullptr;
-    hipEvent_t ev_[8] = {};             // per frame slot (2): local start, local end, global end, state copied
+    // per frame slot (2): local start / end, global start / end (timing), state copied
+    enum { kEvLocal0, kEvLocal1, kEvGlobal0, kEvGlobal1, kEvRead, kEvPerSlot };
+    hipEvent_t ev_[2 * kEvPerSlot] = {};
+    int gate_rows_ = 0;                 // frames whose end gate the last generate evaluated (gate dump rows)
 
     uint8_t *blob_ = nullptr;
     LayerW g_[kLayers] = {}, local_ = {};

@@ -115,10 +115,12 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
 
     hip_check(hipSetDevice(device_), "hipSetDevice");
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
-    // per readback slot: three timing events around the launches (recorded only
-    // when the caller asks for timing) and one completion event (no timestamp)
-    for (int i = 0; i < 8; ++i)
-        hip_check((i & 3) == 3 ? hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming) : hipEventCreate(&ev_[i]),
+    // per readback slot: four timing events around the two launches (recorded
+    // only when the caller asks for timing) and one completion event of the
+    // state readback (no timestamp)
+    for (int i = 0; i < 2 * kEvPerSlot; ++i)
+        hip_check(i % kEvPerSlot == kEvRead ? hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming)
+                                            : hipEventCreate(&ev_[i]),
                   "hipEventCreate");
     hip_check(hipMalloc(&blob_, bytes), "hipMalloc(weights)");
     hip_check(hipMemcpy(blob_, blob, bytes, hipMemcpyHostToDevice), "upload weights");
@@ -203,7 +205,6 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
             d.ln1_w = L.ln1_w; d.ln1_b = L.ln1_b; d.ln2_w = L.ln2_w; d.ln2_b = L.ln2_b;
             d.k_cache = kv_layer(0, l); d.v_cache = kv_layer(1, l); d.ctx_stride = max_ctx_;
             d.rope_cos = rope_; d.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
-            d.state = state_; d.ll = ll_; d.err = &state_->ll_err; d.instance = l;
         }
         hip_check(hipMalloc(&layer_args_, sizeof(LayerArgs) * kLayers), "hipMalloc(layer args)");
         hip_check(hipMemcpy(layer_args_, la.data(), sizeof(LayerArgs) * kLayers, hipMemcpyHostToDevice),
@@ -711,6 +712,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
                   "forced h2d");
     }
     hip_check(hipMemsetAsync(counts_, 0, sizeof(int) * kNVq * kCodebook, stream_), "counts clear");
+    gate_rows_ = 0;
     hstate_->frame = 0;
     hstate_->stop = 0;
     hstate_->min_frames = p.min_frames;
@@ -722,73 +724,84 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     clear_exchange();
     hip_check(hipStreamSynchronize(stream_), "sync");
 
-    // Frame f + 1 is enqueued before frame f's results are read, so the GPU
-    // never waits for the host.  A frame enqueued after the one the end gate
-    // stops is a no-op on the device (every kernel tests state->stop first),
-    // and the host drops it.  Each frame copies its state into its own readback
-    // slot (frames alternate between two) and records an event when it is done.
-    struct Enq {
-        bool global = false;
-    } enq[2];
-    int pos_next = pos_;  // position once every enqueued frame has run its global step
+    // Frame f is two launches: its local half L(f), followed by the copy of the
+    // decode state (codes, stop flag) into readback slot f & 1 and an event, then
+    // its global step G(f) on the frame's codes.  The host waits for frame f's
+    // state, runs on_frame(f), and only then enqueues L(f + 1) and G(f + 1) --
+    // while G(f) still runs on the device, so the GPU does not wait for the host.
+    // As in the reference's loop (llm.cpp:643-713), G(f) runs whatever on_frame(f)
+    // does, and a cancel flag raised there stops the loop before frame f + 1.
+    // A G(f) enqueued behind an L(f) that the end gate stopped is a no-op on the
+    // device (every kernel tests state->stop first); the host does not count it.
+    bool global_enq[2] = {false, false};
+    int pos_next = pos_;  // position once every enqueued global step has run
     auto enqueue = [&](int f) {
         const int slot = f & 1;
-        hipEvent_t *ev = ev_ + 4 * slot;
-        if (timing) hip_check(hipEventRecord(ev[0], stream_), "event");
+        hipEvent_t *ev = ev_ + kEvPerSlot * slot;
+        if (timing) hip_check(hipEventRecord(ev[kEvLocal0], stream_), "event");
         launch_frame_local(stream_, gate_dump != nullptr, hstate_->cfg.greedy != 0);
-        if (timing) hip_check(hipEventRecord(ev[1], stream_), "event");
-        enq[slot].global = f + 1 < max_frames && pos_next < max_ctx_;
-        if (enq[slot].global) {
-            launch_global(stream_);
-            ++pos_next;
-        }
-        if (timing) hip_check(hipEventRecord(ev[2], stream_), "event");
+        if (timing) hip_check(hipEventRecord(ev[kEvLocal1], stream_), "event");
         if (logits_dump)
             hip_check(hipMemcpyAsync(logits_dump + (size_t)f * kNVq * kCodebook, logits_,
                                      sizeof(float) * kNVq * kCodebook, hipMemcpyDeviceToHost, stream_),
                       "logits d2h");
         hip_check(hipMemcpyAsync(hread_ + slot, state_, sizeof(DevState), hipMemcpyDeviceToHost, stream_),
                   "state d2h");
-        hip_check(hipEventRecord(ev[3], stream_), "event");
+        hip_check(hipEventRecord(ev[kEvRead], stream_), "event");
+        global_enq[slot] = f + 1 < max_frames && pos_next < max_ctx_;
+        if (global_enq[slot]) {
+            if (timing) hip_check(hipEventRecord(ev[kEvGlobal0], stream_), "event");
+            launch_global(stream_);
+            if (timing) hip_check(hipEventRecord(ev[kEvGlobal1], stream_), "event");
+            ++pos_next;
+        }
+    };
+    // FrameTiming of a frame whose global step has finished (llm.h:34-37)
+    auto frame_timing = [&](int f) {
+        const int slot = f & 1;
+        const hipEvent_t *ev = ev_ + kEvPerSlot * slot;
+        float lm = 0.f, gm = 0.f;
+        hip_check(hipEventElapsedTime(&lm, ev[kEvLocal0], ev[kEvLocal1]), "elapsed");
+        if (global_enq[slot]) hip_check(hipEventElapsedTime(&gm, ev[kEvGlobal0], ev[kEvGlobal1]), "elapsed");
+        timing[2 * f] = gm;
+        timing[2 * f + 1] = lm;
     };
     auto cancelled = [&] { return cancel_ != nullptr && __atomic_load_n(cancel_, __ATOMIC_RELAXED); };
 
     int frames = 0;
     if (pos_ < max_ctx_ && !cancelled()) {
         enqueue(0);
-        for (int f = 0; f < max_frames; ++f) {
+        for (int f = 0;; ++f) {
             const int slot = f & 1;
-            const bool next = f + 1 < max_frames && pos_next < max_ctx_ && !cancelled();
-            if (next) enqueue(f + 1);
-            hip_check(hipEventSynchronize(ev_[4 * slot + 3]), "sync");
+            hip_check(hipEventSynchronize(ev_[kEvPerSlot * slot + kEvRead]), "sync");
             const DevState &hs = hread_[slot];
-            hstate_->ll_err = hs.ll_err;
+            hstate_->ll_err = hs.ll_err;  // the local half's and the previous global step's
             check_exchange();
+            if (timing && f > 0) frame_timing(f - 1);  // G(f - 1) ran before L(f)
             if (gate_dump) {
                 float *gd = gate_dump + 4 * (size_t)f;
                 gd[0] = hs.gate[0];
                 gd[1] = hs.gate[1];
                 gd[2] = (float)hs.gate_argmax;
                 gd[3] = hs.gate_argmax_v;
+                gate_rows_ = f + 1;
             }
             if (hs.stop) break;
             int32_t *row = out_rows + (size_t)f * 17;
             row[0] = 0;
             for (int ch = 0; ch < kNVq; ++ch) row[ch + 1] = hs.codes[ch];
-            if (timing) {
-                float lm = 0.f, gm = 0.f;
-                hip_check(hipEventElapsedTime(&lm, ev_[4 * slot], ev_[4 * slot + 1]), "elapsed");
-                hip_check(hipEventElapsedTime(&gm, ev_[4 * slot + 1], ev_[4 * slot + 2]), "elapsed");
-                timing[2 * f] = enq[slot].global ? gm : 0.0;
-                timing[2 * f + 1] = lm;
-            }
-            if (enq[slot].global) ++pos_;
+            if (global_enq[slot]) ++pos_;
             frames = f + 1;
             if (cb) cb(user, f, row);
-            if (!next) break;
+            if (!global_enq[slot] || pos_next >= max_ctx_ || cancelled()) break;  // last frame, full KV, cancel
+            enqueue(f + 1);
         }
     }
-    hip_check(hipStreamSynchronize(stream_), "sync");  // a frame enqueued past the last one has drained
+    hip_check(hipMemcpyAsync(&hstate_->ll_err, &state_->ll_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+              "state d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");  // the last global step has drained
+    check_exchange();
+    if (timing && frames > 0) frame_timing(frames - 1);
     return frames;
 }
 

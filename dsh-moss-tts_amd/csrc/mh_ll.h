@@ -27,6 +27,23 @@ __device__ __forceinline__ uint64_t ll_load(const uint64_t *w) {
     return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Launch generation of a sliced attention scratch block (gen[0]: generation,
+// gen[1]: workgroups of the current launch that are done).
+__device__ __forceinline__ uint32_t ll_gen_load(const uint32_t *gen) {
+    return __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Called once per workgroup after its last use of the launch's tag: the last of
+// `total` workgroups resets the count and starts the next generation.  Every
+// workgroup has read the generation before it arrives, so no workgroup of this
+// launch can see the new value; the next launch on the stream sees it.
+__device__ __forceinline__ void ll_gen_arrive(uint32_t *gen, uint32_t total) {
+    const uint32_t done = __hip_atomic_fetch_add(gen + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done + 1 == total) {
+        __hip_atomic_store(gen + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // Waits until words [0, n) of src carry `tag` and copies their values to dst
 // (LDS).  Thread t takes words t, t + 256, ... (at most MAXK); all of its loads
 // are in flight together.  Returns false when the thread's budget runs out.

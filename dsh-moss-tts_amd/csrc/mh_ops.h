@@ -99,14 +99,25 @@ struct AttnArgs {
     const DevState *state = nullptr;
     // single row, long context: the keys are cut into `chunks` slices of 256 (one workgroup of
     // 4 waves each, more spans per wave past kMaxChunks); slices 1.. write their partial
-    // (o[64], m, l) as LL words tagged chunk_tag to chunk_part[(h * chunks + c) * kPartStride],
-    // and slice 0 of each head waits for them, merges all in slice order and writes the output
+    // (o[64], m, l) as LL words to chunk_part[(h * chunks + c) * kPartStride], and slice 0 of
+    // each head waits for them, merges all in slice order and writes the output.  The words
+    // carry a tag made from the launch generation chunk_gen[0], which every workgroup reads at
+    // its start; chunk_gen[1] counts the workgroups that are done, and the last of a launch
+    // resets it and bumps the generation -- so consecutive launches on a scratch block (graph
+    // replays included) never share a tag, and a partial left by a launch whose merge gave up
+    // is never read as current.  Both words start at zero.
     int chunks = 0;
     uint64_t *chunk_part = nullptr;
-    uint32_t chunk_tag = 0;          // distinct for consecutive launches on one stream
+    uint32_t *chunk_gen = nullptr;
 };
+// Bytes of a sliced-attention scratch block for `heads` heads: a 256-byte header (the
+// generation and arrival words) followed by the partials [heads][kMaxChunks][kPartStride].
+constexpr size_t kChunkHeader = 256;
 constexpr int kPartStride = 68;
 constexpr int kMaxChunks = 64;
+constexpr size_t chunk_scratch_bytes(int heads) {
+    return kChunkHeader + sizeof(uint64_t) * (size_t)heads * kMaxChunks * kPartStride;
+}
 #ifndef MH_SLICE_WAVES
 #define MH_SLICE_WAVES 4
 #endif
@@ -295,20 +306,15 @@ struct LayerArgs {
     const uint8_t *attn_w = nullptr, *proj_w = nullptr, *fc_in_w = nullptr, *fc_out_w = nullptr;
     const float *attn_b = nullptr, *proj_b = nullptr, *fc_in_b = nullptr, *fc_out_b = nullptr;
     const float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
-    float *x = nullptr;                        // residual stream: block input, replaced by the block output
     void *k_cache = nullptr, *v_cache = nullptr;  // this layer's [head][ctx_stride][64]
     int ctx_stride = 0;
     const float *rope_cos = nullptr, *rope_sin = nullptr;
-    const DevState *state = nullptr;           // pos, stop
-    uint64_t *ll = nullptr;                    // kLayerWords exchange words
-    unsigned *err = nullptr;                   // set when a wait runs out
-    int instance = 0;                          // 0..31, distinct for consecutive launches at one position
 };
 // Whether kLayerGrid workgroups of every fused decode kernel fit the device at once.
 hipError_t decode_layer_fits(int device, bool *fits);
 // The whole global step in one launch: embedding of the row, kLayers blocks, ln_f.
 struct GlobalArgs {
-    const LayerArgs *layers = nullptr;  // kLayers entries in device memory (their x is unused)
+    const LayerArgs *layers = nullptr;  // kLayers entries in device memory
     const uint8_t *wte = nullptr;
     const uint8_t *aemb[kNVq] = {};
     const int *row = nullptr;           // [17] on device

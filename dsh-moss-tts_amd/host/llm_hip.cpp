@@ -246,8 +246,8 @@ std::vector<Row> LlmModel::generate(int max_frames, const SampleParams &p, uint6
     if (max_frames <= 0) return frames;
     const moss_hip_sample_params sp{p.greedy ? 1 : 0, p.temperature, p.top_k, p.top_p, p.repetition_penalty,
                                     p.end_greedy ? 1 : 0, p.min_frames, p.greedy_frames};
-    // frames stop once the position reaches kMaxCtx (llm.cpp:644), so at most this many
-    const int bound = kMaxCtx - position() + 1;
+    // frame f runs while position() + f < kMaxCtx (llm.cpp:644), so at most this many
+    const int bound = kMaxCtx - position();
     int cap = max_frames < bound ? max_frames : bound;
     if (forced && (int)forced->size() < cap) cap = (int)forced->size();
     if (cap <= 0) return frames;
@@ -275,7 +275,7 @@ std::vector<Row> LlmModel::generate(int max_frames, const SampleParams &p, uint6
     if (!gate_dump_path_.empty()) {  // the CSV of llm.cpp:721-731
         if (std::FILE *fp = std::fopen(gate_dump_path_.c_str(), "wb")) {
             std::fprintf(fp, "frame,argmax_id,argmax_minus_slot,slot_minus_end\n");
-            const int rows = n < cap ? n + 1 : n;  // the frame that stopped also evaluated its gate
+            const int rows = moss_hip_llm_gate_rows(h_);  // the frame the gate stopped has a row too
             for (int i = 0; i < rows; ++i) {
                 const float *g = gate.data() + 4 * (size_t)i;  // (l_end, l_slot, argmax_id, argmax_logit)
                 std::fprintf(fp, "%d,%d,%.4f,%.4f\n", i, (int)g[2], g[3] - g[1], g[1] - g[0]);

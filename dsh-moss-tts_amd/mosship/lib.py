@@ -22,6 +22,7 @@ EXPORTED = [
     "moss_hip_llm_position", "moss_hip_llm_get_hidden", "moss_hip_llm_set_hidden", "moss_hip_llm_prefill",
     "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
     "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
+    "moss_hip_llm_gate_rows",
     "moss_hip_llm_kv_export", "moss_hip_llm_kv_import",
     "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
@@ -78,6 +79,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         getattr(L, n).argtypes = [vp]
     L.moss_hip_llm_position.argtypes = [vp]
     L.moss_hip_llm_prefix_pos.argtypes = [vp]
+    L.moss_hip_llm_gate_rows.argtypes = [vp]
     L.moss_hip_llm_get_hidden.argtypes = [vp, vp]
     L.moss_hip_llm_set_hidden.argtypes = [vp, vp]
     L.moss_hip_llm_prefill.argtypes = [vp, vp, i32, i32]
@@ -235,7 +237,7 @@ class HipLLM:
         if logits:
             res["logits"] = ld[:n.value]
         if gate:
-            res["gate"] = gd[:min(n.value + 1, max_frames)]
+            res["gate"] = gd[:self.L.moss_hip_llm_gate_rows(self._h)]
         return res
 
     def set_cancel_flag(self, flag_array: np.ndarray | None):

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 3
+#define MOSS_HIP_ABI_VERSION 4
 
 enum {
     MOSS_HIP_OK = 0,
@@ -58,11 +58,12 @@ typedef struct {
     int use_graphs; /* 1 = replay the global step and the frame as hipGraphs (default), 0 = direct launches */
     int prefill_a16; /* prefill activations: 0 = W8A8, int8 per 32-block (the reference's prefill unless
                         MOSS_A16 is 1/all, csrc/src/gemv.cpp:23-48, llm.cpp:319-328); 1 = W8A16 fp32 */
-    int decode_kernels; /* single-stream decode: 0 = one launch per transformer block of the global step
-                           and one per local step with its audio head (default, when the device holds the
-                           192 workgroups of a launch at once), 1 = one launch per operator (GEMV /
-                           attention / head).  Both follow the reference's arithmetic per value; they
-                           differ in fp32 summation order only. */
+    int decode_kernels; /* single-stream decode: 0 = fused kernels (default, when the device holds every
+                           workgroup of a launch at once): the whole global step is one launch, and the
+                           local half of a greedy frame (17 local steps, 16 audio heads, the end gate)
+                           another; 1 = one launch per operator (GEMV / attention / head), replayed as
+                           hipGraphs.  Both follow the reference's arithmetic per value; they differ in
+                           fp32 summation order only. */
 } moss_hip_llm_options;
 
 /* SampleParams (csrc/include/moss/sampler.h:8-22), field for field. */
@@ -117,8 +118,15 @@ int moss_hip_llm_generate(moss_hip_llm *m, int max_frames, const moss_hip_sample
                           const int32_t *forced, int n_forced, int32_t *out_rows, int *out_frames, double *timing,
                           float *logits_dump, float *gate_dump, moss_hip_frame_cb cb, void *user);
 
-/* LlmModel::set_cancel_flag (llm.h:86): a byte polled (relaxed) once per frame; NULL clears it.
- * std::atomic<bool> is one byte with bool's representation on the supported ABIs. */
+/* Rows of gate_dump the last moss_hip_llm_generate filled: one per frame whose end gate was
+ * evaluated -- the frames it returned, plus the frame the gate stopped (the rows the reference
+ * writes to its gate CSV, llm.cpp:653-679,721-731); 0 when it was called without gate_dump. */
+int moss_hip_llm_gate_rows(const moss_hip_llm *m);
+
+/* LlmModel::set_cancel_flag (llm.h:86): a byte polled (relaxed) before each frame, as
+ * llm.cpp:645 does; a flag raised in the on_frame callback of frame k ends generate after
+ * frame k's global step, with k + 1 frames.  NULL clears it.  std::atomic<bool> is one byte
+ * with bool's representation on the supported ABIs. */
 int moss_hip_llm_set_cancel_flag(moss_hip_llm *m, const volatile uint8_t *flag);
 
 /* Prefix KV (llm.h:52-57, llm.cpp:455-483): device-to-device snapshot / restore. */

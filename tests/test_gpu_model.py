@@ -165,12 +165,50 @@ def test_generate_end_gate_matches_oracle(torch_gpu, oracle, prefilled):
         out = g.generate(6, SampleParams.make(greedy=True, min_frames=0), gate=dump)
         assert len(out["rows"]) == len(ref["rows"])
         assert np.array_equal(out["rows"], ref["rows"])
-        if dump:
-            ng = min(len(out["gate"]), len(ref["gate"]))
-            og, rg = out["gate"][:ng], ref["gate"][:ng]
+        if dump:  # one row per frame whose gate was evaluated, the stopping frame included
+            assert len(out["gate"]) == len(ref["gate"]) == len(ref["rows"]) + (len(ref["rows"]) < 6)
+            og, rg = out["gate"], ref["gate"]
             assert np.array_equal(og[:, 2], rg[:, 2])  # argmax ids
             assert max_rel(og[:, [0, 1, 3]], rg[:, [0, 1, 3]]) <= TOL
         g.close()
+
+
+@pytest.mark.parametrize("k", [0, 3])
+def test_cancel_from_on_frame(torch_gpu, oracle, prefilled, k):
+    """A cancel flag raised by on_frame(k) ends generate after frame k's global
+    step, as the reference's per-frame check does (llm.cpp:643-713): k + 1 frames,
+    position + k + 1 and the hidden state of that global step -- where a run of
+    k + 2 frames ends too (no global step follows its last frame).  A flag raised
+    before generate yields no frame."""
+    blob, rows, kc, vc, h = prefilled
+    print(f"cancel at frame {k}", flush=True)
+    g = HipLLM(blob, kv_fp32=True)
+    g.kv_import(kc, vc, h)
+    flag = np.zeros(1, np.uint8)
+    g.set_cancel_flag(flag)
+    seen = []
+
+    def on_frame(f, row):
+        seen.append((f, row[1:].tolist()))
+        if f == k:
+            flag[0] = 1
+
+    out = g.generate(10, SampleParams.make(greedy=True, min_frames=10), on_frame=on_frame)
+    assert len(out["rows"]) == k + 1 and [f for f, _ in seen] == list(range(k + 1))
+    assert [c for _, c in seen] == out["rows"][:, 1:].tolist()
+    assert g.position == len(rows) + k + 1
+    m = _oracle_from_state(oracle, blob, kc, vc, h, kv_f16=False)
+    ref = m.generate(k + 2, OSP.make(greedy=True, min_frames=10))
+    assert np.array_equal(out["rows"], ref["rows"][:k + 1])
+    assert g.position == m.position
+    assert max_rel(g.hidden(), m.hidden()) <= TOL
+    pos = g.position
+    again = g.generate(3, SampleParams.make(greedy=True, min_frames=3))  # flag still raised
+    assert len(again["rows"]) == 0 and g.position == pos
+    flag[0] = 0
+    g.set_cancel_flag(None)
+    assert len(g.generate(2, SampleParams.make(greedy=True, min_frames=2))["rows"]) == 2
+    g.close()
 
 
 # W8A8 prefill end to end: every GEMM input is re-quantised per 32-block, so an

@@ -179,6 +179,34 @@ def test_attention_decode_graph_replays(torch_gpu, oracle):
         s.synchronize()
 
 
+def test_attention_decode_first_call_under_capture_refused(torch_gpu):
+    """The first sliced call on a stream allocates its scratch, which a graph
+    capture cannot hold: it is refused with ESTATE and nothing is enqueued; an
+    uncaptured call first makes the same capture work."""
+    torch = torch_gpu
+    ctx = 600
+    s = torch.cuda.Stream()
+    q = torch.zeros(768, dtype=torch.float32, device="cuda")
+    k = torch.zeros((12, ctx, 64), dtype=torch.float16, device="cuda")
+    out = torch.zeros(768, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        with pytest.raises(lib.MossHipError) as e:
+            lib.attn_decode(q, k, k, 12, ctx, ctx, out)
+    assert e.value.code == lib.ESTATE
+    with torch.cuda.stream(s):
+        lib.attn_decode(q, k, k, 12, ctx, ctx, out)
+    s.synchronize()
+    graph2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph2, stream=s):
+        lib.attn_decode(q, k, k, 12, ctx, ctx, out)
+    for _ in range(3):
+        graph2.replay()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+
+
 def test_attention_single_key_returns_v(torch_gpu):
     """ctx = 1: softmax over one key is 1, so the output is that key's v exactly."""
     torch = torch_gpu
