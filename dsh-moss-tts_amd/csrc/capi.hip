@@ -66,6 +66,35 @@ uint8_t *attn_scratch(hipStream_t s, int heads) {
     return e.base;
 }
 
+// Scratch of moss_hip_attn_decode_noalloc: the sliced attention's generation
+// header and partials for up to kNoAllocHeads heads, in the code object's own
+// device memory (each device that loads the library holds a copy until the
+// process ends).  Host code uses the address hipGetSymbolAddress returns for the
+// current device, never the array's name.  The generation header starts at zero
+// (static storage) and the kernel's last workgroup resets the arrival count, so
+// no call needs to clear it; the partials need no clearing (their tags are
+// never current for a later launch).
+constexpr int kNoAllocHeads = 16;
+constexpr size_t kNoAllocBytes = mh::chunk_scratch_bytes(kNoAllocHeads);
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint8_t *g_noalloc_ptr[kMaxDevices] = {};  // per device: the address of its `scratch`
+
+uint8_t *noalloc_scratch() {
+    int dev = 0;
+    mh::hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw Status(MOSS_HIP_EUNSUPPORTED, "device ordinal beyond 63");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        mh::hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_noalloc_ptr[dev] = static_cast<uint8_t *>(p);
+    }
+    return g_noalloc_ptr[dev];
+}
+
 template <class F>
 int guard(F &&f) {
     try {
@@ -369,36 +398,62 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// The arguments of both single-query attention entry points; `scratch_of` gives the
+// sliced launch's scratch block for `heads` heads.
+template <class Scratch>
+void attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads, int ctx_stride,
+                 int n_keys, void *out, int out_dtype, void *stream, Scratch &&scratch_of) {
+    if (!q || !k_cache || !v_cache || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
+    if (heads <= 0 || ctx_stride <= 0 || n_keys <= 0 || n_keys > ctx_stride)
+        throw Status(MOSS_HIP_EINVAL, "need 0 < n_keys <= ctx_stride");
+    if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
+        throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
+    mh::AttnArgs a;  // the cache is one page of ctx_stride positions
+    a.q = q;
+    a.k_pool = k_cache;
+    a.v_pool = v_cache;
+    a.page_size = ctx_stride;
+    a.heads = heads;
+    a.q_stride = heads * mh::kHeadDim;
+    a.out_stride = heads * mh::kHeadDim;
+    a.pos0 = n_keys - 1;
+    a.max_keys = n_keys;
+    a.out = out;
+    a.out_f16 = out_dtype == MOSS_HIP_F16;
+    const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
+    const int spans = (n_keys + 63) / 64;
+    if (spans > mh::kOneWgSpans) {  // slices of kSliceWaves spans across workgroups
+        uint8_t *sc = scratch_of(static_cast<hipStream_t>(stream), heads);
+        const int chunks = (spans + mh::kSliceWaves - 1) / mh::kSliceWaves;
+        a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;
+        a.chunk_gen = reinterpret_cast<uint32_t *>(sc);
+        a.chunk_part = reinterpret_cast<uint64_t *>(sc + mh::kChunkHeader);
+    }
+    mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
+}
+
+}  // namespace
+
+extern "C" {
+
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
                          int ctx_stride, int n_keys, void *out, int out_dtype, void *stream) {
     return guard([&] {
-        if (!q || !k_cache || !v_cache || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
-        if (heads <= 0 || ctx_stride <= 0 || n_keys <= 0 || n_keys > ctx_stride)
-            throw Status(MOSS_HIP_EINVAL, "need 0 < n_keys <= ctx_stride");
-        if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
-            throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
-        mh::AttnArgs a;  // the cache is one page of ctx_stride positions
-        a.q = q;
-        a.k_pool = k_cache;
-        a.v_pool = v_cache;
-        a.page_size = ctx_stride;
-        a.heads = heads;
-        a.q_stride = heads * mh::kHeadDim;
-        a.out_stride = heads * mh::kHeadDim;
-        a.pos0 = n_keys - 1;
-        a.max_keys = n_keys;
-        a.out = out;
-        a.out_f16 = out_dtype == MOSS_HIP_F16;
-        const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
-        const int spans = (n_keys + 63) / 64;
-        if (spans > mh::kOneWgSpans) {  // slices of kSliceWaves spans across workgroups
-            uint8_t *sc = attn_scratch(static_cast<hipStream_t>(stream), heads);
-            const int chunks = (spans + mh::kSliceWaves - 1) / mh::kSliceWaves;
-            a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;
-            a.chunk_gen = reinterpret_cast<uint32_t *>(sc);
-            a.chunk_part = reinterpret_cast<uint64_t *>(sc + mh::kChunkHeader);
-        }
-        mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
+        attn_decode(q, k_cache, v_cache, kv_dtype, heads, ctx_stride, n_keys, out, out_dtype, stream, attn_scratch);
+    });
+}
+
+int moss_hip_attn_decode_noalloc(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
+                                 int ctx_stride, int n_keys, void *out, int out_dtype, void *stream) {
+    return guard([&] {
+        if (heads > kNoAllocHeads)
+            throw Status(MOSS_HIP_EINVAL, "moss_hip_attn_decode_noalloc: at most 16 heads (its scratch is sized for 16)");
+        attn_decode(q, k_cache, v_cache, kv_dtype, heads, ctx_stride, n_keys, out, out_dtype, stream,
+                    [](hipStream_t, int) { return noalloc_scratch(); });
     });
 }
 

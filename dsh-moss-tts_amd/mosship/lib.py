@@ -27,6 +27,7 @@ EXPORTED = [
     "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
+    "moss_hip_attn_decode_noalloc",
     "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8",
 ]
 
@@ -104,6 +105,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_batch_generate.argtypes = [vp, i32, i32, C.POINTER(SampleParams), vp, vp, vp, C.POINTER(C.c_double)]
     L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
     L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
+    L.moss_hip_attn_decode_noalloc.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
     _lib = L
     return L
 
@@ -157,12 +159,15 @@ def dequant_rows_q8x4(w, mat_rows: int, cols: int, rows_idx, out, stream=None) -
                                             rows_idx.numel(), C.c_void_p(out.data_ptr()), _stream(stream)))
 
 
-def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, out, stream=None) -> None:
+def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, out, stream=None,
+                noalloc: bool = False) -> None:
+    """moss_hip_attn_decode, or with noalloc=True moss_hip_attn_decode_noalloc (static scratch)."""
     import torch
     dt = {torch.float32: F32, torch.float16: F16}
-    check(load().moss_hip_attn_decode(C.c_void_p(q.data_ptr()), C.c_void_p(k_cache.data_ptr()),
-                                      C.c_void_p(v_cache.data_ptr()), dt[k_cache.dtype], heads, ctx_stride, n_keys,
-                                      C.c_void_p(out.data_ptr()), dt[out.dtype], _stream(stream)))
+    L = load()
+    fn = L.moss_hip_attn_decode_noalloc if noalloc else L.moss_hip_attn_decode
+    check(fn(C.c_void_p(q.data_ptr()), C.c_void_p(k_cache.data_ptr()), C.c_void_p(v_cache.data_ptr()),
+             dt[k_cache.dtype], heads, ctx_stride, n_keys, C.c_void_p(out.data_ptr()), dt[out.dtype], _stream(stream)))
 
 
 # ---------------------------------------------------------------- model

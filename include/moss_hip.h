@@ -210,6 +210,18 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
                          int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
 
+/* moss_hip_attn_decode without any allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under hipGraph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernel and results; heads <= 16
+ * (EINVAL beyond).  Its scratch (557,312 bytes: the sliced launch's generation header and
+ * partials for 16 heads) is a static array in the library's device code, one per GPU, held
+ * until the process ends; the first call on a device looks its address up
+ * (hipGetSymbolAddress), nothing is allocated or cleared per call.  Every call on one GPU
+ * shares that scratch, so calls that overlap on one GPU (other streams, concurrent graph
+ * replays) race: serialise them. */
+int moss_hip_attn_decode_noalloc(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
+                                 int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
