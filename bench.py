@@ -3,24 +3,34 @@
 Workload (one "step" = one decoded frame): batch 1, a seeded random-init model
 with the reference's dims (12 layers, d 768, 12x64 heads, FF 3072, vocab 16384,
 W8A16 Q8_0_4X4 weights), KV cache prefilled to context 512 with N(0,1) values
-(fp16 cache), greedy decoding (min_frames = steps, so the end gate never stops
-it), two fused kernel launches per frame.  A frame is what the reference's "ms/frame" counts:
-local 1-layer transformer x 17, 16 audio heads + greedy picks, the W8A8 end
-gate, and the 12-layer global step.  The global step alone is also reported.
+(fp16 cache), --steps greedy frames (min_frames = steps, so the end gate never
+stops it; 256 frames fill the cache to position 767), two fused kernel launches
+per frame.  A frame is what the reference's "ms/frame" counts: local 1-layer
+transformer x 17, 16 audio heads + greedy picks, the W8A8 end gate, and the
+12-layer global step.  The frame is timed without per-launch events; a second
+run of the same frames records HIP events around each launch on the model's
+stream, which gives the global-step and local-half times.
 
-The roofline object describes the W8A16 GEMV kernel at large N (K = 768,
-N = 262144, weights cycled through a 1 GiB pool so they stream from HBM, not
-the 256 MB Infinity Cache): algorithmic bytes (N/4)(K/32)*136 + 2K + 2N per
-launch over its average duration from HIP events on its stream.
+roofline: the frame's dominant kernel (the longer of decode_global_kernel and
+decode_local_kernel): algorithmic bytes per launch over its average launch
+duration from those events.  roofline_decode holds both kernels, roofline_gemv
+the W8A16 GEMV at large N (K = 768, N = 262144, weights cycled through a 1 GiB
+pool so they stream from HBM, not the 256 MB Infinity Cache).
 
 cpu_baseline: the reference's own AVX2 CPU path (oracle/_ref, compiled from the
-reference sources) decoding from the same context-512 state on this host.
+reference sources) decoding the same frames from the same context-512 state on
+this host, at T = 4 threads (its published setting) and T = the CPU share of
+this process (physical cores, affinity, cgroup quota and OMP_NUM_THREADS,
+whichever is smallest); host_cpu reports lscpu's model, sockets and cores.
 
-Also reported: single-query decode attention (12 x 64 heads, fp16 K/V) at
-contexts 128, 512, 1024 and 2048, warm and cold, beside the reference's AVX2
-attention on one host core; the 256-row prefill (ms; W8A8 as the reference's prefill, against
-the 5.0 POP/s int8 MFMA peak, and W8A16 against the 2.5 PFLOP/s fp16 peak) and 64 streams with contexts ~ U[64, 1024] decoded 128 frames in
-lock-step (aggregate frames/s), each next to the reference on the host cores.
+Also reported: the single GEMV (K = 768, N = 2304) replayed from a graph beside
+the reference's gemv_par; single-query decode attention (12 x 64 heads, fp16
+K/V) at contexts 128, 512, 1024 and 2048, warm and cold, beside the reference's
+AVX2 attention on one host core; the 256-row prefill (ms; W8A8 as the
+reference's prefill, against the 5.0 POP/s int8 MFMA peak, and W8A16 against
+the 2.5 PFLOP/s fp16 peak) and 64 streams with contexts ~ U[64, 1024] decoded
+128 frames in lock-step (aggregate frames/s), each next to the reference on the
+host cores.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
                        [--mode full|gemv|attn|decode|prefill|streams]
@@ -47,6 +57,7 @@ CAL_BYTES = 256 << 20
 # `bench.py --mode gemv` (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; KiB per dispatch
 # scaled by the 256 MiB calibration copy of that same run: fetch x2.0, write x1.0).
 GEMV_TRAFFIC_BYTES = 214_956_032
+CONFIG0_BYTES = 1_886_208  # (2304/4)(768/32)*136 weights + 2*768 x + 2*2304 y (fp16)
 
 
 def log(*a):
@@ -132,25 +143,40 @@ def bench_gemv(reps: int = 60):
         out[mode] = {"us": us, "GBps": algo / us / 1e3}
     out["algo_bytes"] = algo
     out["pool_buffers"] = pool_n
-    # config 0 shape (K=768, N=2304): latency-bound, reported for completeness
+    # the single GEMV at K=768, N=2304 (fp16 in/out): 200 launches captured in a graph
+    # and replayed, so the time is the kernel's, not the host's launch rate
     w0 = torch.from_numpy(mf.synth_q8x4(rng, 2304, 768).reshape(-1)).cuda()
     y0 = torch.empty(2304, dtype=torch.float16, device="cuda")
-    for _ in range(10):
-        lib.gemv_q8x4(w0, 2304, 768, x, y0)
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        for _ in range(10):
+            lib.gemv_q8x4(w0, 2304, 768, x, y0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        for _ in range(200):
+            lib.gemv_q8x4(w0, 2304, 768, x, y0)
+    graph.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for _ in range(200):
-        lib.gemv_q8x4(w0, 2304, 768, x, y0)
-    e1.record(s)
+    e0.record()
+    graph.replay()
+    e1.record()
     torch.cuda.synchronize()
     us0 = e0.elapsed_time(e1) * 1e3 / 200
-    out["config0"] = {"us": us0, "GBps": 1886208 / us0 / 1e3}
-    # calibration for hardware byte counters: one plain device copy of exactly 256 MiB
+    out["config0"] = {"us": us0, "GBps": CONFIG0_BYTES / us0 / 1e3, "timing": "200 launches replayed from a graph"}
+    calibration_copy()
+    return out
+
+
+def calibration_copy():
+    """One plain device copy of exactly 256 MiB: what FETCH_SIZE / WRITE_SIZE read for it
+    scales the hardware byte counters of the kernels profiled in the same run."""
+    import torch
     cal_src = torch.ones(CAL_BYTES, dtype=torch.uint8, device="cuda")
     cal_dst = torch.empty_like(cal_src)
     cal_dst.copy_(cal_src)
     torch.cuda.synchronize()
-    return out
 
 
 PREFILL_ROWS = 256
@@ -292,31 +318,62 @@ def bench_streams(blob, steps: int = STREAM_STEPS):
             "ms_per_step": out["ms"] / steps, "global_stack_GBps": step_bytes / (out["ms"] / steps * 1e-3) / 1e9}
 
 
-def _cpu_model_name():
+def host_cpu():
+    """The host's CPU as lscpu reports it, and the share of it this process may use:
+    the smallest of the physical cores, the CPUs in its affinity mask, its cgroup
+    quota and OMP_NUM_THREADS (the per-GPU share a shared GPU host sets)."""
+    import subprocess
+    info = {"model": "", "sockets": None, "physical_cores": None, "logical_cpus": os.cpu_count()}
     try:
-        with open("/proc/cpuinfo") as f:
-            return next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
-    except (OSError, StopIteration):
-        return ""
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {ln.split(":", 1)[0].strip(): ln.split(":", 1)[1].strip() for ln in txt.splitlines() if ":" in ln}
+        info["model"] = kv.get("Model name", "")
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per = int(kv.get("Core(s) per socket", "0") or 0)
+        info["sockets"] = sockets or None
+        info["physical_cores"] = sockets * per or None
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    if not info["model"]:
+        try:
+            with open("/proc/cpuinfo") as f:
+                info["model"] = next(ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name"))
+        except (OSError, StopIteration):
+            pass
+    limits = [n for n in (info["physical_cores"], len(os.sched_getaffinity(0))) if n]
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            limits.append(max(1, int(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        limits.append(int(os.environ["OMP_NUM_THREADS"]))
+    info["cpu_share"] = max(1, min(limits)) if limits else 1
+    return info
 
 
-def cpu_prefill(blob):
-    """Reference prefill of the same 256 rows: W8A8 (its release default) in this process,
-    A16 (MOSS_A16=1, the numerics the GPU path follows) in a child process."""
+def cpu_prefill(blob, threads: int):
+    """Reference prefill of the same 256 rows on `threads` threads: W8A8 (its release
+    default) in this process, A16 (MOSS_A16=1) in a child process (the mode is read
+    once per process, gemv.cpp:26-35)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import REF_SO, RefCpu
     if not os.path.exists(REF_SO):
         return None
     rows = prefill_rows()
     r = RefCpu(a16_mode="decode")
-    m = r.model(blob, threads=4)
+    m = r.model(blob, threads=threads)
+    m.prefill(rows[:16])  # warm the thread pool and the weights
     t0 = time.perf_counter()
     m.prefill(rows)
     w8a8 = (time.perf_counter() - t0) * 1e3
     m.close()
     code = ("import sys, time, numpy as np; sys.path[:0] = [%r, %r]; from oracle import RefCpu;"
             "from mosship import moss_format as mf; r = RefCpu(a16_mode='1'); blob = open(sys.argv[1], 'rb').read();"
-            "rows = np.load(sys.argv[2]); m = r.model(blob, threads=4); t0 = time.perf_counter(); m.prefill(rows);"
+            "rows = np.load(sys.argv[2]); m = r.model(blob, threads=int(sys.argv[3])); m.prefill(rows[:16]);"
+            "t0 = time.perf_counter(); m.prefill(rows);"
             "print((time.perf_counter() - t0) * 1e3)" % (os.path.join(ROOT, "oracle"), os.path.join(ROOT, "dsh-moss-tts_amd")))
     import subprocess
     with tempfile.TemporaryDirectory() as td:
@@ -324,13 +381,13 @@ def cpu_prefill(blob):
         with open(bp, "wb") as f:
             f.write(blob)
         np.save(rp, rows)
-        a16 = float(subprocess.run([sys.executable, "-c", code, bp, rp], check=True, capture_output=True,
-                                   text=True).stdout.strip().splitlines()[-1])
-    return {"w8a8_ms": w8a8, "a16_ms": a16, "threads": 4}
+        a16 = float(subprocess.run([sys.executable, "-c", code, bp, rp, str(threads)], check=True,
+                                   capture_output=True, text=True).stdout.strip().splitlines()[-1])
+    return {"w8a8_ms": w8a8, "a16_ms": a16, "threads": threads}
 
 
-def cpu_streams(blob, frames: int = 12, threads: int = 4):
-    """P = floor(cores / T) concurrent reference LlmModels (T threads each) decoding greedy
+def cpu_streams(blob, share: int, threads: int, frames: int = 32):
+    """P = share // T concurrent reference LlmModels (T threads each) decoding greedy
     frames from their own states; contexts ~ U[64, 640] (the reference caps at 768)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import threading
@@ -340,15 +397,14 @@ def cpu_streams(blob, frames: int = 12, threads: int = 4):
     from mosship import moss_format as mf
     if not os.path.exists(REF_SO):
         return None
-    cores = min(os.cpu_count() or 1, 16)
-    procs = max(1, cores // threads)
+    procs = max(1, share // threads)
     ctx = stream_contexts(lo=64, hi=640)[:procs]
     rng = np.random.default_rng(99)
     r = RefCpu(a16_mode="decode")
     models, paths = [], []
     td = tempfile.mkdtemp(prefix="mossref_streams_")
     for i in range(procs):
-        n = int(ctx[i])
+        n = int(ctx[i % len(ctx)])
         k = rng.standard_normal((12, n, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
         v = rng.standard_normal((12, n, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
         rows = mf.text_rows(rng.integers(0, mf.VOCAB, n))
@@ -379,11 +435,33 @@ def cpu_streams(blob, frames: int = 12, threads: int = 4):
     os.rmdir(td)
     return {"frames_per_s": sum(counts) / wall, "instances": procs, "threads_each": threads, "cores": procs * threads,
             "sample": f"{procs} concurrent LlmModel x {threads} threads, {frames} greedy frames each, "
-                      f"ctx {ctx.tolist()}"}
+                      f"ctx ~ U[64, 640]"}
 
 
-def cpu_baseline(blob, state, frames: int = 48):
-    """The compiled reference (oracle/_ref) decoding from the same ctx-512 state."""
+def cpu_gemv(share: int):
+    """The reference's gemv_par (MOSS_A16 on: row_dot_q8_4x4_actf32) on the single-GEMV
+    shape K=768, N=2304: median of 1000 calls at T = 1 and T = the CPU share."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import REF_SO, RefCpu
+
+    from mosship import moss_format as mf
+    if not os.path.exists(REF_SO):
+        return None
+    rng = np.random.default_rng(42)
+    w = mf.synth_q8x4(rng, 2304, 768).reshape(-1)
+    x = rng.standard_normal(768).astype(np.float16).astype(np.float32)
+    r = RefCpu(a16_mode="decode")
+    out = {}
+    for t in sorted({1, share}):
+        us = r.gemv_median_us(w, 2304, 768, x, threads=t, reps=1000)
+        out[f"T{t}"] = {"us": round(us, 2), "GBps": round(CONFIG0_BYTES / us / 1e3, 2)}
+    return out
+
+
+def cpu_baseline(blob, state, frames: int, share: int):
+    """The compiled reference (oracle/_ref) decoding the same frames from the same
+    ctx-512 state (MOSS_A16=decode, its release setting) at T = 4 (its published
+    setting, README.md:40) and T = the CPU share; the faster is the baseline."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import REF_SO, RefCpu, SampleParams
 
@@ -391,33 +469,70 @@ def cpu_baseline(blob, state, frames: int = 48):
     if not os.path.exists(REF_SO):
         return None
     k, v, hidden, rows = state
-    threads = 4  # the reference's published setting (README.md:40)
     r = RefCpu(a16_mode="decode")
-    m = r.model(blob, threads=threads)
+    runs = {}
     with tempfile.TemporaryDirectory() as td:
         path = os.path.join(td, "ctx512.state")
         with open(path, "wb") as f:
             f.write(mf.write_state(k, v, hidden, rows, mf.fp_weights(blob)))
-        m.load_state(path, rows, ignore_fp=False)
-        p = SampleParams.make(greedy=True, min_frames=frames)
-        m.generate(3, p)  # 3-frame warmup (the reference's protocol)
-        m.load_state(path, rows, ignore_fp=False)
-        t0 = time.perf_counter()
-        out = m.generate(frames, p, timing=True)
-        t1 = time.perf_counter()
-    n = len(out["rows"])
-    t = out["timing"]
-    m.close()
-    cpu_model = _cpu_model_name()
+        for threads in sorted({4, share}):
+            m = r.model(blob, threads=threads)
+            m.load_state(path, rows, ignore_fp=False)
+            p = SampleParams.make(greedy=True, min_frames=frames)
+            m.generate(3, p)  # 3-frame warmup (the reference's protocol)
+            m.load_state(path, rows, ignore_fp=False)
+            t0 = time.perf_counter()
+            out = m.generate(frames, p, timing=True)
+            t1 = time.perf_counter()
+            n = len(out["rows"])
+            t = out["timing"]
+            m.close()
+            runs[threads] = {"ms_per_frame": (t1 - t0) * 1e3 / n, "frames": n,
+                             "global_ms": float(np.mean(t[:-1, 0])) if n > 1 else 0.0,
+                             "local_ms": float(np.mean(t[:, 1]))}
+    best = min(runs, key=lambda th: runs[th]["ms_per_frame"])
+    b = runs[best]
     return {
-        "value": (t1 - t0) * 1e3 / n,
+        "value": round(b["ms_per_frame"], 3),
         "unit": "ms/frame",
-        "cores": threads,
+        "cores": best,
         "kind": "reference",
-        "sample": f"{n} greedy frames from the ctx-512 state, MOSS_A16=decode, {threads} threads, "
-                  f"global {np.mean(t[:-1, 0]) * n / max(n - 1, 1):.2f} + local {np.mean(t[:, 1]):.2f} ms/frame; "
-                  f"host {cpu_model}",
+        "sample": f"{b['frames']} greedy frames from the ctx-512 state (the GPU run's frames), MOSS_A16=decode; "
+                  f"faster of T=" + " and T=".join(str(th) for th in sorted(runs)) + " threads",
+        "by_threads": {str(th): {kk: round(vv, 3) for kk, vv in rr.items()} for th, rr in runs.items()},
     }
+
+
+# Algorithmic bytes of the two launches of a batch-1 greedy frame (fp16 KV):
+#  global step at position p: 12 layers of Q8_0_4X4 weights 90,243,072 + fp32 vectors
+#  485,376 + embedding rows 13,872 + K/V read 36,864 (p + 1) + K/V write 36,864;
+#  local half: 17 local steps x 7,566,336 + 16 audio heads 13,369,344 + the gate's
+#  2 rows and the picks 15,504.
+GLOBAL_FIXED_BYTES = 90_243_072 + 485_376 + 13_872 + 36_864
+LOCAL_BYTES = 17 * 7_566_336 + 13_369_344 + 15_504
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (calibrated as the
+# GEMV's) over `bench.py --mode decode`; None where not measured
+DECODE_TRAFFIC = {"decode_global_kernel": None, "decode_local_kernel": None}
+
+
+def global_bytes(p: int) -> int:
+    return GLOBAL_FIXED_BYTES + 36_864 * (p + 1)
+
+
+def decode_rooflines(d):
+    """Roofline objects of the frame's two kernels from the event-timed run: algorithmic
+    bytes per launch (the global step's averaged over the positions it ran at) over the
+    average launch duration."""
+    p0, n = CTX, d["frames"]
+    gb = float(np.mean([global_bytes(p) for p in range(p0, p0 + n - 1)])) if n > 1 else float(global_bytes(p0))
+    out = {}
+    for name, ms, nbytes in (("decode_global_kernel", d["global_ms_event"], gb),
+                             ("decode_local_kernel", d["local_ms_event"], float(LOCAL_BYTES))):
+        ach = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC[name],
+                     "algo_bytes_per_launch": round(nbytes), "us_per_launch": round(ms * 1e3, 2)}
+    return out
 
 
 def main():
@@ -458,8 +573,10 @@ def main():
         return
     log("decode")
     d = bench_decode(blob, state, args.steps, args.warmup)
+    roof = decode_rooflines(d)
     if args.mode == "decode":
-        print(json.dumps({"decode": d}), flush=True)
+        calibration_copy()
+        print(json.dumps({"decode": d, "rooflines": roof}), flush=True)
         return
     log("gemv roofline")
     g = bench_gemv()
@@ -470,15 +587,32 @@ def main():
     pf16 = bench_prefill(blob, a16=True)
     log("64 streams")
     st = bench_streams(blob)
-    cpu = cpu_pf = cpu_st = cpu_at = None
+    host = host_cpu()
+    cpu = cpu_pf = cpu_at = cpu_gv = None
+    cpu_st = {}
     if not args.no_cpu:
-        log("cpu baseline (reference)")
-        cpu = cpu_baseline(blob, state)
+        share = host["cpu_share"]
+        log(f"cpu baseline (reference), share {share} cores")
+        cpu = cpu_baseline(blob, state, args.steps, share)
+        cpu_gv = cpu_gemv(share)
         cpu_at = cpu_attention()
-        cpu_pf = cpu_prefill(blob)
-        cpu_st = cpu_streams(blob)
-    # global step at position 512: weights + vectors + embed + fp16 KV read/write
-    global_bytes = 90243072 + 485376 + 13872 + 36864 * (CTX + 1) + 36864
+        cpu_pf = cpu_prefill(blob, share)
+        for t in sorted({1, 4}):
+            r = cpu_streams(blob, share, t)
+            if r:
+                cpu_st[f"T{t}"] = r
+    best_st = max(cpu_st.values(), key=lambda r: r["frames_per_s"]) if cpu_st else None
+    # the roofline object is the frame's dominant kernel (the longer of its two launches)
+    dom = max(roof.values(), key=lambda r: r["us_per_launch"])
+    gemv_roof = {
+        "kernel": f"gemv_stream_kernel (fp16 in/out), N={GEMV_N} K={GEMV_K}, weights cycled over "
+                  f"{g['pool_buffers']} buffers (cold)",
+        "bound": "hbm", "achieved": round(g["cold"]["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(g["cold"]["GBps"] / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES,
+        "traffic_note": "bytes/launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated), "
+                        f"{GEMV_TRAFFIC_BYTES / g['algo_bytes']:.3f}x the algorithmic bytes",
+    }
+    end = d["end_position"]
     line = {
         "metric": "LLM decode ms/frame (bs1, ctx 512); frames/s @64 streams; GEMV GB/s",
         "value": round(d["ms_per_frame"], 4),
@@ -492,35 +626,28 @@ def main():
         "vs_baseline": None,
         "dtype": "w8a16 (int8 weights, fp32 activations/accumulation, fp16 KV)",
         "data": "synthetic (seeded random-init weights with the reference's dims; N(0,1) fp16 KV at ctx 512)",
-        "config": {"workload": "LLM decode, batch 1, ctx 512 -> 767, 256 greedy frames, two fused launches per "
-                               "frame (full frame = 17 local steps + 16 heads + end gate + 12-layer global step)",
+        "config": {"workload": f"LLM decode, batch 1, from ctx {CTX}: {d['frames']} greedy frames (positions "
+                               f"{CTX}..{end}), two fused launches per frame (full frame = 17 local steps + "
+                               f"16 heads + end gate + 12-layer global step)",
                    "global_batch": 1, "seq_len": CTX, "parallelism": "none (1 GPU)"},
         "frames_per_s": round(1e3 / d["ms_per_frame"], 1),
         "global_step_ms": round(d["global_ms_event"], 4),
         "local_ms_per_frame": round(d["local_ms_event"], 4),
-        "global_step_GBps": round(global_bytes / (d["global_ms_event"] * 1e-3) / 1e9, 1),
+        "roofline": dom,
+        "roofline_decode": roof,
+        "roofline_gemv": gemv_roof,
         "gemv": {"cold_GBps": round(g["cold"]["GBps"], 1), "warm_GBps": round(g["warm"]["GBps"], 1),
-                 "config0_us": round(g["config0"]["us"], 3), "config0_GBps": round(g["config0"]["GBps"], 1)},
-        "roofline": {
-            "kernel": f"gemv_stream_kernel (fp16 in/out), N={GEMV_N} K={GEMV_K}, weights cycled over "
-                      f"{g['pool_buffers']} buffers (cold)",
-            "bound": "hbm",
-            "achieved": round(g["cold"]["GBps"], 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(g["cold"]["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": GEMV_TRAFFIC_BYTES,
-            "traffic_note": "bytes/launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated), "
-                            f"{GEMV_TRAFFIC_BYTES / g['algo_bytes']:.3f}x the algorithmic bytes",
-        },
+                 "config0_us": round(g["config0"]["us"], 3), "config0_GBps": round(g["config0"]["GBps"], 1),
+                 "config0_timing": g["config0"]["timing"], "cpu_ref": cpu_gv},
         "attention_decode": {"ctx": at, "cpu_ref": cpu_at},
         "prefill_256": {"mode": "w8a8 (the reference's prefill)", "ms": round(pf["ms"], 3),
                         "TOP/s": round(pf["TFLOPs"], 2), "mfma_frac": round(pf["mfma_frac"], 4),
                         "a16_ms": round(pf16["ms"], 3), "a16_mfma_frac": round(pf16["mfma_frac"], 4),
                         "cpu_ref": cpu_pf},
         "streams_64": {"frames_per_s": round(st["frames_per_s"], 1), "ms_per_step": round(st["ms_per_step"], 4),
-                       "global_stack_GBps": round(st["global_stack_GBps"], 1), "cpu_ref": cpu_st,
-                       "vs_cpu": round(st["frames_per_s"] / cpu_st["frames_per_s"], 1) if cpu_st else None},
+                       "global_stack_GBps": round(st["global_stack_GBps"], 1), "cpu_ref": cpu_st or None,
+                       "vs_cpu": round(st["frames_per_s"] / best_st["frames_per_s"], 1) if best_st else None},
+        "host_cpu": host,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -306,6 +306,9 @@ class RefCpu:
         L.ref_pool_create.argtypes = [C.c_int, C.c_int]
         L.ref_pool_destroy.argtypes = [C.c_void_p]
         L.ref_gemv_par.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        L.ref_gemv_par_median_us.restype = C.c_double
+        L.ref_gemv_par_median_us.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                             C.c_int]
         L.ref_gemm_par.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
         L.ref_attention_window.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_int,
                                            C.c_int, _f32p, _f32p, C.c_int]
@@ -368,6 +371,15 @@ class RefCpu:
         if pool is None:
             self.lib.ref_pool_destroy(p)
         return y
+
+    def gemv_median_us(self, w, rows, cols, x, threads=1, reps=1000):
+        """Median time of one gemv_par call (reference thread pool of `threads`)."""
+        w, x = _u8(w), _f32(x)
+        y = np.empty(rows, np.float32)
+        p = self.lib.ref_pool_create(threads, cols)
+        us = self.lib.ref_gemv_par_median_us(p, w.ctypes.data, rows, cols, x.ctypes.data, y.ctypes.data, reps)
+        self.lib.ref_pool_destroy(p)
+        return us
 
     def gemm(self, w, rows, cols, x, threads=1):
         w, x = _u8(w), _f32(x).reshape(-1, cols)

@@ -7,6 +7,8 @@
 // oracle/_ref/libmossref.so.  Nothing in the product links it.
 //
 // Each wrapper names the reference entry point it forwards to.
+#include <chrono>
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -110,6 +112,22 @@ void ref_pool_destroy(void *p) { delete static_cast<RefPool *>(p); }
 // gemv.cpp:245 (gemv_par over a Q8_0_4X4 Matrix)
 void ref_gemv_par(void *p, const void *w, int rows, int cols, const float *x, float *y) {
     gemv_par(q8x4(w, rows, cols), x, y, static_cast<RefPool *>(p)->pool);
+}
+
+// gemv_par timed: `reps` calls after `reps / 10` warm-up calls; returns the
+// median call time in microseconds (the CPU side of the single-GEMV benchmark)
+double ref_gemv_par_median_us(void *p, const void *w, int rows, int cols, const float *x, float *y, int reps) {
+    const Matrix m = q8x4(w, rows, cols);
+    GemvPoolScratch &pool = static_cast<RefPool *>(p)->pool;
+    for (int i = 0; i < reps / 10 + 1; ++i) gemv_par(m, x, y, pool);
+    std::vector<double> t(reps > 0 ? reps : 1);
+    for (auto &ti : t) {
+        const auto t0 = std::chrono::steady_clock::now();
+        gemv_par(m, x, y, pool);
+        ti = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+    }
+    std::nth_element(t.begin(), t.begin() + t.size() / 2, t.end());
+    return t[t.size() / 2];
 }
 
 // gemv.cpp:276 (gemm_par over a Q8_0_4X4 Matrix)
