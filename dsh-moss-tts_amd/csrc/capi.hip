@@ -125,7 +125,7 @@ mh::Batch &batch_of(moss_hip_batch *b) {
 }
 
 moss_hip_llm_options defaults(const moss_hip_llm_options *opt) {
-    moss_hip_llm_options o{0, 0, 0, 1, 0, 0};
+    moss_hip_llm_options o{0, 0, 0, 1, 0, 0, 0};
     if (opt) o = *opt;
     return o;
 }
@@ -384,6 +384,23 @@ int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_d
         const auto pro = x_dtype == MOSS_HIP_F16 ? mh::PRO_F16 : mh::PRO_F32;
         const auto epi = y_dtype == MOSS_HIP_F16 ? mh::EPI_F16 : mh::EPI_F32;
         mh::hip_check(mh::launch_gemv(a, pro, epi, mh::KV_F16, static_cast<hipStream_t>(stream)), "gemv launch");
+    });
+}
+
+int moss_hip_gemv_q8x4_w8a8(const void *w, int rows, int cols, const float *x, float *y, void *stream) {
+    return guard([&] {
+        if (!w || !x || !y) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (rows <= 0 || rows % 4 || cols <= 0 || cols % 256 || cols > 4096)
+            throw Status(MOSS_HIP_EINVAL, "shape must satisfy rows % 4 == 0, cols % 256 == 0, cols <= 4096");
+        mh::GemvArgs a;
+        a.w = static_cast<const uint8_t *>(w);
+        a.rows = rows;
+        a.cols = cols;
+        a.x = x;
+        a.y = y;
+        a.a8 = 1;
+        mh::hip_check(mh::launch_gemv(a, mh::PRO_F32, mh::EPI_F32, mh::KV_F16, static_cast<hipStream_t>(stream)),
+                      "gemv launch");
     });
 }
 

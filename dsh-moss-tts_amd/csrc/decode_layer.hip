@@ -34,6 +34,7 @@
 //   P  b < 192: proj group b (4 waves), partials merged first  -> LL x + attn
 //   M  b < 192: fc_in groups 4b + w, LN2 first                  -> LL h
 //   F  b < 192: fc_out group b (4 waves)                        -> x (memory)
+#include <algorithm>
 #include <type_traits>
 
 #include "mh_gemv.h"
@@ -150,10 +151,13 @@ __device__ __forceinline__ float rawk(const SpanRaw<KV> &r, int c, int e) {  // 
     }
 }
 
-template <int KV>
+// A8: every GEMV in W8A8 (the activation quantised per 32-block in LDS, quant_act_lds),
+// the reference's decode with MOSS_A16 unset (csrc/src/gemv.cpp:23-48,245-274).
+template <int KV, bool A8>
 __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
 #pragma clang fp contract(off)
     __shared__ float act[kFF];                 // GEMV activation
+    __shared__ float da[kFF / 32];             // its block scales (A8)
     __shared__ float xin[kHidden];             // block input (x), the last block's output at the end
     __shared__ float xm[kHidden];              // x after the attention sub-block (fc_out's residual)
     __shared__ float pbuf[kMaxUnits * 66];     // gathered attention partials
@@ -288,8 +292,12 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
 #pragma unroll
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
+            if constexpr (A8) {
+                quant_act_lds(act, da, kHidden);
+                __syncthreads();
+            }
             STAGE_TS(1);
-            const float yv = gs.dot(act, part);
+            const float yv = gs.template dot<A8>(act, part, da);
             const float partner = xshfl<4>(yv);
             if (gs.storer()) {  // bias, RoPE (llm.cpp:234-236), KV write (llm.cpp:224-225)
                 float out = e.apply(r, yv, partner);
@@ -527,8 +535,12 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 }
                 __syncthreads();
             }
+            if constexpr (A8) {
+                quant_act_lds(act, da, kHidden);
+                __syncthreads();
+            }
             STAGE_TS(7);
-            const float yv = gs.dot(act, part);
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
             STAGE_TS(8);
         }
@@ -556,8 +568,12 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
 #pragma unroll
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
+            if constexpr (A8) {
+                quant_act_lds(act, da, kHidden);
+                __syncthreads();
+            }
             STAGE_TS(10);
-            const float yv = gs.dot(act, part);
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
             STAGE_TS(11);
             __syncthreads();  // every wave is done with act before stage F gathers into it
@@ -574,8 +590,12 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 if (t == 0) atomicOr(g.err, 1u);
                 return;
             }
+            if constexpr (A8) {
+                quant_act_lds(act, da, kFF);
+                __syncthreads();
+            }
             STAGE_TS(12);
-            const float yv = gs.dot(act, part);
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) ll_put(LL + kLLO + r, xm[r] + (yv + eb), tag);  // llm.cpp:245
             STAGE_TS(13);
         }
@@ -613,10 +633,17 @@ hipError_t decode_layer_fits(int device, bool *fits) {
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return e;
     int per_cu16 = 0, per_cu32 = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu16, decode_global_kernel<KV_F16>, 256, 0);
-    if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu32, decode_global_kernel<KV_F32>, 256, 0);
-    if (e != hipSuccess) return e;
+    for (int v = 0; v < 2; ++v) {  // the W8A16 and the W8A8 builds
+        int p16 = 0, p32 = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &p16, v ? decode_global_kernel<KV_F16, true> : decode_global_kernel<KV_F16, false>, 256, 0);
+        if (e != hipSuccess) return e;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &p32, v ? decode_global_kernel<KV_F32, true> : decode_global_kernel<KV_F32, false>, 256, 0);
+        if (e != hipSuccess) return e;
+        per_cu16 = v ? std::min(per_cu16, p16) : p16;
+        per_cu32 = v ? std::min(per_cu32, p32) : p32;
+    }
     int per_cu_local = 0;
     e = decode_local_occupancy(&per_cu_local);
     if (e != hipSuccess) return e;
@@ -639,10 +666,17 @@ hipError_t launch_decode_global(const GlobalArgs &a, KvType kv, hipStream_t s) {
         return hipErrorInvalidValue;
     for (int ch = 0; ch < kNVq; ++ch)
         if (!a.aemb[ch]) return hipErrorInvalidValue;
-    if (kv == KV_F16)
-        hipLaunchKernelGGL(decode_global_kernel<KV_F16>, dim3(kLayerGrid), dim3(256), 0, s, a);
-    else
-        hipLaunchKernelGGL(decode_global_kernel<KV_F32>, dim3(kLayerGrid), dim3(256), 0, s, a);
+    if (kv == KV_F16) {
+        if (a.a8)
+            hipLaunchKernelGGL((decode_global_kernel<KV_F16, true>), dim3(kLayerGrid), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_global_kernel<KV_F16, false>), dim3(kLayerGrid), dim3(256), 0, s, a);
+    } else {
+        if (a.a8)
+            hipLaunchKernelGGL((decode_global_kernel<KV_F32, true>), dim3(kLayerGrid), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((decode_global_kernel<KV_F32, false>), dim3(kLayerGrid), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 

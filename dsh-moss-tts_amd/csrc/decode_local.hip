@@ -78,9 +78,12 @@ namespace {
     } while (0)
 #endif
 
+// A8: every GEMV in W8A8 (quant_act_lds), the reference's decode with MOSS_A16 unset.
+template <bool A8>
 __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma clang fp contract(off)
     __shared__ float act[kFF + 1];
+    __shared__ float da[kFF / 32];  // block scales of act (A8)
     __shared__ float xm[kHidden];
     __shared__ float qkv[3 * kHidden];             // q | k | v of this position
     __shared__ float sc[kHeads][kLocalLen + 1];
@@ -163,7 +166,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma unroll
                 for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
                 __syncthreads();
-                const float yv = gs.dot(act, part);
+                if constexpr (A8) {
+                    quant_act_lds(act, da, kHidden);
+                    __syncthreads();
+                }
+                const float yv = gs.template dot<A8>(act, part, da);
                 const float partner = xshfl<4>(yv);
                 if (gs.storer()) ll_put(LL + kLQ + r, e.apply(r, yv, partner), tag);  // k, v cached by stage A
                 __syncthreads();
@@ -324,7 +331,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             }
             if (gs.storer() && with_code)  // lookup_row (llm.cpp:697)
                 eres = q8x4_elem(aemb_in, kHidden / 32, __float_as_int(act[kHidden]), r);
-            const float yv = gs.dot(act, part);
+            if constexpr (A8) {  // act[0, 768) only: the code at act[kHidden] stays
+                quant_act_lds(act, da, kHidden);
+                __syncthreads();
+            }
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
             STAGE_TS(4);
             __syncthreads();  // act is reused by stage F
@@ -353,7 +364,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma unroll
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
-            const float yv = gs.dot(act, part);
+            if constexpr (A8) {
+                quant_act_lds(act, da, kHidden);
+                __syncthreads();
+            }
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
             STAGE_TS(6);
             __syncthreads();  // every wave is done with act before stage F gathers into it
@@ -370,8 +385,12 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 if (t == 0) atomicOr(a.err, 1u);
                 return;
             }
+            if constexpr (A8) {
+                quant_act_lds(act, da, kFF);
+                __syncthreads();
+            }
             STAGE_TS(7);
-            const float yv = gs.dot(act, part);
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) {
                 const float xo = xm[r] + (yv + eb);  // llm.cpp:245
                 a.x_out[r] = xo;
@@ -403,7 +422,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
 #pragma unroll
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
-            const float yv = gs.dot(act, part);
+            if constexpr (A8) {
+                quant_act_lds(act, da, kHidden);
+                __syncthreads();
+            }
+            const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) {
                 logits_out[gs.row()] = yv;
                 if (lpos < a.lpos_last || a.final_pick) ll_put(LL + kLL + gs.row(), yv, tag);  // the next pick
@@ -452,7 +475,12 @@ extern "C" int mh_local_trace_read(unsigned long long *out) {
 #endif
 
 hipError_t decode_local_occupancy(int *per_cu) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_local_kernel, 256, 0);
+    int p16 = 0, p8 = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&p16, decode_local_kernel<false>, 256, 0);
+    if (e != hipSuccess) return e;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&p8, decode_local_kernel<true>, 256, 0);
+    *per_cu = p16 < p8 ? p16 : p8;
+    return e;
 }
 
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s) {
@@ -472,7 +500,10 @@ hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s) {
     if (a.lpos_last > a.lpos && a.lpos_last >= 2 && a.pick && !a.head) return hipErrorInvalidValue;
     if (a.final_pick && (!a.pick || !a.head || a.lpos_last < 1 || !a.counts || !a.forced)) return hipErrorInvalidValue;
     // one more workgroup for the end gate
-    hipLaunchKernelGGL(decode_local_kernel, dim3(kLayerGrid + (a.gate ? 1 : 0)), dim3(256), 0, s, a);
+    if (a.a8)
+        hipLaunchKernelGGL(decode_local_kernel<true>, dim3(kLayerGrid + (a.gate ? 1 : 0)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(decode_local_kernel<false>, dim3(kLayerGrid + (a.gate ? 1 : 0)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

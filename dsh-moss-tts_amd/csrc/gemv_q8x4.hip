@@ -280,11 +280,15 @@ __device__ __forceinline__ void finish_row(const GemvArgs &a, int r, float v, fl
     epi_store<EPI, KV>(a, r, v, partner, epi_load<EPI>(a, r));
 }
 
-template <int PRO, int EPI, int SPLIT, int KV, int NB>
+// A8: W8A8 rows -- the staged activation is quantised per 32-block in LDS
+// (quant_act_lds) and every block sum scaled by fp32(d_w * d_a), as the
+// reference's decode with MOSS_A16 unset (csrc/src/gemv.cpp:229-274).
+template <int PRO, int EPI, int SPLIT, int KV, int NB, bool A8>
 __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     extern __shared__ float act[];
     __shared__ float red[4];
     __shared__ float part[4][4];
+    __shared__ float da[4096 / 32];  // block scales of act (A8)
     // A frame that has ended (state->stop) makes this a no-op.  The flag is read
     // here but tested after the prologue, so its load overlaps the weight and
     // activation loads instead of delaying them (the prologue only writes
@@ -313,6 +317,10 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     stage_activation<PRO>(a, act, red);
     __syncthreads();
     if (stopped) return;
+    if constexpr (A8) {
+        quant_act_lds(act, da, a.cols);
+        __syncthreads();
+    }
 
     for (int gb = gfirst; gb < ngroups; gb += gridDim.x * GPW) {
         const int g = gb + gslot;
@@ -323,7 +331,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
             const uint8_t *grp = a.w + (size_t)g * nb * kBlockBytes;
             for (int base = b0; base < b1; base += 4 * NB) {
                 if (base != b0 || gb != gfirst) load_batch<NB>(grp, base + bl, b1, u, kk, qv, dh);
-                acc = dot_batch<NB>(act, base + bl, b1, j, qv, dh, acc);
+                acc = dot_batch<NB, A8>(act, base + bl, b1, j, qv, dh, acc, da);
             }
         }
         acc = row_lane_sum(acc);
@@ -341,7 +349,7 @@ __global__ __launch_bounds__(256) void gemv_q8x4_kernel(GemvArgs a) {
     }
 }
 
-template <int PRO, int EPI, int SPLIT, int KV>
+template <int PRO, int EPI, int SPLIT, int KV, bool A8>
 hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int ngroups = a.rows / 4;
@@ -350,15 +358,15 @@ hipError_t launch_nb(const GemvArgs &a, int nbatch, hipStream_t s) {
     grid = grid > 4096 ? 4096 : grid;
     const size_t lds = (size_t)a.cols * sizeof(float);
     switch (nbatch) {
-        case 2: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 2>), dim3(grid), dim3(256), lds, s, a); break;
-        case 3: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 3>), dim3(grid), dim3(256), lds, s, a); break;
-        case 6: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 6>), dim3(grid), dim3(256), lds, s, a); break;
-        default: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 8>), dim3(grid), dim3(256), lds, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 2, A8>), dim3(grid), dim3(256), lds, s, a); break;
+        case 3: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 3, A8>), dim3(grid), dim3(256), lds, s, a); break;
+        case 6: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 6, A8>), dim3(grid), dim3(256), lds, s, a); break;
+        default: hipLaunchKernelGGL((gemv_q8x4_kernel<PRO, EPI, SPLIT, KV, 8, A8>), dim3(grid), dim3(256), lds, s, a); break;
     }
     return hipGetLastError();
 }
 
-template <int PRO, int EPI, int KV>
+template <int PRO, int EPI, int KV, bool A8>
 hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     // blocks per wave -> batch size (iterations of 4 blocks), one of 2, 3, 6, 8
@@ -366,9 +374,9 @@ hipError_t launch_split(const GemvArgs &a, int split, hipStream_t s) {
     const int its = (per + 3) / 4;
     const int nbatch = its <= 2 ? 2 : its <= 3 ? 3 : its <= 6 ? 6 : 8;
     switch (split) {
-        case 4: return launch_nb<PRO, EPI, 4, KV>(a, nbatch, s);
-        case 2: return launch_nb<PRO, EPI, 2, KV>(a, nbatch, s);
-        default: return launch_nb<PRO, EPI, 1, KV>(a, nbatch, s);
+        case 4: return launch_nb<PRO, EPI, 4, KV, A8>(a, nbatch, s);
+        case 2: return launch_nb<PRO, EPI, 2, KV, A8>(a, nbatch, s);
+        default: return launch_nb<PRO, EPI, 1, KV, A8>(a, nbatch, s);
     }
 }
 
@@ -419,9 +427,10 @@ __device__ __forceinline__ void issue_unit(const uint8_t *src, uint8_t *slot, in
                                          MH_STREAM_CPOL);
 }
 
-// Partial dot of one unit (24 blocks x 4 rows) from LDS.
+// Partial dot of one unit (24 blocks x 4 rows) from LDS (A8: ds = the unit's block scales).
+template <bool A8>
 __device__ __forceinline__ float unit_dot(const uint8_t *slot, const float *xs, int bl, int u, int kk, int j,
-                                          float acc) {
+                                          float acc, const float *ds) {
 #pragma unroll
     for (int it = 0; it < kUnitBlocks / 4; ++it) {
         const int b = 4 * it + bl;
@@ -438,7 +447,12 @@ __device__ __forceinline__ float unit_dot(const uint8_t *slot, const float *xs, 
         sm = fmaf((float)(int8_t)(q.y >> 8), x1.y, sm);
         sm = fmaf((float)(int8_t)(q.y >> 16), x1.z, sm);
         sm = fmaf((float)(int8_t)(q.y >> 24), x1.w, sm);
-        acc = fmaf(sm, d, acc);
+        if constexpr (A8) {
+            const float scale = d * ds[b];
+            acc = fmaf(sm, scale, acc);
+        } else {
+            acc = fmaf(sm, d, acc);
+        }
     }
     return acc;
 }
@@ -447,8 +461,8 @@ __device__ __forceinline__ float unit_dot(const uint8_t *slot, const float *xs, 
 // with unit t + stages - 1, wait for unit t in `cur`, accumulate it, and on a
 // group's last slice reduce and store.  The restrict-qualified slots let the
 // compiler keep the DMA into `refill` in flight while it reads `cur`.
-template <int EPI, int KV>
-__device__ __forceinline__ void stream_step(const GemvArgs &a, const float *act, int t, int units, int P,
+template <int EPI, int KV, bool A8>
+__device__ __forceinline__ void stream_step(const GemvArgs &a, const float *act, const float *da, int t, int units, int P,
                                             const uint8_t *next_src, uint8_t *__restrict__ refill,
                                             const uint8_t *__restrict__ cur, int g, int ngroups, float &acc) {
     const int lane = threadIdx.x & 63;
@@ -460,7 +474,7 @@ __device__ __forceinline__ void stream_step(const GemvArgs &a, const float *act,
         wait_vmcnt<0>();
     }
     const int slice = t % P;
-    acc = unit_dot(cur, act + slice * kUnitBlocks * 32, bl, u, kk, j, acc);
+    acc = unit_dot<A8>(cur, act + slice * kUnitBlocks * 32, bl, u, kk, j, acc, da + slice * kUnitBlocks);
     if (slice == P - 1) {
         float yv = acc;
         yv = row_lane_sum(yv);
@@ -470,12 +484,13 @@ __device__ __forceinline__ void stream_step(const GemvArgs &a, const float *act,
     }
 }
 
-template <int PRO, int EPI, int KV>
+template <int PRO, int EPI, int KV, bool A8>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs a) {
     constexpr int S = kStreamStages;
     __shared__ __attribute__((aligned(16))) uint8_t ring[S][4][kUnitBytes];
     extern __shared__ float act[];
     __shared__ float red[4];
+    __shared__ float da[4096 / 32];  // block scales of act (A8)
     if (a.state != nullptr && a.state->stop) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nb = a.cols >> 5;
@@ -493,6 +508,10 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs a) {
 
     stage_activation<PRO>(a, act, red);
     __syncthreads();
+    if constexpr (A8) {
+        quant_act_lds(act, da, a.cols);
+        __syncthreads();
+    }
 
     float acc = 0.0f;
     // unrolled by the ring size so every step names its two slots statically
@@ -500,19 +519,19 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < S; ++r) {
             if (t + r >= units) break;
-            stream_step<EPI, KV>(a, act, t + r, units, P, src(t + r + S - 1), ring[(r + S - 1) % S][wave],
+            stream_step<EPI, KV, A8>(a, act, da, t + r, units, P, src(t + r + S - 1), ring[(r + S - 1) % S][wave],
                                  ring[r][wave], gfirst + ((t + r) / P) * gstride, ngroups, acc);
         }
     }
 }
 
-template <int PRO, int EPI, int KV>
+template <int PRO, int EPI, int KV, bool A8>
 hipError_t launch_stream(const GemvArgs &a, hipStream_t s) {
     const int ngroups = a.rows / 4;
     const size_t lds = (size_t)a.cols * sizeof(float);
     int grid = (ngroups + 3) / 4;
     grid = grid > 256 * MH_STREAM_WG_PER_CU ? 256 * MH_STREAM_WG_PER_CU : grid;  // MH_STREAM_WG_PER_CU 4-wave workgroups per CU
-    hipLaunchKernelGGL((gemv_stream_kernel<PRO, EPI, KV>), dim3(grid), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((gemv_stream_kernel<PRO, EPI, KV, A8>), dim3(grid), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
@@ -547,28 +566,43 @@ hipError_t launch_gemv(const GemvArgs &a, Prologue pro, Epilogue epi, KvType kv,
     if (pro == PRO_AMERGE && (!a.attn_part || a.attn_splits <= 0 || a.attn_splits > kMaxMergeSplits))
         return hipErrorInvalidValue;
     if (epi == EPI_QKV && a.rows != 3 * kHidden) return hipErrorInvalidValue;
+    if (a.a8 && a.cols % 256 != 0) return hipErrorInvalidValue;  // quant_act_lds: whole waves per block
     const int split = pick_split(a.rows, a.cols);
     const bool stream = use_stream(a.rows, a.cols);
+#define MH_LAUNCH(P, E, A8)                                                                     \
+    do {                                                                                        \
+        if (stream) {                                                                           \
+            if (E == EPI_QKV && kv == KV_F32) return launch_stream<P, E, KV_F32, A8>(a, s);    \
+            return launch_stream<P, E, KV_F16, A8>(a, s);                                       \
+        }                                                                                       \
+        if (E == EPI_QKV && kv == KV_F32) return launch_split<P, E, KV_F32, A8>(a, split, s);  \
+        return launch_split<P, E, KV_F16, A8>(a, split, s);                                     \
+    } while (0)
+// combinations served in W8A16 only
 #define MH_CASE(P, E)                                                                           \
     if (pro == P && epi == E) {                                                                 \
-        if (stream) {                                                                           \
-            if (E == EPI_QKV && kv == KV_F32) return launch_stream<P, E, KV_F32>(a, s);        \
-            return launch_stream<P, E, KV_F16>(a, s);                                           \
-        }                                                                                       \
-        if (E == EPI_QKV && kv == KV_F32) return launch_split<P, E, KV_F32>(a, split, s);    \
-        return launch_split<P, E, KV_F16>(a, split, s);                                         \
+        if (a.a8) return hipErrorInvalidValue;                                                  \
+        MH_LAUNCH(P, E, false);                                                                 \
     }
-    MH_CASE(PRO_F32, EPI_F32)
+// combinations served in W8A16 or W8A8 (the decode's, and the operator layer's fp32 GEMV)
+#define MH_CASE_A8(P, E)                                                                        \
+    if (pro == P && epi == E) {                                                                 \
+        if (a.a8) MH_LAUNCH(P, E, true);                                                        \
+        MH_LAUNCH(P, E, false);                                                                 \
+    }
+    MH_CASE_A8(PRO_F32, EPI_F32)
     MH_CASE(PRO_F16, EPI_F16)
     MH_CASE(PRO_F16, EPI_F32)
     MH_CASE(PRO_F32, EPI_F16)
-    MH_CASE(PRO_LN, EPI_QKV)
-    MH_CASE(PRO_LN, EPI_GELU)
-    MH_CASE(PRO_F32, EPI_RESID)
-    MH_CASE(PRO_LN, EPI_F32)
-    MH_CASE(PRO_LATTN, EPI_RESID)
-    MH_CASE(PRO_AMERGE, EPI_RESID)
-    MH_CASE(PRO_PICK, EPI_QKV)
+    MH_CASE_A8(PRO_LN, EPI_QKV)
+    MH_CASE_A8(PRO_LN, EPI_GELU)
+    MH_CASE_A8(PRO_F32, EPI_RESID)
+    MH_CASE_A8(PRO_LN, EPI_F32)
+    MH_CASE_A8(PRO_LATTN, EPI_RESID)
+    MH_CASE_A8(PRO_AMERGE, EPI_RESID)
+    MH_CASE_A8(PRO_PICK, EPI_QKV)
+#undef MH_CASE_A8
+#undef MH_LAUNCH
 #undef MH_CASE
     return hipErrorInvalidValue;
 }

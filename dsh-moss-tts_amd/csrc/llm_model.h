@@ -102,6 +102,7 @@ private:
 
     int device_ = 0, max_ctx_ = kMaxCtx, use_graphs_ = 1;
     bool prefill_a16_ = false;  // prefill GEMMs on fp32 activations (else W8A8)
+    int decode_a8_ = 0;         // decode GEMVs in W8A8 (the reference with MOSS_A16 unset), else W8A16
     bool fused_layers_ = false; // global step as one decode_layer launch per layer, local steps as decode_local
     float *qkv_table_ = nullptr;   // [1 + 15 * 1024][2304] local q|k|v of (lpos >= 1, input code)
     void build_qkv_table();

@@ -66,6 +66,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     kv_esize_ = kvt_ == KV_F32 ? 4 : 2;
     use_graphs_ = opt.use_graphs;
     prefill_a16_ = opt.prefill_a16 != 0;
+    decode_a8_ = opt.decode_a8 != 0 ? 1 : 0;
     if (opt.decode_kernels != 0 && opt.decode_kernels != 1) throw Status(MOSS_HIP_EINVAL, "decode_kernels: 0 or 1");
     const uint8_t *b = static_cast<const uint8_t *>(blob);
     auto idx = parse_index(b, bytes);
@@ -267,7 +268,7 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         for (int ch = 0; ch < kNVq; ++ch) g.aemb[ch] = aemb_[ch];
         g.row = row_dev;
         g.lnf_w = lnf_w_; g.lnf_b = lnf_b_; g.hidden = hidden_;
-        g.state = state_; g.ll = ll_; g.err = &state_->ll_err;
+        g.state = state_; g.ll = ll_; g.err = &state_->ll_err; g.a8 = decode_a8_;
         hip_check(launch_decode_global(g, kvt_, s), "decode global step");
         return;
     }
@@ -286,7 +287,7 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         a.bias = L.attn_b; a.q_out = q_;
         a.k_cache = kv_layer(0, l); a.v_cache = kv_layer(1, l); a.ctx_stride = max_ctx_;
         a.rope_cos = rope_; a.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
-        a.pos_ptr = pos; a.state = state_;
+        a.pos_ptr = pos; a.state = state_; a.a8 = decode_a8_;
         hip_check(launch_gemv(a, PRO_LN, EPI_QKV, kvt_, s), "qkv gemv");
 
         AttnArgs t;  // the cache is one page of max_ctx positions; split-KV partials per 64 keys
@@ -297,18 +298,18 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         GemvArgs p;  // the partials are merged in the proj prologue
         p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
         p.attn_part = attn_part_; p.attn_splits = (max_ctx_ + 63) / 64; p.pos_ptr = pos;
-        p.y = x_; p.bias = L.proj_b; p.state = state_;
+        p.y = x_; p.bias = L.proj_b; p.state = state_; p.a8 = decode_a8_;
         hip_check(launch_gemv(p, PRO_AMERGE, EPI_RESID, kvt_, s), "proj gemv");
 
         GemvArgs f1;
         f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;
         f1.x = x_; f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
-        f1.y = mlp_; f1.bias = L.fc_in_b; f1.state = state_;
+        f1.y = mlp_; f1.bias = L.fc_in_b; f1.state = state_; f1.a8 = decode_a8_;
         hip_check(launch_gemv(f1, PRO_LN, EPI_GELU, kvt_, s), "fc_in gemv");
 
         GemvArgs f2;
         f2.w = L.fc_out_w; f2.rows = kHidden; f2.cols = kFF;
-        f2.x = mlp_; f2.y = x_; f2.bias = L.fc_out_b; f2.state = state_;
+        f2.x = mlp_; f2.y = x_; f2.bias = L.fc_out_b; f2.state = state_; f2.a8 = decode_a8_;
         hip_check(launch_gemv(f2, PRO_F32, EPI_RESID, kvt_, s), "fc_out gemv");
     }
     hip_check(launch_layernorm(x_, lnf_w_, lnf_b_, hidden_, state_, 1, s), "ln_f");
@@ -338,6 +339,7 @@ void Model::build_qkv_table() {
         a.rope_cos = rope_ + (size_t)lpos * kRopeHalf;
         a.rope_sin = rope_ + ((size_t)rope_n_ + lpos) * kRopeHalf;
         a.pos_const = 0;
+        a.a8 = decode_a8_;
         hip_check(launch_gemv(a, PRO_LN, EPI_QKV, KV_F32, stream_), "qkv table row");
     };
     try {
@@ -372,7 +374,7 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos, int pic
     a.bias = L.attn_b; a.q_out = q_;
     a.k_cache = lk; a.v_cache = lv; a.ctx_stride = kLocalLen;
     a.rope_cos = rope_; a.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
-    a.pos_const = lpos; a.state = state_;
+    a.pos_const = lpos; a.state = state_; a.a8 = decode_a8_;
     if (pick_ch >= 0) {
         a.pick_logits = logits_ + (size_t)pick_ch * kCodebook;
         a.pick_counts = counts_ + (size_t)pick_ch * kCodebook;
@@ -388,18 +390,18 @@ void Model::enqueue_local_step(hipStream_t s, const float *in, int lpos, int pic
     GemvArgs p;
     p.w = L.proj_w; p.rows = kHidden; p.cols = kHidden;
     p.x = q_; p.k_cache = lk; p.v_cache = lv; p.ctx_stride = kLocalLen; p.pos_const = lpos;
-    p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_;
+    p.y = lres_; p.resid_in = in; p.bias = L.proj_b; p.state = state_; p.a8 = decode_a8_;
     hip_check(launch_gemv(p, PRO_LATTN, EPI_RESID, KV_F32, s), "local proj");
 
     GemvArgs f1;
     f1.w = L.fc_in_w; f1.rows = kFF; f1.cols = kHidden;
     f1.x = lres_; f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
-    f1.y = mlp_; f1.bias = L.fc_in_b; f1.state = state_;
+    f1.y = mlp_; f1.bias = L.fc_in_b; f1.state = state_; f1.a8 = decode_a8_;
     hip_check(launch_gemv(f1, PRO_LN, EPI_GELU, KV_F32, s), "local fc_in");
 
     GemvArgs f2;
     f2.w = L.fc_out_w; f2.rows = kHidden; f2.cols = kFF;
-    f2.x = mlp_; f2.y = lres_; f2.bias = L.fc_out_b; f2.state = state_;
+    f2.x = mlp_; f2.y = lres_; f2.bias = L.fc_out_b; f2.state = state_; f2.a8 = decode_a8_;
     hip_check(launch_gemv(f2, PRO_F32, EPI_RESID, KV_F32, s), "local fc_out");
 }
 
@@ -420,6 +422,7 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
         base.lk = lkv_; base.lv = lkv_ + (size_t)kHeads * kLocalLen * kHeadDim;
         base.rope_cos = rope_; base.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
         base.state = state_; base.ll = ll_; base.err = &state_->ll_err; base.x_out = lres_;
+        base.a8 = decode_a8_;
         for (int ch = 0; ch < kNVq; ++ch) base.aemb[ch] = aemb_[ch];
         base.qkv_table = qkv_table_;
         base.logits = logits_;
@@ -468,7 +471,7 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
         GemvArgs t;
         t.w = wte_; t.rows = kVocab; t.cols = kHidden;
         t.x = lres_; t.ln_w = llnf_w_; t.ln_b = llnf_b_;
-        t.y = text_logits_; t.state = state_;
+        t.y = text_logits_; t.state = state_; t.a8 = decode_a8_;
         hip_check(launch_gemv(t, PRO_LN, EPI_F32, KV_F32, s), "text head");
         hip_check(launch_gate_text(text_logits_, state_, s), "gate");
     } else {
@@ -479,7 +482,7 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
         GemvArgs h;
         h.w = aemb_[ch]; h.rows = kCodebook; h.cols = kHidden;
         h.x = lres_; h.ln_w = llnf_w_; h.ln_b = llnf_b_;
-        h.y = logits_ + (size_t)ch * kCodebook; h.state = state_;
+        h.y = logits_ + (size_t)ch * kCodebook; h.state = state_; h.a8 = decode_a8_;
         hip_check(launch_gemv(h, PRO_LN, EPI_F32, KV_F32, s), "audio head");
         SampleArgs sa;
         sa.logits = logits_ + (size_t)ch * kCodebook;

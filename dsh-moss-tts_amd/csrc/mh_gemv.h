@@ -29,9 +29,13 @@ __device__ __forceinline__ void load_batch(const uint8_t *grp, int first_b, int 
     }
 }
 
-template <int NB>
+// A8: act holds the W8A8 activation (integers as floats, see quant_act_lds) and
+// da its fp32 block scales: the 8-term sum is then an exact integer, and it is
+// scaled by fp32(d_w * d_a), the per-block factor of row_dot_q8_4x4 (reference
+// csrc/src/gemv_avx2.cpp:105-121); only the fp32 summation order differs.
+template <int NB, bool A8 = false>
 __device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1, int j, const uint2 (&qv)[NB],
-                                           const uint16_t (&dh)[NB], float acc) {
+                                           const uint16_t (&dh)[NB], float acc, const float *da = nullptr) {
 #pragma unroll
     for (int it = 0; it < NB; ++it) {
         const int b = first_b + 4 * it;
@@ -47,10 +51,29 @@ __device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1
             s = fmaf((float)(int8_t)(q.y >> 8), x1.y, s);
             s = fmaf((float)(int8_t)(q.y >> 16), x1.z, s);
             s = fmaf((float)(int8_t)(q.y >> 24), x1.w, s);
-            acc = fmaf(s, h2f(dh[it]), acc);
+            if constexpr (A8) {
+                const float scale = h2f(dh[it]) * da[b];
+                acc = fmaf(s, scale, acc);
+            } else {
+                acc = fmaf(s, h2f(dh[it]), acc);
+            }
         }
     }
     return acc;
+}
+
+// The W8A8 activation (quantize_row_q8_0_scaled, reference csrc/src/quant.cpp:28-54,
+// via quantize_activation, quant.cpp:45) in place: act[0, K) becomes its int8 values
+// (as floats, exact) and da[K / 32] the fp32 block scales d = amax / 127.  Called
+// by all 256 threads of the workgroup between two barriers; K % 256 == 0, so each
+// block of 32 values is 32 consecutive lanes of one wave.
+__device__ __forceinline__ void quant_act_lds(float *act, float *da, int K) {
+    for (int i = tix(); i < K; i += 256) {
+        float d;
+        const int q = quant_block32(act[i], &d);
+        act[i] = (float)q;
+        if ((i & 31) == 0) da[i >> 5] = d;
+    }
 }
 
 // Sum of a row's 16 lanes (lanes 16*bl + 4*kk + j for the row kk): every lane

@@ -125,9 +125,11 @@ struct GemvStage {
         const int lane = tix() & 63;
         return ks == 0 && lane < 16 && (lane & 3) == 0;
     }
-    __device__ __forceinline__ float dot(const float *act, float (*part)[4]) const {
+    // A8: act / da as quant_act_lds leaves them (W8A8 row dots)
+    template <bool A8 = false>
+    __device__ __forceinline__ float dot(const float *act, float (*part)[4], const float *da = nullptr) const {
         const int wave = tix() >> 6, lane = tix() & 63, kk = (lane & 15) >> 2, j = lane & 3;
-        float acc = dot_batch<NB>(act, b0 + (lane >> 4), b0 + per, j, qv, dh, 0.0f);
+        float acc = dot_batch<NB, A8>(act, b0 + (lane >> 4), b0 + per, j, qv, dh, 0.0f, da);
         acc = row_lane_sum(acc);
         if constexpr (SPLIT == 1) {
             return acc;

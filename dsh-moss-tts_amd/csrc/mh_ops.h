@@ -62,6 +62,7 @@ struct GemvArgs {
     DevState *pick_state = nullptr;
     float *pick_raw = nullptr;  // workgroup 0 stores the picked aemb row (the step's residual input)
     const DevState *state = nullptr;  // when non-null, the kernel is a no-op once state->stop is set
+    int a8 = 0;  // W8A8: the staged activation quantised per 32-block (decode prologues only)
 };
 
 // Launch y = W x with the given prologue/epilogue; kv selects the KV cache type for EPI_QKV.
@@ -323,6 +324,7 @@ struct GlobalArgs {
     DevState *state = nullptr;          // pos (read, then bumped by workgroup 0), stop
     uint64_t *ll = nullptr;             // kLayerWords exchange words
     unsigned *err = nullptr;            // set when a wait runs out
+    int a8 = 0;                         // W8A8 GEMVs (activations quantised per 32-block), else W8A16
 };
 hipError_t launch_decode_global(const GlobalArgs &a, KvType kv, hipStream_t s);
 
@@ -353,6 +355,7 @@ struct LocalArgs {
     const uint8_t *wte = nullptr;
     int final_pick = 0;                // 1: after the last position, the greedy pick of its channel, the
                                        // frame's code counts, row[0] = slot and frame + 1 (sample_kernel's work)
+    int a8 = 0;                        // W8A8 GEMVs (activations quantised per 32-block), else W8A16
 };
 hipError_t decode_local_occupancy(int *per_cu);
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s);

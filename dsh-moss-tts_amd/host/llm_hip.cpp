@@ -84,10 +84,15 @@ bool LlmModel::load(const std::string &path, std::string *err) {
         if (err) *err = "weights file too small or unreadable: " + path;
         return false;
     }
-    moss_hip_llm_options opt{0, 0, 0, 1, 0, 0};
+    moss_hip_llm_options opt{0, 0, 0, 1, 0, 0, 0};
     if (const char *d = std::getenv("MOSS_HIP_DEVICE")) opt.device = std::atoi(d);
-    // the reference's switch (gemv.cpp:23-48): MOSS_A16=1/all keeps fp32 activations in the prefill too
-    if (const char *a16 = std::getenv("MOSS_A16")) opt.prefill_a16 = (a16[0] == '1' || std::strcmp(a16, "all") == 0);
+    // the reference's switch (gemv.cpp:23-48), read as it reads it: unset (or any other value) =
+    // W8A8 prefill and decode; "decode" = W8A8 prefill, W8A16 decode; "1" / "all" = W8A16 both
+    const char *a16 = std::getenv("MOSS_A16");
+    const int mode = a16 == nullptr ? 0 : (a16[0] == '1' || std::strcmp(a16, "all") == 0) ? 1
+                                          : std::strcmp(a16, "decode") == 0 ? 2 : 0;
+    opt.prefill_a16 = mode == 1;
+    opt.decode_a8 = mode == 0;
     if (const char *kv = std::getenv("MOSS_HIP_KV")) opt.kv_dtype = std::strcmp(kv, "fp32") == 0 ? 1 : 0;
     moss_hip_llm *h = nullptr;
     if (moss_hip_llm_create(data.data(), data.size(), &opt, &h) != MOSS_HIP_OK) {

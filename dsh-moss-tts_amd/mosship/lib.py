@@ -28,7 +28,7 @@ EXPORTED = [
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
     "moss_hip_attn_decode_noalloc",
-    "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8",
+    "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8", "moss_hip_gemv_q8x4_w8a8",
 ]
 
 
@@ -40,7 +40,7 @@ class MossHipError(RuntimeError):
 
 class Options(C.Structure):
     _fields_ = [("device", C.c_int), ("max_ctx", C.c_int), ("kv_dtype", C.c_int), ("use_graphs", C.c_int),
-                ("prefill_a16", C.c_int), ("decode_kernels", C.c_int)]
+                ("prefill_a16", C.c_int), ("decode_kernels", C.c_int), ("decode_a8", C.c_int)]
 
 
 class SampleParams(C.Structure):
@@ -91,6 +91,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_llm_kv_export.argtypes = [vp, i32, vp, vp]
     L.moss_hip_llm_kv_import.argtypes = [vp, i32, vp, vp, vp]
     L.moss_hip_gemv_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp]
+    L.moss_hip_gemv_q8x4_w8a8.argtypes = [vp, i32, i32, vp, vp, vp]
     L.moss_hip_gemm_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
     L.moss_hip_quantize_rows.argtypes = [vp, i32, i32, vp, vp, vp]
     L.moss_hip_gemm_q8x4_w8a8.argtypes = [vp, i32, i32, vp, vp, i32, vp, vp]
@@ -136,6 +137,12 @@ def gemv_q8x4(w, rows: int, cols: int, x, y, stream=None) -> None:
                                     C.c_void_p(y.data_ptr()), dt[y.dtype], _stream(stream)))
 
 
+def gemv_q8x4_w8a8(w, rows: int, cols: int, x, y, stream=None) -> None:
+    """y = W x with x quantised per 32-block (the reference's W8A8 gemv_par); x, y fp32."""
+    check(load().moss_hip_gemv_q8x4_w8a8(C.c_void_p(w.data_ptr()), rows, cols, C.c_void_p(x.data_ptr()),
+                                         C.c_void_p(y.data_ptr()), _stream(stream)))
+
+
 def gemm_q8x4(w, rows: int, cols: int, x, m: int, y, stream=None) -> None:
     """Y[m][rows] = X[m][cols] W^T on the matrix cores (fp32 x / y device tensors)."""
     check(load().moss_hip_gemm_q8x4(C.c_void_p(w.data_ptr()), rows, cols, C.c_void_p(x.data_ptr()), m,
@@ -176,12 +183,12 @@ class HipLLM:
     """Python view of the GPU LlmModel (moss_hip_llm_*)."""
 
     def __init__(self, blob: bytes, device: int = 0, max_ctx: int = 0, kv_fp32: bool = False, graphs: bool = True,
-                 prefill_a16: bool = False, per_op: bool = False):
+                 prefill_a16: bool = False, per_op: bool = False, decode_a8: bool = False):
         L = self.L = load()
         self._h = C.c_void_p()
         buf = np.frombuffer(blob, dtype=np.uint8)
         opt = Options(device, max_ctx, 1 if kv_fp32 else 0, 1 if graphs else 0, 1 if prefill_a16 else 0,
-                      1 if per_op else 0)
+                      1 if per_op else 0, 1 if decode_a8 else 0)
         check(L.moss_hip_llm_create(_ptr(buf), buf.size, C.byref(opt), C.byref(self._h)))
 
     def close(self):

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 4
+#define MOSS_HIP_ABI_VERSION 5
 
 enum {
     MOSS_HIP_OK = 0,
@@ -64,6 +64,11 @@ typedef struct {
                            another; 1 = one launch per operator (GEMV / attention / head), replayed as
                            hipGraphs.  Both follow the reference's arithmetic per value; they differ in
                            fp32 summation order only. */
+    int decode_a8;  /* decode activations (csrc/src/gemv.cpp:23-48, 229-274): 0 = W8A16, fp32 activations
+                       (the reference with MOSS_A16=decode/1/all, the release setting); 1 = W8A8, each decode
+                       GEMV's input quantised per 32-block (quantize_activation, quant.cpp:45) and the
+                       int8 row dot of row_dot_q8_4x4 (gemv_avx2.cpp:105-121) -- the reference's default,
+                       MOSS_A16 unset.  The end gate is W8A8 in both (llm.cpp:274-315). */
 } moss_hip_llm_options;
 
 /* SampleParams (csrc/include/moss/sampler.h:8-22), field for field. */
@@ -178,6 +183,12 @@ enum { MOSS_HIP_F32 = 0, MOSS_HIP_F16 = 1 };
  * x_dtype / y_dtype: MOSS_HIP_F32 or MOSS_HIP_F16.  rows % 4 == 0, cols % 128 == 0, cols <= 4096. */
 int moss_hip_gemv_q8x4(const void *w, int rows, int cols, const void *x, int x_dtype, void *y, int y_dtype,
                        void *stream);
+
+/* y[rows] = W[rows][cols] x in W8A8 -- gemv_par with MOSS_A16 unset (csrc/src/gemv.cpp:229-274): x
+ * quantised once per 32-block (quantize_activation, csrc/src/quant.cpp:45-54), each row the int8 row
+ * dot of row_dot_q8_4x4 (csrc/src/gemv_avx2.cpp:105-121).  x, y fp32; rows % 4 == 0,
+ * cols % 256 == 0, cols <= 4096. */
+int moss_hip_gemv_q8x4_w8a8(const void *w, int rows, int cols, const float *x, float *y, void *stream);
 
 /* Y[m][rows] = X[m][cols] W^T on the matrix cores -- gemm_par (csrc/include/moss/gemv.h:54,
  * csrc/src/gemv.cpp:276-309) in its A16 mode.  x, y fp32; rows % 16 == 0, cols % 32 == 0. */

@@ -462,6 +462,7 @@ struct mo_model {
     mo_vec lnf_w, lnf_b, llnf_w, llnf_b;
     mo_mat wte, aemb[MO_NVQ];
     int max_ctx, kv_f16;
+    int decode_a8;                   /* decode GEMVs in W8A8 (MOSS_A16 unset), else W8A16 */
     float *gk, *gv;                  /* [12][max_ctx][768] */
     float *lk, *lv;                  /* [17][768] */
     float *cos_t, *sin_t;            /* [max_ctx][384] */
@@ -599,6 +600,26 @@ void mo_model_destroy(mo_model *m) {
 }
 
 void mo_model_set_kv_f16(mo_model *m, int on) { m->kv_f16 = on; }
+void mo_model_set_decode_a8(mo_model *m, int on) { m->decode_a8 = on; }
+
+/* gemv_par in decode (reference csrc/src/gemv.cpp:229-274): W8A16 rows
+ * (row_dot_q8_4x4_actf32) when act16_enabled(), else the activation quantised
+ * once per 32-block (quantize_activation, quant.cpp:45-54) and W8A8 rows
+ * (row_dot_q8_4x4, gemv_avx2.cpp:105-121) -- the reference's default mode. */
+static void decode_gemv(const mo_model *m, const uint8_t *w, int rows, int cols, const float *x, float *y) {
+    if (!m->decode_a8) {
+        mo_gemv_a16(w, rows, cols, x, y);
+        return;
+    }
+    int nb = cols / 32;
+    int8_t *q = (int8_t *)malloc((size_t)cols);
+    float *d = (float *)malloc(sizeof(float) * (size_t)nb);
+    mo_quantize_row_q8(x, cols, q, NULL, d);
+#pragma omp parallel for schedule(static) if (rows >= 512)
+    for (int r = 0; r < rows; ++r) y[r] = mo_row_dot_w8a8(w + (size_t)(r / 4) * nb * 136, nb, r % 4, q, d);
+    free(q);
+    free(d);
+}
 void mo_model_reset(mo_model *m) { m->pos = 0; }
 int mo_model_position(const mo_model *m) { return m->pos; }
 const float *mo_model_hidden(const mo_model *m) { return m->hidden; }
@@ -652,7 +673,7 @@ static float kv_round(const mo_model *m, float v) {
 static void block_forward(mo_model *m, const mo_layer *L, int local, int layer, int pos, float *x, float *qkv,
                           float *att, float *mlp) {
     mo_layernorm(x, L->ln1_w.data, L->ln1_b.data, m->ln);
-    mo_gemv_a16(L->attn_w.data, 3 * MO_HIDDEN, MO_HIDDEN, m->ln, qkv);
+    decode_gemv(m, L->attn_w.data, 3 * MO_HIDDEN, MO_HIDDEN, m->ln, qkv);
     for (int i = 0; i < 3 * MO_HIDDEN; ++i) qkv[i] += L->attn_b.data[i];
     mo_rope_apply(qkv, pos, m->cos_t, m->sin_t);
     mo_rope_apply(qkv + MO_HIDDEN, pos, m->cos_t, m->sin_t);
@@ -663,12 +684,12 @@ static void block_forward(mo_model *m, const mo_layer *L, int local, int layer, 
         vc[(size_t)pos * MO_HIDDEN + i] = local ? qkv[2 * MO_HIDDEN + i] : kv_round(m, qkv[2 * MO_HIDDEN + i]);
     }
     mo_attention_core(kc, vc, MO_HIDDEN, pos + 1, qkv, att, m->scores);
-    mo_gemv_a16(L->proj_w.data, MO_HIDDEN, MO_HIDDEN, att, m->res);
+    decode_gemv(m, L->proj_w.data, MO_HIDDEN, MO_HIDDEN, att, m->res);
     for (int i = 0; i < MO_HIDDEN; ++i) x[i] += m->res[i] + L->proj_b.data[i];
     mo_layernorm(x, L->ln2_w.data, L->ln2_b.data, m->ln);
-    mo_gemv_a16(L->fc_in_w.data, MO_FF, MO_HIDDEN, m->ln, mlp);
+    decode_gemv(m, L->fc_in_w.data, MO_FF, MO_HIDDEN, m->ln, mlp);
     for (int i = 0; i < MO_FF; ++i) mlp[i] = mo_gelu_new(mlp[i] + L->fc_in_b.data[i]);
-    mo_gemv_a16(L->fc_out_w.data, MO_HIDDEN, MO_FF, mlp, m->res);
+    decode_gemv(m, L->fc_out_w.data, MO_HIDDEN, MO_FF, mlp, m->res);
     for (int i = 0; i < MO_HIDDEN; ++i) x[i] += m->res[i] + L->fc_out_b.data[i];
 }
 
@@ -692,13 +713,12 @@ void mo_model_local_step(mo_model *m, const float *in, float *out) {
 
 /* reference csrc/src/llm.cpp:268-270 */
 void mo_model_audio_logits(mo_model *m, int ch, const float *hidden, float *logits) {
-    mo_gemv_a16(m->aemb[ch].data, MO_CODEBOOK, MO_HIDDEN, hidden, logits);
+    decode_gemv(m, m->aemb[ch].data, MO_CODEBOOK, MO_HIDDEN, hidden, logits);
 }
 
-/* reference csrc/src/llm.cpp:266 (text_logits: gemv_par over wte; A16 in the
- * release decode mode) */
+/* reference csrc/src/llm.cpp:266 (text_logits: gemv_par over wte) */
 void mo_model_text_logits(mo_model *m, const float *hidden, float *logits) {
-    mo_gemv_a16(m->wte.data, MO_VOCAB, MO_HIDDEN, hidden, logits);
+    decode_gemv(m, m->wte.data, MO_VOCAB, MO_HIDDEN, hidden, logits);
 }
 
 /* reference csrc/src/llm.cpp:274-315 (Q8_0_4X4 branch: W8A8 AVX2 row dot on

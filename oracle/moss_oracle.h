@@ -98,6 +98,9 @@ void mo_model_destroy(mo_model *m);
 /* kv_f16 != 0: global K/V are rounded to fp16 when written (emulates an fp16 KV cache;
  * the 17-position local cache stays fp32) */
 void mo_model_set_kv_f16(mo_model *m, int on);
+/* on != 0: decode GEMVs (global and local blocks, audio and text heads) in W8A8, the
+ * reference with MOSS_A16 unset (gemv.cpp:23-48,229-274); 0 (default): W8A16 */
+void mo_model_set_decode_a8(mo_model *m, int on);
 void mo_model_reset(mo_model *m);
 int mo_model_position(const mo_model *m);
 const float *mo_model_hidden(const mo_model *m);

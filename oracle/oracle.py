@@ -90,6 +90,7 @@ class Oracle:
         L.mo_model_create.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_char_p]
         L.mo_model_destroy.argtypes = [C.c_void_p]
         L.mo_model_set_kv_f16.argtypes = [C.c_void_p, C.c_int]
+        L.mo_model_set_decode_a8.argtypes = [C.c_void_p, C.c_int]
         L.mo_model_reset.argtypes = [C.c_void_p]
         L.mo_model_position.restype = C.c_int
         L.mo_model_position.argtypes = [C.c_void_p]
@@ -192,12 +193,13 @@ class Oracle:
                                         prev_a.ctypes.data if prev_a.size else None, prev_a.size, C.byref(st),
                                         scratch)
 
-    def model(self, blob: bytes, max_ctx: int = 768, kv_f16: bool = False) -> "OracleModel":
-        return OracleModel(self, blob, max_ctx, kv_f16)
+    def model(self, blob: bytes, max_ctx: int = 768, kv_f16: bool = False, decode_a8: bool = False) -> "OracleModel":
+        """decode_a8: decode GEMVs in W8A8 (the reference with MOSS_A16 unset), else W8A16."""
+        return OracleModel(self, blob, max_ctx, kv_f16, decode_a8)
 
 
 class OracleModel:
-    def __init__(self, o: Oracle, blob: bytes, max_ctx: int, kv_f16: bool):
+    def __init__(self, o: Oracle, blob: bytes, max_ctx: int, kv_f16: bool, decode_a8: bool = False):
         self.o, self.lib = o, o.lib
         self._blob = C.create_string_buffer(bytes(blob), len(blob))
         err = C.create_string_buffer(256)
@@ -205,6 +207,7 @@ class OracleModel:
         if not self.h:
             raise RuntimeError(err.value.decode())
         self.lib.mo_model_set_kv_f16(self.h, int(kv_f16))
+        self.lib.mo_model_set_decode_a8(self.h, int(decode_a8))
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     L = lib.load()
     missing = [s for s in declared_symbols() if not hasattr(L, s)]
     assert not missing, missing
-    assert L.moss_hip_abi_version() == 4
+    assert L.moss_hip_abi_version() == 5
 
 
 def test_error_paths_without_gpu():

@@ -72,6 +72,28 @@ def test_gemv_large_n_sampled(torch_gpu, oracle):
     assert np.isfinite(got).all()
 
 
+@pytest.mark.parametrize("rows,cols", [(2304, 768), (768, 3072), (3072, 768), (1024, 768), (8, 256), (16384, 768)])
+def test_gemv_w8a8_vs_oracle(torch_gpu, oracle, rows, cols):
+    """The W8A8 GEMV (the reference's gemv_par with MOSS_A16 unset; the register kernel
+    below 8192 rows, the LDS-streaming one from 8192, e.g. the text head): the activation
+    quantisation is bit-exact and every block's integer dot exact, so only the fp32
+    summation order differs from the oracle's AVX2-order W8A8 rows (<= 1e-5), while the
+    W8A16 product of the same input is much farther away."""
+    torch = torch_gpu
+    rng = np.random.default_rng(rows + cols)
+    w = mf.synth_q8x4(rng, rows, cols)
+    x = (rng.standard_normal(cols) * 2).astype(np.float32)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    lib.gemv_q8x4_w8a8(_dev(torch, w.reshape(-1)), rows, cols, _dev(torch, x), y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    ref = oracle.gemm(w, rows, cols, x[None], a16=False)[0]
+    a16 = oracle.gemv(w, rows, cols, x)
+    print(f"w8a8 gemv {rows}x{cols}: max rel {max_rel(got, ref):.2e} (vs w8a16 {max_rel(a16, ref):.2e})", flush=True)
+    assert max_rel(got, ref) <= 1e-5
+    assert max_rel(a16, ref) > 100 * max(max_rel(got, ref), 1e-7)
+
+
 def test_dequant_rows_bit_exact(torch_gpu, oracle):
     torch = torch_gpu
     rng = np.random.default_rng(11)

@@ -1,10 +1,15 @@
 """Randomised bit-exact agreement of the C oracle with the compiled reference (CPU;
 skipped where oracle/_ref was not built)."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
+from conftest import ROOT
 
 from mosship import moss_format as mf
-from oracle import SampleParams
+from oracle import REF_SO, SampleParams
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
@@ -93,3 +98,58 @@ def test_gate_dump_mode_bit_exact(oracle, ref, golden_model, tmp_path):
         l_end, l_slot, am_o, av = go["gate"][f]
         assert int(fr) == f and int(am) == int(am_o)
         assert f"{av - l_slot:.4f}" == am_slot and f"{l_slot - l_end:.4f}" == slot_end
+
+
+# The reference in its default activation mode (MOSS_A16 unset: W8A8 decode and
+# prefill, gemv.cpp:23-48).  The mode is read once per process, so it runs in a
+# child process; it writes its outputs for the parent to compare.
+_A8_CHILD = """
+import sys, numpy as np
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+from oracle import RefCpu, SampleParams
+r = RefCpu(a16_mode="off")
+assert r.lib.ref_act16_enabled() == 0
+blob = open(sys.argv[3], "rb").read()
+rows = np.load(sys.argv[4])
+forced = np.load(sys.argv[5])
+m = r.model(blob, threads=3)
+m.prefill(rows)
+p = SampleParams.make(greedy=True, repetition_penalty=1.2, min_frames=6)
+g = m.generate(6, p)["rows"]
+h1 = m.hidden().copy()
+f = m.generate(4, p, forced=forced)["rows"]
+np.savez(sys.argv[6], gen=g, hidden_gen=h1, forced=f, hidden=m.hidden())
+"""
+
+
+def test_w8a8_decode_bit_exact(oracle, golden_model, tmp_path):
+    """The oracle's decode_a8 mode (every decode GEMV quantises its input per 32-block
+    and runs the W8A8 row dot, audio heads included) against the reference run with
+    MOSS_A16 unset: prefill, 6 greedy frames with the 1.2 penalty, 4 teacher-forced
+    frames -- rows and hidden states bit-identical."""
+    if not os.path.exists(REF_SO):
+        pytest.skip("oracle/_ref/libmossref.so not built here")
+    blob, _ = golden_model
+    rng = np.random.default_rng(21)
+    rows = mf.text_rows(rng.integers(0, mf.VOCAB, 24))
+    rows[6:12, 1:] = rng.integers(0, 1024, (6, 16))
+    forced = np.concatenate([np.full((4, 1), mf.SLOT), rng.integers(0, 1024, (4, 16))], axis=1).astype(np.int32)
+    paths = [str(tmp_path / n) for n in ("m.moss", "rows.npy", "forced.npy", "out.npz")]
+    open(paths[0], "wb").write(blob)
+    np.save(paths[1], rows)
+    np.save(paths[2], forced)
+    subprocess.run([sys.executable, "-c", _A8_CHILD, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "dsh-moss-tts_amd"),
+                    *paths], check=True, timeout=300)
+    ref = np.load(paths[3])
+    o = oracle.model(blob, decode_a8=True)
+    o.prefill(rows)
+    p = SampleParams.make(greedy=True, repetition_penalty=1.2, min_frames=6)
+    assert np.array_equal(o.generate(6, p)["rows"], ref["gen"])
+    assert np.array_equal(o.hidden(), ref["hidden_gen"])
+    assert np.array_equal(o.generate(4, p, forced=forced)["rows"], ref["forced"])
+    assert np.array_equal(o.hidden(), ref["hidden"])
+    # the W8A16 decode of the same state differs: the mode switch reaches the decode GEMVs
+    o16 = oracle.model(blob)
+    o16.prefill(rows)
+    o16.generate(6, p)
+    assert not np.array_equal(o16.hidden(), ref["hidden_gen"])
