@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "batch_model.h"
+#include "codec.h"
 
 using mh::Status;
 
@@ -18,6 +19,10 @@ struct moss_hip_llm {
 
 struct moss_hip_batch {
     mh::Batch *impl;
+};
+
+struct moss_hip_codec {
+    mh::Codec *impl;
 };
 
 namespace {
@@ -124,6 +129,25 @@ mh::Batch &batch_of(moss_hip_batch *b) {
     return *b->impl;
 }
 
+mh::Codec &codec_of(moss_hip_codec *c) {
+    if (c == nullptr || c->impl == nullptr) throw Status(MOSS_HIP_EINVAL, "null codec handle");
+    return *c->impl;
+}
+
+std::vector<uint8_t> read_file(const char *path) {
+    if (path == nullptr) throw Status(MOSS_HIP_EINVAL, "null path");
+    std::FILE *f = std::fopen(path, "rb");
+    if (!f) throw Status(MOSS_HIP_EINVAL, std::string("cannot open weights file: ") + path);
+    std::fseek(f, 0, SEEK_END);
+    const long size = std::ftell(f);
+    std::fseek(f, 0, SEEK_SET);
+    std::vector<uint8_t> data(size > 0 ? (size_t)size : 0);
+    const size_t got = data.empty() ? 0 : std::fread(data.data(), 1, data.size(), f);
+    std::fclose(f);
+    if (size <= 16 || got != data.size()) throw Status(MOSS_HIP_EFORMAT, std::string("short weights file: ") + path);
+    return data;
+}
+
 moss_hip_llm_options defaults(const moss_hip_llm_options *opt) {
     moss_hip_llm_options o{0, 0, 0, 1, 0, 0, 0};
     if (opt) o = *opt;
@@ -155,15 +179,7 @@ int moss_hip_llm_create(const void *blob, size_t bytes, const moss_hip_llm_optio
 int moss_hip_llm_create_from_file(const char *path, const moss_hip_llm_options *opt, moss_hip_llm **out) {
     return guard([&] {
         if (path == nullptr || out == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");
-        std::FILE *f = std::fopen(path, "rb");
-        if (!f) throw Status(MOSS_HIP_EINVAL, std::string("cannot open weights file: ") + path);
-        std::fseek(f, 0, SEEK_END);
-        const long size = std::ftell(f);
-        std::fseek(f, 0, SEEK_SET);
-        std::vector<uint8_t> data(size > 0 ? (size_t)size : 0);
-        const size_t got = data.empty() ? 0 : std::fread(data.data(), 1, data.size(), f);
-        std::fclose(f);
-        if (size <= 16 || got != data.size()) throw Status(MOSS_HIP_EFORMAT, std::string("short weights file: ") + path);
+        const std::vector<uint8_t> data = read_file(path);
         const int rc = moss_hip_llm_create(data.data(), data.size(), opt, out);
         if (rc != MOSS_HIP_OK) throw Status(rc, g_err);
     });
@@ -471,6 +487,67 @@ int moss_hip_attn_decode_noalloc(const float *q, const void *k_cache, const void
             throw Status(MOSS_HIP_EINVAL, "moss_hip_attn_decode_noalloc: at most 16 heads (its scratch is sized for 16)");
         attn_decode(q, k_cache, v_cache, kv_dtype, heads, ctx_stride, n_keys, out, out_dtype, stream,
                     [](hipStream_t, int) { return noalloc_scratch(); });
+    });
+}
+
+int moss_hip_codec_create(const void *blob, size_t bytes, const moss_hip_codec_options *opt, moss_hip_codec **out) {
+    return guard([&] {
+        if (out == nullptr || blob == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");
+        *out = nullptr;
+        moss_hip_codec_options o{};
+        if (opt) o = *opt;
+        auto *h = new moss_hip_codec{nullptr};
+        try {
+            h->impl = new mh::Codec(blob, bytes, o);
+        } catch (...) {
+            delete h;
+            throw;
+        }
+        *out = h;
+    });
+}
+
+int moss_hip_codec_create_from_file(const char *path, const moss_hip_codec_options *opt, moss_hip_codec **out) {
+    return guard([&] {
+        if (out == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");
+        const std::vector<uint8_t> data = read_file(path);
+        const int rc = moss_hip_codec_create(data.data(), data.size(), opt, out);
+        if (rc != MOSS_HIP_OK) throw Status(rc, g_err);
+    });
+}
+
+void moss_hip_codec_destroy(moss_hip_codec *c) {
+    if (!c) return;
+    delete c->impl;
+    delete c;
+}
+
+int moss_hip_codec_samples_per_frame(const moss_hip_codec *c) { return (c && c->impl) ? c->impl->samples_per_frame() : -1; }
+
+int moss_hip_codec_reset_stream(moss_hip_codec *c) {
+    return guard([&] { codec_of(c).reset_stream(); });
+}
+
+int moss_hip_codec_decode_chunk(moss_hip_codec *c, const int32_t *codes, int frames, float *out) {
+    return guard([&] {
+        if (!out) throw Status(MOSS_HIP_EINVAL, "null output");
+        codec_of(c).decode_chunk(codes, frames, out);
+    });
+}
+
+int moss_hip_codec_decode(moss_hip_codec *c, const int32_t *codes, int frames, float *out) {
+    return guard([&] {
+        if (!out) throw Status(MOSS_HIP_EINVAL, "null output");
+        codec_of(c).decode(codes, frames, out);
+    });
+}
+
+double moss_hip_codec_last_ms(const moss_hip_codec *c) { return (c && c->impl) ? c->impl->last_ms() : -1.0; }
+
+int moss_hip_codec_stage_ms(const moss_hip_codec *c, double out4[4]) {
+    return guard([&] {
+        if (c == nullptr || c->impl == nullptr || out4 == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");
+        for (int i = 0; i < 4; ++i) out4[i] = c->impl->stage_ms()[i];
     });
 }
 

@@ -10,6 +10,7 @@
 #include <array>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/moss_hip.h"
@@ -23,6 +24,16 @@ struct Status : std::runtime_error {
 };
 
 void hip_check(hipError_t e, const char *what);
+
+// One tensor of a .moss v1 index (reference csrc/src/weights.cpp:27-125).
+struct MossEntry {
+    uint8_t dtype = 0, ndim = 0;
+    uint32_t dims[3] = {0, 0, 0};
+    uint64_t off = 0, nbytes = 0;
+};
+// name -> entry; throws Status(EFORMAT) on a malformed index
+std::unordered_map<std::string, MossEntry> parse_moss_index(const uint8_t *blob, size_t bytes);
+bool is_vector(const MossEntry &e);
 
 // SampleParams of the C ABI -> the device copy.  Greedy as sample_token decides
 // it (sampler.cpp:23: greedy || top_k == 1).

@@ -16,31 +16,23 @@ void hip_check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw Status(MOSS_HIP_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-namespace {
-
-struct Entry {
-    uint8_t dtype = 0, ndim = 0;
-    uint32_t dims[3] = {0, 0, 0};
-    uint64_t off = 0, nbytes = 0;
-};
-
 // .moss v1 index (reference csrc/src/weights.cpp:27-125): "MOSW", u32 version = 1,
 // u32 n; 80-byte entries: name[48], u8 dtype, u8 ndim, u32 dims[3] @52, u64 offset
 // @64, u64 nbytes @72.
-std::unordered_map<std::string, Entry> parse_index(const uint8_t *blob, size_t bytes) {
+std::unordered_map<std::string, MossEntry> parse_moss_index(const uint8_t *blob, size_t bytes) {
     if (bytes < 16 || std::memcmp(blob, "MOSW", 4) != 0) throw Status(MOSS_HIP_EFORMAT, "not a .moss file (bad magic)");
     uint32_t version = 0, n = 0;
     std::memcpy(&version, blob + 4, 4);
     std::memcpy(&n, blob + 8, 4);
     if (version != 1) throw Status(MOSS_HIP_EFORMAT, "unsupported .moss version " + std::to_string(version));
     if (16 + (size_t)n * 80 > bytes) throw Status(MOSS_HIP_EFORMAT, ".moss index truncated");
-    std::unordered_map<std::string, Entry> out;
+    std::unordered_map<std::string, MossEntry> out;
     for (uint32_t i = 0; i < n; ++i) {
         const uint8_t *e = blob + 16 + (size_t)i * 80;
         char name[49];
         std::memcpy(name, e, 48);
         name[48] = 0;
-        Entry en;
+        MossEntry en;
         en.dtype = e[48];
         en.ndim = e[49];
         std::memcpy(en.dims, e + 52, 12);
@@ -52,7 +44,9 @@ std::unordered_map<std::string, Entry> parse_index(const uint8_t *blob, size_t b
     return out;
 }
 
-bool is_vector(const Entry &e) { return e.ndim == 1 || (e.dims[0] == 1 && e.dims[2] == 1); }
+bool is_vector(const MossEntry &e) { return e.ndim == 1 || (e.dims[0] == 1 && e.dims[2] == 1); }
+
+namespace {
 
 constexpr size_t kStateRowOff = offsetof(DevState, row);
 
@@ -69,7 +63,7 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     decode_a8_ = opt.decode_a8 != 0 ? 1 : 0;
     if (opt.decode_kernels != 0 && opt.decode_kernels != 1) throw Status(MOSS_HIP_EINVAL, "decode_kernels: 0 or 1");
     const uint8_t *b = static_cast<const uint8_t *>(blob);
-    auto idx = parse_index(b, bytes);
+    auto idx = parse_moss_index(b, bytes);
 
     // Resolve every tensor LlmModel::load needs (llm.cpp:44-70) before touching the GPU.
     std::unordered_map<std::string, uint64_t> off;

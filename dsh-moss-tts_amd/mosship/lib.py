@@ -29,6 +29,9 @@ EXPORTED = [
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
     "moss_hip_attn_decode_noalloc",
     "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8", "moss_hip_gemv_q8x4_w8a8",
+    "moss_hip_codec_create", "moss_hip_codec_create_from_file", "moss_hip_codec_destroy",
+    "moss_hip_codec_samples_per_frame", "moss_hip_codec_reset_stream", "moss_hip_codec_decode_chunk",
+    "moss_hip_codec_decode", "moss_hip_codec_last_ms", "moss_hip_codec_stage_ms",
 ]
 
 
@@ -41,6 +44,11 @@ class MossHipError(RuntimeError):
 class Options(C.Structure):
     _fields_ = [("device", C.c_int), ("max_ctx", C.c_int), ("kv_dtype", C.c_int), ("use_graphs", C.c_int),
                 ("prefill_a16", C.c_int), ("decode_kernels", C.c_int), ("decode_a8", C.c_int)]
+
+
+class CodecOptions(C.Structure):
+    """moss_hip_codec_options."""
+    _fields_ = [("device", C.c_int), ("max_chunk_frames", C.c_int), ("contexts", C.c_int * 4), ("eager", C.c_int)]
 
 
 class SampleParams(C.Structure):
@@ -107,6 +115,17 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
     L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
     L.moss_hip_attn_decode_noalloc.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
+    L.moss_hip_codec_create.argtypes = [vp, C.c_size_t, C.POINTER(CodecOptions), C.POINTER(vp)]
+    L.moss_hip_codec_create_from_file.argtypes = [C.c_char_p, C.POINTER(CodecOptions), C.POINTER(vp)]
+    L.moss_hip_codec_destroy.argtypes = [vp]
+    L.moss_hip_codec_destroy.restype = None
+    L.moss_hip_codec_samples_per_frame.argtypes = [vp]
+    L.moss_hip_codec_reset_stream.argtypes = [vp]
+    L.moss_hip_codec_decode_chunk.argtypes = [vp, vp, i32, vp]
+    L.moss_hip_codec_decode.argtypes = [vp, vp, i32, vp]
+    L.moss_hip_codec_last_ms.argtypes = [vp]
+    L.moss_hip_codec_last_ms.restype = C.c_double
+    L.moss_hip_codec_stage_ms.argtypes = [vp, C.POINTER(C.c_double)]
     _lib = L
     return L
 
@@ -326,3 +345,55 @@ class HipBatch:
         check(self.L.moss_hip_batch_generate(self._h, n_streams, frames, C.byref(params),
                                              None if sd is None else _ptr(sd), _ptr(out), _ptr(nf), C.byref(ms)))
         return {"rows": out[:frames], "frames": nf, "ms": ms.value}
+
+
+class HipCodec:
+    """The GPU audio codec decoder (moss::AudioDecoder, csrc/include/moss/decoder.h:14-83).
+
+    codes: int array [16][frames] (quantizer-major) in [0, 1024); results are float32 arrays
+    of frames * samples_per_frame interleaved stereo samples."""
+
+    def __init__(self, blob: bytes, max_chunk_frames: int = 0, contexts=(0, 0, 0, 0), eager: bool = False,
+                 device: int = 0):
+        L = load()
+        o = CodecOptions(device, max_chunk_frames, (C.c_int * 4)(*contexts), int(eager))
+        h = C.c_void_p()
+        self._blob = np.frombuffer(blob, dtype=np.uint8)
+        check(L.moss_hip_codec_create(_ptr(self._blob), len(blob), C.byref(o), C.byref(h)))
+        self._h = h
+        self.samples_per_frame = L.moss_hip_codec_samples_per_frame(h)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            load().moss_hip_codec_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def _run(self, fn, codes):
+        c = np.ascontiguousarray(codes, dtype=np.int32)
+        if c.ndim != 2 or c.shape[0] != 16:
+            raise ValueError("codes must be [16][frames]")
+        out = np.empty(c.shape[1] * self.samples_per_frame, np.float32)
+        check(fn(self._h, _ptr(c), c.shape[1], _ptr(out)))
+        return out
+
+    def reset_stream(self) -> None:
+        check(load().moss_hip_codec_reset_stream(self._h))
+
+    def decode_chunk(self, codes) -> np.ndarray:
+        return self._run(load().moss_hip_codec_decode_chunk, codes)
+
+    def decode(self, codes) -> np.ndarray:
+        return self._run(load().moss_hip_codec_decode, codes)
+
+    @property
+    def last_ms(self) -> float:
+        return load().moss_hip_codec_last_ms(self._h)
+
+    @property
+    def stage_ms(self):
+        out = (C.c_double * 4)()
+        check(load().moss_hip_codec_stage_ms(self._h, out))
+        return list(out)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 5
+#define MOSS_HIP_ABI_VERSION 6
 
 enum {
     MOSS_HIP_OK = 0,
@@ -232,6 +232,46 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
  * replays) race: serialise them. */
 int moss_hip_attn_decode_noalloc(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
                                  int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
+
+/* ---- Audio codec decoder (codes -> 48 kHz stereo PCM) --------------------------------
+ * The GPU replacement of moss::AudioDecoder (reference csrc/include/moss/decoder.h:14-83,
+ * csrc/src/decoder.cpp:26-281): the MOSS-Audio-Tokenizer-Nano decoder of a decoder .moss
+ * (decoder_f16.moss: fp16 matrices, fp32 vectors and codebooks).  A host-side
+ * moss::AudioDecoder with the reference's public surface sits on top
+ * (dsh-moss-tts_amd/host/moss/decoder.h, host/decoder_hip.cpp).  Codes are
+ * quantizer-major [16][frames] int32 in [0, 1024); output is frames * 7680 interleaved
+ * stereo float samples (L, R, L, R, ...).  Same threading rule as the model handle. */
+typedef struct moss_hip_codec moss_hip_codec;
+
+typedef struct {
+    int device;           /* HIP device ordinal */
+    int max_chunk_frames; /* a chunk is run in pieces of at most this many frames; 0 = 32.  Sizes the
+                             activation buffers and the K/V rings (window + 32 * this positions at the last
+                             stage).  Results do not depend on it beyond fp32 rounding. */
+    int contexts[4];      /* per-stage attention windows in positions; 0 = the reference's 500, 800, 1200, 1600
+                             (decoder.cpp:21; other values are for tests of the window) */
+    int eager;            /* 0 = decode_chunk replays a hipGraph per piece size (default); 1 = direct launches */
+} moss_hip_codec_options;
+
+/* AudioDecoder::AudioDecoder + load (decoder.h:19-21, decoder.cpp:26-70): parses the file,
+ * checks every tensor the reference loads, uploads them, allocates the stream state.
+ * opt may be NULL (defaults).  Matrices must be F16 (dtype 0) or F32 (dtype 3), their
+ * column counts multiples of 32 and row counts multiples of 16. */
+int moss_hip_codec_create(const void *blob, size_t bytes, const moss_hip_codec_options *opt, moss_hip_codec **out);
+int moss_hip_codec_create_from_file(const char *path, const moss_hip_codec_options *opt, moss_hip_codec **out);
+void moss_hip_codec_destroy(moss_hip_codec *c);
+int moss_hip_codec_samples_per_frame(const moss_hip_codec *c); /* 7680 for the release decoder */
+/* AudioDecoder::reset_stream (decoder.cpp:105-115): positions back to 0, rings emptied. */
+int moss_hip_codec_reset_stream(moss_hip_codec *c);
+/* AudioDecoder::decode_chunk (decoder.cpp:203-221): the next `frames` frames of the stream
+ * (every layer attends to its cached keys of earlier chunks within its window); out receives
+ * frames * samples_per_frame floats.  Codes outside [0, 1024) -> EINVAL, nothing run. */
+int moss_hip_codec_decode_chunk(moss_hip_codec *c, const int32_t *codes, int frames, float *out);
+/* AudioDecoder::decode (decoder.cpp:247-281): a whole utterance from position 0, on a state
+ * of its own (the stream is untouched); sets last_ms and the four stage times. */
+int moss_hip_codec_decode(moss_hip_codec *c, const int32_t *codes, int frames, float *out);
+double moss_hip_codec_last_ms(const moss_hip_codec *c);             /* decoder.h:31 */
+int moss_hip_codec_stage_ms(const moss_hip_codec *c, double out4[4]); /* decoder.h:32 */
 
 #ifdef __cplusplus
 }

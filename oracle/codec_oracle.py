@@ -149,8 +149,11 @@ def decode(blob_or_weights, codes, windows=cf.CONTEXTS):
 class Stream:
     """Streaming decode (decoder.cpp:100-221): chunks in order, state per stage/layer."""
 
-    def __init__(self, blob_or_weights):
+    def __init__(self, blob_or_weights, contexts=cf.CONTEXTS):
+        """`contexts`: per-stage windows (the reference's by default; others for tests of
+        the window, as decode's `windows`)."""
         self.w = load(blob_or_weights) if isinstance(blob_or_weights, (bytes, bytearray)) else blob_or_weights
+        self.contexts = tuple(contexts)
         self.offset = [0] * len(cf.STAGES)
         self.cache = [[{"k": np.zeros((0, cf.D_MODEL)), "v": np.zeros((0, cf.D_MODEL)),
                         "pos": np.zeros(0, np.int64)} for _ in range(nl)] for nl in cf.LAYERS]
@@ -158,7 +161,7 @@ class Stream:
     def chunk(self, codes):
         w = self.w
         x = quantize_front(w, np.asarray(codes))
-        for si, (s, p, nl, context) in enumerate(zip(cf.STAGES, cf.PATCHES, cf.LAYERS, cf.CONTEXTS)):
+        for si, (s, p, nl, context) in enumerate(zip(cf.STAGES, cf.PATCHES, cf.LAYERS, self.contexts)):
             x = patch(x, p)
             y = x @ w[f"d{s}.in.w"].T
             pos = self.offset[si] + np.arange(y.shape[0])

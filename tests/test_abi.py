@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     L = lib.load()
     missing = [s for s in declared_symbols() if not hasattr(L, s)]
     assert not missing, missing
-    assert L.moss_hip_abi_version() == 5
+    assert L.moss_hip_abi_version() == 6
 
 
 def test_error_paths_without_gpu():
@@ -33,3 +33,6 @@ def test_error_paths_without_gpu():
     assert b"null" in L.moss_hip_last_error()
     assert L.moss_hip_llm_global_step(None, None) == lib.EINVAL
     assert L.moss_hip_llm_position(None) == -1
+    assert L.moss_hip_codec_create(None, 0, None, ctypes.byref(h)) == lib.EINVAL
+    assert L.moss_hip_codec_decode_chunk(None, None, 1, None) == lib.EINVAL
+    assert L.moss_hip_codec_samples_per_frame(None) == -1
