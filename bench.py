@@ -32,8 +32,12 @@ the 2.5 PFLOP/s fp16 peak) and 64 streams with contexts ~ U[64, 1024] decoded
 128 frames in lock-step (aggregate frames/s), each next to the reference on the
 host cores.
 
+The audio codec decoder (decode_chunk, the engine's 8-frame chunks on a stream
+past every window; ms/frame and the real-time factor, 80 ms of audio per frame)
+is reported beside the reference AudioDecoder on min(6, share) host threads.
+
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
-                       [--mode full|gemv|attn|decode|prefill|streams]
+                       [--mode full|gemv|attn|decode|prefill|streams|codec]
 """
 from __future__ import annotations
 
@@ -318,6 +322,84 @@ def bench_streams(blob, steps: int = STREAM_STEPS):
             "ms_per_step": out["ms"] / steps, "global_stack_GBps": step_bytes / (out["ms"] / steps * 1e-3) / 1e9}
 
 
+CODEC_WARM_FRAMES = 130   # fills every stage's window (d1: 500 positions = 125 frames)
+CODEC_CHUNK = 8           # the engine's default chunk_frames (engine.h:35)
+CODEC_CHUNKS = 16
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def codec_flops(blob, frames: int) -> float:
+    """Algorithmic flops of `frames` frames of the codec decoder at steady state (every
+    window full): the GEMMs (2 flops per multiply-add) and the windowed attention (QK^T and
+    PV: 2 x 2 flops per query, key and channel)."""
+    from mosship import codec_format as cf
+    from mosship.moss_format import read_moss_index
+    idx = read_moss_index(blob)
+    dims = {n: (r, c) for n, (_, r, c, _, _) in idx.items()}
+    f = frames * (cf.NQ * cf.Z_DIM * cf.CB_DIM * 2 + 2 * dims["q.out.w"][0] * dims["q.out.w"][1])
+    rows = frames
+    for s, p, nl, w in zip(cf.STAGES, cf.PATCHES, cf.LAYERS, cf.CONTEXTS):
+        rows *= p
+        f += 2 * rows * (dims[f"d{s}.in.w"][0] * dims[f"d{s}.in.w"][1] + dims[f"d{s}.out.w"][0] * dims[f"d{s}.out.w"][1])
+        for n in range(nl):
+            lp = f"d{s}.l{n}."
+            macs = sum(dims[lp + m][0] * dims[lp + m][1] for m in ("attn.w", "proj.w", "f1.w", "f2.w"))
+            f += 2 * rows * macs + 4 * rows * w * cf.D_MODEL
+    return float(f)
+
+
+def bench_codec(chunks: int = CODEC_CHUNKS):
+    """Streaming codec decode (decoder.cpp:203-221) on the GPU: a stream warmed past every
+    stage's window, then `chunks` chunks of 8 frames through decode_chunk (codes from the
+    host, samples back to the host, one hipGraph replay per chunk), timed on the host."""
+    from mosship import HipCodec
+    from mosship import codec_format as cf
+    from mosship.moss_format import DT_F16
+    blob = cf.synth_codec(seed=3, dtype=DT_F16)
+    rng = np.random.default_rng(5)
+    c = HipCodec(blob)
+    c.reset_stream()
+    c.decode_chunk(rng.integers(0, cf.CB_SIZE, (cf.NQ, CODEC_WARM_FRAMES)))
+    codes = [rng.integers(0, cf.CB_SIZE, (cf.NQ, CODEC_CHUNK)).astype(np.int32) for _ in range(chunks)]
+    c.decode_chunk(codes[0])  # graph for 8-frame pieces captured
+    t0 = time.perf_counter()
+    for cc in codes:
+        c.decode_chunk(cc)
+    ms = (time.perf_counter() - t0) * 1e3 / chunks
+    # whole-utterance decode of 64 frames (the reference's decode(), stage times from events)
+    c.decode(rng.integers(0, cf.CB_SIZE, (cf.NQ, 64)))
+    whole = {"frames": 64, "ms": round(c.last_ms, 3), "stage_ms": [round(x, 3) for x in c.stage_ms]}
+    c.close()
+    fl = codec_flops(blob, CODEC_CHUNK)
+    tfs = fl / (ms * 1e-3) / 1e12
+    return {"chunk_frames": CODEC_CHUNK, "ms_per_chunk": round(ms, 4), "ms_per_frame": round(ms / CODEC_CHUNK, 4),
+            "rtf": round(ms / CODEC_CHUNK / 80.0, 5), "gflop_per_chunk": round(fl / 1e9, 3),
+            "TFLOPs": round(tfs, 2), "fp32_mfma_frac": round(tfs / FP32_MFMA_PEAK_TFLOPS, 4), "whole_decode": whole,
+            "blob": blob}
+
+
+def cpu_codec(blob, threads: int, chunks: int = 4):
+    """The reference AudioDecoder (oracle/_ref) on the same protocol: the stream warmed
+    past every window, then `chunks` chunks of 8 frames, `threads` threads."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import RefCpu, RefDecoder
+    from mosship import codec_format as cf
+    rng = np.random.default_rng(5)
+    d = RefDecoder(RefCpu(a16_mode="decode"), blob, threads=threads)
+    try:
+        d.reset_stream()
+        d.decode_chunk(rng.integers(0, cf.CB_SIZE, (cf.NQ, CODEC_WARM_FRAMES)))
+        codes = [rng.integers(0, cf.CB_SIZE, (cf.NQ, CODEC_CHUNK)).astype(np.int32) for _ in range(chunks)]
+        t0 = time.perf_counter()
+        for cc in codes:
+            d.decode_chunk(cc)
+        ms = (time.perf_counter() - t0) * 1e3 / chunks
+    finally:
+        d.close()
+    return {"ms_per_frame": round(ms / CODEC_CHUNK, 3), "threads": threads,
+            "sample": f"{chunks} chunks of {CODEC_CHUNK} frames after {CODEC_WARM_FRAMES} warm-up frames"}
+
+
 def host_cpu():
     """The host's CPU as lscpu reports it, and the share of it this process may use:
     the smallest of the physical cores, the CPUs in its affinity mask, its cgroup
@@ -541,7 +623,8 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams"], default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec"],
+                    default="full")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -560,6 +643,11 @@ def main():
         return
     if args.mode == "attn":
         print(json.dumps({"attention_decode": bench_attention()}), flush=True)
+        return
+    if args.mode == "codec":
+        cd = bench_codec()
+        cd.pop("blob")
+        print(json.dumps({"codec": cd}), flush=True)
         return
 
     log("generating synthetic model + ctx-512 state")
@@ -587,8 +675,11 @@ def main():
     pf16 = bench_prefill(blob, a16=True)
     log("64 streams")
     st = bench_streams(blob)
+    log("codec decoder")
+    cd = bench_codec()
+    cblob = cd.pop("blob")
     host = host_cpu()
-    cpu = cpu_pf = cpu_at = cpu_gv = None
+    cpu = cpu_pf = cpu_at = cpu_gv = cpu_cd = None
     cpu_st = {}
     if not args.no_cpu:
         share = host["cpu_share"]
@@ -597,6 +688,7 @@ def main():
         cpu_gv = cpu_gemv(share)
         cpu_at = cpu_attention()
         cpu_pf = cpu_prefill(blob, share)
+        cpu_cd = cpu_codec(cblob, min(6, share))
         for t in sorted({1, 4}):
             r = cpu_streams(blob, share, t)
             if r:
@@ -647,6 +739,8 @@ def main():
         "streams_64": {"frames_per_s": round(st["frames_per_s"], 1), "ms_per_step": round(st["ms_per_step"], 4),
                        "global_stack_GBps": round(st["global_stack_GBps"], 1), "cpu_ref": cpu_st or None,
                        "vs_cpu": round(st["frames_per_s"] / best_st["frames_per_s"], 1) if best_st else None},
+        "codec": dict(cd, cpu_ref=cpu_cd,
+                      vs_cpu=round(cpu_cd["ms_per_frame"] / cd["ms_per_frame"], 1) if cpu_cd else None),
         "host_cpu": host,
         "cpu_baseline": cpu,
     }

@@ -28,9 +28,6 @@ __device__ __forceinline__ float exp_f(float x) {  // e^x; e^-inf = 0
     return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
-constexpr int KC = 256;       // contraction columns staged per pass
-constexpr int AST = KC + 4;   // LDS row stride (floats): rows start 4 banks apart
-
 // 8 consecutive weights of one row, raw (fp16: one 16-byte load; fp32: two).
 template <int WF32>
 struct W8 {
@@ -59,152 +56,160 @@ struct W8 {
     }
 };
 
-// Stage rows m0..m0+15 of the activation source, columns k0..k0+kn, into As (zeros
-// past row M).
-template <int PRO>
-__device__ __forceinline__ void stage_a(const CodecGemmArgs &g, float *As, int m0, int k0, int kn, int t) {
-    if constexpr (PRO == CPRO_ROWS) {
-        const int q4 = kn >> 2;
-        for (int i = t; i < 16 * q4; i += 256) {
-            const int r = i / q4, c4 = i - r * q4, m = m0 + r;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < g.M) v = *reinterpret_cast<const float4 *>(g.a + (size_t)m * g.lda + k0 + 4 * c4);
-            *reinterpret_cast<float4 *>(As + r * AST + 4 * c4) = v;
-        }
-    } else if constexpr (PRO == CPRO_LN) {
-        // audio_layernorm (audio_layer.cpp:17-28): two-pass mean / variance over 256, eps 1e-5
-        const int lane = t & 63, wave = t >> 6;
-        const float4 w = *reinterpret_cast<const float4 *>(g.ln_w + 4 * lane);
-        const float4 b = *reinterpret_cast<const float4 *>(g.ln_b + 4 * lane);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r = 4 * wave + j, m = m0 + r;
-            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < g.M) {  // uniform over the wave
-                const float4 x = *reinterpret_cast<const float4 *>(g.a + (size_t)m * g.lda + 4 * lane);
-                const float mean = wave_sum((x.x + x.y) + (x.z + x.w)) / 256.0f;
-                const float d0 = x.x - mean, d1 = x.y - mean, d2 = x.z - mean, d3 = x.w - mean;
-                const float var = wave_sum((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3)) / 256.0f;
-                const float inv = 1.0f / sqrtf(var + 1e-5f);
-                o = make_float4(d0 * inv * w.x + b.x, d1 * inv * w.y + b.y, d2 * inv * w.z + b.z, d3 * inv * w.w + b.w);
-            }
-            *reinterpret_cast<float4 *>(As + r * AST + 4 * lane) = o;
-        }
-    } else {
-        // merge of the split-KV partials: sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s
-        for (int i = t; i < 16 * 64; i += 256) {
-            const int r = i >> 6, c4 = i & 63, h = c4 >> 4, m = m0 + r;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < g.M) {
-                float mx = -INFINITY;
-                for (int s = 0; s < g.splits; ++s) mx = fmaxf(mx, g.st[((size_t)s * g.M + m) * kCodecHeads + h].x);
-                float den = 0.f;
-                for (int s = 0; s < g.splits; ++s) {
-                    const float2 st = g.st[((size_t)s * g.M + m) * kCodecHeads + h];
-                    const float f = exp_f(st.x - mx);
-                    den += f * st.y;
-                    const float4 o = *reinterpret_cast<const float4 *>(g.o + ((size_t)s * g.M + m) * kCodecDModel + 4 * c4);
-                    v.x += f * o.x;
-                    v.y += f * o.y;
-                    v.z += f * o.z;
-                    v.w += f * o.w;
-                }
-                const float inv = 1.0f / den;
-                v = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
-            }
-            *reinterpret_cast<float4 *>(As + r * AST + 4 * c4) = v;
-        }
-    }
-}
+// Y[m][n] = sum_k A[m][k] W[n][k] over a 16-row x 16-column tile.  The contraction is
+// cut into chunks of 32 columns; wave w takes chunks [w nch/4, (w+1) nch/4) of every
+// round of 1024 columns and reads its A and W straight from global memory (each lane
+// 8 consecutive columns of one A row and one W row per chunk, all of the wave's chunks in
+// flight before the first MFMA); the 4 partial tiles are summed in LDS and thread t
+// finishes element (t / 16, t % 16).  Prologues transform A as it is loaded:
+// CPRO_LN with per-row (mean, 1/std) from LDS, CPRO_MERGE with wave w = head w.
+constexpr int kWaveChunks = 8;  // chunks of 32 per wave per round (rounds of 1024 columns)
 
-// Y[m][n] = sum_k A[m][k] W[n][k] over a 16-row x 64-column tile: wave w owns columns
-// 16w..16w+15 over the whole contraction, A comes from LDS, W from global memory
-// (a pass's 8 chunks of 32 columns are all in flight before its A is staged).
 template <int PRO, int EPI, int WF32>
 __global__ __launch_bounds__(256) void codec_gemm_kernel(const CodecGemmArgs g) {
-    __shared__ __align__(16) float As[16 * AST];
+    __shared__ float red[4][256];
+    __shared__ float2 rowst[16];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, col = lane & 15, grp = lane >> 4;
-    const int m0 = blockIdx.y * 16;
-    const int n = blockIdx.x * 64 + wave * 16 + col;
-    const bool nvalid = n < g.N;  // N % 16 == 0: whole waves are in or out
-    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < g.K; k0 += KC) {
-        const int kn = min(KC, g.K - k0);  // multiple of 32
-        const int nch = kn >> 5;
-        W8<WF32> wr[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            if (nvalid && c < nch)
-                wr[c].load(g.w, (size_t)n * g.K + k0 + 32 * c + 8 * grp);
-            else
-                wr[c].zero();
+    const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+    const int am = m0 + col;        // A row this lane feeds
+    const bool avalid = am < g.M;
+    const int n = n0 + col;          // W row this lane feeds (N % 16 == 0: always valid)
+
+    // CPRO_MERGE: this lane's (row am, head = wave) split weights e^(m_s - M) / sum_s e^(m_s - M) l_s
+    float mx = 0.f, inv_den = 0.f;
+    if constexpr (PRO == CPRO_MERGE) {
+        if (avalid) {
+            mx = -INFINITY;
+            for (int s = 0; s < g.splits; ++s) mx = fmaxf(mx, g.st[((size_t)s * g.M + am) * kCodecHeads + wave].x);
+            float den = 0.f;
+            for (int s = 0; s < g.splits; ++s) {
+                const float2 st = g.st[((size_t)s * g.M + am) * kCodecHeads + wave];
+                den += exp_f(st.x - mx) * st.y;
+            }
+            inv_den = 1.0f / den;
         }
-        stage_a<PRO>(g, As, m0, k0, kn, t);
-        __syncthreads();
+    }
+
+    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < g.K; k0 += 32 * 4 * kWaveChunks) {
+        const int nch = min(4 * kWaveChunks, (g.K - k0) >> 5);
+        const int c0 = wave * nch / 4, c1 = (wave + 1) * nch / 4;
+        float4 av[kWaveChunks][2];
+        W8<WF32> wr[kWaveChunks];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            if (c < nch) {
-                const float4 a0 = *reinterpret_cast<const float4 *>(As + col * AST + 32 * c + 8 * grp);
-                const float4 a1 = *reinterpret_cast<const float4 *>(As + col * AST + 32 * c + 8 * grp + 4);
-                acc0 = mfma4(a0.x, wr[c].get(0), acc0);
-                acc1 = mfma4(a0.y, wr[c].get(1), acc1);
-                acc0 = mfma4(a0.z, wr[c].get(2), acc0);
-                acc1 = mfma4(a0.w, wr[c].get(3), acc1);
-                acc0 = mfma4(a1.x, wr[c].get(4), acc0);
-                acc1 = mfma4(a1.y, wr[c].get(5), acc1);
-                acc0 = mfma4(a1.z, wr[c].get(6), acc0);
-                acc1 = mfma4(a1.w, wr[c].get(7), acc1);
+        for (int c = 0; c < kWaveChunks; ++c) {
+            const int kk = k0 + 32 * (c0 + c) + 8 * grp;
+            if (c0 + c < c1) {
+                wr[c].load(g.w, (size_t)n * g.K + kk);
+                if constexpr (PRO == CPRO_MERGE) {
+                    av[c][0] = av[c][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (avalid) {
+                        for (int s = 0; s < g.splits; ++s) {
+                            const float2 st = g.st[((size_t)s * g.M + am) * kCodecHeads + wave];
+                            const float f = exp_f(st.x - mx);
+                            const float4 *o = reinterpret_cast<const float4 *>(g.o + ((size_t)s * g.M + am) * kCodecDModel + kk);
+                            const float4 o0 = o[0], o1 = o[1];
+                            av[c][0].x += f * o0.x;
+                            av[c][0].y += f * o0.y;
+                            av[c][0].z += f * o0.z;
+                            av[c][0].w += f * o0.w;
+                            av[c][1].x += f * o1.x;
+                            av[c][1].y += f * o1.y;
+                            av[c][1].z += f * o1.z;
+                            av[c][1].w += f * o1.w;
+                        }
+                    }
+                } else {
+                    const float4 *src = reinterpret_cast<const float4 *>(g.a + (size_t)(avalid ? am : 0) * g.lda + kk);
+                    av[c][0] = avalid ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    av[c][1] = avalid ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            } else {
+                wr[c].zero();
+                av[c][0] = av[c][1] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
-        __syncthreads();
+        if constexpr (PRO == CPRO_LN) {  // K == 256: one round; the loads above are in flight
+            // audio_layernorm (audio_layer.cpp:17-28): two-pass mean / variance over 256, eps 1e-5
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 4 * wave + j, m = m0 + r;
+                if (m < g.M) {  // uniform over the wave
+                    const float4 x = *reinterpret_cast<const float4 *>(g.a + (size_t)m * g.lda + 4 * lane);
+                    const float mean = wave_sum((x.x + x.y) + (x.z + x.w)) / 256.0f;
+                    const float d0 = x.x - mean, d1 = x.y - mean, d2 = x.z - mean, d3 = x.w - mean;
+                    const float var = wave_sum((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3)) / 256.0f;
+                    if (lane == 0) rowst[r] = make_float2(mean, 1.0f / sqrtf(var + 1e-5f));
+                } else if (lane == 0) {
+                    rowst[r] = make_float2(0.f, 0.f);
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int c = 0; c < kWaveChunks; ++c) {
+            if (c0 + c < c1) {
+                float a[8] = {av[c][0].x, av[c][0].y, av[c][0].z, av[c][0].w,
+                              av[c][1].x, av[c][1].y, av[c][1].z, av[c][1].w};
+                if constexpr (PRO == CPRO_LN) {
+                    const int kk = k0 + 32 * (c0 + c) + 8 * grp;
+                    const float2 rs = rowst[col];
+                    const float4 w0 = *reinterpret_cast<const float4 *>(g.ln_w + kk);
+                    const float4 w1 = *reinterpret_cast<const float4 *>(g.ln_w + kk + 4);
+                    const float4 b0 = *reinterpret_cast<const float4 *>(g.ln_b + kk);
+                    const float4 b1 = *reinterpret_cast<const float4 *>(g.ln_b + kk + 4);
+                    const float lw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                    const float lb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) a[i] = avalid ? (a[i] - rs.x) * rs.y * lw[i] + lb[i] : 0.f;
+                } else if constexpr (PRO == CPRO_MERGE) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) a[i] *= inv_den;
+                }
+                acc0 = mfma4(a[0], wr[c].get(0), acc0);
+                acc1 = mfma4(a[1], wr[c].get(1), acc1);
+                acc0 = mfma4(a[2], wr[c].get(2), acc0);
+                acc1 = mfma4(a[3], wr[c].get(3), acc1);
+                acc0 = mfma4(a[4], wr[c].get(4), acc0);
+                acc1 = mfma4(a[5], wr[c].get(5), acc1);
+                acc0 = mfma4(a[6], wr[c].get(6), acc0);
+                acc1 = mfma4(a[7], wr[c].get(7), acc1);
+            }
+        }
     }
     const floatx4 acc = acc0 + acc1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][(4 * grp + i) * 16 + col] = acc[i];
+    __syncthreads();
+    const int r = t >> 4, cn = t & 15, m = m0 + r, nn = n0 + cn;
+    const float v = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+    if (m >= g.M) return;
 
     if constexpr (EPI == CEPI_QKV) {
-        // RoPE pairs (2i, 2i+1) are adjacent columns, held by lanes l and l ^ 1
-        float partner[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) partner[i] = xshfl<1>(acc[i]);
-        if (!nvalid) return;
-        const int region = n / kCodecDModel, c = n - region * kCodecDModel;
-        const int pos0 = *g.pos0;
-        const float fr = g.freq[(c & (kCodecHeadDim - 1)) >> 1];
+        const int region = nn / kCodecDModel, c = nn - region * kCodecDModel;
+        const int pos = *g.pos0 + m;
+        float out = v;
+        if (region < 2) {
+            // audio_rope (audio_layer.cpp:30-44): pairs (2i, 2i+1), angle = float(pos) * freq in fp32
+            const int tp = t ^ 1;
+            const float partner = (red[0][tp] + red[1][tp]) + (red[2][tp] + red[3][tp]);
+            const float ang = (float)pos * g.freq[(c & (kCodecHeadDim - 1)) >> 1];
+            float sn, cs;
+            sincosf(ang, &sn, &cs);
+            out = (c & 1) ? partner * sn + v * cs : v * cs - partner * sn;
+        }
         float *dst = region == 0 ? g.q : (region == 1 ? g.kc : g.vc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + 4 * grp + i;
-            if (m >= g.M) break;
-            const int pos = pos0 + m;
-            float v = acc[i];
-            if (region < 2) {
-                // audio_rope (audio_layer.cpp:30-44): angle = float(pos) * freq in fp32
-                const float ang = (float)pos * fr;
-                float sn, cs;
-                sincosf(ang, &sn, &cs);
-                v = (c & 1) ? partner[i] * sn + v * cs : v * cs - partner[i] * sn;
-            }
-            const size_t row = region == 0 ? (size_t)m : (size_t)(pos % g.ring);
-            dst[row * kCodecDModel + c] = v;
-        }
+        const size_t row = region == 0 ? (size_t)m : (size_t)(pos % g.ring);
+        dst[row * kCodecDModel + c] = out;
+    } else if constexpr (EPI == CEPI_STORE) {
+        const int p = g.patch;
+        g.y[((size_t)m * p + nn % p) * g.ldy + nn / p] = g.bias ? v + g.bias[nn] : v;
+    } else if constexpr (EPI == CEPI_GELU) {
+        // audio_gelu (audio_layer.cpp:46)
+        g.y[(size_t)m * g.ldy + nn] = 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
     } else {
-        if (!nvalid) return;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = m0 + 4 * grp + i;
-            if (m >= g.M) break;
-            const float v = acc[i];
-            if constexpr (EPI == CEPI_STORE) {
-                const int p = g.patch;
-                const int pr = n % p;
-                g.y[((size_t)m * p + pr) * g.ldy + n / p] = g.bias ? v + g.bias[n] : v;
-            } else if constexpr (EPI == CEPI_GELU) {
-                // audio_gelu (audio_layer.cpp:46)
-                g.y[(size_t)m * g.ldy + n] = 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
-            } else {
-                float *y = g.y + (size_t)m * g.ldy + n;
-                *y = *y + g.ls[n] * v;
-            }
-        }
+        float *y = g.y + (size_t)m * g.ldy + nn;
+        *y = *y + g.ls[nn] * v;
     }
 }
 
@@ -249,32 +254,45 @@ __global__ __launch_bounds__(256) void codec_attn_kernel(const CodecAttnArgs a) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    for (int b = b0 + wave; b < b1; b += 4) {
+    // block b's operands: K rows kb + l%16 (this lane's 16 columns of the head), V rows
+    // kb + 4g + s (4 columns); keys past khi read as zeros (their scores are masked)
+    auto load_block = [&](int b, float (&kv)[16], float4 (&vv)[4]) {
         const int kb = klo + 16 * b;
-        float kv[16];
-        {
-            const int kp = kb + col;
-            const bool ok = kp <= khi;
-            const float4 *src = reinterpret_cast<const float4 *>(a.kc + (size_t)((ok ? kp : klo) % a.ring) * kCodecDModel + hoff + 16 * grp);
+        const int kp = kb + col;
+        const bool ok = kp <= khi;
+        const float4 *src = reinterpret_cast<const float4 *>(a.kc + (size_t)((ok ? kp : klo) % a.ring) * kCodecDModel + hoff + 16 * grp);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v = ok ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                kv[4 * i] = v.x;
-                kv[4 * i + 1] = v.y;
-                kv[4 * i + 2] = v.z;
-                kv[4 * i + 3] = v.w;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = ok ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            kv[4 * i] = v.x;
+            kv[4 * i + 1] = v.y;
+            kv[4 * i + 2] = v.z;
+            kv[4 * i + 3] = v.w;
         }
-        float4 vv[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const int kp = kb + 4 * grp + s;
-            vv[s] = kp <= khi ? *reinterpret_cast<const float4 *>(a.vc + (size_t)(kp % a.ring) * kCodecDModel + hoff + 4 * col)
+            const int kq = kb + 4 * grp + s;
+            vv[s] = kq <= khi ? *reinterpret_cast<const float4 *>(a.vc + (size_t)(kq % a.ring) * kCodecDModel + hoff + 4 * col)
                               : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+    };
+    float kv[16];
+    float4 vv[4];
+    if (b0 + wave < b1) load_block(b0 + wave, kv, vv);
+    for (int b = b0 + wave; b < b1; b += 4) {
+        const int kb = klo + 16 * b;
+        // the wave's next block is in flight while this one is computed
+        float kn[16];
+        float4 vn[4];
+        const bool more = b + 4 < b1;
+        if (more) load_block(b + 4, kn, vn);
+        floatx4 sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sc = mfma4(kv[i], qv[i], sc);
+        for (int i = 0; i < 16; i += 2) {
+            sc0 = mfma4(kv[i], qv[i], sc0);
+            sc1 = mfma4(kv[i + 1], qv[i + 1], sc1);
+        }
+        const floatx4 sc = sc0 + sc1;
         float p[4], bmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -300,6 +318,12 @@ __global__ __launch_bounds__(256) void codec_attn_kernel(const CodecAttnArgs a) 
             o[1] = mfma4(vv[s].y, p[s], o[1]);
             o[2] = mfma4(vv[s].z, p[s], o[2]);
             o[3] = mfma4(vv[s].w, p[s], o[3]);
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) kv[i] = kn[i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = vn[i];
         }
     }
     lrun += xshfl<16>(lrun);
@@ -367,7 +391,7 @@ __global__ void codec_advance_kernel(int *pos0, Rows4 rows) {
 
 template <int PRO, int EPI>
 int launch_w(const CodecGemmArgs &g, hipStream_t s) {
-    const dim3 grid((g.N + 63) / 64, (g.M + 15) / 16);
+    const dim3 grid(g.N / 16, (g.M + 15) / 16);
     if (g.w_f32)
         hipLaunchKernelGGL((codec_gemm_kernel<PRO, EPI, 1>), grid, dim3(256), 0, s, g);
     else

@@ -217,24 +217,25 @@ Codec::Codec(const void *blob, size_t bytes, const moss_hip_codec_options &opt) 
 }
 
 Codec::~Codec() {
-    hipSetDevice(device_);
-    if (stream_) hipStreamSynchronize(stream_);
-    for (auto &kv : graphs_) hipGraphExecDestroy(kv.second);
+    (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (auto &kv : graphs_) (void)hipGraphExecDestroy(kv.second);
     free_state(stream_state_);
     if (whole_alloc_) free_state(whole_state_);
     for (auto &e : ev_)
-        if (e) hipEventDestroy(e);
+        if (e) (void)hipEventDestroy(e);
     void *dev[] = {wdev_, freq_, codes_dev_, z_, xa_, xb_, y_, qb_, h_, ao_, ast_, out_dev_};
     for (void *p : dev)
-        if (p) hipFree(p);
-    if (codes_host_) hipHostFree(codes_host_);
-    if (out_host_) hipHostFree(out_host_);
-    if (stream_) hipStreamDestroy(stream_);
+        if (p) (void)hipFree(p);
+    if (codes_host_) (void)hipHostFree(codes_host_);
+    if (out_host_) (void)hipHostFree(out_host_);
+    if (stream_) (void)hipStreamDestroy(stream_);
 }
 
 // Key splits of a stage's attention for a piece of `rows` rows: enough workgroups to
 // cover the chip (~512 = row tiles x 4 heads x splits), each split keeping >= 8 key
-// blocks of 16 (two per wave) of the steady-state window.
+// blocks of 16 (two per wave) of the steady-state window.  (More splits, ~2048
+// workgroups, measured no faster and cost the proj GEMM's merge more.)
 int Codec::splits_for(int stage, int rows) const {
     const int tiles = (rows + 15) / 16;
     const int blocks = (stages_[stage].window + 15 + 15) / 16;
@@ -259,9 +260,9 @@ void Codec::alloc_state(CodecState &st) {
 }
 
 void Codec::free_state(CodecState &st) {
-    if (st.pos0) hipFree(st.pos0);
-    for (float *p : st.k) hipFree(p);
-    for (float *p : st.v) hipFree(p);
+    if (st.pos0) (void)hipFree(st.pos0);
+    for (float *p : st.k) (void)hipFree(p);
+    for (float *p : st.v) (void)hipFree(p);
     st.pos0 = nullptr;
     st.k.clear();
     st.v.clear();
@@ -445,13 +446,13 @@ void Codec::run_piece(CodecState &st, const int32_t *codes, int frames, float *o
             try {
                 enqueue(st, frames, nullptr);
             } catch (...) {
-                hipStreamEndCapture(s, &g);
-                if (g) hipGraphDestroy(g);
+                (void)hipStreamEndCapture(s, &g);
+                if (g) (void)hipGraphDestroy(g);
                 throw;
             }
             hip_check(hipStreamEndCapture(s, &g), "end capture");
             const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-            hipGraphDestroy(g);
+            (void)hipGraphDestroy(g);
             hip_check(e, "hipGraphInstantiate");
             it = graphs_.emplace(frames, ge).first;
         }

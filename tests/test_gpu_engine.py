@@ -1,5 +1,6 @@
 """The reference's TtsEngine (csrc/src/engine.cpp, compiled unchanged) end to end on
-the GPU drop-in LlmModel vs the same engine on the reference's own llm.cpp (GPU).
+the GPU drop-in LlmModel vs the same engine on the reference's own llm.cpp (GPU), and
+on both GPU drop-ins (LlmModel and the codec's AudioDecoder).
 
 oracle/_ref/engine_gpu and oracle/_ref/engine_cpu are one harness
 (oracle/engine_main.cpp) linked against the two LlmModels; the tokenizer, prompt
@@ -10,7 +11,9 @@ restore_prefix and prefill per chunk, generate on the engine's producer thread w
 on_frame feeding its queue), synthesize again, synthesize with a cancel flag raised
 after the first chunk's audio.  A second process on the same directory starts from
 the .mosskv prefix cache the first one wrote (load_prefix), and the CPU engine loads
-the cache the GPU engine wrote.
+the cache the GPU engine wrote.  oracle/_ref/engine_gpu_codec links the GPU
+AudioDecoder (host/codec/moss/decoder.h, host/decoder_hip.cpp) as well: the engine's
+decode_chunk calls (a first chunk of 4 frames, then 8) stream through the GPU codec.
 
 The tokenizer is the reference's own test fixture (csrc/tests/data/tokenizer.mossvocab,
 copied as data into tests/golden/); the model and the codec are seeded synthetic
@@ -22,7 +25,7 @@ import subprocess
 
 import numpy as np
 import pytest
-from conftest import GOLDEN, ROOT
+from conftest import GOLDEN, ROOT, max_rel
 
 from mosship import codec_format as cf
 from mosship import moss_format as mf
@@ -82,6 +85,22 @@ def test_engine_release_mode(torch_gpu, weights, tmp_path):
     gr, gp = run_engine("engine_gpu", weights, str(tmp_path / "gpu"), 0, True, 8, env)
     cr, cp = run_engine("engine_cpu", weights, str(tmp_path / "cpu"), 0, True, 8, env)
     _compare(gr, gp, cr, cp, 8, exact=False)
+
+
+def test_engine_gpu_codec_matches_cpu(torch_gpu, weights, tmp_path):
+    """Both drop-ins (A16 mode, so the codes are the CPU engine's): the engine's runs
+    match the CPU engine's, and the PCM from the GPU codec matches the reference codec's
+    to <= 1e-3 (max |diff| / max |pcm| per run; the measured error is printed)."""
+    if not os.path.exists(os.path.join(REF_DIR, "engine_gpu_codec")):
+        pytest.skip("oracle/_ref/engine_gpu_codec not built")
+    gr, gp = run_engine("engine_gpu_codec", weights, str(tmp_path / "gpuc"), 0, True, 8, ENV)
+    cr, cp = run_engine("engine_cpu", weights, str(tmp_path / "cpu"), 0, True, 8, ENV)
+    _compare(gr, gp, cr, cp, 8, exact=False)
+    for i in range(3):
+        assert gp[i].shape == cp[i].shape
+        err = max_rel(gp[i], cp[i])
+        print(f"run {i + 1}: GPU codec PCM max_rel {err:.2e} over {gp[i].size} samples", flush=True)
+        assert err <= 1e-3
 
 
 def _compare(gr, gp, cr, cp, frames, exact):
