@@ -196,6 +196,7 @@ int moss_hip_llm_reset(moss_hip_llm *m) {
 }
 
 int moss_hip_llm_position(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->position() : -1; }
+int moss_hip_llm_fallbacks(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->fallbacks() : -1; }
 
 int moss_hip_llm_get_hidden(moss_hip_llm *m, float *out) {
     return guard([&] {

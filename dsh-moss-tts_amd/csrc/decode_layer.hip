@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
     const int pos = g.state->pos;
     const int t = threadIdx.x;
     const int b = blockIdx.x;
-    int budget = kPollBudget;
+    int budget = g.poll_budget > 0 ? g.poll_budget : kPollBudget;
     uint64_t *LL = g.ll;
 
     // embed_row (llm.cpp:114-157): x = wte[row[0]] + sum over channels of

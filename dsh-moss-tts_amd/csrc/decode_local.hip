@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
     DevState *st = a.state;
     if (st->stop) return;  // written only between frames: the same for every workgroup
     const uint32_t tag_base = (uint32_t)(st->pos + 1) << 5;
-    int budget = kPollBudget;
+    int budget = a.poll_budget > 0 ? a.poll_budget : kPollBudget;
     uint64_t *LL = a.ll;
 
     // ---- the end gate (llm.cpp:653-679) in a workgroup of its own (the last):

@@ -69,6 +69,7 @@ public:
 
     void reset();
     int position() const { return pos_; }
+    int fallbacks() const { return fallbacks_; }
     void get_hidden(float *out);
     void set_hidden(const float *in);
     void prefill(const int32_t *rows, int n, int start);
@@ -115,6 +116,17 @@ private:
     bool prefill_a16_ = false;  // prefill GEMMs on fp32 activations (else W8A8)
     int decode_a8_ = 0;         // decode GEMVs in W8A8 (the reference with MOSS_A16 unset), else W8A16
     bool fused_layers_ = false; // global step as one decode_layer launch per layer, local steps as decode_local
+    // Poll rounds a wait of the fused kernels may take (0: kPollBudget, ~0.05 s).  MOSS_HIP_POLL_BUDGET
+    // = "N" or "N@K" overrides it (from the K-th fused launch of the model on), so tests can make
+    // the waits run out at a chosen launch and exercise the fallback below.
+    int poll_budget_ = 0, poll_budget_from_ = 0;
+    long fused_launches_ = 0;
+    int next_poll_budget() { return fused_launches_++ >= poll_budget_from_ ? poll_budget_ : 0; }
+    // A fused launch whose wait ran out (the device did not hold every workgroup at once, e.g.
+    // another stream occupied CUs) is redone on the per-operator path from the last good state;
+    // the rest of that call stays per operator.  fallbacks_ counts such recoveries.
+    int fallbacks_ = 0;
+    bool can_fall_back() const { return max_ctx_ <= 64 * 16; }
     float *qkv_table_ = nullptr;   // [1 + 15 * 1024][2304] local q|k|v of (lpos >= 1, input code)
     void build_qkv_table();
     uint64_t *ll_ = nullptr;    // kLayerWords exchange words of the fused layer launches

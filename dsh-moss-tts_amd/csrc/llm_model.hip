@@ -6,6 +6,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstddef>
+#include <cstdlib>
 #include <cstring>
 #include <unordered_map>
 #include <vector>
@@ -61,6 +62,10 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     use_graphs_ = opt.use_graphs;
     prefill_a16_ = opt.prefill_a16 != 0;
     decode_a8_ = opt.decode_a8 != 0 ? 1 : 0;
+    if (const char *b = std::getenv("MOSS_HIP_POLL_BUDGET")) {
+        poll_budget_ = std::max(0, std::atoi(b));
+        if (const char *at = std::strchr(b, '@')) poll_budget_from_ = std::max(0, std::atoi(at + 1));
+    }
     if (opt.decode_kernels != 0 && opt.decode_kernels != 1) throw Status(MOSS_HIP_EINVAL, "decode_kernels: 0 or 1");
     const uint8_t *b = static_cast<const uint8_t *>(blob);
     auto idx = parse_moss_index(b, bytes);
@@ -263,6 +268,7 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         g.row = row_dev;
         g.lnf_w = lnf_w_; g.lnf_b = lnf_b_; g.hidden = hidden_;
         g.state = state_; g.ll = ll_; g.err = &state_->ll_err; g.a8 = decode_a8_;
+        g.poll_budget = next_poll_budget();
         hip_check(launch_decode_global(g, kvt_, s), "decode global step");
         return;
     }
@@ -417,6 +423,7 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
         base.rope_cos = rope_; base.rope_sin = rope_ + (size_t)rope_n_ * kRopeHalf;
         base.state = state_; base.ll = ll_; base.err = &state_->ll_err; base.x_out = lres_;
         base.a8 = decode_a8_;
+        base.poll_budget = next_poll_budget();
         for (int ch = 0; ch < kNVq; ++ch) base.aemb[ch] = aemb_[ch];
         base.qkv_table = qkv_table_;
         base.logits = logits_;
@@ -586,6 +593,26 @@ void Model::global_step(const int32_t *row) {
     hip_check(hipMemcpyAsync(&hstate_->ll_err, &state_->ll_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
               "state d2h");
     hip_check(hipStreamSynchronize(stream_), "sync");
+    if (hstate_->ll_err != 0 && fused_layers_ && can_fall_back()) {
+        // the step is a function of the row, the position and the cache below it: redo it
+        // per operator (it rewrites the K/V row at pos and the hidden state)
+        ++fallbacks_;
+        hstate_->ll_err = 0;
+        write_state_header();
+        hip_check(hipMemcpyAsync(reinterpret_cast<uint8_t *>(state_) + kStateRowOff, row, 17 * sizeof(int32_t),
+                                 hipMemcpyHostToDevice, stream_),
+                  "row h2d");
+        hip_check(hipMemsetAsync(&state_->ll_err, 0, sizeof(unsigned), stream_), "exchange error clear");
+        fused_layers_ = false;
+        try {
+            launch_global(stream_);
+        } catch (...) {
+            fused_layers_ = true;
+            throw;
+        }
+        fused_layers_ = true;
+        hip_check(hipStreamSynchronize(stream_), "sync");
+    }
     check_exchange();
     ++pos_;
 }
@@ -719,7 +746,15 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     rng_seed_host(seed, hstate_->rng);  // Rng rng; rng.seed(seed) (llm.cpp:638-639)
     write_state_header();
     clear_exchange();
+    DevState start_state;  // the device state before L(0): where a recovery at frame 0 restarts
+    hip_check(hipMemcpyAsync(&start_state, state_, sizeof(DevState), hipMemcpyDeviceToHost, stream_), "state d2h");
     hip_check(hipStreamSynchronize(stream_), "sync");
+    // a recovery switches this call to the per-operator path; the next call tries the fused one again
+    struct FusedRestore {
+        bool &flag;
+        bool saved;
+        ~FusedRestore() { flag = saved; }
+    } fused_restore{fused_layers_, fused_layers_};
 
     // Frame f is two launches: its local half L(f), followed by the copy of the
     // decode state (codes, stop flag) into readback slot f & 1 and an event, then
@@ -764,6 +799,32 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
         timing[2 * f + 1] = lm;
     };
     auto cancelled = [&] { return cancel_ != nullptr && __atomic_load_n(cancel_, __ATOMIC_RELAXED); };
+    // Frame f's readback reports a fused launch whose wait ran out: L(f), or G(f - 1) whose hidden
+    // state L(f) started from.  Frames 0 .. f - 1 are good.  Put the device back to the state
+    // after L(f - 1) (read back then; the start of the call for f = 0) with the repetition counts
+    // of frames 0 .. f - 1 (from their rows), redo G(f - 1) and enqueue frame f again -- all per
+    // operator, which needs no co-resident workgroups.  G(f), enqueued behind the failed L(f), is
+    // superseded: it wrote only the K/V row and hidden state that the new G(f) rewrites.
+    auto recover = [&](int f) {
+        hip_check(hipStreamSynchronize(stream_), "sync");
+        ++fallbacks_;
+        fused_layers_ = false;
+        DevState st = f == 0 ? start_state : hread_[(f - 1) & 1];
+        st.ll_err = 0;
+        hip_check(hipMemcpyAsync(state_, &st, sizeof(DevState), hipMemcpyHostToDevice, stream_), "state h2d");
+        std::vector<int> cnt((size_t)kNVq * kCodebook, 0);
+        for (int g = 0; g < f; ++g)
+            for (int ch = 0; ch < kNVq; ++ch) {
+                const int used = forced ? forced[(size_t)g * 17 + ch + 1] : out_rows[(size_t)g * 17 + ch + 1];
+                ++cnt[(size_t)ch * kCodebook + used];
+            }
+        hip_check(hipMemcpyAsync(counts_, cnt.data(), cnt.size() * sizeof(int), hipMemcpyHostToDevice, stream_),
+                  "counts h2d");
+        if (f > 0 && global_enq[(f - 1) & 1]) launch_global(stream_);
+        if (global_enq[f & 1]) --pos_next;
+        enqueue(f);
+        hip_check(hipEventSynchronize(ev_[kEvPerSlot * (f & 1) + kEvRead]), "sync");
+    };
 
     int frames = 0;
     if (pos_ < max_ctx_ && !cancelled()) {
@@ -771,8 +832,13 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
         for (int f = 0;; ++f) {
             const int slot = f & 1;
             hip_check(hipEventSynchronize(ev_[kEvPerSlot * slot + kEvRead]), "sync");
+            if (hread_[slot].ll_err != 0) {  // the local half's or the previous global step's
+                hstate_->ll_err = hread_[slot].ll_err;
+                if (!fused_layers_ || !can_fall_back()) check_exchange();  // throws
+                recover(f);
+            }
             const DevState &hs = hread_[slot];
-            hstate_->ll_err = hs.ll_err;  // the local half's and the previous global step's
+            hstate_->ll_err = hs.ll_err;
             check_exchange();
             if (timing && f > 0) frame_timing(f - 1);  // G(f - 1) ran before L(f)
             if (gate_dump) {
@@ -797,6 +863,18 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     hip_check(hipMemcpyAsync(&hstate_->ll_err, &state_->ll_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
               "state d2h");
     hip_check(hipStreamSynchronize(stream_), "sync");  // the last global step has drained
+    if (hstate_->ll_err != 0 && frames > 0 && global_enq[(frames - 1) & 1] && fused_layers_ && can_fall_back()) {
+        // the last frame's global step ran out: redo it per operator from the state after its local half
+        ++fallbacks_;
+        fused_layers_ = false;
+        DevState st = hread_[(frames - 1) & 1];
+        st.ll_err = 0;
+        hip_check(hipMemcpyAsync(state_, &st, sizeof(DevState), hipMemcpyHostToDevice, stream_), "state h2d");
+        launch_global(stream_);
+        hip_check(hipMemcpyAsync(&hstate_->ll_err, &state_->ll_err, sizeof(unsigned), hipMemcpyDeviceToHost, stream_),
+                  "state d2h");
+        hip_check(hipStreamSynchronize(stream_), "sync");
+    }
     check_exchange();
     if (timing && frames > 0) frame_timing(frames - 1);
     return frames;

@@ -325,6 +325,7 @@ struct GlobalArgs {
     uint64_t *ll = nullptr;             // kLayerWords exchange words
     unsigned *err = nullptr;            // set when a wait runs out
     int a8 = 0;                         // W8A8 GEMVs (activations quantised per 32-block), else W8A16
+    int poll_budget = 0;                // poll rounds a wait may take before it gives up (kPollBudget)
 };
 hipError_t launch_decode_global(const GlobalArgs &a, KvType kv, hipStream_t s);
 
@@ -356,6 +357,7 @@ struct LocalArgs {
     int final_pick = 0;                // 1: after the last position, the greedy pick of its channel, the
                                        // frame's code counts, row[0] = slot and frame + 1 (sample_kernel's work)
     int a8 = 0;                        // W8A8 GEMVs (activations quantised per 32-block), else W8A16
+    int poll_budget = 0;               // poll rounds a wait may take before it gives up (kPollBudget)
 };
 hipError_t decode_local_occupancy(int *per_cu);
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s);

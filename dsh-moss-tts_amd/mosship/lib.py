@@ -22,7 +22,7 @@ EXPORTED = [
     "moss_hip_llm_position", "moss_hip_llm_get_hidden", "moss_hip_llm_set_hidden", "moss_hip_llm_prefill",
     "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
     "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
-    "moss_hip_llm_gate_rows",
+    "moss_hip_llm_gate_rows", "moss_hip_llm_fallbacks",
     "moss_hip_llm_kv_export", "moss_hip_llm_kv_import",
     "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
@@ -89,6 +89,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_llm_position.argtypes = [vp]
     L.moss_hip_llm_prefix_pos.argtypes = [vp]
     L.moss_hip_llm_gate_rows.argtypes = [vp]
+    L.moss_hip_llm_fallbacks.argtypes = [vp]
     L.moss_hip_llm_get_hidden.argtypes = [vp, vp]
     L.moss_hip_llm_set_hidden.argtypes = [vp, vp]
     L.moss_hip_llm_prefill.argtypes = [vp, vp, i32, i32]
@@ -225,6 +226,11 @@ class HipLLM:
     @property
     def prefix_pos(self) -> int:
         return self.L.moss_hip_llm_prefix_pos(self._h)
+
+    @property
+    def fallbacks(self) -> int:
+        """Fused decode launches redone on the per-operator path (moss_hip_llm_fallbacks)."""
+        return self.L.moss_hip_llm_fallbacks(self._h)
 
     def reset(self):
         check(self.L.moss_hip_llm_reset(self._h))

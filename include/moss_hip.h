@@ -128,6 +128,14 @@ int moss_hip_llm_generate(moss_hip_llm *m, int max_frames, const moss_hip_sample
  * writes to its gate CSV, llm.cpp:653-679,721-731); 0 when it was called without gate_dump. */
 int moss_hip_llm_gate_rows(const moss_hip_llm *m);
 
+/* Fused decode launches this model has redone on the per-operator path.  The fused kernels
+ * (decode_kernels = 0) need every workgroup of a launch resident at once; when one of their
+ * bounded waits runs out (another stream or process held CUs), the step is redone per
+ * operator from the last good state and the rest of that call stays per operator, so results
+ * do not change beyond fp32 summation order.  No counterpart in the reference (its decode
+ * has no such path); for monitoring. */
+int moss_hip_llm_fallbacks(const moss_hip_llm *m);
+
 /* LlmModel::set_cancel_flag (llm.h:86): a byte polled (relaxed) before each frame, as
  * llm.cpp:645 does; a flag raised in the on_frame callback of frame k ends generate after
  * frame k's global step, with k + 1 frames.  NULL clears it.  std::atomic<bool> is one byte
