@@ -592,9 +592,12 @@ def cpu_baseline(blob, state, frames: int, share: int):
 #  2 rows and the picks 15,504.
 GLOBAL_FIXED_BYTES = 90_243_072 + 485_376 + 13_872 + 36_864
 LOCAL_BYTES = 17 * 7_566_336 + 13_369_344 + 15_504
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (calibrated as the
-# GEMV's) over `bench.py --mode decode`; None where not measured
-DECODE_TRAFFIC = {"decode_global_kernel": None, "decode_local_kernel": None}
+# Bytes per launch that leave the XCDs' L2 (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over
+# the default `bench.py --mode decode`, positions 512..767; KiB per dispatch scaled as the GEMV's:
+# fetch x2.0, write x1.0, from the 256 MiB calibration copy of the same runs).  The global step
+# fetches 1.08x its algorithmic bytes; the local half 0.22x (its layer's weights, re-read by each
+# of the 17 local steps, stay in L2).
+DECODE_TRAFFIC = {"decode_global_kernel": 123_908_065, "decode_local_kernel": 31_675_238}
 
 
 def global_bytes(p: int) -> int:
