@@ -391,6 +391,7 @@ __global__ void codec_advance_kernel(int *pos0, Rows4 rows) {
 
 template <int PRO, int EPI>
 int launch_w(const CodecGemmArgs &g, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     const dim3 grid(g.N / 16, (g.M + 15) / 16);
     if (g.w_f32)
         hipLaunchKernelGGL((codec_gemm_kernel<PRO, EPI, 1>), grid, dim3(256), 0, s, g);
@@ -422,6 +423,7 @@ int codec_gemm_launch(int pro, int epi, const CodecGemmArgs &g, hipStream_t s) {
 }
 
 int codec_attn_launch(const CodecAttnArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (a.M <= 0 || a.splits < 1 || a.window <= 0 || a.ring <= 0 || !a.q || !a.kc || !a.vc || !a.pos0 || !a.o || !a.st)
         return MOSS_HIP_EINVAL;
     const dim3 grid((a.M + 15) / 16, kCodecHeads, a.splits);
@@ -430,12 +432,14 @@ int codec_attn_launch(const CodecAttnArgs &a, hipStream_t s) {
 }
 
 int codec_front_launch(const CodecFrontArgs &a, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (a.frames <= 0 || !a.codes || !a.z) return MOSS_HIP_EINVAL;
     hipLaunchKernelGGL(codec_front_kernel, dim3(a.frames), dim3(kCodecZ), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : MOSS_HIP_EDEVICE;
 }
 
 int codec_advance_launch(int *pos0, const int *rows, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
     Rows4 r;
     for (int i = 0; i < kCodecStages; ++i) r.r[i] = rows[i];
     hipLaunchKernelGGL(codec_advance_kernel, dim3(1), dim3(64), 0, s, pos0, r);

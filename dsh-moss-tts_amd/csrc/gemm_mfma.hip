@@ -348,6 +348,45 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     for (int t = 0; t < NT; ++t) red[wave][t][lane] = acc[t];
     __syncthreads();
     // lane holds rows m_base + 4kq + i, column n_base + 16t + l16
+    if constexpr (EPI == EPI_GELU && NT >= 2) {
+        if (g.q8_out != nullptr) {  // uniform
+            // wave w finishes row 4kq + w of every subtile: a 32-block is subtiles (2b, 2b + 1)
+            // across the 16 lanes of a kq group, so its amax is a 16-lane reduction
+            const int i = wave, m = m_base + 4 * kq + i;
+            float h[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float v = red[0][t][lane][i];
+                v += red[1][t][lane][i];
+                v += red[2][t][lane][i];
+                v += red[3][t][lane][i];
+                const int n = n_base + 16 * t + l16;
+                h[t] = gelu_new(v + g.bias[n]);
+                if (m < g.M) g.y[(size_t)m * g.ldy + n] = h[t];
+            }
+#pragma unroll
+            for (int b = 0; b < NT / 2; ++b) {
+                // quant_block32's arithmetic (quantize_activation, quant.cpp:45-55)
+                float amax = fmaxf(fabsf(h[2 * b]), fabsf(h[2 * b + 1]));
+                amax = fmaxf(amax, xshfl<1>(amax));
+                amax = fmaxf(amax, xshfl<2>(amax));
+                amax = fmaxf(amax, xshfl<4>(amax));
+                amax = fmaxf(amax, xshfl<8>(amax));
+                const float d = amax / 127.0f;
+                const float id = d > 0.0f ? 1.0f / d : 0.0f;
+                int q0 = (int)rintf(h[2 * b] * id), q1 = (int)rintf(h[2 * b + 1] * id);
+                q0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
+                q1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
+                if (m < g.M) {
+                    int8_t *qrow = g.q8_out + (size_t)m * g.N + n_base + 32 * b;
+                    qrow[l16] = (int8_t)q0;
+                    qrow[16 + l16] = (int8_t)q1;
+                    if (l16 == 0) g.d8_out[(size_t)m * (g.N / 32) + n_base / 32 + b] = d;
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int p = wave; p < 4 * NT; p += 4) {
         const int t = p >> 2, i = p & 3;
@@ -367,10 +406,11 @@ hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int mt = (g.M + 15) / 16;
     const int kz = EPI == EPI_PART ? (g.ksplit > 0 ? g.ksplit : gemm_ksplit(g.M, g.N, g.K)) : 1;
-    // the widest column tile that still gives ~192 workgroups
+    // the widest column tile that still gives ~192 workgroups (a quantising epilogue needs
+    // whole 32-blocks in a tile: at least 32 columns)
     if (g.N % 64 == 0 && (g.N / 64) * mt * kz >= 192) {
         hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8, LN>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
-    } else if (g.N % 32 == 0 && (g.N / 32) * mt * kz >= 192) {
+    } else if (g.N % 32 == 0 && ((g.N / 32) * mt * kz >= 192 || g.q8_out != nullptr)) {
         hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8, LN>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
     } else {
         hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
@@ -410,6 +450,7 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
         if (!g.part || z > 16 || z > nb) return hipErrorInvalidValue;
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
+    if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || g.ldy < g.N)) return hipErrorInvalidValue;
     // LayerNorm prologue: fp32 rows of at most 4 waves x 2 chunks of blocks, whole K in the workgroup
     if (g.ln_w != nullptr && (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))
         return hipErrorInvalidValue;

@@ -164,8 +164,10 @@ private:
     int rows_cap_ = 0;
     float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_o_ = nullptr, *pre_h_ = nullptr;  // prefill rows
     float *pre_part_ = nullptr;          // split-K partials of the prefill proj / fc_out GEMMs
-    int8_t *pre_q8_ = nullptr;           // W8A8 prefill: the current GEMM's int8 activations [m][<=3072]
-    float *pre_d8_ = nullptr;            //   and their block scales [m][<=96]
+    int8_t *pre_q8_ = nullptr;           // W8A8 prefill: the current GEMM's int8 activations [m][<=768]
+    float *pre_d8_ = nullptr;            //   and their block scales [m][<=24]
+    int8_t *pre_q8h_ = nullptr;          // W8A8 prefill: fc_in's output quantised by its epilogue [m][3072]
+    float *pre_d8h_ = nullptr;           //   and its block scales [m][96]
     DevState *state_ = nullptr;          // device
     DevState *hstate_ = nullptr;         // pinned host mirror
     DevState *hread_ = nullptr;          // [2] pinned per-frame state readback (frames alternate)

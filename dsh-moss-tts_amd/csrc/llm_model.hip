@@ -236,7 +236,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_part_, pre_q8_, pre_d8_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_};
+    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -631,12 +631,12 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     if (m <= 0) return;
     check_rows(rows, m);
     if (m > rows_cap_) {
-        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_};
+        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_};
         for (void *p : bufs)
             if (p) hip_check(hipFree(p), "free prefill buffers");
         rows_dev_ = nullptr;
-        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = pre_part_ = pre_d8_ = nullptr;
-        pre_q8_ = nullptr;
+        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = pre_part_ = pre_d8_ = pre_d8h_ = nullptr;
+        pre_q8_ = pre_q8h_ = nullptr;
         rows_cap_ = 0;
         hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
         hip_check(hipMalloc(&pre_x_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
@@ -646,8 +646,10 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * (size_t)m), "hipMalloc(prefill)");
         const int kz = std::max(gemm_ksplit(m, kHidden, kHidden), gemm_ksplit(m, kHidden, kFF));
         hip_check(hipMalloc(&pre_part_, sizeof(float) * kHidden * (size_t)m * kz), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_q8_, (size_t)kFF * m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_d8_, sizeof(float) * (kFF / 32) * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_q8_, (size_t)kHidden * m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_d8_, sizeof(float) * (kHidden / 32) * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_q8h_, (size_t)kFF * m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_d8h_, sizeof(float) * (kFF / 32) * (size_t)m), "hipMalloc(prefill)");
         rows_cap_ = m;
     }
     hip_check(hipMemcpyAsync(rows_dev_, rows, sizeof(int) * 17 * (size_t)m, hipMemcpyHostToDevice, stream_), "rows h2d");
@@ -698,12 +700,18 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
         f1.y = pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         operand(f1);
+        if (a8) {  // fc_out's int8 operand, quantised in fc_in's epilogue
+            f1.q8_out = pre_q8h_;
+            f1.d8_out = pre_d8h_;
+        }
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
-        if (a8) hip_check(launch_quant_rows(pre_h_, kFF, kFF, m, pre_q8_, pre_d8_, s), "prefill quant h");
         GemmArgs f2;
         f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
         f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
-        operand(f2);
+        if (a8) {
+            f2.a8 = pre_q8h_;
+            f2.d8 = pre_d8h_;
+        }
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
         const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce
         hip_check(launch_resid_ln_rows(pre_part_, f2.ksplit, m, L.fc_out_b, pre_x_, kHidden, pre_x_,

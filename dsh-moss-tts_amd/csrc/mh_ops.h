@@ -164,6 +164,10 @@ struct GemmArgs {
     // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
     // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
     const float *ln_w = nullptr, *ln_b = nullptr;
+    // EPI_GELU with q8_out (16*NT >= 32 columns per tile): the stored rows are also quantised
+    // per 32-block (quantize_activation, quant.cpp:45) into q8_out[M][N] / d8_out[M][N / 32]
+    int8_t *q8_out = nullptr;
+    float *d8_out = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
 // The K split launch_gemm uses for an EPI_PART GEMM of this shape (1..16).
