@@ -334,6 +334,197 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma_f32x4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Causal attention of 16 consecutive prompt rows x one head on the matrix cores (the
+// prefill: row r at position pos0 + r attends keys 0 .. pos0 + r of one cache page,
+// llm.cpp:349-392 over attention_core, llm.cpp:189-217).  Each of the 4 waves takes every
+// 4th block of 16 keys with an online softmax, fp32 on v_mfma_f32_16x16x4_f32 (K/V widened
+// from the cache's fp16 exactly):
+//   S^T = K Q^T: A = K[key kb + l%16][16g + t], B = Q[row l%16][16g + t], t = 0..15
+//   O^T = V^T P^T per column group j: A = V[key kb + 4g + s][4(l%16) + j], B = P[row][kb + 4g + s]
+// so the lane with row l%16 holds S^T for keys kb + 4g + i and O for columns 16g..16g+15
+// (g = l/16).  The waves merge through LDS; the output is normalised (and, under W8A8,
+// quantised per 32-block as quant_block32 does) and written as the row-per-workgroup kernel
+// writes it.
+template <int KV>
+__global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
+    __shared__ float red[4][16 * 64 + 32];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, col = lane & 15, grp = lane >> 4;
+    const int m0 = blockIdx.x * 16, h = blockIdx.y;
+    const int mlast = min(m0 + 15, a.rows - 1);
+    const int nkeys = min(a.pos0 + mlast + 1, a.max_keys);  // keys of the tile's last row
+    const int nkb = (nkeys + 15) >> 4;
+    const int mq = m0 + col, qpos = a.pos0 + mq;
+    const bool qvalid = mq < a.rows;
+    constexpr unsigned esz = KV == KV_F16 ? 2 : 4;
+    const char *kbase = (const char *)a.k_pool + (size_t)h * a.page_size * kHeadDim * esz;
+    const char *vbase = (const char *)a.v_pool + (size_t)h * a.page_size * kHeadDim * esz;
+
+    float qv[16];
+    {
+        const float4 *src = reinterpret_cast<const float4 *>(a.q + (size_t)(qvalid ? mq : 0) * a.q_stride + h * kHeadDim + 16 * grp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = qvalid ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            qv[4 * i] = v.x;
+            qv[4 * i + 1] = v.y;
+            qv[4 * i + 2] = v.z;
+            qv[4 * i + 3] = v.w;
+        }
+    }
+    // block b: this lane's 16 K dims of key kb + col, and 4 V dims of keys kb + 4g + s;
+    // keys past nkeys read the last key (their scores are masked)
+    auto load_block = [&](int b, float (&kv)[16], float4 (&vv)[4]) {
+        const int kb = 16 * b;
+        const int kk = min(kb + col, nkeys - 1);
+        if constexpr (KV == KV_F16) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(kbase + ((size_t)kk * kHeadDim + 16 * grp) * esz);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint4 u = src[i];
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float2 f = __half22float2(*reinterpret_cast<const __half2 *>(&w[j]));
+                    kv[8 * i + 2 * j] = f.x;
+                    kv[8 * i + 2 * j + 1] = f.y;
+                }
+            }
+        } else {
+            const float4 *src = reinterpret_cast<const float4 *>(kbase + ((size_t)kk * kHeadDim + 16 * grp) * esz);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = src[i];
+                kv[4 * i] = v.x;
+                kv[4 * i + 1] = v.y;
+                kv[4 * i + 2] = v.z;
+                kv[4 * i + 3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kq = min(kb + 4 * grp + s, nkeys - 1);
+            const char *p = vbase + ((size_t)kq * kHeadDim + 4 * col) * esz;
+            if constexpr (KV == KV_F16) {
+                const uint2 u = *reinterpret_cast<const uint2 *>(p);
+                const float2 x = __half22float2(*reinterpret_cast<const __half2 *>(&u.x));
+                const float2 y = __half22float2(*reinterpret_cast<const __half2 *>(&u.y));
+                vv[s] = make_float4(x.x, x.y, y.x, y.y);
+            } else {
+                vv[s] = *reinterpret_cast<const float4 *>(p);
+            }
+        }
+    };
+    float mrun = -INFINITY, lrun = 0.f;
+    floatx4 o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float kv[16];
+    float4 vv[4];
+    if (wave < nkb) load_block(wave, kv, vv);
+    for (int b = wave; b < nkb; b += 4) {
+        const int kb = 16 * b;
+        float kn[16];
+        float4 vn[4];
+        const bool more = b + 4 < nkb;
+        if (more) load_block(b + 4, kn, vn);  // the wave's next block in flight
+        floatx4 sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            sc0 = mfma_f32x4(kv[i], qv[i], sc0);
+            sc1 = mfma_f32x4(kv[i + 1], qv[i + 1], sc1);
+        }
+        const floatx4 sc = sc0 + sc1;
+        float p[4], bmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int kp = kb + 4 * grp + i;
+            const bool vis = qvalid && kp <= qpos && kp < nkeys;
+            p[i] = vis ? sc[i] * 0.125f : -INFINITY;  // (q . k) / sqrt(64), llm.cpp:200
+            bmax = fmaxf(bmax, p[i]);
+        }
+        bmax = fmaxf(bmax, xshfl<16>(bmax));
+        bmax = fmaxf(bmax, xshfl<32>(bmax));
+        const float mnew = fmaxf(mrun, bmax);
+        const float msafe = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = expf(mrun - msafe);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = expf(p[i] - msafe);
+        lrun = lrun * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        mrun = mnew;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] *= alpha;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            o[0] = mfma_f32x4(vv[s].x, p[s], o[0]);
+            o[1] = mfma_f32x4(vv[s].y, p[s], o[1]);
+            o[2] = mfma_f32x4(vv[s].z, p[s], o[2]);
+            o[3] = mfma_f32x4(vv[s].w, p[s], o[3]);
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) kv[i] = kn[i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = vn[i];
+        }
+    }
+    lrun += xshfl<16>(lrun);
+    lrun += xshfl<32>(lrun);
+    float *R = red[wave];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) R[(16 * grp + 4 * i + j) * 16 + col] = o[j][i];
+    if (grp == 0) {
+        R[1024 + col] = mrun;
+        R[1040 + col] = lrun;
+    }
+    __syncthreads();
+    // thread t: row q = t / 16, columns 4 (t % 16) .. + 3 of the head
+    const int q = t >> 4, d4 = t & 15, m = m0 + q;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, red[w][1024 + q]);
+    const float msafe = mx == -INFINITY ? 0.f : mx;
+    float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float f = expf(red[w][1024 + q] - msafe);
+        l += f * red[w][1040 + q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += f * red[w][(4 * d4 + e) * 16 + q];
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    float ov[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ov[e] = acc[e] * inv;
+    if (a.q8 != nullptr) {  // uniform: W8A8 copy, quant_block32's arithmetic over 8 threads x 4 values
+        float amax = fmaxf(fmaxf(fabsf(ov[0]), fabsf(ov[1])), fmaxf(fabsf(ov[2]), fabsf(ov[3])));
+        amax = fmaxf(amax, xshfl<1>(amax));
+        amax = fmaxf(amax, xshfl<2>(amax));
+        amax = fmaxf(amax, xshfl<4>(amax));
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        if (m < a.rows) {
+            int8_t *qrow = a.q8 + (size_t)m * kHidden + h * kHeadDim + 4 * d4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                int qq = (int)rintf(ov[e] * id);
+                qrow[e] = (int8_t)(qq < -127 ? -127 : (qq > 127 ? 127 : qq));
+            }
+            if ((d4 & 7) == 0) a.d8[(size_t)m * (kHidden / 32) + 2 * h + (d4 >> 3)] = d;
+        }
+    }
+    if (m >= a.rows) return;
+    float *orow = (float *)a.out + (size_t)m * a.out_stride + h * kHeadDim + 4 * d4;
+    *reinterpret_cast<float4 *>(orow) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+}
+
 }  // namespace
 
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
@@ -351,6 +542,21 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
                           kSliceWaves * 64 * (a.chunks - 1) >= a.max_keys))
         return hipErrorInvalidValue;
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
+}
+
+hipError_t launch_attn_tiles(const AttnArgs &a, KvType kv, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (a.heads != kHeads || a.rows <= 0 || a.max_keys <= 0 || a.page_size < a.max_keys || !a.out || a.out_f16 ||
+        !a.q || !a.k_pool || !a.v_pool || a.part || a.page_table || a.row_pos || a.row_stream || a.chunks ||
+        a.pos_stride != 1 || a.pos0 < 0 || a.pos0 + a.rows > a.max_keys || a.q_stride % 4 || a.out_stride % 4 ||
+        (a.q8 != nullptr && !a.d8))
+        return hipErrorInvalidValue;
+    const dim3 grid((a.rows + 15) / 16, kHeads);
+    if (kv == KV_F16)
+        hipLaunchKernelGGL(attn_tile_kernel<KV_F16>, grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(attn_tile_kernel<KV_F32>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace mh

@@ -687,7 +687,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
         t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = pre_o_;
         t.q8 = q8; t.d8 = d8;
-        hip_check(launch_attn(t, kvt_, s), "prefill attention");
+        hip_check(launch_attn_tiles(t, kvt_, s), "prefill attention");
         GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
         p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
         p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);

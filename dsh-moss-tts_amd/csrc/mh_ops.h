@@ -130,6 +130,9 @@ constexpr size_t chunk_scratch_bytes(int heads) {
 constexpr int kSliceWaves = MH_SLICE_WAVES;
 constexpr int kOneWgSpans = MH_ONE_WG_SPANS;
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s);
+// The prefill's form on the matrix cores: 16 rows x one head per workgroup, rows r at
+// positions pos0 + r of one cache page (no page table, per-row positions or split output).
+hipError_t launch_attn_tiles(const AttnArgs &a, KvType kv, hipStream_t s);
 
 // W8A16 GEMM on the matrix cores: Y[M][N] = A[M][K] W[N][K]^T with an epilogue.
 struct GemmArgs {
