@@ -43,10 +43,12 @@ public:
 
 private:
     struct Graphs {
-        hipGraphExec_t local = nullptr, global = nullptr;
+        hipGraphExec_t local = nullptr, local_greedy = nullptr, global = nullptr;
     };
-    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos);
-    void enqueue_frame_local(hipStream_t s, int n);
+    // attn = false: the step's attention output is already in o_ (the fused pick + attention)
+    void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, bool attn = true);
+    // greedy: channel picks fused with the next position's attention (greedy frames only)
+    void enqueue_frame_local(hipStream_t s, int n, bool greedy);
     void enqueue_global(hipStream_t s, int n);
     Graphs &graphs_for(int n);
     StreamState state() const;

@@ -87,6 +87,7 @@ Batch::~Batch() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     for (auto &kv : graphs_) {
         if (kv.second.local) (void)hipGraphExecDestroy(kv.second.local);
+        if (kv.second.local_greedy) (void)hipGraphExecDestroy(kv.second.local_greedy);
         if (kv.second.global) (void)hipGraphExecDestroy(kv.second.global);
     }
     void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
@@ -193,7 +194,7 @@ void Batch::kv_export(int s, int n_pos, float *k, float *v) {
 // kernel that follows it.  At lpos >= 1 the block input is an embedding row, so LN1 + QKV
 // is a row of the load-time q|k|v table, already written into q_ and the local
 // caches by the previous kernel.
-void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos) {
+void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, bool attn) {
     const LayerW &L = *w_.local;
     float *lk = lkv_, *lv = lkv_ + (size_t)S_ * kHeads * kLocalLen * kHeadDim;
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
@@ -205,10 +206,12 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
         q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
         hip_check(launch_gemm(q, EPI_QKV, KV_F32, s), "local qkv");
     }
-    AttnArgs t;
-    t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen; t.stream_stride = 1;
-    t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out = o_;
-    hip_check(launch_attn(t, KV_F32, s), "local attention");
+    if (attn) {
+        AttnArgs t;
+        t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen; t.stream_stride = 1;
+        t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out = o_;
+        hip_check(launch_attn(t, KV_F32, s), "local attention");
+    }
     GemmArgs p;
     p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
     p.y = lres_; p.ldy = kHidden; p.bias = L.proj_b; p.resid_in = in; p.resid_stride = in_stride;
@@ -227,8 +230,10 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
               "local fc_out reduce + ln_f");
 }
 
-// The local half of a frame for n streams (llm.cpp:648-698).
-void Batch::enqueue_frame_local(hipStream_t s, int n) {
+// The local half of a frame for n streams (llm.cpp:648-698).  Greedy frames (the host knows
+// which frames are greedy) fuse each channel's pick into the next position's attention:
+// 15 launches fewer per frame.
+void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
     const StreamState st = state();
     enqueue_local_step(s, n, hidden_, kHidden, 0);
     hip_check(launch_gate_rows(lres_, w_.llnf_w, w_.llnf_b, w_.wte, st, n, s), "gate");
@@ -242,18 +247,36 @@ void Batch::enqueue_frame_local(hipStream_t s, int n) {
     qkv.lpos = 1;
     hip_check(launch_local_qkv_rows(qkv, n, s), "local qkv rows");
     for (int ch = 0; ch < kNVq; ++ch) {
-        if (ch == 0)
+        if (ch == 0) {
             enqueue_local_step(s, n, w_.slot_in, 0, 1);
-        else
+        } else if (greedy) {  // channel ch - 1's pick, lpos ch + 1's q|k|v row and attention, in one launch
+            PickAttnArgs pa;
+            pa.logits = logits_;
+            pa.ch = ch - 1;
+            pa.aemb = w_.aemb[ch - 1];
+            pa.next_in = next_in_;
+            pa.st = st;
+            pa.rows = w_.qkv_table + (1 + (size_t)(ch - 1) * kCodebook) * 3 * kHidden;
+            pa.lk = qkv.lk;
+            pa.lv = qkv.lv;
+            pa.lpos = ch + 1;
+            pa.o = o_;
+            hip_check(launch_local_pick_attn(pa, n, s), "pick + local attention");
+            enqueue_local_step(s, n, next_in_, kHidden, ch + 1, false);
+        } else {
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
+        }
         GemmArgs hd;  // the tied audio head on the local ln_f of the step's output
         hd.w = w_.aemb[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
         hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
+        if (greedy && ch + 1 < kNVq) continue;  // picked by the next position's launch
         LocalQkv next = qkv;  // the input of lpos ch + 2 is channel ch's code
         next.rows = ch + 1 < kNVq ? w_.qkv_table + (1 + (size_t)ch * kCodebook) * 3 * kHidden : nullptr;
         next.lpos = ch + 2;
-        hip_check(launch_sample_rows(logits_, ch, w_.aemb[ch], next_in_, st, n, ch == kNVq - 1, next, s), "sample");
+        hip_check(launch_sample_rows(logits_, ch, w_.aemb[ch], next_in_, st, n, ch == kNVq - 1, next, s,
+                                     greedy && ch == kNVq - 1 ? 1 : 0),
+                  "sample");
     }
 }
 
@@ -309,11 +332,13 @@ Batch::Graphs &Batch::graphs_for(int n) {
     if (it != graphs_.end()) return it->second;
     Graphs g;
     hipGraph_t graph = nullptr;
-    hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
-    enqueue_frame_local(stream_, n);
-    hip_check(hipStreamEndCapture(stream_, &graph), "end capture");
-    hip_check(hipGraphInstantiate(&g.local, graph, nullptr, nullptr, 0), "instantiate");
-    (void)hipGraphDestroy(graph);
+    for (int greedy = 0; greedy < 2; ++greedy) {
+        hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
+        enqueue_frame_local(stream_, n, greedy != 0);
+        hip_check(hipStreamEndCapture(stream_, &graph), "end capture");
+        hip_check(hipGraphInstantiate(greedy ? &g.local_greedy : &g.local, graph, nullptr, nullptr, 0), "instantiate");
+        (void)hipGraphDestroy(graph);
+    }
     hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "begin capture");
     enqueue_global(stream_, n);
     hip_check(hipStreamEndCapture(stream_, &graph), "end capture");
@@ -360,8 +385,11 @@ double Batch::generate(int n, int frames, const moss_hip_sample_params &p, const
     hip_check(hipMemcpyAsync(rng_, rs.data(), rs.size() * sizeof(uint32_t), hipMemcpyHostToDevice, stream_), "rng h2d");
     hip_check(hipStreamSynchronize(stream_), "sync");
     hip_check(hipEventRecord(ev_[0], stream_), "event");
+    const SampleCfg cfg = sample_cfg(p);
     for (int f = 0; f < frames; ++f) {
-        hip_check(hipGraphLaunch(g.local, stream_), "graph launch");
+        // the device's rule for a greedy frame (sample_rows_kernel): cfg.greedy || frame < greedy_frames
+        const bool greedy = cfg.greedy || f < cfg.greedy_frames;
+        hip_check(hipGraphLaunch(greedy ? g.local_greedy : g.local, stream_), "graph launch");
         hip_check(hipMemcpyAsync(hist_active_ + (size_t)f * S_, active_, n, hipMemcpyDeviceToDevice, stream_), "hist");
         hip_check(hipMemcpyAsync(hist_codes_ + (size_t)f * S_ * kNVq, codes_, sizeof(int) * n * kNVq,
                                  hipMemcpyDeviceToDevice, stream_),

@@ -588,7 +588,7 @@ __global__ __launch_bounds__(256) void local_qkv_rows_kernel(LocalQkv a) { local
 // by the batched engine, so the used code is the pick.
 __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, int ch, const uint8_t *aemb,
                                                           float *next_in, StreamState st, int last_channel,
-                                                          LocalQkv next) {
+                                                          LocalQkv next, int count_prev) {
     __shared__ PickLds L;
     const int srow = blockIdx.x, t = threadIdx.x;
     float *nxt = next_in + (size_t)srow * kHidden;
@@ -623,6 +623,8 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
             st.codes[srow * kNVq + ch] = idx;
             st.row[srow * (kNVq + 1) + ch + 1] = idx;
             cnt[idx] += 1;
+            if (count_prev)  // the previous channel's pick, counted late by the fused path (below)
+                st.counts[((size_t)srow * kNVq + ch - 1) * kCodebook + st.codes[srow * kNVq + ch - 1]] += 1;
             if (last_channel) st.row[srow * (kNVq + 1)] = kSlotToken;
         }
     }
@@ -651,6 +653,79 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
             }
         }
     }
+}
+
+// Greedy frames of the batch engine: the pick of channel c = lpos - 2 (sample_rows_kernel's
+// greedy branch, llm.cpp:683-691 per stream) fused with what follows it at local position
+// lpos, one workgroup per (head, stream): every head's workgroup makes the same pick from the
+// same logits and counts, writes its 64 columns of the next residual input aemb[c][code]
+// and its head's q|k|v slice of the load-time table row, and runs its head's attention over
+// the stream's local keys 0..lpos (llm.cpp:189-217).  The pick's count is added by the next
+// channel's launch (the one reading counts[c + 1]), so no workgroup reads a count another
+// one is changing; the last channel's sample kernel adds the last two.
+__global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs a) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ float qkv[3][kHeadDim];
+    __shared__ float es[kLocalLen];
+    const int h = blockIdx.x, srow = blockIdx.y, t = threadIdx.x;
+    const StreamState &st = a.st;
+    const float *lg = a.logits + (size_t)srow * kCodebook;
+    const int *cnt = st.counts + ((size_t)srow * kNVq + a.ch) * kCodebook;
+    PickIn in;
+#pragma unroll
+    for (int k = 0; k < kCodebook / 256; ++k) {
+        in.vals[k] = lg[t + 256 * k];
+        in.cnt[k] = cnt[t + 256 * k];
+    }
+    const bool active = st.active[srow] != 0;  // the same for the whole workgroup
+    const float pen = st.ctrl->rep_penalty;
+    int idx = 0;  // inactive: row 0 keeps the next inputs defined
+    if (active) {
+        if (pen == 1.0f)
+#pragma unroll
+            for (int k = 0; k < kCodebook / 256; ++k) in.cnt[k] = 0;
+        idx = greedy_pick_reduce(in, pen, bv, bi);
+        idx = idx >= kCodebook ? 0 : idx;  // every value NaN: the reference's scan stays at 0
+        if (h == 0 && t == 0) {
+            st.codes[srow * kNVq + a.ch] = idx;
+            st.row[srow * (kNVq + 1) + a.ch + 1] = idx;
+            if (a.ch > 0)
+                st.counts[((size_t)srow * kNVq + a.ch - 1) * kCodebook + st.codes[srow * kNVq + a.ch - 1]] += 1;
+        }
+    }
+    const size_t kvrow = ((size_t)srow * kHeads + h) * kLocalLen;
+    if (t < 3 * kHeadDim) {  // this head's q, k, v of the table row (lpos, code)
+        const int sec = t >> 6, d = t & 63;
+        const float v = a.rows[(size_t)idx * 3 * kHidden + sec * kHidden + h * kHeadDim + d];
+        qkv[sec][d] = v;
+        if (sec == 1) a.lk[(kvrow + a.lpos) * kHeadDim + d] = v;
+        if (sec == 2) a.lv[(kvrow + a.lpos) * kHeadDim + d] = v;
+    } else {  // this head's 64 columns of the next residual input
+        const int d = t - 3 * kHeadDim;
+        a.next_in[(size_t)srow * kHidden + h * kHeadDim + d] = q8x4_elem(a.aemb, kHidden / 32, idx, h * kHeadDim + d);
+    }
+    __syncthreads();
+    if (t >= 64) return;
+    // wave 0: lane k scores key k (the new key lpos from LDS), then lane d accumulates column d
+    const int nk = a.lpos + 1;
+    float sc = -INFINITY;
+    if (t < nk) {
+        const float *kr = t == a.lpos ? qkv[1] : a.lk + (kvrow + t) * kHeadDim;
+        float d = 0.0f;
+#pragma unroll 16
+        for (int i = 0; i < kHeadDim; ++i) d = fmaf(qkv[0][i], kr[i], d);
+        sc = d * 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
+    }
+    const float mx = wave_max(sc);
+    const float e = t < nk ? expf(sc - mx) : 0.0f;
+    const float l = wave_sum(e);
+    if (t < kLocalLen) es[t] = e;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float o = 0.0f;
+    for (int k = 0; k < nk; ++k) o = fmaf(es[k], k == a.lpos ? qkv[2][t] : a.lv[(kvrow + k) * kHeadDim + t], o);
+    a.o[(size_t)srow * kHidden + h * kHeadDim + t] = o / l;
 }
 
 __global__ void advance_rows_kernel(StreamState st, int streams) {
@@ -761,12 +836,22 @@ hipError_t launch_gate_rows(const float *x_raw, const float *lnf_w, const float 
 }
 
 hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
-                              int streams, int last_channel, const LocalQkv &next, hipStream_t s) {
+                              int streams, int last_channel, const LocalQkv &next, hipStream_t s, int count_prev) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (next.rows && (!next.q_out || !next.lk || !next.lv || next.lpos < 1 || next.lpos >= kLocalLen))
         return hipErrorInvalidValue;
+    if (count_prev && ch < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL(sample_rows_kernel, dim3(streams), dim3(256), 0, s, logits, ch, aemb, next_in, st,
-                       last_channel, next);
+                       last_channel, next, count_prev);
+    return hipGetLastError();
+}
+
+hipError_t launch_local_pick_attn(const PickAttnArgs &a, int streams, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (!a.logits || !a.aemb || !a.next_in || !a.rows || !a.lk || !a.lv || !a.o || streams <= 0 || a.ch < 0 ||
+        a.ch >= kNVq - 1 || a.lpos != a.ch + 2)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(local_pick_attn_kernel, dim3(kHeads, streams), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -290,7 +290,21 @@ struct LocalQkv {
     int lpos = 0;
 };
 hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, float *next_in, const StreamState &st,
-                              int streams, int last_channel, const LocalQkv &next, hipStream_t s);
+                              int streams, int last_channel, const LocalQkv &next, hipStream_t s, int count_prev = 0);
+// Greedy frames: channel ch's pick fused with local position lpos = ch + 2's table row and
+// attention, one workgroup per (head, stream); the pick's count is added by the next launch.
+struct PickAttnArgs {
+    const float *logits = nullptr;  // [S][1024] logits of channel ch
+    int ch = 0;
+    const uint8_t *aemb = nullptr;  // aemb[ch]: the next residual input's row
+    float *next_in = nullptr;       // [S][768]
+    StreamState st;
+    const float *rows = nullptr;    // q|k|v table rows of channel ch's inputs at lpos: [1024][2304]
+    float *lk = nullptr, *lv = nullptr;  // local KV [S][heads][17][64] (fp32)
+    int lpos = 0;
+    float *o = nullptr;             // [S][768] attention output
+};
+hipError_t launch_local_pick_attn(const PickAttnArgs &a, int streams, hipStream_t s);
 // The same copy of one shared row (lpos 1: wte[slot]) for every stream.
 hipError_t launch_local_qkv_rows(const LocalQkv &a, int streams, hipStream_t s);
 // pos[s] += 1 for active streams; streams reaching capacity become inactive.

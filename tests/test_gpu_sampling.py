@@ -81,12 +81,17 @@ def test_sampled_free_running_and_end_gate(torch_gpu, oracle, state):
         g.close()
 
 
-def test_batch_sampled_vs_oracle(torch_gpu, oracle, state):
-    """Each stream of the batched engine samples like its own LlmModel with its own seed."""
+@pytest.mark.parametrize("greedy_frames", [0, 2])
+def test_batch_sampled_vs_oracle(torch_gpu, oracle, state, greedy_frames):
+    """Each stream of the batched engine samples like its own LlmModel with its own seed.
+    greedy_frames = 2: the first two frames run the greedy frame graph (channel picks fused
+    into the next position's attention, repetition counts added a launch later), the rest
+    the sampled one, on the same counts."""
     blob, k, v, h = state
     n_pos = k.shape[1]
     seeds = [11, 22, 33, 44, 55]
-    kw = dict(temperature=0.8, top_k=25, top_p=0.95, repetition_penalty=1.2, min_frames=5)
+    kw = dict(temperature=0.8, top_k=25, top_p=0.95, repetition_penalty=1.2, min_frames=5,
+              greedy_frames=greedy_frames)
     g = HipLLM(blob)
     b = HipBatch(g, max_streams=8, capacity=128, kv_fp32=True)
     hs = [h * (1.0 + 0.1 * s) for s in range(len(seeds))]  # distinct streams
