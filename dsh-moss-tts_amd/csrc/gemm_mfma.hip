@@ -21,6 +21,23 @@
 #include "mh_ops.h"
 
 namespace mh {
+#ifdef MH_GEMM_TRACE
+// Start and end time (100 MHz device clock) of every workgroup of the last
+// launch, in builds with -DMH_GEMM_TRACE only (a profiling build).
+__device__ unsigned long long mh_gemm_ts[8192][2];
+#define GT_START const unsigned long long gt0_ = __builtin_amdgcn_s_memrealtime();
+#define GT_END                                                                           \
+    if (threadIdx.x == 0) {                                                              \
+        const int id_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); \
+        if (id_ < 8192) {                                                                \
+            mh_gemm_ts[id_][0] = gt0_;                                                   \
+            mh_gemm_ts[id_][1] = __builtin_amdgcn_s_memrealtime();                       \
+        }                                                                                \
+    }
+#else
+#define GT_START
+#define GT_END
+#endif
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -110,10 +127,30 @@ __device__ __forceinline__ void gemm_finish(const GemmArgs &g, int m, int n, flo
 }
 
 
+// Operands through buffer resources: the lane's byte offset at the wave's first
+// block is one VGPR per operand; the block within a chunk is the instruction's
+// immediate offset and the chunk base and column subtile an SGPR offset, so a
+// load costs no address arithmetic.  A load past a resource's last byte returns
+// 0 instead of faulting, so every load is unconditional (blocks past the wave's
+// last one, or rows past M, are read and never used).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer word 3 (32-bit data format)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+template <bool A8>
+struct Src {
+    rsrc_t a, ad, w;  // activations (fp32, or int8 under W8A8), their block scales, weights
+    int va, vad;      // lane offsets of the activations and their scale at the wave's first block
+    int vw, vs;       // lane offsets of its weight run and its column's scale (column subtile 0)
+    int wt;           // bytes from one 16-column subtile to the next (4 groups)
+};
+
 // One chunk of KB scale blocks: this lane's 8 activations per block (fp32, or
 // int8 + the block scale of the lane's row under W8A8) and its 8 weights +
-// scale per block and column subtile.  Block indices are clamped so every load
-// is unconditional (blocks past nb are loaded but not used).
+// scale per block and column subtile.
 template <int NT, bool A8>
 struct Chunk {
     float xa[A8 ? 1 : KB][8];
@@ -123,46 +160,50 @@ struct Chunk {
     uint32_t db[KB][NT];
 };
 
+constexpr int kCpolNT = 2;  // non-temporal: the weights are read once per launch
+
 template <int NT, bool A8>
-__device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, int nb, const float *arow_p,
-                                             const int8_t *arow_q, const float *arow_d) {
+__device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
-        const int b = min(b0 + j, nb - 1);
         if constexpr (A8) {
-            c.xq[j] = *(const uint64_t *)(arow_q + 32 * b);
-            c.xd[j] = arow_d[b];
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.a, s.va + 32 * j, 32 * b0, 0);
+            c.xq[j] = ((uint64_t)q[1] << 32) | q[0];
+            c.xd[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s.ad, s.vad + 4 * j, 4 * b0, 0));
         } else {
-            const float4 x0 = *(const float4 *)(arow_p + 32 * b);
-            const float4 x1 = *(const float4 *)(arow_p + 32 * b + 4);
-            c.xa[j][0] = x0.x; c.xa[j][1] = x0.y; c.xa[j][2] = x0.z; c.xa[j][3] = x0.w;
-            c.xa[j][4] = x1.x; c.xa[j][5] = x1.y; c.xa[j][6] = x1.z; c.xa[j][7] = x1.w;
+            // the whole vector is reinterpreted: a bit cast of one element of the
+            // builtin's vector type reads element 0
+            const floatx4 x0 =
+                __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(s.a, s.va + 128 * j, 128 * b0, 0));
+            const floatx4 x1 = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(s.a, s.va + 128 * j + 16, 128 * b0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                c.xa[j][i] = x0[i];
+                c.xa[j][4 + i] = x1[i];
+            }
         }
     }
 }
 
 template <int NT, bool A8>
-__device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, int nb, const uint8_t *const (&wcol)[NT],
-                                             int krow, int kq) {
+__device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
-        const int b = min(b0 + j, nb - 1);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint8_t *blk = wcol[t] + (size_t)b * kBlockBytes;
-            const uint64_t raw = __builtin_nontemporal_load((const uint64_t *)(blk + 8 + 32 * krow + 8 * kq));
-            c.qb[j][t] = make_uint2((uint32_t)raw, (uint32_t)(raw >> 32));
-            c.db[j][t] = *(const uint16_t *)(blk + 2 * krow);
+            const int so = t * s.wt + kBlockBytes * b0;
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.w, s.vw + kBlockBytes * j, so, kCpolNT);
+            c.qb[j][t] = make_uint2(q[0], q[1]);
+            c.db[j][t] = __builtin_amdgcn_raw_buffer_load_b16(s.w, s.vs + kBlockBytes * j, so, 0);
         }
     }
 }
 
 template <int NT, bool A8>
-__device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, int nb, const float *arow_p,
-                                           const int8_t *arow_q, const float *arow_d,
-                                           const uint8_t *const (&wcol)[NT], int krow, int kq) {
-    load_chunk_a<NT, A8>(c, b0, nb, arow_p, arow_q, arow_d);
-    load_chunk_b<NT, A8>(c, b0, nb, wcol, krow, kq);
+__device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
+    load_chunk_a<NT, A8>(c, b0, s);
+    load_chunk_b<NT, A8>(c, b0, s);
 }
 
 typedef int intx4 __attribute__((ext_vector_type(4)));
@@ -222,28 +263,38 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
 template <int EPI, int KV, int NT, bool A8, bool LN>
 __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
+    GT_START
     __shared__ floatx4 red[4][NT][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
     const int m_base = blockIdx.y * 16;
     const int n_base = blockIdx.x * 16 * NT;
     const int nb_all = g.K >> 5;
     // K slice z: blocks [z * nb_all / Z, (z + 1) * nb_all / Z); wave w its w-th quarter
-    const int z0 = (int)(((long)blockIdx.z * nb_all) / gridDim.z);
-    const int nbz = (int)(((long)(blockIdx.z + 1) * nb_all) / gridDim.z) - z0;
+    const int z0 = (int)((blockIdx.z * (unsigned)nb_all) / gridDim.z);
+    const int nbz = (int)(((blockIdx.z + 1) * (unsigned)nb_all) / gridDim.z) - z0;
     const int kb0 = z0 + (wave * nbz) / 4;
     const int nb = z0 + ((wave + 1) * nbz) / 4 - kb0;  // 0 when the slice has fewer than 4 blocks
     const int arow = min(m_base + l16, g.M - 1);      // rows past M read row M-1, never stored
-    const float *arow_p = A8 ? nullptr : g.a + (size_t)arow * g.lda + 8 * kq + 32 * kb0;
-    const int8_t *arow_q = A8 ? g.a8 + (size_t)arow * g.lda + 8 * kq + 32 * kb0 : nullptr;
-    const float *arow_d = A8 ? g.d8 + (size_t)arow * (g.lda / 32) + kb0 : nullptr;
-    const uint8_t *wcol[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int n = n_base + 16 * t + l16;
-        wcol[t] = g.w + ((size_t)(n >> 2) * nb_all + kb0) * kBlockBytes;
-    }
     const int krow = l16 & 3;
+    Src<A8> src;
+    {
+        const uint32_t a_elems = (uint32_t)((g.M - 1) * g.lda + g.K);
+        if constexpr (A8) {
+            src.a = make_rsrc(g.a8, a_elems);
+            src.ad = make_rsrc(g.d8, 4u * (uint32_t)((g.M - 1) * (g.lda / 32) + nb_all));
+            src.va = arow * g.lda + 8 * kq + 32 * kb0;
+            src.vad = 4 * (arow * (g.lda / 32) + kb0);
+        } else {
+            src.a = make_rsrc(g.a, 4u * a_elems);
+            src.va = 4 * (arow * g.lda + 8 * kq + 32 * kb0);
+        }
+        src.w = make_rsrc(g.w, (uint32_t)(g.N / 4) * (uint32_t)nb_all * kBlockBytes);
+        const int grp = (n_base >> 2) + (l16 >> 2);  // this lane's group in column subtile 0
+        src.vw = (grp * nb_all + kb0) * kBlockBytes + 8 + 32 * krow + 8 * kq;
+        src.vs = (grp * nb_all + kb0) * kBlockBytes + 2 * krow;
+        src.wt = 4 * nb_all * kBlockBytes;
+    }
 
     floatx4 acc[NT];
 #pragma unroll
@@ -258,8 +309,8 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         // loaded value waits for that load, and loads complete in order)
         constexpr int LNR = (4 * 2 * KB * 32 + 255) / 256;
         Chunk<NT, A8> ca, cb;
-        load_chunk_a<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d);
-        load_chunk_a<NT, A8>(cb, KB, nb, arow_p, arow_q, arow_d);  // clamped: valid past nb
+        load_chunk_a<NT, A8>(ca, 0, src);
+        load_chunk_a<NT, A8>(cb, KB, src);
         float lw[LNR], lb[LNR];
 #pragma unroll
         for (int i = 0; i < LNR; ++i) {
@@ -267,8 +318,8 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             lw[i] = g.ln_w[c];
             lb[i] = g.ln_b[c];
         }
-        load_chunk_b<NT, A8>(ca, 0, nb, wcol, krow, kq);
-        load_chunk_b<NT, A8>(cb, KB, nb, wcol, krow, kq);
+        load_chunk_b<NT, A8>(ca, 0, src);
+        load_chunk_b<NT, A8>(cb, KB, src);
 #pragma unroll
         for (int i = 0; i < LNR; ++i) {
             const int c = (int)threadIdx.x + 256 * i;
@@ -334,13 +385,13 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         if (KB < nb) mfma_chunk<NT, A8>(cb, KB, nb, kq, acc);
     } else if (nb > 0) {
         Chunk<NT, A8> ca, cb;
-        load_chunk<NT, A8>(ca, 0, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+        load_chunk<NT, A8>(ca, 0, src);
         for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
-            load_chunk<NT, A8>(cb, b0 + KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);  // clamped: valid past nb
+            load_chunk<NT, A8>(cb, b0 + KB, src);
             mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
             if (b0 + KB >= nb) break;
             if (b0 + 2 * KB < nb)  // (uniform) a chunk past the wave's blocks is not requested
-                load_chunk<NT, A8>(ca, b0 + 2 * KB, nb, arow_p, arow_q, arow_d, wcol, krow, kq);
+                load_chunk<NT, A8>(ca, b0 + 2 * KB, src);
             mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
         }
     }
@@ -384,6 +435,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
                     if (l16 == 0) g.d8_out[(size_t)m * (g.N / 32) + n_base / 32 + b] = d;
                 }
             }
+            GT_END
             return;
         }
     }
@@ -399,6 +451,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         const float partner = xshfl<1>(v);  // column n ^ 1, same row
         if (m < g.M) gemm_finish<EPI, KV>(g, m, n, v, partner);
     }
+    GT_END
 }
 
 template <int EPI, int KV, bool A8, bool LN>
@@ -465,3 +518,8 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
 }
 
 }  // namespace mh
+#ifdef MH_GEMM_TRACE
+extern "C" int mh_gemm_trace_read(unsigned long long *out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(mh::mh_gemm_ts), sizeof(mh::mh_gemm_ts));
+}
+#endif
