@@ -85,43 +85,75 @@ __device__ __forceinline__ half8 i8x8_to_h8(uint2 q) {
     return r;
 }
 
+// What the epilogue needs of a lane's row, computed once: a lane stores one row
+// of every column subtile of its tile.  A tile (16, 32 or 64 columns) lies inside
+// one section (q, k or v) and one head of the QKV output.
+struct EpiRow {
+    float *out = nullptr;        // the row's output at column 0 (q_out's row under QKV)
+    const float *res = nullptr;  // EPI_RESID: the row's residual input
+    const float *rc = nullptr, *rs = nullptr;  // EPI_QKV: RoPE factors at the row's position
+    void *pool = nullptr;        // EPI_QKV, k or v section: the row's K/V slot (d = 0) in its page
+    int sec = 0;                 // EPI_QKV: 0 q, 1 k, 2 v
+};
+
 template <int EPI, int KV>
-__device__ __forceinline__ void gemm_finish(const GemmArgs &g, int m, int n, float v, float partner) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ EpiRow epi_row(const GemmArgs &g, int m, int n_base) {
+    EpiRow r;
+    const int mm = min(m, g.M - 1);  // rows past M store nothing; their lookups stay in bounds
     if constexpr (EPI == EPI_PART) {
-        g.part[((size_t)blockIdx.z * g.M + m) * g.N + n] = v;
-    } else if constexpr (EPI == EPI_F32) {
-        g.y[(size_t)m * g.ldy + n] = v;
+        r.out = g.part + ((size_t)blockIdx.z * g.M + mm) * g.N;
+    } else if constexpr (EPI == EPI_F32 || EPI == EPI_GELU) {
+        r.out = g.y + (size_t)mm * g.ldy;
     } else if constexpr (EPI == EPI_RESID) {
-        float *y = g.y + (size_t)m * g.ldy + n;
-        const float xin = g.resid_in ? g.resid_in[(size_t)m * g.resid_stride + n] : *y;
-        *y = xin + (v + g.bias[n]);
+        r.out = g.y + (size_t)mm * g.ldy;
+        r.res = g.resid_in ? g.resid_in + (size_t)mm * g.resid_stride : r.out;
+    } else {  // EPI_QKV
+        r.sec = n_base / kHidden;
+        const int h = (n_base - r.sec * kHidden) >> 6;
+        const int s = g.row_stream ? g.row_stream[mm] : mm * g.stream_stride;
+        const int pos = g.row_pos ? g.row_pos[mm] : g.pos0 + mm * g.pos_stride;
+        r.rc = g.rope_cos + (size_t)pos * kRopeHalf;
+        r.rs = g.rope_sin + (size_t)pos * kRopeHalf;
+        if (r.sec == 0) {
+            r.out = g.q_out + (size_t)mm * kHidden;
+        } else if (g.row_active == nullptr || g.row_active[mm]) {
+            const int page = g.page_table ? g.page_table[(size_t)s * g.table_stride + pos / g.page_size] : s;
+            const size_t slot = (((size_t)page * kHeads + h) * g.page_size + pos % g.page_size) * kHeadDim;
+            void *pool = r.sec == 1 ? g.k_pool : g.v_pool;
+            r.pool = KV == KV_F16 ? (void *)((__half *)pool + slot) : (void *)((float *)pool + slot);
+        }
+    }
+    return r;
+}
+
+template <int EPI, int KV>
+__device__ __forceinline__ void gemm_finish(const GemmArgs &g, const EpiRow &r, int n, float v, float partner) {
+#pragma clang fp contract(off)
+    if constexpr (EPI == EPI_PART || EPI == EPI_F32) {
+        r.out[n] = v;
+    } else if constexpr (EPI == EPI_RESID) {
+        const float xin = r.res[n];
+        r.out[n] = xin + (v + g.bias[n]);
     } else if constexpr (EPI == EPI_GELU) {
-        g.y[(size_t)m * g.ldy + n] = gelu_new(v + g.bias[n]);
+        r.out[n] = gelu_new(v + g.bias[n]);
     } else {  // EPI_QKV: bias, RoPE at the row's position, q -> q_out, k/v -> KV pages
         const float val = v + g.bias[n];
-        const int sec = n / kHidden, within = n - sec * kHidden;
-        const int h = within >> 6, d = within & 63;
-        const int s = g.row_stream ? g.row_stream[m] : m * g.stream_stride;
-        const int pos = g.row_pos ? g.row_pos[m] : g.pos0 + m * g.pos_stride;
+        const int d = n & 63;
         float out = val;
-        if (sec < 2) {
+        if (r.sec < 2) {
             const float pv = partner + g.bias[n ^ 1];
-            const float c = g.rope_cos[pos * kRopeHalf + (d >> 1)];
-            const float sn = g.rope_sin[pos * kRopeHalf + (d >> 1)];
+            const float c = r.rc[d >> 1];
+            const float sn = r.rs[d >> 1];
             const float p0 = val * c, p1 = pv * sn;
             out = (d & 1) == 0 ? p0 - p1 : p0 + p1;
         }
-        if (sec == 0) {
-            g.q_out[(size_t)m * kHidden + within] = out;
-        } else if (g.row_active == nullptr || g.row_active[m]) {
-            const int page = g.page_table ? g.page_table[(size_t)s * g.table_stride + pos / g.page_size] : s;
-            const size_t idx = (((size_t)page * kHeads + h) * g.page_size + pos % g.page_size) * kHeadDim + d;
-            void *pool = sec == 1 ? g.k_pool : g.v_pool;
+        if (r.sec == 0) {
+            r.out[n] = out;
+        } else if (r.pool != nullptr) {
             if constexpr (KV == KV_F16)
-                ((__half *)pool)[idx] = __float2half_rn(out);
+                ((__half *)r.pool)[d] = __float2half_rn(out);
             else
-                ((float *)pool)[idx] = out;
+                ((float *)r.pool)[d] = out;
         }
     }
 }
@@ -405,12 +437,13 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             // across the 16 lanes of a kq group, so its amax is a 16-lane reduction
             const int i = wave, m = m_base + 4 * kq + i;
             float h[NT];
+            const float *redf = (const float *)&red[0][0][lane] + i;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                float v = red[0][t][lane][i];
-                v += red[1][t][lane][i];
-                v += red[2][t][lane][i];
-                v += red[3][t][lane][i];
+                float v = redf[4 * (t * 64)];
+                v += redf[4 * ((NT + t) * 64)];
+                v += redf[4 * ((2 * NT + t) * 64)];
+                v += redf[4 * ((3 * NT + t) * 64)];
                 const int n = n_base + 16 * t + l16;
                 h[t] = gelu_new(v + g.bias[n]);
                 if (m < g.M) g.y[(size_t)m * g.ldy + n] = h[t];
@@ -439,17 +472,20 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             return;
         }
     }
+    // wave w finishes row 4kq + w of every column subtile (component w of each
+    // lane's partials: one 4-byte LDS read each, at an offset uniform in the wave)
+    const int i = wave, m = m_base + 4 * kq + i;
+    const EpiRow r = epi_row<EPI, KV>(g, m, n_base);
+    const float *redf = (const float *)&red[0][0][lane] + i;
 #pragma unroll
-    for (int p = wave; p < 4 * NT; p += 4) {
-        const int t = p >> 2, i = p & 3;
-        float v = red[0][t][lane][i];
-        v += red[1][t][lane][i];
-        v += red[2][t][lane][i];
-        v += red[3][t][lane][i];
+    for (int t = 0; t < NT; ++t) {
+        float v = redf[4 * (t * 64)];
+        v += redf[4 * ((NT + t) * 64)];
+        v += redf[4 * ((2 * NT + t) * 64)];
+        v += redf[4 * ((3 * NT + t) * 64)];
         const int n = n_base + 16 * t + l16;
-        const int m = m_base + 4 * kq + i;
         const float partner = xshfl<1>(v);  // column n ^ 1, same row
-        if (m < g.M) gemm_finish<EPI, KV>(g, m, n, v, partner);
+        if (m < g.M) gemm_finish<EPI, KV>(g, r, n, v, partner);
     }
     GT_END
 }
