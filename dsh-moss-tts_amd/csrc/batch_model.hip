@@ -200,7 +200,7 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     if (lpos == 0) {  // `in` is the global hidden state, one row per stream
         GemmArgs q;
-        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = in; q.lda = in_stride; q.M = n;
+        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a = in; q.lda = in_stride; q.M = n;
         q.ln_w = L.ln1_w; q.ln_b = L.ln1_b;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = lk; q.v_pool = lv; q.page_size = kLocalLen;
         q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
@@ -213,16 +213,16 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
         hip_check(launch_attn(t, KV_F32, s), "local attention");
     }
     GemmArgs p;
-    p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
+    p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
     p.y = lres_; p.ldy = kHidden; p.bias = L.proj_b; p.resid_in = in; p.resid_stride = in_stride;
     hip_check(launch_gemm(p, EPI_RESID, KV_F32, s), "local proj");
     GemmArgs f1;
-    f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = lres_; f1.lda = kHidden; f1.M = n;
+    f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = lres_; f1.lda = kHidden; f1.M = n;
     f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
     f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
     hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
     GemmArgs f2;  // split K: the reduce adds bias and residual, then the local ln_f for the head
-    f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
+    f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
     f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
     hip_check(launch_gemm(f2, EPI_PART, KV_F32, s), "local fc_out");
     hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b, a_,
@@ -267,7 +267,7 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
         }
         GemmArgs hd;  // the tied audio head on the local ln_f of the step's output
-        hd.w = w_.aemb[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
+        hd.w = w_.aemb[ch]; hd.wm = w_.aemb_m[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
         hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
         if (greedy && ch + 1 < kNVq) continue;  // picked by the next position's launch
@@ -294,7 +294,7 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
         void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
         GemmArgs q;  // on LN1(x) in a_
-        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
+        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
         q.page_table = table_; q.table_stride = pages_; q.page_size = kPage;
         q.stream_stride = 1; q.row_pos = pos_d_; q.row_active = active_; q.rope_cos = rc; q.rope_sin = rs;
@@ -304,16 +304,16 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         t.stream_stride = 1; t.row_pos = pos_d_; t.rows = n; t.max_keys = cap_; t.out = o_;
         hip_check(launch_attn(t, kvt_, s), "attention");
         GemmArgs p;  // x += proj + b
-        p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
+        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
         p.y = x_; p.ldy = kHidden; p.bias = L.proj_b;
         hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "proj");
         GemmArgs f1;  // LN2 in the prologue
-        f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = x_; f1.lda = kHidden; f1.M = n;
+        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = x_; f1.lda = kHidden; f1.M = n;
         f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
         f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
         GemmArgs f2;  // split K; the reduce adds bias and residual
-        f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
+        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
         f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
         // then LN1 of the next layer into a_, or ln_f into hidden (active streams only)

@@ -172,6 +172,15 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, kRsrcWord3);
 }
 
+// Weights in the matrix-core order (tile_q8x4_mfma): for each 16-row subtile s
+// of W and scale block b, one 544-byte unit at (s * K/32 + b) * 544 holding the
+// 512 quants in MFMA lane order -- lane l = c + 16 kq takes the 8 bytes at 8 l
+// (row 16 s + c, columns 32 b + 8 kq .. + 7) as its B operand -- then the 16
+// rows' fp16 scales.  A column-subtile load is 4 whole 128-byte lines; in the
+// Q8_0_4X4 order it gathers 4 groups' 128-byte runs that start 8 bytes into
+// 136-byte blocks (8 lines), plus 4 more lines for the scales.
+constexpr int kTileBytes = 544;
+
 template <bool A8>
 struct Src {
     rsrc_t a, ad, w;  // activations (fp32, or int8 under W8A8), their block scales, weights
@@ -192,7 +201,9 @@ struct Chunk {
     uint32_t db[KB][NT];
 };
 
-constexpr int kCpolNT = 2;  // non-temporal: the weights are read once per launch
+// weights: default caching -- every row tile of the launch reads them again (a
+// non-temporal hint measured slower end to end: 0.83 vs 0.78 ms per 256-row prefill)
+constexpr int kCpolW = 0;
 
 template <int NT, bool A8>
 __device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
@@ -218,24 +229,27 @@ __device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src
     }
 }
 
-template <int NT, bool A8>
+// TL: weights in the matrix-core order (one 544-byte unit per subtile and block)
+// instead of Q8_0_4X4 (4 groups of 136-byte blocks per subtile)
+template <int NT, bool A8, bool TL>
 __device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
+    constexpr int UB = TL ? kTileBytes : kBlockBytes;  // bytes from one block to the next
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int so = t * s.wt + kBlockBytes * b0;
-            const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.w, s.vw + kBlockBytes * j, so, kCpolNT);
+            const int so = t * s.wt + UB * b0;
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.w, s.vw + UB * j, so, kCpolW);
             c.qb[j][t] = make_uint2(q[0], q[1]);
-            c.db[j][t] = __builtin_amdgcn_raw_buffer_load_b16(s.w, s.vs + kBlockBytes * j, so, 0);
+            c.db[j][t] = __builtin_amdgcn_raw_buffer_load_b16(s.w, s.vs + UB * j, so, 0);
         }
     }
 }
 
-template <int NT, bool A8>
+template <int NT, bool A8, bool TL>
 __device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
     load_chunk_a<NT, A8>(c, b0, s);
-    load_chunk_b<NT, A8>(c, b0, s);
+    load_chunk_b<NT, A8, TL>(c, b0, s);
 }
 
 typedef int intx4 __attribute__((ext_vector_type(4)));
@@ -292,7 +306,7 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
 // quarter (at most 8 blocks: K <= 1024) is loaded first, the row sums of the
 // 4 waves meet in LDS (two passes: mean, then the squared deviations), and the
 // values are normalised in registers with ln_w / ln_b staged in LDS.
-template <int EPI, int KV, int NT, bool A8, bool LN>
+template <int EPI, int KV, int NT, bool A8, bool LN, bool TL>
 __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
     GT_START
@@ -321,11 +335,17 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             src.a = make_rsrc(g.a, 4u * a_elems);
             src.va = 4 * (arow * g.lda + 8 * kq + 32 * kb0);
         }
-        src.w = make_rsrc(g.w, (uint32_t)(g.N / 4) * (uint32_t)nb_all * kBlockBytes);
-        const int grp = (n_base >> 2) + (l16 >> 2);  // this lane's group in column subtile 0
-        src.vw = (grp * nb_all + kb0) * kBlockBytes + 8 + 32 * krow + 8 * kq;
-        src.vs = (grp * nb_all + kb0) * kBlockBytes + 2 * krow;
-        src.wt = 4 * nb_all * kBlockBytes;
+        src.w = make_rsrc(TL ? g.wm : g.w, (uint32_t)(g.N / 16) * (uint32_t)nb_all * kTileBytes);
+        if constexpr (TL) {
+            const int unit = ((n_base >> 4) * nb_all + kb0) * kTileBytes;  // column subtile 0, first block
+            src.vw = unit + 8 * lane;
+            src.vs = unit + 512 + 2 * l16;
+        } else {
+            const int grp = (n_base >> 2) + (l16 >> 2);  // this lane's group in column subtile 0
+            src.vw = (grp * nb_all + kb0) * kBlockBytes + 8 + 32 * krow + 8 * kq;
+            src.vs = (grp * nb_all + kb0) * kBlockBytes + 2 * krow;
+        }
+        src.wt = nb_all * kTileBytes;  // 16 rows of W: 4 groups of 136-byte blocks, or one tile per block
     }
 
     floatx4 acc[NT];
@@ -350,8 +370,8 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             lw[i] = g.ln_w[c];
             lb[i] = g.ln_b[c];
         }
-        load_chunk_b<NT, A8>(ca, 0, src);
-        load_chunk_b<NT, A8>(cb, KB, src);
+        load_chunk_b<NT, A8, TL>(ca, 0, src);
+        load_chunk_b<NT, A8, TL>(cb, KB, src);
 #pragma unroll
         for (int i = 0; i < LNR; ++i) {
             const int c = (int)threadIdx.x + 256 * i;
@@ -417,13 +437,13 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         if (KB < nb) mfma_chunk<NT, A8>(cb, KB, nb, kq, acc);
     } else if (nb > 0) {
         Chunk<NT, A8> ca, cb;
-        load_chunk<NT, A8>(ca, 0, src);
+        load_chunk<NT, A8, TL>(ca, 0, src);
         for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
-            load_chunk<NT, A8>(cb, b0 + KB, src);
+            load_chunk<NT, A8, TL>(cb, b0 + KB, src);
             mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
             if (b0 + KB >= nb) break;
             if (b0 + 2 * KB < nb)  // (uniform) a chunk past the wave's blocks is not requested
-                load_chunk<NT, A8>(ca, b0 + 2 * KB, src);
+                load_chunk<NT, A8, TL>(ca, b0 + 2 * KB, src);
             mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
         }
     }
@@ -490,7 +510,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     GT_END
 }
 
-template <int EPI, int KV, bool A8, bool LN>
+template <int EPI, int KV, bool A8, bool LN, bool TL>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int mt = (g.M + 15) / 16;
@@ -498,22 +518,36 @@ hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     // the widest column tile that still gives ~192 workgroups (a quantising epilogue needs
     // whole 32-blocks in a tile: at least 32 columns)
     if (g.N % 64 == 0 && (g.N / 64) * mt * kz >= 192) {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8, LN>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8, LN, TL>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
     } else if (g.N % 32 == 0 && ((g.N / 32) * mt * kz >= 192 || g.q8_out != nullptr)) {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8, LN>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8, LN, TL>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
     } else {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN, TL>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
     }
     return hipGetLastError();
 }
 
+template <int EPI, int KV, bool TL>
+hipError_t launch_l(const GemmArgs &g, hipStream_t s) {
+    if (g.a8 != nullptr) return launch_nt<EPI, KV, true, false, TL>(g, s);
+    if constexpr (EPI != EPI_PART) {
+        if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL>(g, s);
+    }
+    return launch_nt<EPI, KV, false, false, TL>(g, s);
+}
+
 template <int EPI, int KV>
 hipError_t launch_a(const GemmArgs &g, hipStream_t s) {
-    if (g.a8 != nullptr) return launch_nt<EPI, KV, true, false>(g, s);
-    if constexpr (EPI != EPI_PART) {
-        if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true>(g, s);
-    }
-    return launch_nt<EPI, KV, false, false>(g, s);
+    return g.wm != nullptr ? launch_l<EPI, KV, true>(g, s) : launch_l<EPI, KV, false>(g, s);
+}
+
+__global__ __launch_bounds__(64) void tile_q8x4_mfma_kernel(const uint8_t *w, int nb_all, uint8_t *out) {
+    const int sub = blockIdx.x, b = blockIdx.y, l = threadIdx.x;
+    const int c = l & 15, kq = l >> 4, n = 16 * sub + c;
+    const uint8_t *blk = w + ((size_t)(n >> 2) * nb_all + b) * kBlockBytes;
+    uint8_t *unit = out + ((size_t)sub * nb_all + b) * kTileBytes;
+    *(uint64_t *)(unit + 8 * l) = *(const uint64_t *)(blk + 8 + 32 * (n & 3) + 8 * kq);
+    if (kq == 0) *(uint16_t *)(unit + 512 + 2 * c) = *(const uint16_t *)(blk + 2 * (n & 3));
 }
 }  // namespace
 
@@ -528,6 +562,13 @@ int gemm_ksplit(int M, int N, int K) {
     z = z > nb / 12 ? nb / 12 : z;
     z = z > 16 ? 16 : z;
     return z < 1 ? 1 : z;
+}
+
+hipError_t tile_q8x4_mfma(const uint8_t *w, int N, int K, uint8_t *out, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (!w || !out || N <= 0 || K <= 0 || N % 16 || K % 32) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(tile_q8x4_mfma_kernel, dim3(N / 16, K / 32), dim3(64), 0, s, w, K / 32, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s) {

@@ -58,6 +58,10 @@ struct LayerW {
     const float *fc_in_b;
     const uint8_t *fc_out_w;
     const float *fc_out_b;
+    // the four matrices again in the matrix-core order (tile_q8x4_mfma) read by
+    // the GEMMs of the prefill and the batch engine; null: the GEMMs read the
+    // Q8_0_4X4 copy (MOSS_HIP_GEMM_TILED=0)
+    const uint8_t *attn_wm, *proj_wm, *fc_in_wm, *fc_out_wm;
 };
 
 class Model {
@@ -95,11 +99,13 @@ public:
         const float *lnf_w, *lnf_b, *llnf_w, *llnf_b;
         const uint8_t *wte;
         const uint8_t *const *aemb;  // [kNVq]
+        const uint8_t *const *aemb_m;  // [kNVq] in the matrix-core order (null entries: none)
         const float *slot_in;        // dequantised wte[kSlotToken]
         const float *qkv_table;      // [1 + 15 * 1024][2304] local q|k|v of (lpos >= 1, input code)
     };
     Weights weights() const {
-        return Weights{g_, &local_, lnf_w_, lnf_b_, llnf_w_, llnf_b_, wte_, aemb_.data(), slot_in_, qkv_table_};
+        return Weights{g_, &local_, lnf_w_, lnf_b_, llnf_w_, llnf_b_, wte_, aemb_.data(), aemb_m_.data(), slot_in_,
+                       qkv_table_};
     }
 
 private:
@@ -146,6 +152,9 @@ private:
     const float *lnf_w_ = nullptr, *lnf_b_ = nullptr, *llnf_w_ = nullptr, *llnf_b_ = nullptr;
     const uint8_t *wte_ = nullptr;
     std::array<const uint8_t *, kNVq> aemb_{};
+    uint8_t *wm_ = nullptr;              // the GEMM matrices in the matrix-core order (LayerW::*_wm, aemb_m_)
+    std::array<const uint8_t *, kNVq> aemb_m_{};
+    void tile_gemm_weights();
 
     // device buffers
     void *kv_ = nullptr;                 // [2][layers][heads][max_ctx][64]

@@ -227,7 +227,37 @@ Model::Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt) {
     hip_check(launch_dequant_rows(wte_, kVocab, kHidden, rows_dev_, 1, slot_in_, stream_), "dequant slot row");
     hip_check(hipStreamSynchronize(stream_), "sync");
     build_qkv_table();  // the fused local steps and the batch engine look their q|k|v up
+    tile_gemm_weights();
     if (use_graphs_) build_graphs();
+}
+
+// The prefill and batch-engine GEMMs read a copy of their matrices in the
+// matrix-core order (one 544-byte unit per 16 rows and scale block, quants in
+// MFMA lane order): a load of the GEMM then reads whole cache lines.  Same size
+// as the Q8_0_4X4 matrices, which the decode GEMVs keep reading.
+void Model::tile_gemm_weights() {
+    if (const char *t = std::getenv("MOSS_HIP_GEMM_TILED"))
+        if (std::strcmp(t, "0") == 0) return;
+    const size_t bytes_layer = ((size_t)3 * kHidden * kHidden + (size_t)kHidden * kHidden + 2ull * kFF * kHidden) / 32 * 34;
+    const size_t bytes_head = (size_t)kCodebook * kHidden / 32 * 34;
+    hip_check(hipMalloc(&wm_, (kLayers + 1) * bytes_layer + kNVq * bytes_head), "hipMalloc(tiled weights)");
+    uint8_t *p = wm_;
+    auto tile = [&](const uint8_t *w, int n, int k) {
+        hip_check(tile_q8x4_mfma(w, n, k, p, stream_), "tile weights");
+        const uint8_t *r = p;
+        p += (size_t)n * k / 32 * 34;
+        return r;
+    };
+    auto tile_layer = [&](LayerW &L) {
+        L.attn_wm = tile(L.attn_w, 3 * kHidden, kHidden);
+        L.proj_wm = tile(L.proj_w, kHidden, kHidden);
+        L.fc_in_wm = tile(L.fc_in_w, kFF, kHidden);
+        L.fc_out_wm = tile(L.fc_out_w, kHidden, kFF);
+    };
+    for (auto &L : g_) tile_layer(L);
+    tile_layer(local_);
+    for (int ch = 0; ch < kNVq; ++ch) aemb_m_[ch] = tile(aemb_[ch], kCodebook, kHidden);
+    hip_check(hipStreamSynchronize(stream_), "sync");
 }
 
 Model::~Model() {
@@ -236,7 +266,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_};
+    void *bufs[] = {blob_, wm_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -677,7 +707,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
         GemmArgs q;
-        q.w = L.attn_w; q.N = 3 * kHidden; q.K = kHidden; q.a = pre_a_; q.lda = kHidden; q.M = m;
+        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a = pre_a_; q.lda = kHidden; q.M = m;
         q.bias = L.attn_b; q.q_out = pre_q_;
         q.k_pool = kv_layer(0, l); q.v_pool = kv_layer(1, l); q.page_size = max_ctx_;
         q.pos0 = start; q.rope_cos = rc; q.rope_sin = rs;
@@ -689,7 +719,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         t.q8 = q8; t.d8 = d8;
         hip_check(launch_attn_tiles(t, kvt_, s), "prefill attention");
         GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
-        p.w = L.proj_w; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
+        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
         p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);
         operand(p);
         hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
@@ -697,7 +727,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
                                        pre_a_, nullptr, s, q8, d8),
                   "prefill proj reduce + ln2");
         GemmArgs f1;
-        f1.w = L.fc_in_w; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
+        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
         f1.y = pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         operand(f1);
         if (a8) {  // fc_out's int8 operand, quantised in fc_in's epilogue
@@ -706,7 +736,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         }
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
         GemmArgs f2;
-        f2.w = L.fc_out_w; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
+        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
         f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
         if (a8) {
             f2.a8 = pre_q8h_;

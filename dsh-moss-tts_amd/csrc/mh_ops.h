@@ -137,6 +137,7 @@ hipError_t launch_attn_tiles(const AttnArgs &a, KvType kv, hipStream_t s);
 // W8A16 GEMM on the matrix cores: Y[M][N] = A[M][K] W[N][K]^T with an epilogue.
 struct GemmArgs {
     const uint8_t *w = nullptr;  // Q8_0_4X4, N x K
+    const uint8_t *wm = nullptr; // the same weights in the matrix-core order (tile_q8x4_mfma), read instead of w when set
     int N = 0, K = 0;
     const float *a = nullptr;    // fp32 activations [M][lda]
     int lda = 0, M = 0;
@@ -173,6 +174,9 @@ struct GemmArgs {
     float *d8_out = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
+// Copy of a Q8_0_4X4 N x K matrix in the matrix-core order the GEMM reads through
+// GemmArgs::wm (same size: N/16 * K/32 units of 544 bytes).
+hipError_t tile_q8x4_mfma(const uint8_t *w, int N, int K, uint8_t *out, hipStream_t s);
 // The K split launch_gemm uses for an EPI_PART GEMM of this shape (1..16).
 int gemm_ksplit(int M, int N, int K);
 

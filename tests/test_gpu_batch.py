@@ -82,6 +82,33 @@ def test_batch_generate_vs_oracle(torch_gpu, oracle, setup):
     assert min(agree) >= 0.99
 
 
+def test_batch_tiled_weights_bit_identical(torch_gpu, setup, monkeypatch):
+    """The batch GEMMs (global layers, local layer, audio heads) read the matrices in the
+    matrix-core order; with MOSS_HIP_GEMM_TILED=0 the Q8_0_4X4 ones: 3 sampled frames give
+    bit-identical codes, hidden states and KV."""
+    blob, lens, states = setup
+    p = SampleParams.make(greedy=False, temperature=0.9, top_k=40, top_p=0.9, min_frames=3, repetition_penalty=1.2)
+    res = []
+    for tiled in ("1", "0"):
+        print(f"batch tiled={tiled}", flush=True)
+        monkeypatch.setenv("MOSS_HIP_GEMM_TILED", tiled)
+        g = HipLLM(blob)
+        monkeypatch.delenv("MOSS_HIP_GEMM_TILED")
+        b = HipBatch(g, max_streams=8, capacity=256)
+        for s, (k, v, h) in enumerate(states):
+            b.set_stream(s, k, v, h)
+        out = b.generate(len(lens), 3, p, seeds=np.arange(11, 11 + len(lens)))
+        res.append((out["rows"], [b.hidden(s) for s in range(len(lens))],
+                    [b.kv_export(s, b.position(s)) for s in range(len(lens))]))
+        b.close()
+        g.close()
+    (ra, ha, ka), (rb, hb, kb) = res
+    assert np.array_equal(ra, rb)
+    for s in range(len(lens)):
+        assert np.array_equal(ha[s], hb[s])
+        assert np.array_equal(ka[s][0], kb[s][0]) and np.array_equal(ka[s][1], kb[s][1])
+
+
 def test_batch_end_gate_per_stream(torch_gpu, oracle, setup):
     """min_frames = 0: each stream stops on its own end gate, like its own LlmModel."""
     blob, lens, states = setup

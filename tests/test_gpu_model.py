@@ -257,6 +257,27 @@ def test_prefill_vs_oracle(torch_gpu, oracle, golden_model, a16):
     gm.close()
 
 
+@pytest.mark.parametrize("a16", [False, True])
+def test_prefill_tiled_weights_bit_identical(torch_gpu, golden_model, monkeypatch, a16):
+    """The prefill GEMMs read a copy of the matrices in the matrix-core order made at load;
+    with MOSS_HIP_GEMM_TILED=0 they read the Q8_0_4X4 matrices.  The MFMA operands and
+    their order are the same, so hidden state and KV are bit-identical (256 rows)."""
+    blob, _ = golden_model
+    rows = mf.text_rows(np.random.default_rng(8).integers(0, mf.VOCAB, 256))
+    rows[100:140, 1:] = np.random.default_rng(9).integers(0, 1024, (40, 16))
+    out = []
+    for tiled in ("1", "0"):
+        print(f"prefill a16={a16} tiled={tiled}", flush=True)
+        monkeypatch.setenv("MOSS_HIP_GEMM_TILED", tiled)
+        gm = HipLLM(blob, prefill_a16=a16)
+        monkeypatch.delenv("MOSS_HIP_GEMM_TILED")
+        gm.prefill(rows)
+        out.append((gm.hidden(), *gm.kv_export(len(rows))))
+        gm.close()
+    for a, b in zip(*out):
+        assert np.array_equal(a, b)
+
+
 def test_snapshot_restore_prefix(torch_gpu, prefilled):
     blob, rows, k, v, h = prefilled
     g = HipLLM(blob)
