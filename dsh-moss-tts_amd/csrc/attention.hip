@@ -305,8 +305,8 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     if (a.q8 != nullptr) {  // W8A8 copy for the proj GEMM: this head's 64 outputs are two blocks
         float d;
         const int q = quant_block32(res, &d);
-        a.q8[(size_t)r * kHidden + h * kHeadDim + lane] = (int8_t)q;
-        if ((lane & 31) == 0) a.d8[(size_t)r * (kHidden / 32) + 2 * h + (lane >> 5)] = d;
+        a.q8[q8t_at(r, h * kHeadDim + lane, kHidden)] = (int8_t)q;
+        if ((lane & 31) == 0) a.d8[d8t_at(r, 2 * h + (lane >> 5), kHidden)] = d;
     }
 }
 
@@ -511,13 +511,14 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
         const float d = amax / 127.0f;
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
         if (m < a.rows) {
-            int8_t *qrow = a.q8 + (size_t)m * kHidden + h * kHeadDim + 4 * d4;
+            // 4 consecutive columns: one aligned 4-byte run of the matrix-core order
+            int8_t *qrun = a.q8 + q8t_at(m, h * kHeadDim + 4 * d4, kHidden);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 int qq = (int)rintf(ov[e] * id);
-                qrow[e] = (int8_t)(qq < -127 ? -127 : (qq > 127 ? 127 : qq));
+                qrun[e] = (int8_t)(qq < -127 ? -127 : (qq > 127 ? 127 : qq));
             }
-            if ((d4 & 7) == 0) a.d8[(size_t)m * (kHidden / 32) + 2 * h + (d4 >> 3)] = d;
+            if ((d4 & 7) == 0) a.d8[d8t_at(m, 2 * h + (d4 >> 3), kHidden)] = d;
         }
     }
     if (m >= a.rows) return;

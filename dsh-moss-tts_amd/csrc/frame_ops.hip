@@ -399,7 +399,8 @@ hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType k
 namespace mh {
 namespace {
 
-// Row r's 768 values o (thread t holds t, t+256, t+512) to int8 blocks of 32.
+// Row r's 768 values o (thread t holds t, t+256, t+512) to int8 blocks of 32, in the
+// matrix-core order of the prefill GEMMs (q8t_at / d8t_at).
 __device__ __forceinline__ void quant_row_768(const float (&o)[3], int r, int8_t *q8, float *d8) {
     const int t = threadIdx.x;
 #pragma unroll
@@ -407,8 +408,8 @@ __device__ __forceinline__ void quant_row_768(const float (&o)[3], int r, int8_t
         const int c = t + 256 * i;
         float d;
         const int q = quant_block32(o[i], &d);
-        q8[(size_t)r * kHidden + c] = (int8_t)q;
-        if ((c & 31) == 0) d8[(size_t)r * (kHidden / 32) + (c >> 5)] = d;
+        q8[q8t_at(r, c, kHidden)] = (int8_t)q;
+        if ((c & 31) == 0) d8[d8t_at(r, c >> 5, kHidden)] = d;
     }
 }
 

@@ -205,14 +205,17 @@ struct Chunk {
 // non-temporal hint measured slower end to end: 0.83 vs 0.78 ms per 256-row prefill)
 constexpr int kCpolW = 0;
 
-template <int NT, bool A8>
+// AT: W8A8 activations in the matrix-core order (q8t_at / d8t_at): a block of the
+// wave's 16 rows is one 512-byte unit and 16 scales
+template <int NT, bool A8, bool AT>
 __device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
+    constexpr int QB = AT ? 512 : 32, DB = AT ? 64 : 4;  // bytes from one block to the next
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
         if constexpr (A8) {
-            const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.a, s.va + 32 * j, 32 * b0, 0);
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.a, s.va + QB * j, QB * b0, 0);
             c.xq[j] = ((uint64_t)q[1] << 32) | q[0];
-            c.xd[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s.ad, s.vad + 4 * j, 4 * b0, 0));
+            c.xd[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s.ad, s.vad + DB * j, DB * b0, 0));
         } else {
             // the whole vector is reinterpreted: a bit cast of one element of the
             // builtin's vector type reads element 0
@@ -246,9 +249,9 @@ __device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, const Src
     }
 }
 
-template <int NT, bool A8, bool TL>
+template <int NT, bool A8, bool TL, bool AT>
 __device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
-    load_chunk_a<NT, A8>(c, b0, s);
+    load_chunk_a<NT, A8, AT>(c, b0, s);
     load_chunk_b<NT, A8, TL>(c, b0, s);
 }
 
@@ -306,7 +309,7 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
 // quarter (at most 8 blocks: K <= 1024) is loaded first, the row sums of the
 // 4 waves meet in LDS (two passes: mean, then the squared deviations), and the
 // values are normalised in registers with ln_w / ln_b staged in LDS.
-template <int EPI, int KV, int NT, bool A8, bool LN, bool TL>
+template <int EPI, int KV, int NT, bool A8, bool LN, bool TL, bool AT>
 __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
     GT_START
@@ -326,7 +329,14 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     Src<A8> src;
     {
         const uint32_t a_elems = (uint32_t)((g.M - 1) * g.lda + g.K);
-        if constexpr (A8) {
+        if constexpr (A8 && AT) {  // K = lda; rows padded to 16
+            const uint32_t units = (uint32_t)((g.M + 15) / 16) * (uint32_t)(g.lda / 32);
+            const int unit = (m_base / 16) * (g.lda / 32) + kb0;  // this row tile's first block
+            src.a = make_rsrc(g.a8, units * 512u);
+            src.ad = make_rsrc(g.d8, units * 64u);
+            src.va = unit * 512 + 8 * lane;
+            src.vad = unit * 64 + 4 * l16;
+        } else if constexpr (A8) {
             src.a = make_rsrc(g.a8, a_elems);
             src.ad = make_rsrc(g.d8, 4u * (uint32_t)((g.M - 1) * (g.lda / 32) + nb_all));
             src.va = arow * g.lda + 8 * kq + 32 * kb0;
@@ -361,8 +371,8 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         // loaded value waits for that load, and loads complete in order)
         constexpr int LNR = (4 * 2 * KB * 32 + 255) / 256;
         Chunk<NT, A8> ca, cb;
-        load_chunk_a<NT, A8>(ca, 0, src);
-        load_chunk_a<NT, A8>(cb, KB, src);
+        load_chunk_a<NT, A8, AT>(ca, 0, src);
+        load_chunk_a<NT, A8, AT>(cb, KB, src);
         float lw[LNR], lb[LNR];
 #pragma unroll
         for (int i = 0; i < LNR; ++i) {
@@ -437,13 +447,13 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         if (KB < nb) mfma_chunk<NT, A8>(cb, KB, nb, kq, acc);
     } else if (nb > 0) {
         Chunk<NT, A8> ca, cb;
-        load_chunk<NT, A8, TL>(ca, 0, src);
+        load_chunk<NT, A8, TL, AT>(ca, 0, src);
         for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
-            load_chunk<NT, A8, TL>(cb, b0 + KB, src);
+            load_chunk<NT, A8, TL, AT>(cb, b0 + KB, src);
             mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
             if (b0 + KB >= nb) break;
             if (b0 + 2 * KB < nb)  // (uniform) a chunk past the wave's blocks is not requested
-                load_chunk<NT, A8, TL>(ca, b0 + 2 * KB, src);
+                load_chunk<NT, A8, TL, AT>(ca, b0 + 2 * KB, src);
             mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
         }
     }
@@ -481,11 +491,11 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
                 int q0 = (int)rintf(h[2 * b] * id), q1 = (int)rintf(h[2 * b + 1] * id);
                 q0 = q0 < -127 ? -127 : (q0 > 127 ? 127 : q0);
                 q1 = q1 < -127 ? -127 : (q1 > 127 ? 127 : q1);
-                if (m < g.M) {
-                    int8_t *qrow = g.q8_out + (size_t)m * g.N + n_base + 32 * b;
-                    qrow[l16] = (int8_t)q0;
-                    qrow[16 + l16] = (int8_t)q1;
-                    if (l16 == 0) g.d8_out[(size_t)m * (g.N / 32) + n_base / 32 + b] = d;
+                if (m < g.M) {  // in the matrix-core order (q8t_at / d8t_at)
+                    const int k0 = n_base + 32 * b;
+                    g.q8_out[q8t_at(m, k0 + l16, g.N)] = (int8_t)q0;
+                    g.q8_out[q8t_at(m, k0 + 16 + l16, g.N)] = (int8_t)q1;
+                    if (l16 == 0) g.d8_out[d8t_at(m, k0 >> 5, g.N)] = d;
                 }
             }
             GT_END
@@ -510,7 +520,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     GT_END
 }
 
-template <int EPI, int KV, bool A8, bool LN, bool TL>
+template <int EPI, int KV, bool A8, bool LN, bool TL, bool AT>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int mt = (g.M + 15) / 16;
@@ -518,22 +528,24 @@ hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     // the widest column tile that still gives ~192 workgroups (a quantising epilogue needs
     // whole 32-blocks in a tile: at least 32 columns)
     if (g.N % 64 == 0 && (g.N / 64) * mt * kz >= 192) {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8, LN, TL>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 4, A8, LN, TL, AT>), dim3(g.N / 64, mt, kz), dim3(256), 0, s, g);
     } else if (g.N % 32 == 0 && ((g.N / 32) * mt * kz >= 192 || g.q8_out != nullptr)) {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8, LN, TL>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 2, A8, LN, TL, AT>), dim3(g.N / 32, mt, kz), dim3(256), 0, s, g);
     } else {
-        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN, TL>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN, TL, AT>), dim3(g.N / 16, mt, kz), dim3(256), 0, s, g);
     }
     return hipGetLastError();
 }
 
 template <int EPI, int KV, bool TL>
 hipError_t launch_l(const GemmArgs &g, hipStream_t s) {
-    if (g.a8 != nullptr) return launch_nt<EPI, KV, true, false, TL>(g, s);
+    if (g.a8 != nullptr)
+        return g.a8_tiled ? launch_nt<EPI, KV, true, false, TL, true>(g, s)
+                          : launch_nt<EPI, KV, true, false, TL, false>(g, s);
     if constexpr (EPI != EPI_PART) {
-        if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL>(g, s);
+        if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL, false>(g, s);
     }
-    return launch_nt<EPI, KV, false, false, TL>(g, s);
+    return launch_nt<EPI, KV, false, false, TL, false>(g, s);
 }
 
 template <int EPI, int KV>
@@ -580,6 +592,7 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
         if (!g.part || z > 16 || z > nb) return hipErrorInvalidValue;
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
+    if (g.a8_tiled && (g.a8 == nullptr || g.lda != g.K)) return hipErrorInvalidValue;
     if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || g.ldy < g.N)) return hipErrorInvalidValue;
     // LayerNorm prologue: fp32 rows of at most 4 waves x 2 chunks of blocks, whole K in the workgroup
     if (g.ln_w != nullptr && (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))

@@ -676,10 +676,17 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * (size_t)m), "hipMalloc(prefill)");
         const int kz = std::max(gemm_ksplit(m, kHidden, kHidden), gemm_ksplit(m, kHidden, kFF));
         hip_check(hipMalloc(&pre_part_, sizeof(float) * kHidden * (size_t)m * kz), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_q8_, (size_t)kHidden * m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_d8_, sizeof(float) * (kHidden / 32) * (size_t)m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_q8h_, (size_t)kFF * m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_d8h_, sizeof(float) * (kFF / 32) * (size_t)m), "hipMalloc(prefill)");
+        // W8A8 operands in the matrix-core order: rows padded to 16 (the padding rows are
+        // read by the GEMMs and never stored; zeroed once)
+        const size_t m16 = (size_t)(m + 15) / 16 * 16;
+        hip_check(hipMalloc(&pre_q8_, (size_t)kHidden * m16), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_d8_, sizeof(float) * (kHidden / 32) * m16), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_q8h_, (size_t)kFF * m16), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_d8h_, sizeof(float) * (kFF / 32) * m16), "hipMalloc(prefill)");
+        hip_check(hipMemsetAsync(pre_q8_, 0, (size_t)kHidden * m16, stream_), "memset(prefill)");
+        hip_check(hipMemsetAsync(pre_d8_, 0, sizeof(float) * (kHidden / 32) * m16, stream_), "memset(prefill)");
+        hip_check(hipMemsetAsync(pre_q8h_, 0, (size_t)kFF * m16, stream_), "memset(prefill)");
+        hip_check(hipMemsetAsync(pre_d8h_, 0, sizeof(float) * (kFF / 32) * m16, stream_), "memset(prefill)");
         rows_cap_ = m;
     }
     hip_check(hipMemcpyAsync(rows_dev_, rows, sizeof(int) * 17 * (size_t)m, hipMemcpyHostToDevice, stream_), "rows h2d");
@@ -697,9 +704,10 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     int8_t *q8 = a8 ? pre_q8_ : nullptr;
     float *d8 = a8 ? pre_d8_ : nullptr;
     auto operand = [&](GemmArgs &g) {
-        if (a8) {
+        if (a8) {  // written in the matrix-core order by the kernel before
             g.a8 = pre_q8_;
             g.d8 = pre_d8_;
+            g.a8_tiled = true;
         }
     };
     hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, pre_a_, m, s, nullptr, q8, d8), "prefill ln1");
@@ -741,6 +749,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         if (a8) {
             f2.a8 = pre_q8h_;
             f2.d8 = pre_d8h_;
+            f2.a8_tiled = true;
         }
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
         const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce

@@ -362,6 +362,21 @@ __device__ __forceinline__ int quant_block32(float x, float *d_out) {
     return q;
 }
 
+// W8A8 activations as the prefill writes them for its GEMMs (GemmArgs::a8_tiled), in
+// the order the matrix cores take them: an M x K int8 matrix is one 512-byte unit per
+// 16 rows and 32-column block, unit (m / 16) * (K / 32) + k / 32, in which row m % 16,
+// columns 8j .. 8j + 7 of the block are the 8 bytes at 8 * (m % 16 + 16 j) -- the A
+// operand of lane m % 16 + 16 j of a 16x16x32 MFMA -- so a GEMM reads a block of 16
+// rows as 4 whole cache lines; the block scales are 16 floats per unit.  Buffers hold
+// the row count rounded up to 16.
+__device__ __forceinline__ size_t q8t_at(int m, int k, int K) {
+    const size_t unit = (size_t)(m >> 4) * (K >> 5) + (k >> 5);
+    return unit * 512 + 8 * ((m & 15) + 16 * ((k & 31) >> 3)) + (k & 7);
+}
+__device__ __forceinline__ size_t d8t_at(int m, int blk, int K) {
+    return ((size_t)(m >> 4) * (K >> 5) + blk) * 16 + (m & 15);
+}
+
 // gelu_new (reference csrc/src/llm.cpp:22-25)
 __device__ __forceinline__ float gelu_new(float v) {
 #pragma clang fp contract(off)

@@ -94,7 +94,8 @@ struct AttnArgs {
     // keys [64 s, 64 s + 64) to part[(h * splits + s) * kPartStride]: o[64], running max m,
     // sum l; splits = ceil(max_keys / 64).  A consumer merges them (PRO_AMERGE).
     float *part = nullptr;
-    // optional W8A8 copy of the (normalised) output rows: q8[r][768] int8, d8[r][24] block scales
+    // optional W8A8 copy of the (normalised) output rows: int8 + block scales in the
+    // matrix-core order (q8t_at / d8t_at, rows padded to 16)
     int8_t *q8 = nullptr;
     float *d8 = nullptr;
     const DevState *state = nullptr;
@@ -162,14 +163,17 @@ struct GemmArgs {
     float *part = nullptr;
     int ksplit = 0;
     // W8A8 (reference gemv_avx2.cpp:105-121 per block): when a8 is non-null the activations are
-    // int8 a8[M][lda] with fp32 block scales d8[M][lda / 32], and `a` is unused
+    // int8 a8[M][lda] with fp32 block scales d8[M][lda / 32], and `a` is unused;
+    // a8_tiled: a8 / d8 are in the matrix-core order instead (q8t_at / d8t_at with K = lda)
     const int8_t *a8 = nullptr;
     const float *d8 = nullptr;
+    bool a8_tiled = false;
     // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
     // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
     const float *ln_w = nullptr, *ln_b = nullptr;
     // EPI_GELU with q8_out (16*NT >= 32 columns per tile): the stored rows are also quantised
-    // per 32-block (quantize_activation, quant.cpp:45) into q8_out[M][N] / d8_out[M][N / 32]
+    // per 32-block (quantize_activation, quant.cpp:45) into q8_out / d8_out in the matrix-core
+    // order (q8t_at / d8t_at with K = N, rows padded to 16)
     int8_t *q8_out = nullptr;
     float *d8_out = nullptr;
 };
@@ -187,6 +191,8 @@ int gemm_ksplit(int M, int N, int K);
 hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
                                 int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
                                 const unsigned char *mask, hipStream_t s, int8_t *q8 = nullptr, float *d8 = nullptr);
+// (q8 / d8 of launch_resid_ln_rows and launch_ln_rows: the W8A8 copy of out in the
+// matrix-core order, q8t_at / d8t_at, rows padded to 16)
 
 // W8A8 activation quantisation of rows (quant.cpp:28-54): q8[r][K] int8 and d8[r][K/32]
 // fp32 block scales from x[r * x_stride + k].  K % 256 == 0.
