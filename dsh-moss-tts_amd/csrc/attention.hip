@@ -521,7 +521,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
             if ((d4 & 7) == 0) a.d8[d8t_at(m, 2 * h + (d4 >> 3), kHidden)] = d;
         }
     }
-    if (m >= a.rows) return;
+    if (m >= a.rows || a.out == nullptr) return;  // (no fp32 rows when only the W8A8 copy is read)
     float *orow = (float *)a.out + (size_t)m * a.out_stride + h * kHeadDim + 4 * d4;
     *reinterpret_cast<float4 *>(orow) = make_float4(ov[0], ov[1], ov[2], ov[3]);
 }
@@ -547,7 +547,8 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
 
 hipError_t launch_attn_tiles(const AttnArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (a.heads != kHeads || a.rows <= 0 || a.max_keys <= 0 || a.page_size < a.max_keys || !a.out || a.out_f16 ||
+    if (a.heads != kHeads || a.rows <= 0 || a.max_keys <= 0 || a.page_size < a.max_keys || (!a.out && !a.q8) ||
+        a.out_f16 ||
         !a.q || !a.k_pool || !a.v_pool || a.part || a.page_table || a.row_pos || a.row_stream || a.chunks ||
         a.pos_stride != 1 || a.pos0 < 0 || a.pos0 + a.rows > a.max_keys || a.q_stride % 4 || a.out_stride % 4 ||
         (a.q8 != nullptr && !a.d8))

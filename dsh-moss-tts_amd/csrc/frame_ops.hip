@@ -423,8 +423,9 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stri
 #pragma unroll
     for (int i = 0; i < 3; ++i) v[i] = xr[t + 256 * i];
     layernorm_768(v, w, b, o, red);
+    if (out != nullptr)  // (null: only the W8A8 copy is read)
 #pragma unroll
-    for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+        for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
     if (q8 != nullptr) quant_row_768(o, r, q8, d8);
 }
 
@@ -472,8 +473,9 @@ __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, i
     if (ln_w == nullptr || (mask != nullptr && !mask[r])) return;
     float o[3];
     layernorm_768(v, ln_w, ln_b, o, red);
+    if (out != nullptr)  // (null: only the W8A8 copy is read)
 #pragma unroll
-    for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+        for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
     if (q8 != nullptr) quant_row_768(o, r, q8, d8);
 }
 
@@ -795,7 +797,7 @@ hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const fl
                           hipStream_t s, const unsigned char *mask, int8_t *q8, float *d8) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    if (q8 && !d8) return hipErrorInvalidValue;
+    if ((q8 && !d8) || (!out && !q8)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask, q8, d8);
     return hipGetLastError();
 }
@@ -805,7 +807,7 @@ hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const f
                                 const unsigned char *mask, hipStream_t s, int8_t *q8, float *d8) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x || (ln_w && (!ln_b || !out)) ||
+    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x || (ln_w && (!ln_b || (!out && !q8))) ||
         (q8 && (!d8 || !ln_w)))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(resid_ln_rows_kernel, dim3(rows), dim3(256), 0, s, part, ksplit, rows, bias, resid,

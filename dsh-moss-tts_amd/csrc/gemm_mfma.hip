@@ -476,7 +476,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
                 v += redf[4 * ((3 * NT + t) * 64)];
                 const int n = n_base + 16 * t + l16;
                 h[t] = gelu_new(v + g.bias[n]);
-                if (m < g.M) g.y[(size_t)m * g.ldy + n] = h[t];
+                if (m < g.M && g.y != nullptr) g.y[(size_t)m * g.ldy + n] = h[t];
             }
 #pragma unroll
             for (int b = 0; b < NT / 2; ++b) {
@@ -593,7 +593,9 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
     if (g.a8_tiled && (g.a8 == nullptr || g.lda != g.K)) return hipErrorInvalidValue;
-    if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || g.ldy < g.N)) return hipErrorInvalidValue;
+    if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || (g.y && g.ldy < g.N)))
+        return hipErrorInvalidValue;
+    if (g.q8_out == nullptr && epi != EPI_PART && epi != EPI_QKV && !g.y) return hipErrorInvalidValue;
     // LayerNorm prologue: fp32 rows of at most 4 waves x 2 chunks of blocks, whole K in the workgroup
     if (g.ln_w != nullptr && (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))
         return hipErrorInvalidValue;

@@ -710,7 +710,9 @@ void Model::prefill(const int32_t *rows, int n, int start) {
             g.a8_tiled = true;
         }
     };
-    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, pre_a_, m, s, nullptr, q8, d8), "prefill ln1");
+    // under W8A8 the GEMMs read only the int8 copies: the fp32 rows are not written
+    float *a_rows = a8 ? nullptr : pre_a_;
+    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, a_rows, m, s, nullptr, q8, d8), "prefill ln1");
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
@@ -723,7 +725,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "prefill qkv");
         AttnArgs t;
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
-        t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = pre_o_;
+        t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = a8 ? nullptr : pre_o_;
         t.q8 = q8; t.d8 = d8;
         hip_check(launch_attn_tiles(t, kvt_, s), "prefill attention");
         GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
@@ -732,11 +734,11 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         operand(p);
         hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
         hip_check(launch_resid_ln_rows(pre_part_, p.ksplit, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
-                                       pre_a_, nullptr, s, q8, d8),
+                                       a_rows, nullptr, s, q8, d8),
                   "prefill proj reduce + ln2");
         GemmArgs f1;
         f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
-        f1.y = pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+        f1.y = a8 ? nullptr : pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
         operand(f1);
         if (a8) {  // fc_out's int8 operand, quantised in fc_in's epilogue
             f1.q8_out = pre_q8h_;
@@ -754,7 +756,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
         const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce
         hip_check(launch_resid_ln_rows(pre_part_, f2.ksplit, m, L.fc_out_b, pre_x_, kHidden, pre_x_,
-                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, pre_a_,
+                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, a_rows,
                                        nullptr, s, last ? nullptr : q8, last ? nullptr : d8),
                   "prefill fc_out reduce");
     }

@@ -171,7 +171,7 @@ struct GemmArgs {
     // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
     // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
     const float *ln_w = nullptr, *ln_b = nullptr;
-    // EPI_GELU with q8_out (16*NT >= 32 columns per tile): the stored rows are also quantised
+    // EPI_GELU with q8_out (16*NT >= 32 columns per tile; y may then be null: no fp32 rows): the stored rows are also quantised
     // per 32-block (quantize_activation, quant.cpp:45) into q8_out / d8_out in the matrix-core
     // order (q8t_at / d8t_at with K = N, rows padded to 16)
     int8_t *q8_out = nullptr;
@@ -192,7 +192,7 @@ hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const f
                                 int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
                                 const unsigned char *mask, hipStream_t s, int8_t *q8 = nullptr, float *d8 = nullptr);
 // (q8 / d8 of launch_resid_ln_rows and launch_ln_rows: the W8A8 copy of out in the
-// matrix-core order, q8t_at / d8t_at, rows padded to 16)
+// matrix-core order, q8t_at / d8t_at, rows padded to 16; out may be null when q8 is set)
 
 // W8A8 activation quantisation of rows (quant.cpp:28-54): q8[r][K] int8 and d8[r][K/32]
 // fp32 block scales from x[r * x_stride + k].  K % 256 == 0.
