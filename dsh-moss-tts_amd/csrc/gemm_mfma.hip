@@ -126,25 +126,48 @@ __device__ __forceinline__ EpiRow epi_row(const GemmArgs &g, int m, int n_base) 
     return r;
 }
 
-template <int EPI, int KV>
-__device__ __forceinline__ void gemm_finish(const GemmArgs &g, const EpiRow &r, int n, float v, float partner) {
+// The epilogue's operands of a lane's NT values (column n_base + 16t + l16 of its row):
+// loaded when the workgroup starts, so they are in registers when the sums are.
+template <int NT>
+struct EpiOps {
+    float b[NT], bp[NT], c[NT], sn[NT], res[NT];  // bias, partner column's bias, RoPE, residual
+};
+
+template <int EPI, int NT>
+__device__ __forceinline__ void epi_load(const GemmArgs &g, const EpiRow &r, int n_base, int l16, EpiOps<NT> &o) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = n_base + 16 * t + l16;
+        if constexpr (EPI == EPI_RESID || EPI == EPI_GELU || EPI == EPI_QKV) o.b[t] = g.bias[n];
+        if constexpr (EPI == EPI_RESID) o.res[t] = r.res[n];
+        if constexpr (EPI == EPI_QKV) {
+            if (r.sec < 2) {  // uniform
+                const int d = n & 63;
+                o.bp[t] = g.bias[n ^ 1];
+                o.c[t] = r.rc[d >> 1];
+                o.sn[t] = r.rs[d >> 1];
+            }
+        }
+    }
+}
+
+template <int EPI, int KV, int NT>
+__device__ __forceinline__ void gemm_finish(const EpiRow &r, const EpiOps<NT> &o, int t, int n, float v,
+                                            float partner) {
 #pragma clang fp contract(off)
     if constexpr (EPI == EPI_PART || EPI == EPI_F32) {
         r.out[n] = v;
     } else if constexpr (EPI == EPI_RESID) {
-        const float xin = r.res[n];
-        r.out[n] = xin + (v + g.bias[n]);
+        r.out[n] = o.res[t] + (v + o.b[t]);
     } else if constexpr (EPI == EPI_GELU) {
-        r.out[n] = gelu_new(v + g.bias[n]);
+        r.out[n] = gelu_new(v + o.b[t]);
     } else {  // EPI_QKV: bias, RoPE at the row's position, q -> q_out, k/v -> KV pages
-        const float val = v + g.bias[n];
+        const float val = v + o.b[t];
         const int d = n & 63;
         float out = val;
         if (r.sec < 2) {
-            const float pv = partner + g.bias[n ^ 1];
-            const float c = r.rc[d >> 1];
-            const float sn = r.rs[d >> 1];
-            const float p0 = val * c, p1 = pv * sn;
+            const float pv = partner + o.bp[t];
+            const float p0 = val * o.c[t], p1 = pv * o.sn[t];
             out = (d & 1) == 0 ? p0 - p1 : p0 + p1;
         }
         if (r.sec == 0) {
@@ -326,6 +349,12 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     const int nb = z0 + ((wave + 1) * nbz) / 4 - kb0;  // 0 when the slice has fewer than 4 blocks
     const int arow = min(m_base + l16, g.M - 1);      // rows past M read row M-1, never stored
     const int krow = l16 & 3;
+    // the epilogue: wave w finishes row 4kq + w of every column subtile; its operands
+    // are requested first (loads complete in order, so these never delay the operands')
+    const int erow = m_base + 4 * kq + wave;
+    const EpiRow er = epi_row<EPI, KV>(g, erow, n_base);
+    EpiOps<NT> eo;
+    epi_load<EPI, NT>(g, er, n_base, l16, eo);
     Src<A8> src;
     {
         const uint32_t a_elems = (uint32_t)((g.M - 1) * g.lda + g.K);
@@ -465,7 +494,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         if (g.q8_out != nullptr) {  // uniform
             // wave w finishes row 4kq + w of every subtile: a 32-block is subtiles (2b, 2b + 1)
             // across the 16 lanes of a kq group, so its amax is a 16-lane reduction
-            const int i = wave, m = m_base + 4 * kq + i;
+            const int i = wave, m = erow;
             float h[NT];
             const float *redf = (const float *)&red[0][0][lane] + i;
 #pragma unroll
@@ -475,7 +504,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
                 v += redf[4 * ((2 * NT + t) * 64)];
                 v += redf[4 * ((3 * NT + t) * 64)];
                 const int n = n_base + 16 * t + l16;
-                h[t] = gelu_new(v + g.bias[n]);
+                h[t] = gelu_new(v + eo.b[t]);
                 if (m < g.M && g.y != nullptr) g.y[(size_t)m * g.ldy + n] = h[t];
             }
 #pragma unroll
@@ -502,10 +531,9 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             return;
         }
     }
-    // wave w finishes row 4kq + w of every column subtile (component w of each
-    // lane's partials: one 4-byte LDS read each, at an offset uniform in the wave)
-    const int i = wave, m = m_base + 4 * kq + i;
-    const EpiRow r = epi_row<EPI, KV>(g, m, n_base);
+    // component w of each lane's partials: one 4-byte LDS read each, at an offset
+    // uniform in the wave
+    const int i = wave, m = erow;
     const float *redf = (const float *)&red[0][0][lane] + i;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -515,7 +543,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         v += redf[4 * ((3 * NT + t) * 64)];
         const int n = n_base + 16 * t + l16;
         const float partner = xshfl<1>(v);  // column n ^ 1, same row
-        if (m < g.M) gemm_finish<EPI, KV>(g, r, n, v, partner);
+        if (m < g.M) gemm_finish<EPI, KV, NT>(er, eo, t, n, v, partner);
     }
     GT_END
 }
