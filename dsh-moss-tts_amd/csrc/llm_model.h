@@ -64,6 +64,9 @@ struct LayerW {
     const uint8_t *attn_wm, *proj_wm, *fc_in_wm, *fc_out_wm;
 };
 
+// K slices of the W8A8 prefill's fc_out GEMM from 128 rows on
+constexpr int kPrefillFcOutSplit = 4;
+
 class Model {
 public:
     Model(const void *blob, size_t bytes, const moss_hip_llm_options &opt);
