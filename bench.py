@@ -196,7 +196,7 @@ def prefill_rows(seed: int = 7):
     return mf.text_rows(rng.integers(0, mf.VOCAB, PREFILL_ROWS))  # codes = pad, as make_text_row
 
 
-def bench_prefill(blob, reps: int = 5, a16: bool = False):
+def bench_prefill(blob, reps: int = 20, a16: bool = False):
     """256-row prefill from position 0 (KV written for decode), MFMA GEMMs: W8A8 (int8
     activations, the reference's prefill) by default, W8A16 with a16=True."""
     import torch
