@@ -314,8 +314,9 @@ template <int KV>
 hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     // waves per workgroup from the key capacity the launch is sized for (fixed
-    // for a captured graph): one wave per 64 keys up to 4 waves, which then take
-    // several spans each (measured faster than 8 or 16 waves at 64 streams x ~540 keys)
+    // for a captured graph): one wave up to 64 keys, else 2 waves taking every
+    // other span (at 64 streams x ~540 keys: 47.9k frames/s against 47.6k with
+    // 4 waves; 8 or 16 waves measured slower still)
     const int spans = (a.max_keys + 63) / 64;
     if (a.part != nullptr) {  // split-KV: one single-wave workgroup per (head, span)
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, true>), dim3(a.heads, spans), dim3(64), 0, s, a);
@@ -330,7 +331,7 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
     if (spans <= 1)
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, false>), grid, dim3(64), 0, s, a);
     else
-        hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((attn_rows_kernel<KV, 2, false>), grid, dim3(128), 0, s, a);
     return hipGetLastError();
 }
 
