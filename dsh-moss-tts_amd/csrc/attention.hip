@@ -298,7 +298,9 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     }
     const float res = O / L;
     const size_t oi = (size_t)r * a.out_stride + h * kHeadDim + lane;
-    if (a.out_f16)
+    if (a.out_hl != nullptr)  // for the next GEMM: hi / lo halves in the matrix-core order
+        store_hl(a.out_hl, r, h * kHeadDim + lane, kHidden, res);
+    else if (a.out_f16)
         ((__half *)a.out)[oi] = __float2half_rn(res);
     else
         ((float *)a.out)[oi] = res;
@@ -522,7 +524,13 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
             if ((d4 & 7) == 0) a.d8[d8t_at(m, 2 * h + (d4 >> 3), kHidden)] = d;
         }
     }
-    if (m >= a.rows || a.out == nullptr) return;  // (no fp32 rows when only the W8A8 copy is read)
+    if (m >= a.rows) return;
+    if (a.out_hl != nullptr) {  // for the next GEMM: hi / lo halves in the matrix-core order
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store_hl(a.out_hl, m, h * kHeadDim + 4 * d4 + e, kHidden, ov[e]);
+        return;
+    }
+    if (a.out == nullptr) return;  // (no fp32 rows when only the W8A8 copy is read)
     float *orow = (float *)a.out + (size_t)m * a.out_stride + h * kHeadDim + 4 * d4;
     *reinterpret_cast<float4 *>(orow) = make_float4(ov[0], ov[1], ov[2], ov[3]);
 }
@@ -531,9 +539,10 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
 
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (a.heads <= 0 || a.rows <= 0 || a.max_keys <= 0 || a.page_size <= 0 || (!a.out && !a.part) || !a.q ||
-        !a.k_pool || !a.v_pool)
+    if (a.heads <= 0 || a.rows <= 0 || a.max_keys <= 0 || a.page_size <= 0 || (!a.out && !a.part && !a.out_hl) ||
+        !a.q || !a.k_pool || !a.v_pool)
         return hipErrorInvalidValue;
+    if (a.out_hl != nullptr && (a.part != nullptr || a.chunks != 0 || a.heads != kHeads)) return hipErrorInvalidValue;
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
     if (a.q8 != nullptr && (!a.d8 || a.part != nullptr || a.heads != kHeads)) return hipErrorInvalidValue;
     // every slice holds at least one live span and reaches the end of the kernel (no stop
@@ -548,7 +557,8 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
 
 hipError_t launch_attn_tiles(const AttnArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (a.heads != kHeads || a.rows <= 0 || a.max_keys <= 0 || a.page_size < a.max_keys || (!a.out && !a.q8) ||
+    if (a.heads != kHeads || a.rows <= 0 || a.max_keys <= 0 || a.page_size < a.max_keys ||
+        (!a.out && !a.q8 && !a.out_hl) ||
         a.out_f16 ||
         !a.q || !a.k_pool || !a.v_pool || a.part || a.page_table || a.row_pos || a.row_stream || a.chunks ||
         a.pos_stride != 1 || a.pos0 < 0 || a.pos0 + a.rows > a.max_keys || a.q_stride % 4 || a.out_stride % 4 ||

@@ -5,6 +5,10 @@
 #include <cstring>
 
 namespace mh {
+namespace {
+// a float buffer holding fp16 hi / lo halves in the matrix-core order (hlt_at)
+inline uint8_t *hl(float *p) { return reinterpret_cast<uint8_t *>(p); }
+}  // namespace
 
 Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
     : model_(model), w_(model.weights()), S_(max_streams), cap_(capacity), kvt_(kv) {
@@ -52,11 +56,14 @@ Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
         hip_check(hipMalloc(p, n * sizeof(float)), "hipMalloc(batch)");
         hip_check(hipMemset(*p, 0, n * sizeof(float)), "memset(batch)");
     };
+    // a_, o_ and h_ are read only by GEMMs, as fp16 hi / lo halves in the matrix-core
+    // order (hlt_at: 4 bytes a value, rows padded to 16)
+    const size_t s16 = (size_t)(S_ + 15) / 16 * 16;
     fm(&x_, (size_t)S_ * kHidden);
-    fm(&a_, (size_t)S_ * kHidden);
+    fm(&a_, s16 * kHidden);
     fm(&q_, (size_t)S_ * kHidden);
-    fm(&o_, (size_t)S_ * kHidden);
-    fm(&h_, (size_t)S_ * kFF);
+    fm(&o_, s16 * kHidden);
+    fm(&h_, s16 * kFF);
     fm(&hidden_, (size_t)S_ * kHidden);
     fm(&lres_, (size_t)S_ * kHidden);
     fm(&next_in_, (size_t)S_ * kHidden);
@@ -209,24 +216,24 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     if (attn) {
         AttnArgs t;
         t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen; t.stream_stride = 1;
-        t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out = o_;
+        t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out_hl = hl(o_);
         hip_check(launch_attn(t, KV_F32, s), "local attention");
     }
     GemmArgs p;
-    p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
+    p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = hl(o_); p.lda = kHidden; p.M = n;
     p.y = lres_; p.ldy = kHidden; p.bias = L.proj_b; p.resid_in = in; p.resid_stride = in_stride;
     hip_check(launch_gemm(p, EPI_RESID, KV_F32, s), "local proj");
     GemmArgs f1;
     f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = lres_; f1.lda = kHidden; f1.M = n;
     f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
-    f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+    f1.y_hl = hl(h_); f1.bias = L.fc_in_b;
     hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
     GemmArgs f2;  // split K: the reduce adds bias and residual, then the local ln_f for the head
-    f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
+    f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = hl(h_); f2.lda = kFF; f2.M = n;
     f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
     hip_check(launch_gemm(f2, EPI_PART, KV_F32, s), "local fc_out");
-    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b, a_,
-                                   nullptr, s),
+    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b,
+                                   nullptr, nullptr, s, nullptr, nullptr, hl(a_)),
               "local fc_out reduce + ln_f");
 }
 
@@ -260,14 +267,15 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
             pa.lk = qkv.lk;
             pa.lv = qkv.lv;
             pa.lpos = ch + 1;
-            pa.o = o_;
+            pa.o_hl = hl(o_);
             hip_check(launch_local_pick_attn(pa, n, s), "pick + local attention");
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1, false);
         } else {
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
         }
         GemmArgs hd;  // the tied audio head on the local ln_f of the step's output
-        hd.w = w_.aemb[ch]; hd.wm = w_.aemb_m[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a = a_; hd.lda = kHidden; hd.M = n;
+        hd.w = w_.aemb[ch]; hd.wm = w_.aemb_m[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a_hl = hl(a_); hd.lda = kHidden;
+        hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
         hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
         if (greedy && ch + 1 < kNVq) continue;  // picked by the next position's launch
@@ -287,41 +295,43 @@ void Batch::enqueue_global(hipStream_t s, int n) {
     e.wte = w_.wte;
     for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = w_.aemb[ch];
     hip_check(launch_embed_rows(e, row_, n, x_, s), "embed");
-    hip_check(launch_ln_rows(x_, kHidden, w_.global[0].ln1_w, w_.global[0].ln1_b, a_, n, s), "ln1");
+    hip_check(launch_ln_rows(x_, kHidden, w_.global[0].ln1_w, w_.global[0].ln1_b, nullptr, n, s, nullptr, nullptr,
+                             nullptr, hl(a_)),
+              "ln1");
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = w_.global[l];
         void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
         void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
-        GemmArgs q;  // on LN1(x) in a_
-        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a = a_; q.lda = kHidden; q.M = n;
+        GemmArgs q;  // on LN1(x) in a_ (hi / lo halves)
+        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a_hl = hl(a_); q.lda = kHidden; q.M = n;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
         q.page_table = table_; q.table_stride = pages_; q.page_size = kPage;
         q.stream_stride = 1; q.row_pos = pos_d_; q.row_active = active_; q.rope_cos = rc; q.rope_sin = rs;
         hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "qkv");
         AttnArgs t;
         t.q = q_; t.k_pool = kp; t.v_pool = vp; t.page_table = table_; t.table_stride = pages_; t.page_size = kPage;
-        t.stream_stride = 1; t.row_pos = pos_d_; t.rows = n; t.max_keys = cap_; t.out = o_;
+        t.stream_stride = 1; t.row_pos = pos_d_; t.rows = n; t.max_keys = cap_; t.out_hl = hl(o_);
         hip_check(launch_attn(t, kvt_, s), "attention");
         GemmArgs p;  // x += proj + b
-        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a = o_; p.lda = kHidden; p.M = n;
+        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = hl(o_); p.lda = kHidden; p.M = n;
         p.y = x_; p.ldy = kHidden; p.bias = L.proj_b;
         hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "proj");
         GemmArgs f1;  // LN2 in the prologue
         f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = x_; f1.lda = kHidden; f1.M = n;
         f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
-        f1.y = h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+        f1.y_hl = hl(h_); f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
         GemmArgs f2;  // split K; the reduce adds bias and residual
-        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a = h_; f2.lda = kFF; f2.M = n;
+        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = hl(h_); f2.lda = kFF; f2.M = n;
         f2.part = part_; f2.ksplit = gemm_ksplit(n, kHidden, kFF);
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
         // then LN1 of the next layer into a_, or ln_f into hidden (active streams only)
         const bool last = l + 1 == kLayers;
         hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, x_, kHidden, x_,
                                        last ? w_.lnf_w : w_.global[l + 1].ln1_w,
-                                       last ? w_.lnf_b : w_.global[l + 1].ln1_b, last ? hidden_ : a_,
-                                       last ? active_ : nullptr, s),
+                                       last ? w_.lnf_b : w_.global[l + 1].ln1_b, last ? hidden_ : nullptr,
+                                       last ? active_ : nullptr, s, nullptr, nullptr, last ? nullptr : hl(a_)),
                   "fc_out reduce + ln");
     }
     hip_check(launch_advance_rows(st, n, s), "advance");

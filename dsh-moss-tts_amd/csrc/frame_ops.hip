@@ -414,7 +414,8 @@ __device__ __forceinline__ void quant_row_768(const float (&o)[3], int r, int8_t
 }
 
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stride, const float *w, const float *b,
-                                                      float *out, const unsigned char *mask, int8_t *q8, float *d8) {
+                                                      float *out, const unsigned char *mask, int8_t *q8, float *d8,
+                                                      uint8_t *out_hl) {
     __shared__ float red[4];
     const int r = blockIdx.x, t = threadIdx.x;
     if (mask != nullptr && !mask[r]) return;
@@ -423,9 +424,13 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, int x_stri
 #pragma unroll
     for (int i = 0; i < 3; ++i) v[i] = xr[t + 256 * i];
     layernorm_768(v, w, b, o, red);
-    if (out != nullptr)  // (null: only the W8A8 copy is read)
+    if (out_hl != nullptr) {  // for the next GEMM: hi / lo halves in the matrix-core order
+#pragma unroll
+        for (int i = 0; i < 3; ++i) store_hl(out_hl, r, t + 256 * i, kHidden, o[i]);
+    } else if (out != nullptr) {  // (null: only the W8A8 copy is read)
 #pragma unroll
         for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+    }
     if (q8 != nullptr) quant_row_768(o, r, q8, d8);
 }
 
@@ -445,7 +450,7 @@ __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, i
                                                             const float *bias, const float *resid, int resid_stride,
                                                             float *x, const float *ln_w, const float *ln_b,
                                                             float *out, const unsigned char *mask, int8_t *q8,
-                                                            float *d8) {
+                                                            float *d8, uint8_t *out_hl) {
 #pragma clang fp contract(off)
     __shared__ float red[4];
     const int r = blockIdx.x, t = threadIdx.x;
@@ -473,9 +478,13 @@ __global__ __launch_bounds__(256) void resid_ln_rows_kernel(const float *part, i
     if (ln_w == nullptr || (mask != nullptr && !mask[r])) return;
     float o[3];
     layernorm_768(v, ln_w, ln_b, o, red);
-    if (out != nullptr)  // (null: only the W8A8 copy is read)
+    if (out_hl != nullptr) {  // for the next GEMM: hi / lo halves in the matrix-core order
+#pragma unroll
+        for (int i = 0; i < 3; ++i) store_hl(out_hl, r, t + 256 * i, kHidden, o[i]);
+    } else if (out != nullptr) {  // (null: only the W8A8 copy is read)
 #pragma unroll
         for (int i = 0; i < 3; ++i) out[(size_t)r * kHidden + t + 256 * i] = o[i];
+    }
     if (q8 != nullptr) quant_row_768(o, r, q8, d8);
 }
 
@@ -728,7 +737,10 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
     __builtin_amdgcn_wave_barrier();
     float o = 0.0f;
     for (int k = 0; k < nk; ++k) o = fmaf(es[k], k == a.lpos ? qkv[2][t] : a.lv[(kvrow + k) * kHeadDim + t], o);
-    a.o[(size_t)srow * kHidden + h * kHeadDim + t] = o / l;
+    if (a.o_hl != nullptr)  // for the proj GEMM: hi / lo halves in the matrix-core order
+        store_hl(a.o_hl, srow, h * kHeadDim + t, kHidden, o / l);
+    else
+        a.o[(size_t)srow * kHidden + h * kHeadDim + t] = o / l;
 }
 
 __global__ void advance_rows_kernel(StreamState st, int streams) {
@@ -794,24 +806,25 @@ hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int pa
 }
 
 hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const float *b, float *out, int rows,
-                          hipStream_t s, const unsigned char *mask, int8_t *q8, float *d8) {
+                          hipStream_t s, const unsigned char *mask, int8_t *q8, float *d8, uint8_t *out_hl) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    if ((q8 && !d8) || (!out && !q8)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask, q8, d8);
+    if ((q8 && !d8) || (!out && !q8 && !out_hl)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ln_rows_kernel, dim3(rows), dim3(256), 0, s, x, x_stride, w, b, out, mask, q8, d8, out_hl);
     return hipGetLastError();
 }
 
 hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
                                 int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
-                                const unsigned char *mask, hipStream_t s, int8_t *q8, float *d8) {
+                                const unsigned char *mask, hipStream_t s, int8_t *q8, float *d8, uint8_t *out_hl) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (rows <= 0) return hipSuccess;
-    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x || (ln_w && (!ln_b || (!out && !q8))) ||
+    if (!part || ksplit <= 0 || ksplit > 16 || !bias || !resid || !x ||
+        (ln_w && (!ln_b || (!out && !q8 && !out_hl))) ||
         (q8 && (!d8 || !ln_w)))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(resid_ln_rows_kernel, dim3(rows), dim3(256), 0, s, part, ksplit, rows, bias, resid,
-                       resid_stride, x, ln_w, ln_b, out, mask, q8, d8);
+                       resid_stride, x, ln_w, ln_b, out, mask, q8, d8, out_hl);
     return hipGetLastError();
 }
 
@@ -851,7 +864,8 @@ hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, 
 
 hipError_t launch_local_pick_attn(const PickAttnArgs &a, int streams, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (!a.logits || !a.aemb || !a.next_in || !a.rows || !a.lk || !a.lv || !a.o || streams <= 0 || a.ch < 0 ||
+    if (!a.logits || !a.aemb || !a.next_in || !a.rows || !a.lk || !a.lv || (!a.o && !a.o_hl) || streams <= 0 ||
+        a.ch < 0 ||
         a.ch >= kNVq - 1 || a.lpos != a.ch + 2)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(local_pick_attn_kernel, dim3(kHeads, streams), dim3(256), 0, s, a);

@@ -94,6 +94,8 @@ struct EpiRow {
     const float *rc = nullptr, *rs = nullptr;  // EPI_QKV: RoPE factors at the row's position
     void *pool = nullptr;        // EPI_QKV, k or v section: the row's K/V slot (d = 0) in its page
     int sec = 0;                 // EPI_QKV: 0 q, 1 k, 2 v
+    uint8_t *hl = nullptr;       // EPI_GELU with y_hl: the output as hi/lo halves (hlt_at), row m, width N
+    int m = 0, N = 0;
 };
 
 template <int EPI, int KV>
@@ -103,7 +105,12 @@ __device__ __forceinline__ EpiRow epi_row(const GemmArgs &g, int m, int n_base) 
     if constexpr (EPI == EPI_PART) {
         r.out = g.part + ((size_t)blockIdx.z * g.M + mm) * g.N;
     } else if constexpr (EPI == EPI_F32 || EPI == EPI_GELU) {
-        r.out = g.y + (size_t)mm * g.ldy;
+        r.out = g.y ? g.y + (size_t)mm * g.ldy : nullptr;
+        if constexpr (EPI == EPI_GELU) {
+            r.hl = g.y_hl;
+            r.m = mm;
+            r.N = g.N;
+        }
     } else if constexpr (EPI == EPI_RESID) {
         r.out = g.y + (size_t)mm * g.ldy;
         r.res = g.resid_in ? g.resid_in + (size_t)mm * g.resid_stride : r.out;
@@ -160,7 +167,11 @@ __device__ __forceinline__ void gemm_finish(const EpiRow &r, const EpiOps<NT> &o
     } else if constexpr (EPI == EPI_RESID) {
         r.out[n] = o.res[t] + (v + o.b[t]);
     } else if constexpr (EPI == EPI_GELU) {
-        r.out[n] = gelu_new(v + o.b[t]);
+        const float hv = gelu_new(v + o.b[t]);
+        if (r.hl != nullptr)  // uniform: the next GEMM reads the hi/lo halves
+            store_hl(r.hl, r.m, n, r.N, hv);
+        else
+            r.out[n] = hv;
     } else {  // EPI_QKV: bias, RoPE at the row's position, q -> q_out, k/v -> KV pages
         const float val = v + o.b[t];
         const int d = n & 63;
@@ -215,9 +226,10 @@ struct Src {
 // One chunk of KB scale blocks: this lane's 8 activations per block (fp32, or
 // int8 + the block scale of the lane's row under W8A8) and its 8 weights +
 // scale per block and column subtile.
-template <int NT, bool A8>
+template <int NT, bool A8, bool AT>
 struct Chunk {
-    float xa[A8 ? 1 : KB][8];
+    float xa[(A8 || AT) ? 1 : KB][8];
+    half8 xh[(!A8 && AT) ? KB : 1], xl[(!A8 && AT) ? KB : 1];  // fp32 activations pre-split (a_hl)
     uint64_t xq[A8 ? KB : 1];
     float xd[A8 ? KB : 1];
     uint2 qb[KB][NT];
@@ -228,10 +240,11 @@ struct Chunk {
 // non-temporal hint measured slower end to end: 0.83 vs 0.78 ms per 256-row prefill)
 constexpr int kCpolW = 0;
 
-// AT: W8A8 activations in the matrix-core order (q8t_at / d8t_at): a block of the
-// wave's 16 rows is one 512-byte unit and 16 scales
+// AT: activations in the matrix-core order -- W8A8: q8t_at / d8t_at, a block of the
+// wave's 16 rows is one 512-byte unit and 16 scales; fp32: hlt_at, the block's hi and
+// lo fp16 halves are two 1024-byte runs, loaded as the MFMA's A operands
 template <int NT, bool A8, bool AT>
-__device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
+__device__ __forceinline__ void load_chunk_a(Chunk<NT, A8, AT> &c, int b0, const Src<A8> &s) {
     constexpr int QB = AT ? 512 : 32, DB = AT ? 64 : 4;  // bytes from one block to the next
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
@@ -239,6 +252,10 @@ __device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src
             const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.a, s.va + QB * j, QB * b0, 0);
             c.xq[j] = ((uint64_t)q[1] << 32) | q[0];
             c.xd[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s.ad, s.vad + DB * j, DB * b0, 0));
+        } else if constexpr (AT) {
+            c.xh[j] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(s.a, s.va + 2048 * j, 2048 * b0, 0));
+            c.xl[j] =
+                __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(s.a, s.va + 2048 * j + 1024, 2048 * b0, 0));
         } else {
             // the whole vector is reinterpreted: a bit cast of one element of the
             // builtin's vector type reads element 0
@@ -257,8 +274,8 @@ __device__ __forceinline__ void load_chunk_a(Chunk<NT, A8> &c, int b0, const Src
 
 // TL: weights in the matrix-core order (one 544-byte unit per subtile and block)
 // instead of Q8_0_4X4 (4 groups of 136-byte blocks per subtile)
-template <int NT, bool A8, bool TL>
-__device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
+template <int NT, bool A8, bool AT, bool TL>
+__device__ __forceinline__ void load_chunk_b(Chunk<NT, A8, AT> &c, int b0, const Src<A8> &s) {
     constexpr int UB = TL ? kTileBytes : kBlockBytes;  // bytes from one block to the next
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
@@ -273,15 +290,15 @@ __device__ __forceinline__ void load_chunk_b(Chunk<NT, A8> &c, int b0, const Src
 }
 
 template <int NT, bool A8, bool TL, bool AT>
-__device__ __forceinline__ void load_chunk(Chunk<NT, A8> &c, int b0, const Src<A8> &s) {
+__device__ __forceinline__ void load_chunk(Chunk<NT, A8, AT> &c, int b0, const Src<A8> &s) {
     load_chunk_a<NT, A8, AT>(c, b0, s);
-    load_chunk_b<NT, A8, TL>(c, b0, s);
+    load_chunk_b<NT, A8, AT, TL>(c, b0, s);
 }
 
 typedef int intx4 __attribute__((ext_vector_type(4)));
 
-template <int NT, bool A8>
-__device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int nb, int kq, floatx4 (&acc)[NT]) {
+template <int NT, bool A8, bool AT>
+__device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8, AT> &c, int b0, int nb, int kq, floatx4 (&acc)[NT]) {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
@@ -307,7 +324,12 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8> &c, int b0, int n
             }
         } else {
             half8 hi, lo;
-            split_hi_lo(c.xa[j], hi, lo);
+            if constexpr (AT) {
+                hi = c.xh[j];
+                lo = c.xl[j];
+            } else {
+                split_hi_lo(c.xa[j], hi, lo);
+            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const half8 bw = i8x8_to_h8(c.qb[j][t]);
@@ -358,7 +380,11 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     Src<A8> src;
     {
         const uint32_t a_elems = (uint32_t)((g.M - 1) * g.lda + g.K);
-        if constexpr (A8 && AT) {  // K = lda; rows padded to 16
+        if constexpr (!A8 && AT) {  // hi/lo fp16 units of 2048 bytes (hlt_at), K = lda; rows padded to 16
+            const uint32_t units = (uint32_t)((g.M + 15) / 16) * (uint32_t)(g.lda / 32);
+            src.a = make_rsrc(g.a_hl, units * 2048u);
+            src.va = (int)(((m_base / 16) * (g.lda / 32) + kb0) * 2048) + 16 * lane;
+        } else if constexpr (A8 && AT) {  // K = lda; rows padded to 16
             const uint32_t units = (uint32_t)((g.M + 15) / 16) * (uint32_t)(g.lda / 32);
             const int unit = (m_base / 16) * (g.lda / 32) + kb0;  // this row tile's first block
             src.a = make_rsrc(g.a8, units * 512u);
@@ -391,7 +417,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     if constexpr (LN) {
-        static_assert(!A8, "the LayerNorm prologue takes fp32 activations");
+        static_assert(!A8 && !AT, "the LayerNorm prologue takes fp32 activation rows");
         __shared__ float lnw[4 * 2 * KB * 32], lnb[4 * 2 * KB * 32];
         __shared__ float lsum[4][16], lsq[4][16];
         // loads in completion order: the activations, ln_w / ln_b (into registers),
@@ -399,7 +425,7 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         // ln_w / ln_b go to LDS only after every load is issued (an LDS store of a
         // loaded value waits for that load, and loads complete in order)
         constexpr int LNR = (4 * 2 * KB * 32 + 255) / 256;
-        Chunk<NT, A8> ca, cb;
+        Chunk<NT, A8, AT> ca, cb;
         load_chunk_a<NT, A8, AT>(ca, 0, src);
         load_chunk_a<NT, A8, AT>(cb, KB, src);
         float lw[LNR], lb[LNR];
@@ -409,8 +435,8 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             lw[i] = g.ln_w[c];
             lb[i] = g.ln_b[c];
         }
-        load_chunk_b<NT, A8, TL>(ca, 0, src);
-        load_chunk_b<NT, A8, TL>(cb, KB, src);
+        load_chunk_b<NT, A8, AT, TL>(ca, 0, src);
+        load_chunk_b<NT, A8, AT, TL>(cb, KB, src);
 #pragma unroll
         for (int i = 0; i < LNR; ++i) {
             const int c = (int)threadIdx.x + 256 * i;
@@ -472,18 +498,18 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             if (j < nb) norm(ca.xa[j], kb0 + j);
             if (KB + j < nb) norm(cb.xa[j], kb0 + KB + j);
         }
-        mfma_chunk<NT, A8>(ca, 0, nb, kq, acc);
-        if (KB < nb) mfma_chunk<NT, A8>(cb, KB, nb, kq, acc);
+        mfma_chunk<NT, A8, AT>(ca, 0, nb, kq, acc);
+        if (KB < nb) mfma_chunk<NT, A8, AT>(cb, KB, nb, kq, acc);
     } else if (nb > 0) {
-        Chunk<NT, A8> ca, cb;
+        Chunk<NT, A8, AT> ca, cb;
         load_chunk<NT, A8, TL, AT>(ca, 0, src);
         for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
             load_chunk<NT, A8, TL, AT>(cb, b0 + KB, src);
-            mfma_chunk<NT, A8>(ca, b0, nb, kq, acc);
+            mfma_chunk<NT, A8, AT>(ca, b0, nb, kq, acc);
             if (b0 + KB >= nb) break;
             if (b0 + 2 * KB < nb)  // (uniform) a chunk past the wave's blocks is not requested
                 load_chunk<NT, A8, TL, AT>(ca, b0 + 2 * KB, src);
-            mfma_chunk<NT, A8>(cb, b0 + KB, nb, kq, acc);
+            mfma_chunk<NT, A8, AT>(cb, b0 + KB, nb, kq, acc);
         }
     }
 #pragma unroll
@@ -570,6 +596,7 @@ hipError_t launch_l(const GemmArgs &g, hipStream_t s) {
     if (g.a8 != nullptr)
         return g.a8_tiled ? launch_nt<EPI, KV, true, false, TL, true>(g, s)
                           : launch_nt<EPI, KV, true, false, TL, false>(g, s);
+    if (g.a_hl != nullptr) return launch_nt<EPI, KV, false, false, TL, true>(g, s);
     if constexpr (EPI != EPI_PART) {
         if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL, false>(g, s);
     }
@@ -621,9 +648,12 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
     if (g.a8_tiled && (g.a8 == nullptr || g.lda != g.K)) return hipErrorInvalidValue;
+    if (g.a_hl != nullptr && (g.a8 != nullptr || g.ln_w != nullptr || g.lda != g.K)) return hipErrorInvalidValue;
+    if (g.y_hl != nullptr && (epi != EPI_GELU || g.q8_out != nullptr || g.N % 32)) return hipErrorInvalidValue;
     if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || (g.y && g.ldy < g.N)))
         return hipErrorInvalidValue;
-    if (g.q8_out == nullptr && epi != EPI_PART && epi != EPI_QKV && !g.y) return hipErrorInvalidValue;
+    if (g.q8_out == nullptr && g.y_hl == nullptr && epi != EPI_PART && epi != EPI_QKV && !g.y)
+        return hipErrorInvalidValue;
     // LayerNorm prologue: fp32 rows of at most 4 waves x 2 chunks of blocks, whole K in the workgroup
     if (g.ln_w != nullptr && (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))
         return hipErrorInvalidValue;

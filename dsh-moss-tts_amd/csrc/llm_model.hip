@@ -669,11 +669,17 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         pre_q8_ = pre_q8h_ = nullptr;
         rows_cap_ = 0;
         hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
+        // pre_a_, pre_o_, pre_h_: GEMM inputs, as fp16 hi / lo halves in the matrix-core
+        // order under A16 (hlt_at: 4 bytes a value, rows padded to 16)
+        const size_t mp = (size_t)(m + 15) / 16 * 16;
         hip_check(hipMalloc(&pre_x_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_a_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_a_, sizeof(float) * kHidden * mp), "hipMalloc(prefill)");
         hip_check(hipMalloc(&pre_q_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_o_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * (size_t)m), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_o_, sizeof(float) * kHidden * mp), "hipMalloc(prefill)");
+        hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * mp), "hipMalloc(prefill)");
+        hip_check(hipMemsetAsync(pre_a_, 0, sizeof(float) * kHidden * mp, stream_), "memset(prefill)");
+        hip_check(hipMemsetAsync(pre_o_, 0, sizeof(float) * kHidden * mp, stream_), "memset(prefill)");
+        hip_check(hipMemsetAsync(pre_h_, 0, sizeof(float) * kFF * mp, stream_), "memset(prefill)");
         const int kz = std::max(std::max(gemm_ksplit(m, kHidden, kHidden), gemm_ksplit(m, kHidden, kFF)),
                                 kPrefillFcOutSplit);
         hip_check(hipMalloc(&pre_part_, sizeof(float) * kHidden * (size_t)m * kz), "hipMalloc(prefill)");
@@ -711,14 +717,18 @@ void Model::prefill(const int32_t *rows, int n, int start) {
             g.a8_tiled = true;
         }
     };
-    // under W8A8 the GEMMs read only the int8 copies: the fp32 rows are not written
-    float *a_rows = a8 ? nullptr : pre_a_;
-    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, a_rows, m, s, nullptr, q8, d8), "prefill ln1");
+    // the GEMMs read their inputs in the matrix-core order, written so by the kernel
+    // before: int8 + block scales under W8A8, fp16 hi / lo halves under A16
+    uint8_t *a_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_a_);
+    uint8_t *o_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_o_);
+    uint8_t *h_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_h_);
+    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, nullptr, m, s, nullptr, q8, d8, a_hl),
+              "prefill ln1");
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
         GemmArgs q;
-        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a = pre_a_; q.lda = kHidden; q.M = m;
+        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a_hl = a_hl; q.lda = kHidden; q.M = m;
         q.bias = L.attn_b; q.q_out = pre_q_;
         q.k_pool = kv_layer(0, l); q.v_pool = kv_layer(1, l); q.page_size = max_ctx_;
         q.pos0 = start; q.rope_cos = rc; q.rope_sin = rs;
@@ -726,20 +736,20 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "prefill qkv");
         AttnArgs t;
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
-        t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out = a8 ? nullptr : pre_o_;
+        t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out_hl = o_hl;
         t.q8 = q8; t.d8 = d8;
         hip_check(launch_attn_tiles(t, kvt_, s), "prefill attention");
         GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
-        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a = pre_o_; p.lda = kHidden; p.M = m;
+        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = o_hl; p.lda = kHidden; p.M = m;
         p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);
         operand(p);
         hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
         hip_check(launch_resid_ln_rows(pre_part_, p.ksplit, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
-                                       a_rows, nullptr, s, q8, d8),
+                                       nullptr, nullptr, s, q8, d8, a_hl),
                   "prefill proj reduce + ln2");
         GemmArgs f1;
-        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = pre_a_; f1.lda = kHidden; f1.M = m;
-        f1.y = a8 ? nullptr : pre_h_; f1.ldy = kFF; f1.bias = L.fc_in_b;
+        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a_hl = a_hl; f1.lda = kHidden; f1.M = m;
+        f1.y_hl = h_hl; f1.bias = L.fc_in_b;
         operand(f1);
         if (a8) {  // fc_out's int8 operand, quantised in fc_in's epilogue
             f1.q8_out = pre_q8h_;
@@ -747,7 +757,7 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         }
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
         GemmArgs f2;
-        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a = pre_h_; f2.lda = kFF; f2.M = m;
+        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = h_hl; f2.lda = kFF; f2.M = m;
         f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
         // W8A8 with many rows: 4 slices of K = 3072 (6 blocks per wave instead of 24) measured
         // faster (0.668 -> 0.647 ms for 256 rows); A16 is not (its slices re-read fp32 rows)
@@ -760,8 +770,9 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
         const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce
         hip_check(launch_resid_ln_rows(pre_part_, f2.ksplit, m, L.fc_out_b, pre_x_, kHidden, pre_x_,
-                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, a_rows,
-                                       nullptr, s, last ? nullptr : q8, last ? nullptr : d8),
+                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, nullptr,
+                                       nullptr, s, last ? nullptr : q8, last ? nullptr : d8,
+                                       last ? nullptr : a_hl),
                   "prefill fc_out reduce");
     }
     hip_check(launch_layernorm(pre_x_ + (size_t)(m - 1) * kHidden, lnf_w_, lnf_b_, hidden_, nullptr, 0, s), "ln_f");

@@ -377,6 +377,24 @@ __device__ __forceinline__ size_t d8t_at(int m, int blk, int K) {
     return ((size_t)(m >> 4) * (K >> 5) + blk) * 16 + (m & 15);
 }
 
+// fp32 activations as the A16 GEMMs can read them (GemmArgs::a_hl): each value x
+// split into fp16 hi = rtz(x) and lo = rtz(x - hi) (hi + lo keeps ~22 bits), in
+// the matrix-core order -- one 2048-byte unit per 16 rows and 32-column block
+// (unit (m / 16) * (K / 32) + k / 32): the hi halves of lane m % 16 + 16 j's 8
+// values (row m % 16, columns 8j .. 8j + 7 of the block) at 16 * lane, the lo
+// halves 1024 bytes further.  Rows padded to 16.
+__device__ __forceinline__ size_t hlt_at(int m, int k, int K) {  // byte offset of the hi half
+    const size_t unit = (size_t)(m >> 4) * (K >> 5) + (k >> 5);
+    return unit * 2048 + 16 * ((m & 15) + 16 * ((k & 31) >> 3)) + 2 * (k & 7);
+}
+__device__ __forceinline__ void store_hl(uint8_t *hl, int m, int k, int K, float x) {
+    const size_t o = hlt_at(m, k, K);
+    const auto h = __builtin_amdgcn_cvt_pkrtz(x, x);
+    const auto l = __builtin_amdgcn_cvt_pkrtz(x - (float)h[0], x - (float)h[0]);
+    *reinterpret_cast<_Float16 *>(hl + o) = (_Float16)h[0];
+    *reinterpret_cast<_Float16 *>(hl + o + 1024) = (_Float16)l[0];
+}
+
 // gelu_new (reference csrc/src/llm.cpp:22-25)
 __device__ __forceinline__ float gelu_new(float v) {
 #pragma clang fp contract(off)

@@ -98,6 +98,9 @@ struct AttnArgs {
     // matrix-core order (q8t_at / d8t_at, rows padded to 16)
     int8_t *q8 = nullptr;
     float *d8 = nullptr;
+    // the output as hi / lo halves in the matrix-core order (hlt_at, rows padded to 16)
+    // for the next GEMM's a_hl, instead of out (no split-KV or sliced launches)
+    uint8_t *out_hl = nullptr;
     const DevState *state = nullptr;
     // single row, long context: the keys are cut into `chunks` slices of 256 (one workgroup of
     // 4 waves each, more spans per wave past kMaxChunks); slices 1.. write their partial
@@ -168,6 +171,12 @@ struct GemmArgs {
     const int8_t *a8 = nullptr;
     const float *d8 = nullptr;
     bool a8_tiled = false;
+    // fp32 activations already split into fp16 hi / lo halves in the matrix-core order
+    // (hlt_at with K = lda, rows padded to 16): read instead of `a` when set
+    const uint8_t *a_hl = nullptr;
+    // EPI_GELU: the output as hi / lo halves in that order (for the next GEMM's a_hl)
+    // instead of fp32 rows in y
+    uint8_t *y_hl = nullptr;
     // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
     // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
     const float *ln_w = nullptr, *ln_b = nullptr;
@@ -190,9 +199,11 @@ int gemm_ksplit(int M, int N, int K);
 //   their out row.  resid may alias x (in-place residual stream).  N == 768.
 hipError_t launch_resid_ln_rows(const float *part, int ksplit, int rows, const float *bias, const float *resid,
                                 int resid_stride, float *x, const float *ln_w, const float *ln_b, float *out,
-                                const unsigned char *mask, hipStream_t s, int8_t *q8 = nullptr, float *d8 = nullptr);
+                                const unsigned char *mask, hipStream_t s, int8_t *q8 = nullptr, float *d8 = nullptr,
+                                uint8_t *out_hl = nullptr);
 // (q8 / d8 of launch_resid_ln_rows and launch_ln_rows: the W8A8 copy of out in the
-// matrix-core order, q8t_at / d8t_at, rows padded to 16; out may be null when q8 is set)
+// matrix-core order, q8t_at / d8t_at, rows padded to 16; out_hl: out as hi / lo halves in
+// that order (hlt_at) instead of fp32 rows; out may be null when q8 or out_hl is set)
 
 // W8A8 activation quantisation of rows (quant.cpp:28-54): q8[r][K] int8 and d8[r][K/32]
 // fp32 block scales from x[r * x_stride + k].  K % 256 == 0.
@@ -260,7 +271,7 @@ inline void rng_seed_host(uint64_t v, uint32_t s[4]) {
 // rows with mask[r] == 0 are left untouched when mask is non-null.
 hipError_t launch_ln_rows(const float *x, int x_stride, const float *w, const float *b, float *out, int rows,
                           hipStream_t s, const unsigned char *mask = nullptr, int8_t *q8 = nullptr,
-                          float *d8 = nullptr);
+                          float *d8 = nullptr, uint8_t *out_hl = nullptr);
 // x[r] = embedding of rows[r][17] (llm.cpp:148-157)
 hipError_t launch_embed_rows(const EmbedArgs &e, const int *rows, int n, float *x, hipStream_t s);
 
@@ -313,6 +324,7 @@ struct PickAttnArgs {
     float *lk = nullptr, *lv = nullptr;  // local KV [S][heads][17][64] (fp32)
     int lpos = 0;
     float *o = nullptr;             // [S][768] attention output
+    uint8_t *o_hl = nullptr;        // or the output as hi / lo halves (hlt_at, rows padded to 16)
 };
 hipError_t launch_local_pick_attn(const PickAttnArgs &a, int streams, hipStream_t s);
 // The same copy of one shared row (lpos 1: wte[slot]) for every stream.
