@@ -64,7 +64,7 @@ struct LayerW {
     const uint8_t *attn_wm, *proj_wm, *fc_in_wm, *fc_out_wm;
 };
 
-// K slices of the W8A8 prefill's fc_out GEMM from 128 rows on
+// K slices of the prefill's fc_out GEMM from 128 rows on
 constexpr int kPrefillFcOutSplit = 4;
 
 class Model {

@@ -759,9 +759,9 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         GemmArgs f2;
         f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = h_hl; f2.lda = kFF; f2.M = m;
         f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
-        // W8A8 with many rows: 4 slices of K = 3072 (6 blocks per wave instead of 24) measured
-        // faster (0.668 -> 0.647 ms for 256 rows); A16 is not (its slices re-read fp32 rows)
-        if (a8 && m >= 128) f2.ksplit = kPrefillFcOutSplit;
+        // many rows: 4 slices of K = 3072 (6 blocks per wave instead of 24) measured faster
+        // (256 rows: W8A8 0.668 -> 0.647 ms, A16 0.722 -> 0.696 ms)
+        if (m >= 128) f2.ksplit = kPrefillFcOutSplit;
         if (a8) {
             f2.a8 = pre_q8h_;
             f2.d8 = pre_d8h_;
