@@ -276,6 +276,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 return;
             }
         }
+        STAGE_TS(14);
 
         // ---- stage Q: LN1 + QKV, one wave per group
         if (b < kAttnBase) {
@@ -598,6 +599,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) ll_put(LL + kLLO + r, xm[r] + (yv + eb), tag);  // llm.cpp:245
             STAGE_TS(13);
+            if (layer == kLayers - 2) STAGE_TS(15);
         }
 
     }  // layer
