@@ -678,7 +678,7 @@ __global__ __launch_bounds__(256) void sample_rows_kernel(const float *logits, i
 __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs a) {
     __shared__ float bv[4];
     __shared__ int bi[4];
-    __shared__ float qkv[3][kHeadDim];
+    __shared__ __attribute__((aligned(16))) float qkv[3][kHeadDim];  // rows read as float4
     __shared__ float es[kLocalLen];
     const int h = blockIdx.x, srow = blockIdx.y, t = threadIdx.x;
     const StreamState &st = a.st;
@@ -689,6 +689,20 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
     for (int k = 0; k < kCodebook / 256; ++k) {
         in.vals[k] = lg[t + 256 * k];
         in.cnt[k] = cnt[t + 256 * k];
+    }
+    // wave 0: the cached keys 0 .. lpos - 1 of head h do not depend on the pick, so their
+    // rows are requested now, behind the logits (loads complete in order): lane k the K
+    // row of key k, lane d column d of every V row (rows past lpos - 1 read row lpos - 1)
+    const size_t kvrow = ((size_t)srow * kHeads + h) * kLocalLen;
+    const int klast = max(a.lpos - 1, 0);
+    float4 kr[kHeadDim / 4];
+    float vv[kLocalLen];
+    if (t < 64) {
+        const float4 *krow = (const float4 *)(a.lk + (kvrow + min(t, klast)) * kHeadDim);
+#pragma unroll
+        for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = krow[c];
+#pragma unroll
+        for (int k = 0; k < kLocalLen; ++k) vv[k] = a.lv[(kvrow + min(k, klast)) * kHeadDim + t];
     }
     const bool active = st.active[srow] != 0;  // the same for the whole workgroup
     const float pen = st.ctrl->rep_penalty;
@@ -706,7 +720,6 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
                 st.counts[((size_t)srow * kNVq + a.ch - 1) * kCodebook + st.codes[srow * kNVq + a.ch - 1]] += 1;
         }
     }
-    const size_t kvrow = ((size_t)srow * kHeads + h) * kLocalLen;
     if (t < 3 * kHeadDim) {  // this head's q, k, v of the table row (lpos, code)
         const int sec = t >> 6, d = t & 63;
         const float v = a.rows[(size_t)idx * 3 * kHidden + sec * kHidden + h * kHeadDim + d];
@@ -723,10 +736,17 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
     const int nk = a.lpos + 1;
     float sc = -INFINITY;
     if (t < nk) {
-        const float *kr = t == a.lpos ? qkv[1] : a.lk + (kvrow + t) * kHeadDim;
+        if (t == a.lpos)  // the new key, from the table row
+#pragma unroll
+            for (int c = 0; c < kHeadDim / 4; ++c) kr[c] = *(const float4 *)&qkv[1][4 * c];
         float d = 0.0f;
-#pragma unroll 16
-        for (int i = 0; i < kHeadDim; ++i) d = fmaf(qkv[0][i], kr[i], d);
+#pragma unroll
+        for (int c = 0; c < kHeadDim / 4; ++c) {
+            d = fmaf(qkv[0][4 * c], kr[c].x, d);
+            d = fmaf(qkv[0][4 * c + 1], kr[c].y, d);
+            d = fmaf(qkv[0][4 * c + 2], kr[c].z, d);
+            d = fmaf(qkv[0][4 * c + 3], kr[c].w, d);
+        }
         sc = d * 0.125f;  // 1/sqrt(64), applied after the dot as llm.cpp:200 does
     }
     const float mx = wave_max(sc);
@@ -736,7 +756,10 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     float o = 0.0f;
-    for (int k = 0; k < nk; ++k) o = fmaf(es[k], k == a.lpos ? qkv[2][t] : a.lv[(kvrow + k) * kHeadDim + t], o);
+    const float vnew = qkv[2][t];
+#pragma unroll
+    for (int k = 0; k < kLocalLen; ++k)
+        if (k < nk) o = fmaf(es[k], k == a.lpos ? vnew : vv[k], o);
     if (a.o_hl != nullptr)  // for the proj GEMM: hi / lo halves in the matrix-core order
         store_hl(a.o_hl, srow, h * kHeadDim + t, kHidden, o / l);
     else
