@@ -228,7 +228,12 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                     int used;
                     if (picking) {  // greedy pick of channel ch_in (llm.cpp:689-697)
                         if (pick_ll) {
-                            const bool ok = ll_gather<kCodebook / 256>(LL + kLL, kCodebook, tag - 1, lgt, budget);
+                            // waves 1-3 poll the logits: wave 0's cache-row loads, issued
+                            // above, would hold back its polls (loads complete in order)
+                            bool ok = true;
+                            if (t >= 64)
+                                ok = ll_gather_by<(kCodebook + 191) / 192, 192>(LL + kLL, kCodebook, tag - 1, lgt,
+                                                                                 budget, t - 64);
                             if (sync_failed(!ok, &wait_failed)) {
                                 if (t == 0) atomicOr(a.err, 1u);
                                 return;

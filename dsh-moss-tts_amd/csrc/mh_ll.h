@@ -47,6 +47,32 @@ __device__ __forceinline__ void ll_gen_arrive(uint32_t *gen, uint32_t total) {
 // Waits until words [0, n) of src carry `tag` and copies their values to dst
 // (LDS).  Thread t takes words t, t + 256, ... (at most MAXK); all of its loads
 // are in flight together.  Returns false when the thread's budget runs out.
+// ll_gather by NT threads: thread tt (0 <= tt < NT) takes words tt, tt + NT, ...
+template <int MAXK, int NT>
+__device__ __forceinline__ bool ll_gather_by(const uint64_t *src, int n, uint32_t tag, float *dst, int &budget,
+                                             int tt) {
+    uint64_t w[MAXK];
+    uint32_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < MAXK; ++k) {
+        w[k] = ll_load(src + min(tt + NT * k, n - 1));
+        if (tt + NT * k < n) pending |= 1u << k;
+    }
+    while (true) {
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k)
+            if (((pending >> k) & 1u) && (uint32_t)(w[k] >> 32) == tag) {
+                dst[tt + NT * k] = __uint_as_float((uint32_t)w[k]);
+                pending &= ~(1u << k);
+            }
+        if (pending == 0) return true;
+        if (--budget < 0) return false;
+        __builtin_amdgcn_s_sleep(kPollSleep);
+#pragma unroll
+        for (int k = 0; k < MAXK; ++k) w[k] = ll_load(src + min(tt + NT * k, n - 1));
+    }
+}
+
 template <int MAXK>
 __device__ __forceinline__ bool ll_gather(const uint64_t *src, int n, uint32_t tag, float *dst, int &budget) {
     const int t = tix();
