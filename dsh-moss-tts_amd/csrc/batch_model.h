@@ -72,6 +72,8 @@ private:
     float *hidden_ = nullptr, *lres_ = nullptr, *next_in_ = nullptr, *logits_ = nullptr;
     int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr;
     float *part_ = nullptr;                     // [16][S][768] split-K partials
+    float *xhl_ = nullptr;   // proj's output as hi / lo halves (fc_in's operand), rows padded to 16
+    float *xst_ = nullptr;   // its per-16-column LayerNorm statistics [48][S][2]
     BatchCtl *ctrl_ = nullptr;
     uint32_t *rng_ = nullptr;                   // [S][4]
     unsigned char *active_ = nullptr;

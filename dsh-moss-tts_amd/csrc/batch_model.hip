@@ -82,6 +82,8 @@ Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
     im(&row_, (size_t)S_ * (kNVq + 1));
     im(&counts_, (size_t)S_ * kNVq * kCodebook);
     fm(&part_, (size_t)16 * S_ * kHidden);
+    fm(&xhl_, s16 * kHidden);
+    fm(&xst_, (size_t)(kHidden / 16) * S_ * 2);
     hip_check(hipMalloc(&ctrl_, sizeof(BatchCtl)), "hipMalloc(ctrl)");
     hip_check(hipMalloc(&rng_, sizeof(uint32_t) * 4 * S_), "hipMalloc(rng)");
     hip_check(hipMemset(rng_, 0, sizeof(uint32_t) * 4 * S_), "memset(rng)");
@@ -102,7 +104,8 @@ Batch::~Batch() {
         if (kv.second.global) (void)hipGraphExecDestroy(kv.second.global);
     }
     void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
-                    gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_, part_};
+                    gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_, part_,
+                    xhl_,  xst_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (ctrl_h_) (void)hipHostFree(ctrl_h_);
@@ -226,10 +229,11 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     GemmArgs p;
     p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = hl(o_); p.lda = kHidden; p.M = n;
     p.y = lres_; p.ldy = kHidden; p.bias = L.proj_b; p.resid_in = in; p.resid_stride = in_stride;
+    p.y_hl = hl(xhl_); p.y_stats = xst_;  // fc_in's operand and its LN2 statistics
     hip_check(launch_gemm(p, EPI_RESID, KV_F32, s), "local proj");
     GemmArgs f1;
-    f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = lres_; f1.lda = kHidden; f1.M = n;
-    f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
+    f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a_hl = hl(xhl_); f1.lda = kHidden; f1.M = n;
+    f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b; f1.ln_stats = xst_;
     f1.y_hl = hl(h_); f1.bias = L.fc_in_b;
     hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
     GemmArgs f2;  // split K: the reduce adds bias and residual, then the local ln_f for the head
@@ -320,10 +324,11 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         GemmArgs p;  // x += proj + b
         p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = hl(o_); p.lda = kHidden; p.M = n;
         p.y = x_; p.ldy = kHidden; p.bias = L.proj_b;
+        p.y_hl = hl(xhl_); p.y_stats = xst_;  // fc_in's operand and its LN2 statistics
         hip_check(launch_gemm(p, EPI_RESID, kvt_, s), "proj");
-        GemmArgs f1;  // LN2 in the prologue
-        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a = x_; f1.lda = kHidden; f1.M = n;
-        f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b;
+        GemmArgs f1;  // LN2 of the pre-split rows, statistics from proj
+        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a_hl = hl(xhl_); f1.lda = kHidden; f1.M = n;
+        f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b; f1.ln_stats = xst_;
         f1.y_hl = hl(h_); f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
         GemmArgs f2;  // split K; the reduce adds bias and residual

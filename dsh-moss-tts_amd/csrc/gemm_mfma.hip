@@ -114,6 +114,9 @@ __device__ __forceinline__ EpiRow epi_row(const GemmArgs &g, int m, int n_base) 
     } else if constexpr (EPI == EPI_RESID) {
         r.out = g.y + (size_t)mm * g.ldy;
         r.res = g.resid_in ? g.resid_in + (size_t)mm * g.resid_stride : r.out;
+        r.hl = g.y_hl;
+        r.m = mm;
+        r.N = g.N;
     } else {  // EPI_QKV
         r.sec = n_base / kHidden;
         const int h = (n_base - r.sec * kHidden) >> 6;
@@ -165,7 +168,9 @@ __device__ __forceinline__ void gemm_finish(const EpiRow &r, const EpiOps<NT> &o
     if constexpr (EPI == EPI_PART || EPI == EPI_F32) {
         r.out[n] = v;
     } else if constexpr (EPI == EPI_RESID) {
-        r.out[n] = o.res[t] + (v + o.b[t]);
+        const float y = o.res[t] + (v + o.b[t]);
+        r.out[n] = y;
+        if (r.hl != nullptr) store_hl(r.hl, r.m, n, r.N, y);  // uniform
     } else if constexpr (EPI == EPI_GELU) {
         const float hv = gelu_new(v + o.b[t]);
         if (r.hl != nullptr)  // uniform: the next GEMM reads the hi/lo halves
@@ -354,6 +359,57 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8, AT> &c, int b0, i
 // quarter (at most 8 blocks: K <= 1024) is loaded first, the row sums of the
 // 4 waves meet in LDS (two passes: mean, then the squared deviations), and the
 // values are normalised in registers with ln_w / ln_b staged in LDS.
+// LayerNorm row statistics of a workgroup's 16 rows (K = 768) from a producer's
+// per-16-column (mean, M2) pairs (GemmArgs::ln_stats), combined in a fixed order (Chan
+// et al.'s pairwise update; every merge is symmetric in its two sides, so all lanes
+// agree); ln_w / ln_b are staged in lw2 / lb2.  Returns (mean, 1 / sqrt(var + eps)) of
+// row m_base + l16 after one barrier.
+__device__ __forceinline__ float2 ln_rows_from_stats(const GemmArgs &g, int m_base, int l16, float *lw2, float *lb2,
+                                                     float2 *rstat) {
+#pragma clang fp contract(off)
+    const int tr = threadIdx.x >> 4, sub = threadIdx.x & 15;
+    const int sr = min(m_base + tr, g.M - 1);
+    const float2 *ps = reinterpret_cast<const float2 *>(g.ln_stats);
+    float2 p[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) p[i] = ps[(size_t)(3 * sub + i) * g.M + sr];
+    float lw[3], lb[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        lw[i] = g.ln_w[threadIdx.x + 256 * i];
+        lb[i] = g.ln_b[threadIdx.x + 256 * i];
+    }
+    // groups 3 sub .. 3 sub + 2 (16 columns each), then the 16 lanes of the row
+    float mean = p[0].x, m2 = p[0].y;
+    {
+        const float d = p[1].x - mean;
+        mean = (mean + p[1].x) * 0.5f;
+        m2 = (m2 + p[1].y) + d * d * 8.0f;  // 16 x 16 / 32
+    }
+    {
+        const float d = p[2].x - mean;
+        mean = mean + d * (1.0f / 3.0f);              // counts 32 and 16
+        m2 = (m2 + p[2].y) + d * d * (32.0f / 3.0f);  // 32 x 16 / 48
+    }
+    float cnt = 48.0f;
+#pragma unroll
+    for (int k = 1; k < 16; k <<= 1) {
+        const float om = __shfl_xor(mean, k), om2 = __shfl_xor(m2, k);
+        const float d = om - mean;
+        mean = (mean + om) * 0.5f;
+        m2 = (m2 + om2) + d * d * (cnt * 0.5f);
+        cnt *= 2.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        lw2[threadIdx.x + 256 * i] = lw[i];
+        lb2[threadIdx.x + 256 * i] = lb[i];
+    }
+    if (sub == 0) rstat[tr] = make_float2(mean, 1.0f / sqrtf(m2 / (float)kHidden + 1e-5f));
+    __syncthreads();
+    return rstat[l16];
+}
+
 template <int EPI, int KV, int NT, bool A8, bool LN, bool TL, bool AT>
 __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
@@ -417,7 +473,45 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     if constexpr (LN) {
-        static_assert(!A8 && !AT, "the LayerNorm prologue takes fp32 activation rows");
+        static_assert(!A8, "the LayerNorm prologue takes fp32 activation rows");
+    }
+    if constexpr (LN && AT) {
+        // LayerNorm of pre-split rows, the rows' statistics from the producer (their own
+        // two-pass form, read from fp32 rows, measured 9.1 us against 7.9 us here): the
+        // chunks stream as in the plain loop, each joined, normalised and split again in
+        // registers before its MFMAs.  (The fp32 rows with the producer's statistics
+        // measured slower than either.)
+        __shared__ float lnw2[kHidden], lnb2[kHidden];
+        __shared__ float2 rstat[16];
+        Chunk<NT, A8, AT> ca, cb;
+        if (nb > 0) load_chunk<NT, A8, TL, AT>(ca, 0, src);
+        const float2 st = ln_rows_from_stats(g, m_base, l16, lnw2, lnb2, rstat);
+        const float mean = st.x, inv = st.y;
+        auto ln_apply = [&](Chunk<NT, A8, AT> &c, int b0) {  // columns 32 blk + 8 kq + i
+#pragma unroll
+            for (int j = 0; j < KB; ++j)
+                if (b0 + j < nb) {
+                    const int col = 32 * (kb0 + b0 + j) + 8 * kq;
+                    float x[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        float y = ((float)c.xh[j][i] + (float)c.xl[j][i] - mean) * inv;
+                        y = y * lnw2[col + i];
+                        x[i] = y + lnb2[col + i];
+                    }
+                    split_hi_lo(x, c.xh[j], c.xl[j]);
+                }
+        };
+        for (int b0 = 0; b0 < nb; b0 += 2 * KB) {
+            load_chunk<NT, A8, TL, AT>(cb, b0 + KB, src);
+            ln_apply(ca, b0);
+            mfma_chunk<NT, A8, AT>(ca, b0, nb, kq, acc);
+            if (b0 + KB >= nb) break;
+            if (b0 + 2 * KB < nb) load_chunk<NT, A8, TL, AT>(ca, b0 + 2 * KB, src);
+            ln_apply(cb, b0 + KB);
+            mfma_chunk<NT, A8, AT>(cb, b0 + KB, nb, kq, acc);
+        }
+    } else if constexpr (LN && !AT) {
         __shared__ float lnw[4 * 2 * KB * 32], lnb[4 * 2 * KB * 32];
         __shared__ float lsum[4][16], lsq[4][16];
         // loads in completion order: the activations, ln_w / ln_b (into registers),
@@ -570,6 +664,26 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         const int n = n_base + 16 * t + l16;
         const float partner = xshfl<1>(v);  // column n ^ 1, same row
         if (m < g.M) gemm_finish<EPI, KV, NT>(er, eo, t, n, v, partner);
+        if constexpr (EPI == EPI_RESID) {
+            if (g.y_stats != nullptr) {  // uniform: (mean, M2) of the row's 16 columns of subtile t
+#pragma clang fp contract(off)
+                const float y = eo.res[t] + (v + eo.b[t]);  // the value stored
+                float sm = y;
+                sm += xshfl<1>(sm);
+                sm += xshfl<2>(sm);
+                sm += xshfl<4>(sm);
+                sm += xshfl<8>(sm);
+                const float mean = sm * 0.0625f;
+                const float d = y - mean;
+                float q = d * d;
+                q += xshfl<1>(q);
+                q += xshfl<2>(q);
+                q += xshfl<4>(q);
+                q += xshfl<8>(q);
+                if (l16 == 0 && m < g.M)
+                    reinterpret_cast<float2 *>(g.y_stats)[(size_t)((n_base >> 4) + t) * g.M + m] = make_float2(mean, q);
+            }
+        }
     }
     GT_END
 }
@@ -596,6 +710,9 @@ hipError_t launch_l(const GemmArgs &g, hipStream_t s) {
     if (g.a8 != nullptr)
         return g.a8_tiled ? launch_nt<EPI, KV, true, false, TL, true>(g, s)
                           : launch_nt<EPI, KV, true, false, TL, false>(g, s);
+    if constexpr (EPI == EPI_GELU) {
+        if (g.a_hl != nullptr && g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL, true>(g, s);
+    }
     if (g.a_hl != nullptr) return launch_nt<EPI, KV, false, false, TL, true>(g, s);
     if constexpr (EPI != EPI_PART) {
         if (g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL, false>(g, s);
@@ -648,14 +765,22 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
     }
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
     if (g.a8_tiled && (g.a8 == nullptr || g.lda != g.K)) return hipErrorInvalidValue;
-    if (g.a_hl != nullptr && (g.a8 != nullptr || g.ln_w != nullptr || g.lda != g.K)) return hipErrorInvalidValue;
-    if (g.y_hl != nullptr && (epi != EPI_GELU || g.q8_out != nullptr || g.N % 32)) return hipErrorInvalidValue;
+    if (g.a_hl != nullptr && (g.a8 != nullptr || g.lda != g.K)) return hipErrorInvalidValue;
+    // LN of pre-split rows: statistics from a producer's y_stats, fc_in's shape
+    if (g.a_hl != nullptr && g.ln_w != nullptr &&
+        (!g.ln_stats || !g.ln_b || epi != EPI_GELU || g.K != kHidden))
+        return hipErrorInvalidValue;
+    if (g.ln_stats != nullptr && (g.a_hl == nullptr || g.ln_w == nullptr)) return hipErrorInvalidValue;
+    if (g.y_hl != nullptr && ((epi != EPI_GELU && epi != EPI_RESID) || g.q8_out != nullptr || g.N % 32))
+        return hipErrorInvalidValue;
+    if (g.y_stats != nullptr && (epi != EPI_RESID || g.N != kHidden)) return hipErrorInvalidValue;
     if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || (g.y && g.ldy < g.N)))
         return hipErrorInvalidValue;
     if (g.q8_out == nullptr && g.y_hl == nullptr && epi != EPI_PART && epi != EPI_QKV && !g.y)
         return hipErrorInvalidValue;
     // LayerNorm prologue: fp32 rows of at most 4 waves x 2 chunks of blocks, whole K in the workgroup
-    if (g.ln_w != nullptr && (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))
+    if (g.ln_w != nullptr && g.a_hl == nullptr &&
+        (!g.ln_b || g.a8 != nullptr || epi == EPI_PART || g.K > 4 * 2 * KB * 32 || g.K < 4 * 32))
         return hipErrorInvalidValue;
     switch (epi) {
         case EPI_PART: return launch_a<EPI_PART, KV_F16>(g, s);

@@ -175,8 +175,15 @@ struct GemmArgs {
     // (hlt_at with K = lda, rows padded to 16): read instead of `a` when set
     const uint8_t *a_hl = nullptr;
     // EPI_GELU: the output as hi / lo halves in that order (for the next GEMM's a_hl)
-    // instead of fp32 rows in y
+    // instead of fp32 rows in y; EPI_RESID: in addition to y
     uint8_t *y_hl = nullptr;
+    // EPI_RESID, N = 768: for every stored row m and 16-column group j, the group's mean and
+    // sum of squared deviations at y_stats[2 * (j * M + m)] -- the next LayerNorm's row
+    // statistics, combined in a fixed order by the GEMM that reads them (ln_stats)
+    float *y_stats = nullptr;
+    // with a_hl and ln_w (EPI_GELU, K = 768): LN of the pre-split rows, the rows' statistics
+    // combined from ln_stats (a producer's y_stats) instead of formed from the rows
+    const float *ln_stats = nullptr;
     // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
     // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
     const float *ln_w = nullptr, *ln_b = nullptr;
