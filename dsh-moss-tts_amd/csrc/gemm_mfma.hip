@@ -355,10 +355,12 @@ __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8, AT> &c, int b0, i
 // pairs.  A workgroup reads 16 activation rows instead of 64: the panel is
 // what limits a GEMM with M <= 64, read by every column tile.
 //
-// LN: the activation rows are LayerNormed on the way in.  The wave's whole K
-// quarter (at most 8 blocks: K <= 1024) is loaded first, the row sums of the
-// 4 waves meet in LDS (two passes: mean, then the squared deviations), and the
-// values are normalised in registers with ln_w / ln_b staged in LDS.
+// LN: the activation rows are LayerNormed on the way in.  From fp32 rows (AT =
+// false): the wave's whole K quarter (at most 8 blocks: K <= 1024) is loaded first,
+// the row sums of the 4 waves meet in LDS (two passes: mean, then the squared
+// deviations), and the values are normalised in registers with ln_w / ln_b staged
+// in LDS.  From pre-split rows (AT = true, K = 768): the statistics come from the
+// producer (ln_rows_from_stats) and the chunks stream as in the plain loop.
 // LayerNorm row statistics of a workgroup's 16 rows (K = 768) from a producer's
 // per-16-column (mean, M2) pairs (GemmArgs::ln_stats), combined in a fixed order (Chan
 // et al.'s pairwise update; every merge is symmetric in its two sides, so all lanes

@@ -184,8 +184,9 @@ struct GemmArgs {
     // with a_hl and ln_w (EPI_GELU, K = 768): LN of the pre-split rows, the rows' statistics
     // combined from ln_stats (a producer's y_stats) instead of formed from the rows
     const float *ln_stats = nullptr;
-    // LayerNorm prologue (fp32 activations, K <= 1024, no K split): the GEMM multiplies
-    // LN(a_row) = (a - mean) * inv * ln_w + ln_b (llm.cpp:159-171) when ln_w is non-null
+    // LayerNorm prologue: the GEMM multiplies LN(a_row) = (a - mean) * inv * ln_w + ln_b
+    // (llm.cpp:159-171) when ln_w is non-null -- over fp32 rows `a` (K <= 1024, no K
+    // split), or over pre-split rows a_hl with the statistics from ln_stats
     const float *ln_w = nullptr, *ln_b = nullptr;
     // EPI_GELU with q8_out (16*NT >= 32 columns per tile; y may then be null: no fp32 rows): the stored rows are also quantised
     // per 32-block (quantize_activation, quant.cpp:45) into q8_out / d8_out in the matrix-core
