@@ -74,6 +74,7 @@ private:
     float *part_ = nullptr;                     // [16][S][768] split-K partials
     float *xhl_ = nullptr;   // proj's output as hi / lo halves (fc_in's operand), rows padded to 16
     float *xst_ = nullptr;   // its per-16-column LayerNorm statistics [48][S][2]
+    float *pairs_ = nullptr; // the audio head's greedy partials [S][64][2]
     BatchCtl *ctrl_ = nullptr;
     uint32_t *rng_ = nullptr;                   // [S][4]
     unsigned char *active_ = nullptr;

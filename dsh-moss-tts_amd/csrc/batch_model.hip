@@ -84,6 +84,7 @@ Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
     fm(&part_, (size_t)16 * S_ * kHidden);
     fm(&xhl_, s16 * kHidden);
     fm(&xst_, (size_t)(kHidden / 16) * S_ * 2);
+    fm(&pairs_, (size_t)S_ * (kCodebook / 16) * 2);
     hip_check(hipMalloc(&ctrl_, sizeof(BatchCtl)), "hipMalloc(ctrl)");
     hip_check(hipMalloc(&rng_, sizeof(uint32_t) * 4 * S_), "hipMalloc(rng)");
     hip_check(hipMemset(rng_, 0, sizeof(uint32_t) * 4 * S_), "memset(rng)");
@@ -105,7 +106,7 @@ Batch::~Batch() {
     }
     void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
                     gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_, part_,
-                    xhl_,  xst_};
+                    xhl_,  xst_,  pairs_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (ctrl_h_) (void)hipHostFree(ctrl_h_);
@@ -276,6 +277,7 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
             pa.lv = qkv.lv;
             pa.lpos = ch + 1;
             pa.o_hl = hl(o_);
+            pa.pairs = pairs_;
             hip_check(launch_local_pick_attn(pa, n, s), "pick + local attention");
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1, false);
         } else {
@@ -285,6 +287,12 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
         hd.w = w_.aemb[ch]; hd.wm = w_.aemb_m[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a_hl = hl(a_); hd.lda = kHidden;
         hd.M = n;
         hd.y = logits_; hd.ldy = kCodebook;
+        if (greedy && ch + 1 < kNVq) {  // the next launch picks this channel from per-16-code partials
+            hd.pick_pairs = pairs_;
+            hd.pick_counts = st.counts + (size_t)ch * kCodebook;
+            hd.pick_stride = kNVq * kCodebook;
+            hd.pick_pen = &st.ctrl->rep_penalty;
+        }
         hip_check(launch_gemm(hd, EPI_F32, KV_F32, s), "audio head");
         if (greedy && ch + 1 < kNVq) continue;  // picked by the next position's launch
         LocalQkv next = qkv;  // the input of lpos ch + 2 is channel ch's code

@@ -685,10 +685,15 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
     const float *lg = a.logits + (size_t)srow * kCodebook;
     const int *cnt = st.counts + ((size_t)srow * kNVq + a.ch) * kCodebook;
     PickIn in;
+    float2 pair = make_float2(-INFINITY, 0.0f);
+    if (a.pairs != nullptr) {  // the head's partials: 64 per stream, one per lane of each wave
+        pair = reinterpret_cast<const float2 *>(a.pairs)[(size_t)srow * (kCodebook / 16) + (t & 63)];
+    } else {
 #pragma unroll
-    for (int k = 0; k < kCodebook / 256; ++k) {
-        in.vals[k] = lg[t + 256 * k];
-        in.cnt[k] = cnt[t + 256 * k];
+        for (int k = 0; k < kCodebook / 256; ++k) {
+            in.vals[k] = lg[t + 256 * k];
+            in.cnt[k] = cnt[t + 256 * k];
+        }
     }
     // wave 0: the cached keys 0 .. lpos - 1 of head h do not depend on the pick, so their
     // rows are requested now, behind the logits (loads complete in order): lane k the K
@@ -708,10 +713,17 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
     const float pen = st.ctrl->rep_penalty;
     int idx = 0;  // inactive: row 0 keeps the next inputs defined
     if (active) {
-        if (pen == 1.0f)
+        if (a.pairs != nullptr) {  // every wave reduces the 64 pairs itself (lowest index on ties)
+            float best = pair.x;
+            int besti = __float_as_int(pair.y);
+            wave_argmax(best, besti);
+            idx = besti;
+        } else {
+            if (pen == 1.0f)
 #pragma unroll
-            for (int k = 0; k < kCodebook / 256; ++k) in.cnt[k] = 0;
-        idx = greedy_pick_reduce(in, pen, bv, bi);
+                for (int k = 0; k < kCodebook / 256; ++k) in.cnt[k] = 0;
+            idx = greedy_pick_reduce(in, pen, bv, bi);
+        }
         idx = idx >= kCodebook ? 0 : idx;  // every value NaN: the reference's scan stays at 0
         if (h == 0 && t == 0) {
             st.codes[srow * kNVq + a.ch] = idx;

@@ -666,6 +666,28 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
         const int n = n_base + 16 * t + l16;
         const float partner = xshfl<1>(v);  // column n ^ 1, same row
         if (m < g.M) gemm_finish<EPI, KV, NT>(er, eo, t, n, v, partner);
+        if constexpr (EPI == EPI_F32) {
+            if (g.pick_pairs != nullptr) {  // uniform: the 16 lanes of a row hold 16 consecutive columns
+                float best = -INFINITY;
+                int besti = g.N;
+                if (m < g.M) {
+                    const float pen = *g.pick_pen;
+                    const int cnt = pen != 1.0f ? g.pick_counts[(size_t)m * g.pick_stride + n] : 0;
+                    const float pv = penalised(v, cnt, pen);
+                    if (pv > best) {  // greedy_pick_reduce's comparisons
+                        best = pv;
+                        besti = n;
+                    }
+                }
+                argmax_step<1>(best, besti);
+                argmax_step<2>(best, besti);
+                argmax_step<4>(best, besti);
+                argmax_step<8>(best, besti);
+                if (l16 == 0 && m < g.M)
+                    reinterpret_cast<float2 *>(g.pick_pairs)[(size_t)m * (g.N >> 4) + (n >> 4)] =
+                        make_float2(best, __int_as_float(besti));
+            }
+        }
         if constexpr (EPI == EPI_RESID) {
             if (g.y_stats != nullptr) {  // uniform: (mean, M2) of the row's 16 columns of subtile t
 #pragma clang fp contract(off)
@@ -776,6 +798,8 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
     if (g.y_hl != nullptr && ((epi != EPI_GELU && epi != EPI_RESID) || g.q8_out != nullptr || g.N % 32))
         return hipErrorInvalidValue;
     if (g.y_stats != nullptr && (epi != EPI_RESID || g.N != kHidden)) return hipErrorInvalidValue;
+    if (g.pick_pairs != nullptr && (epi != EPI_F32 || g.N % 16 || !g.pick_counts || !g.pick_pen))
+        return hipErrorInvalidValue;
     if (g.q8_out != nullptr && (epi != EPI_GELU || !g.d8_out || g.N % 32 || (g.y && g.ldy < g.N)))
         return hipErrorInvalidValue;
     if (g.q8_out == nullptr && g.y_hl == nullptr && epi != EPI_PART && epi != EPI_QKV && !g.y)

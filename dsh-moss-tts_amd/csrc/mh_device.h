@@ -220,6 +220,13 @@ struct PickIn {
     int cnt[kCodebook / 256];
 };
 
+// v under the repetition penalty applied cnt times (v < 0 ? v * p : v / p)
+__device__ __forceinline__ float penalised(float v, int cnt, float pen) {
+#pragma clang fp contract(off)
+    for (int r = 0; r < cnt; ++r) v = v < 0.0f ? v * pen : v / pen;
+    return v;
+}
+
 __device__ __forceinline__ void greedy_pick_load(const float *logits, const int *counts, float pen, PickIn &in) {
     const int t = threadIdx.x;
 #pragma unroll
@@ -238,8 +245,7 @@ __device__ __forceinline__ int greedy_pick_reduce(const PickIn &in, float pen, f
     int besti = kCodebook;
 #pragma unroll
     for (int k = 0; k < kCodebook / 256; ++k) {  // ascending index per thread
-        float v = vals[k];
-        for (int r = 0; r < cnt[k]; ++r) v = v < 0.0f ? v * pen : v / pen;
+        const float v = penalised(vals[k], cnt[k], pen);
         if (v > best) {
             best = v;
             besti = t + 256 * k;

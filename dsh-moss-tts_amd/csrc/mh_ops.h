@@ -193,6 +193,15 @@ struct GemmArgs {
     // order (q8t_at / d8t_at with K = N, rows padded to 16)
     int8_t *q8_out = nullptr;
     float *d8_out = nullptr;
+    // EPI_F32 with pick_pairs (N % 16 == 0): for every stored row m and 16-column group j,
+    // the greedy pick's partial -- the group's largest value under the repetition penalty
+    // (applied pick_counts[m * pick_stride + n] times, v < 0 ? v * p : v / p, p = *pick_pen)
+    // and its column, the lowest on ties (-inf and N when none can win) -- as the float
+    // pair pick_pairs[2 * (m * N / 16 + j)] (the column's int bits second)
+    float *pick_pairs = nullptr;
+    const int *pick_counts = nullptr;
+    int pick_stride = 0;
+    const float *pick_pen = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s);
 // Copy of a Q8_0_4X4 N x K matrix in the matrix-core order the GEMM reads through
@@ -333,6 +342,9 @@ struct PickAttnArgs {
     int lpos = 0;
     float *o = nullptr;             // [S][768] attention output
     uint8_t *o_hl = nullptr;        // or the output as hi / lo halves (hlt_at, rows padded to 16)
+    // greedy: the head GEMM's per-16-code partials of channel ch ([S][64] pairs,
+    // GemmArgs::pick_pairs) instead of the logits and counts
+    const float *pairs = nullptr;
 };
 hipError_t launch_local_pick_attn(const PickAttnArgs &a, int streams, hipStream_t s);
 // The same copy of one shared row (lpos 1: wte[slot]) for every stream.
