@@ -253,6 +253,20 @@ int moss_hip_llm_prefix_pos(const moss_hip_llm *m) { return (m && m->impl) ? m->
 
 int moss_hip_llm_gate_rows(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->gate_rows() : -1; }
 
+int moss_hip_llm_capture(moss_hip_llm *m, int on) {
+    return guard([&] { model_of(m).set_capture(on != 0); });
+}
+
+int moss_hip_llm_capture_read(moss_hip_llm *m, int what, void *out, size_t bytes, size_t *needed) {
+    return guard([&] {
+        if (what < MOSS_HIP_CAP_GLOBAL || what > MOSS_HIP_CAP_PREFILL) throw Status(MOSS_HIP_EINVAL, "bad capture kind");
+        const size_t n = model_of(m).capture_read(what, out, bytes);
+        if (needed) *needed = n;
+        if (n == 0) throw Status(MOSS_HIP_ESTATE, "nothing of that kind was captured");
+        if (out && bytes < n) throw Status(MOSS_HIP_EINVAL, "output buffer too small");
+    });
+}
+
 int moss_hip_llm_kv_export(moss_hip_llm *m, int n_pos, float *k, float *v) {
     return guard([&] {
         if (n_pos > 0 && (!k || !v)) throw Status(MOSS_HIP_EINVAL, "null buffer");

@@ -219,6 +219,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
     for (int layer = 0; layer < kLayers; ++layer) {
         const LayerArgs a = g.layers[layer];
         const uint32_t tag = ((uint32_t)(pos + 1) << 5) | (uint32_t)layer;
+        // W8A8 quantiser capture of this block (tests only; null in the library's own use)
+        float *const cap = A8 && g.cap ? g.cap + (size_t)layer * MOSS_HIP_CAP_STEP : nullptr;
         // per-block copies of the indices: nothing derived from them is held across blocks
         const int t = tix(), wave = t >> 6, lane = t & 63;
         const int b = bix();
@@ -301,8 +303,17 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
             if constexpr (A8) {
+                float *cp = b == 0 ? cap : nullptr;  // (uniform) quantiser capture, tests only
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_XIN, xin, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_LN1, act, kHidden);
+                }
                 quant_act_lds(act, da, kHidden);
                 __syncthreads();
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_LN1_Q, act, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_LN1_D, da, kHidden / 32);
+                }
             }
             STAGE_TS(1);
             const float yv = gs.template dot<A8>(act, part, da);
@@ -322,6 +333,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                     }
                 }
                 ll_put(LL + kLLQ + r, out, tag);
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_QKV + r] = out;
             }
             STAGE_TS(2);
         }
@@ -566,12 +579,22 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 }
             }
             if constexpr (A8) {
+                float *cp = b == 0 ? cap : nullptr;
+                if (cp) cap_copy(cp + MOSS_HIP_CAP_ATT, act, kHidden);
                 quant_act_lds(act, da, kHidden);
                 __syncthreads();
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_ATT_Q, act, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_ATT_D, da, kHidden / 32);
+                }
             }
             STAGE_TS(7);
             const float yv = gs.template dot<A8>(act, part, da);
-            if (gs.storer()) ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+            if (gs.storer()) {
+                ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_XM + r] = eres + (yv + eb);
+            }
             STAGE_TS(8);
         }
 
@@ -599,12 +622,22 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
             if constexpr (A8) {
+                float *cp = b == 0 ? cap : nullptr;
+                if (cp) cap_copy(cp + MOSS_HIP_CAP_LN2, act, kHidden);
                 quant_act_lds(act, da, kHidden);
                 __syncthreads();
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_LN2_Q, act, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_LN2_D, da, kHidden / 32);
+                }
             }
             STAGE_TS(10);
             const float yv = gs.template dot<A8>(act, part, da);
-            if (gs.storer()) ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+            if (gs.storer()) {
+                ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_H + r] = gelu_new(yv + eb);
+            }
             STAGE_TS(11);
             __syncthreads();  // every wave is done with act before stage F gathers into it
         }
@@ -623,10 +656,18 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             if constexpr (A8) {
                 quant_act_lds(act, da, kFF);
                 __syncthreads();
+                if (b == 0 && cap) {
+                    cap_copy(cap + MOSS_HIP_CAP_H_Q, act, kFF);
+                    cap_copy(cap + MOSS_HIP_CAP_H_D, da, kFF / 32);
+                }
             }
             STAGE_TS(12);
             const float yv = gs.template dot<A8>(act, part, da);
-            if (gs.storer()) ll_put(LL + kLLO + r, xm[r] + (yv + eb), tag);  // llm.cpp:245
+            if (gs.storer()) {
+                ll_put(LL + kLLO + r, xm[r] + (yv + eb), tag);  // llm.cpp:245
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_XOUT + r] = xm[r] + (yv + eb);
+            }
             STAGE_TS(13);
             if (layer == kLayers - 2) STAGE_TS(15);
         }

@@ -145,6 +145,8 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
         const bool live = lpos == 0;  // the block input is the global hidden state: QKV computed here
         const bool picking = !live && ch_in >= 0 && a.pick;
         const bool pick_ll = picking && lpos > a.lpos;  // logits from this launch's previous step
+        // W8A8 quantiser capture of this position (tests only; null in the library's own use)
+        float *const cap = A8 && a.cap ? a.cap + (size_t)lpos * MOSS_HIP_CAP_STEP : nullptr;
 
         // ---- stage Q (lpos 0): LN1 + QKV of the block input, one wave per group
         if (live) {
@@ -167,8 +169,17 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
                 __syncthreads();
                 if constexpr (A8) {
+                    float *cp = b == 0 ? cap : nullptr;  // (uniform)
+                    if (cp) {
+                        cap_copy(cp + MOSS_HIP_CAP_XIN, xm, kHidden);
+                        cap_copy(cp + MOSS_HIP_CAP_LN1, act, kHidden);
+                    }
                     quant_act_lds(act, da, kHidden);
                     __syncthreads();
+                    if (cp) {
+                        cap_copy(cp + MOSS_HIP_CAP_LN1_Q, act, kHidden);
+                        cap_copy(cp + MOSS_HIP_CAP_LN1_D, da, kHidden / 32);
+                    }
                 }
                 const float yv = gs.template dot<A8>(act, part, da);
                 const float partner = xshfl<4>(yv);
@@ -267,6 +278,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 __syncthreads();
             }
             STAGE_TS(2);
+            if constexpr (A8)
+                if (cap && t < 3 * kHeadDim) {
+                    const int i = (t >> 6) * kHidden + h * kHeadDim + (t & 63);
+                    cap[MOSS_HIP_CAP_QKV + i] = qkv[i];
+                }
             if (w0) {
                 const float *qh = &qkv[h * kHeadDim];
                 if (min(lane, n - 1) == lpos)
@@ -337,11 +353,21 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             if (gs.storer() && with_code)  // lookup_row (llm.cpp:697)
                 eres = q8x4_elem(aemb_in, kHidden / 32, __float_as_int(act[kHidden]), r);
             if constexpr (A8) {  // act[0, 768) only: the code at act[kHidden] stays
+                float *cp = b == 0 ? cap : nullptr;
+                if (cp) cap_copy(cp + MOSS_HIP_CAP_ATT, act, kHidden);
                 quant_act_lds(act, da, kHidden);
                 __syncthreads();
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_ATT_Q, act, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_ATT_D, da, kHidden / 32);
+                }
             }
             const float yv = gs.template dot<A8>(act, part, da);
-            if (gs.storer()) ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+            if (gs.storer()) {
+                ll_put(LL + kLX + r, eres + (yv + eb), tag);  // llm.cpp:239
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_XM + r] = eres + (yv + eb);
+            }
             STAGE_TS(4);
             __syncthreads();  // act is reused by stage F
         }
@@ -370,11 +396,21 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
             if constexpr (A8) {
+                float *cp = b == 0 ? cap : nullptr;
+                if (cp) cap_copy(cp + MOSS_HIP_CAP_LN2, act, kHidden);
                 quant_act_lds(act, da, kHidden);
                 __syncthreads();
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_LN2_Q, act, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_LN2_D, da, kHidden / 32);
+                }
             }
             const float yv = gs.template dot<A8>(act, part, da);
-            if (gs.storer()) ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+            if (gs.storer()) {
+                ll_put(LL + kLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_H + r] = gelu_new(yv + eb);
+            }
             STAGE_TS(6);
             __syncthreads();  // every wave is done with act before stage F gathers into it
         }
@@ -393,12 +429,18 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             if constexpr (A8) {
                 quant_act_lds(act, da, kFF);
                 __syncthreads();
+                if (b == 0 && cap) {
+                    cap_copy(cap + MOSS_HIP_CAP_H_Q, act, kFF);
+                    cap_copy(cap + MOSS_HIP_CAP_H_D, da, kFF / 32);
+                }
             }
             STAGE_TS(7);
             const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) {
                 const float xo = xm[r] + (yv + eb);  // llm.cpp:245
                 a.x_out[r] = xo;
+                if constexpr (A8)
+                    if (cap) cap[MOSS_HIP_CAP_XOUT + r] = xo;
                 if (head_w) ll_put(LL + kLO + r, xo, tag);
                 if (live && a.gate) ll_put(LL + kLG + r, xo, tag);  // the gate workgroup's input
             }
@@ -428,8 +470,14 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             for (int i = 0; i < 3; ++i) act[t + 256 * i] = o[i];
             __syncthreads();
             if constexpr (A8) {
+                float *cp = b == 0 ? cap : nullptr;
+                if (cp) cap_copy(cp + MOSS_HIP_CAP_LNF, act, kHidden);
                 quant_act_lds(act, da, kHidden);
                 __syncthreads();
+                if (cp) {
+                    cap_copy(cp + MOSS_HIP_CAP_LNF_Q, act, kHidden);
+                    cap_copy(cp + MOSS_HIP_CAP_LNF_D, da, kHidden / 32);
+                }
             }
             const float yv = gs.template dot<A8>(act, part, da);
             if (gs.storer()) {

@@ -68,8 +68,9 @@ struct PickLds {
     int used;
 };
 
-// Greedy branch (sampler.cpp:23-28): argmax, the lowest index wins ties, index 0
-// when every value is NaN (the reference's scan never moves off 0).
+// Greedy branch (sampler.cpp:23-28): argmax, the lowest index wins ties, NaN values
+// never win; index 0 when the value at index 0 is NaN or every value is NaN (the
+// reference's scan compares with its best so far, so it never moves off a NaN at 0).
 __device__ int pick_greedy(PickLds &L) {
     const int t = threadIdx.x;
     float best = -INFINITY;
@@ -95,7 +96,7 @@ __device__ int pick_greedy(PickLds &L) {
                 b = L.bv[w];
                 idx = L.bi[w];
             }
-        L.pick = idx >= kCodebook ? 0 : idx;
+        L.pick = (idx >= kCodebook || L.vals[0] != L.vals[0]) ? 0 : idx;
     }
     __syncthreads();
     return L.pick;
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(256) void gate_text_kernel(const float *logits, Dev
                 b = bv[w];
                 idx = bi[w];
             }
-        if (idx >= kVocab) {  // all NaN: the reference's scan keeps index 0
+        if (idx >= kVocab || logits[0] != logits[0]) {  // NaN at 0 (or all NaN): the reference's scan keeps index 0
             idx = 0;
             b = logits[0];
         }

@@ -683,6 +683,18 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
                 argmax_step<2>(best, besti);
                 argmax_step<4>(best, besti);
                 argmax_step<8>(best, besti);
+                // a NaN at column 0 wins outright (the reference's scan never leaves index 0,
+                // sampler.cpp:24-26): the pair (+inf, 0) beats every other pair, ties go to
+                // the lowest index
+                int nan0 = (m < g.M && n == 0 && !(v == v)) ? 1 : 0;
+                nan0 |= xshfl<1>(nan0);
+                nan0 |= xshfl<2>(nan0);
+                nan0 |= xshfl<4>(nan0);
+                nan0 |= xshfl<8>(nan0);
+                if (nan0) {
+                    best = INFINITY;
+                    besti = 0;
+                }
                 if (l16 == 0 && m < g.M)
                     reinterpret_cast<float2 *>(g.pick_pairs)[(size_t)m * (g.N >> 4) + (n >> 4)] =
                         make_float2(best, __int_as_float(besti));

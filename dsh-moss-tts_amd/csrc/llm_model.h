@@ -95,6 +95,13 @@ public:
     int device() const { return device_; }
     hipStream_t stream() const { return stream_; }
 
+    // Quantiser capture (tests; moss_hip_llm_capture): W8A8 quantisers also record their
+    // fp32 input, int8 output and scales, and the stage outputs around them.
+    void set_capture(bool on);
+    // Bytes of the last capture of `what` (MOSS_HIP_CAP_GLOBAL / LOCAL / PREFILL), copied to
+    // out when out != nullptr and bytes suffice; 0 when none was taken.
+    size_t capture_read(int what, void *out, size_t bytes);
+
     // Device weights, shared with the batched engine.
     struct Weights {
         const LayerW *global;  // [kLayers]
@@ -186,6 +193,13 @@ private:
     void *snap_ = nullptr;               // prefix snapshot [2][layers][heads][prefix][64]
 
     hipGraphExec_t g_global_ = nullptr, g_local_ = nullptr, g_local_fused_ = nullptr;
+
+    bool capture_ = false;
+    float *cap_dec_ = nullptr;           // [kLayers + kLocalLen][MOSS_HIP_CAP_STEP]: global blocks, local positions
+    uint8_t *cap_pre_ = nullptr;         // prefill capture, [kLayers] x cap_layer_bytes(m)
+    size_t cap_pre_bytes_ = 0;           // its allocation
+    size_t cap_pre_used_ = 0;            // bytes of the last W8A8 prefill captured
+    bool cap_taken_[2] = {false, false}; // a global step / local half was captured
 
     int pos_ = 0, prefix_pos_ = 0;
     const volatile uint8_t *cancel_ = nullptr;

@@ -266,7 +266,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, wm_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_};
+    void *bufs[] = {blob_, wm_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_, cap_dec_, cap_pre_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -299,6 +299,10 @@ void Model::enqueue_global_step(hipStream_t s, const int *row_dev) {
         g.lnf_w = lnf_w_; g.lnf_b = lnf_b_; g.hidden = hidden_;
         g.state = state_; g.ll = ll_; g.err = &state_->ll_err; g.a8 = decode_a8_;
         g.poll_budget = next_poll_budget();
+        if (capture_ && decode_a8_) {
+            g.cap = cap_dec_;
+            cap_taken_[0] = true;
+        }
         hip_check(launch_decode_global(g, kvt_, s), "decode global step");
         return;
     }
@@ -454,6 +458,10 @@ void Model::enqueue_frame_local(hipStream_t s, bool text_gate, bool fused) {
         base.state = state_; base.ll = ll_; base.err = &state_->ll_err; base.x_out = lres_;
         base.a8 = decode_a8_;
         base.poll_budget = next_poll_budget();
+        if (capture_ && decode_a8_) {
+            base.cap = cap_dec_ + (size_t)kLayers * MOSS_HIP_CAP_STEP;
+            cap_taken_[1] = true;
+        }
         for (int ch = 0; ch < kNVq; ++ch) base.aemb[ch] = aemb_[ch];
         base.qkv_table = qkv_table_;
         base.logits = logits_;
@@ -592,6 +600,43 @@ void Model::write_state_header() {
 
 void Model::reset() { pos_ = 0; }
 
+// Per layer of a prefill capture of m rows: fp32 rows (xin, ln1, att, xm, ln2: 768 wide; h:
+// 3072; xout: 768), then the int8 operands (ln1, att, ln2: M16 x 768; h: M16 x 3072) and their
+// block scales (M16 x 24 x 3, M16 x 96), as moss_hip.h lays them out.
+static size_t cap_layer_bytes(size_t m) {
+    const size_t m16 = (m + 15) / 16 * 16;
+    return 4 * m * (6 * kHidden + kFF) + m16 * (3 * kHidden + kFF) + 4 * m16 * (3 * (kHidden / 32) + kFF / 32);
+}
+
+void Model::set_capture(bool on) {
+    if (on && !cap_dec_) {
+        const size_t n = (size_t)(kLayers + kLocalLen) * MOSS_HIP_CAP_STEP;
+        hip_check(hipMalloc(&cap_dec_, sizeof(float) * n), "hipMalloc(capture)");
+        hip_check(hipMemsetAsync(cap_dec_, 0, sizeof(float) * n, stream_), "capture clear");
+        hip_check(hipStreamSynchronize(stream_), "sync");
+    }
+    capture_ = on;
+}
+
+size_t Model::capture_read(int what, void *out, size_t bytes) {
+    const void *src = nullptr;
+    size_t n = 0;
+    if (what == MOSS_HIP_CAP_GLOBAL && cap_taken_[0]) {
+        src = cap_dec_;
+        n = sizeof(float) * kLayers * MOSS_HIP_CAP_STEP;
+    } else if (what == MOSS_HIP_CAP_LOCAL && cap_taken_[1]) {
+        src = cap_dec_ + (size_t)kLayers * MOSS_HIP_CAP_STEP;
+        n = sizeof(float) * kLocalLen * MOSS_HIP_CAP_STEP;
+    } else if (what == MOSS_HIP_CAP_PREFILL && cap_pre_used_ > 0) {
+        src = cap_pre_;
+        n = cap_pre_used_;
+    }
+    if (n == 0 || out == nullptr || bytes < n) return n;
+    hip_check(hipMemcpyAsync(out, src, n, hipMemcpyDeviceToHost, stream_), "capture d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    return n;
+}
+
 void Model::get_hidden(float *out) {
     hip_check(hipMemcpyAsync(out, hidden_, kHidden * 4, hipMemcpyDeviceToHost, stream_), "hidden d2h");
     hip_check(hipStreamSynchronize(stream_), "sync");
@@ -708,6 +753,42 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     // W8A8 (the reference's prefill, llm.cpp:319-328): every GEMM input is also
     // quantised per 32-block by the kernel that produces it
     const bool a8 = !prefill_a16_;
+    // quantiser capture (tests): the producers also write their fp32 rows into the
+    // capture, and each int8 operand and the residual stream are copied there before
+    // the next kernel overwrites them
+    const bool cap = capture_ && a8;
+    const size_t m16 = (size_t)(m + 15) / 16 * 16, cap_lb = cap_layer_bytes(m);
+    if (cap && cap_pre_bytes_ < cap_lb * kLayers) {
+        if (cap_pre_) hip_check(hipFree(cap_pre_), "free capture");
+        cap_pre_ = nullptr;
+        cap_pre_bytes_ = 0;
+        hip_check(hipMalloc(&cap_pre_, cap_lb * kLayers), "hipMalloc(prefill capture)");
+        cap_pre_bytes_ = cap_lb * kLayers;
+    }
+    cap_pre_used_ = 0;
+    auto cap_f = [&](int l, int sec) -> float * {  // 0 xin, 1 ln1, 2 att, 3 xm, 4 ln2, 5 h, 6 xout
+        if (!cap || l >= kLayers) return nullptr;
+        const size_t off = sec <= 5 ? (size_t)sec * m * kHidden : (size_t)5 * m * kHidden + (size_t)m * kFF;
+        return reinterpret_cast<float *>(cap_pre_ + (size_t)l * cap_lb) + off;
+    };
+    const size_t cap_q0 = 4 * (size_t)m * (6 * kHidden + kFF);
+    const size_t cap_d0 = cap_q0 + m16 * (3 * kHidden + kFF);
+    auto cap_copy_q = [&](int l, int sec, const int8_t *q, const float *d) {  // 0 ln1, 1 att, 2 ln2, 3 h
+        if (!cap || l >= kLayers) return;
+        uint8_t *base = cap_pre_ + (size_t)l * cap_lb;
+        const size_t K = sec == 3 ? kFF : kHidden;
+        hip_check(hipMemcpyAsync(base + cap_q0 + m16 * kHidden * sec, q, m16 * K, hipMemcpyDeviceToDevice, s),
+                  "capture q8");
+        hip_check(hipMemcpyAsync(base + cap_d0 + 4 * m16 * (kHidden / 32) * sec, d, 4 * m16 * (K / 32),
+                                 hipMemcpyDeviceToDevice, s),
+                  "capture d8");
+    };
+    auto cap_copy_x = [&](int l, int sec) {
+        if (!cap || l >= kLayers) return;
+        hip_check(hipMemcpyAsync(cap_f(l, sec), pre_x_, sizeof(float) * m * kHidden, hipMemcpyDeviceToDevice, s),
+                  "capture x");
+    };
+    cap_copy_x(0, 0);
     int8_t *q8 = a8 ? pre_q8_ : nullptr;
     float *d8 = a8 ? pre_d8_ : nullptr;
     auto operand = [&](GemmArgs &g) {
@@ -722,8 +803,9 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     uint8_t *a_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_a_);
     uint8_t *o_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_o_);
     uint8_t *h_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_h_);
-    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, nullptr, m, s, nullptr, q8, d8, a_hl),
+    hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, cap_f(0, 1), m, s, nullptr, q8, d8, a_hl),
               "prefill ln1");
+    cap_copy_q(0, 0, pre_q8_, pre_d8_);
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = g_[l];
@@ -738,15 +820,19 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
         t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out_hl = o_hl;
         t.q8 = q8; t.d8 = d8;
+        t.out = cap_f(l, 2);
         hip_check(launch_attn_tiles(t, kvt_, s), "prefill attention");
+        cap_copy_q(l, 1, pre_q8_, pre_d8_);
         GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
         p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = o_hl; p.lda = kHidden; p.M = m;
         p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);
         operand(p);
         hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
         hip_check(launch_resid_ln_rows(pre_part_, p.ksplit, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
-                                       nullptr, nullptr, s, q8, d8, a_hl),
+                                       cap_f(l, 4), nullptr, s, q8, d8, a_hl),
                   "prefill proj reduce + ln2");
+        cap_copy_x(l, 3);
+        cap_copy_q(l, 2, pre_q8_, pre_d8_);
         GemmArgs f1;
         f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.a_hl = a_hl; f1.lda = kHidden; f1.M = m;
         f1.y_hl = h_hl; f1.bias = L.fc_in_b;
@@ -754,8 +840,11 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         if (a8) {  // fc_out's int8 operand, quantised in fc_in's epilogue
             f1.q8_out = pre_q8h_;
             f1.d8_out = pre_d8h_;
+            f1.y = cap_f(l, 5);
+            f1.ldy = kFF;
         }
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "prefill fc_in");
+        cap_copy_q(l, 3, pre_q8h_, pre_d8h_);
         GemmArgs f2;
         f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = h_hl; f2.lda = kFF; f2.M = m;
         f2.part = pre_part_; f2.ksplit = gemm_ksplit(m, kHidden, kFF);
@@ -770,12 +859,16 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "prefill fc_out");
         const bool last = l + 1 == kLayers;  // LN1 of the next layer rides on the reduce
         hip_check(launch_resid_ln_rows(pre_part_, f2.ksplit, m, L.fc_out_b, pre_x_, kHidden, pre_x_,
-                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b, nullptr,
-                                       nullptr, s, last ? nullptr : q8, last ? nullptr : d8,
+                                       last ? nullptr : g_[l + 1].ln1_w, last ? nullptr : g_[l + 1].ln1_b,
+                                       cap_f(l + 1, 1), nullptr, s, last ? nullptr : q8, last ? nullptr : d8,
                                        last ? nullptr : a_hl),
                   "prefill fc_out reduce");
+        cap_copy_x(l, 6);
+        cap_copy_x(l + 1, 0);
+        cap_copy_q(l + 1, 0, pre_q8_, pre_d8_);
     }
     hip_check(launch_layernorm(pre_x_ + (size_t)(m - 1) * kHidden, lnf_w_, lnf_b_, hidden_, nullptr, 0, s), "ln_f");
+    if (cap) cap_pre_used_ = cap_lb * kLayers;
     pos_ = start + m;
     write_state_header();
     hip_check(hipStreamSynchronize(s), "sync");

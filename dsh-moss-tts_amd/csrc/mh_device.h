@@ -241,11 +241,12 @@ __device__ __forceinline__ int greedy_pick_reduce(const PickIn &in, float pen, f
     const int t = threadIdx.x;
     const float *vals = in.vals;
     const int *cnt = in.cnt;
-    float best = -INFINITY;
+    float best = -INFINITY, v0 = 0.0f;
     int besti = kCodebook;
 #pragma unroll
     for (int k = 0; k < kCodebook / 256; ++k) {  // ascending index per thread
         const float v = penalised(vals[k], cnt[k], pen);
+        if (k == 0) v0 = v;
         if (v > best) {
             best = v;
             besti = t + 256 * k;
@@ -254,9 +255,12 @@ __device__ __forceinline__ int greedy_pick_reduce(const PickIn &in, float pen, f
     wave_argmax(best, besti);
     if ((t & 63) == 0) {
         bv[t >> 6] = best;
-        bi[t >> 6] = besti;
+        // thread 0 holds index 0: a NaN there is flagged (sampler.cpp:24-26 never moves off
+        // index 0 then, every comparison with it being false)
+        bi[t >> 6] = (t == 0 && v0 != v0) ? -1 : besti;
     }
     __syncthreads();
+    if (bi[0] < 0) return 0;
     float b = bv[0];
     int idx = bi[0];
     for (int w = 1; w < 4; ++w)

@@ -9,6 +9,7 @@
 // row_dot_q8_4x4_actf32 (reference csrc/src/gemv_avx2.cpp:123-150).
 #pragma once
 #include "mh_device.h"
+#include "moss_hip.h"  // MOSS_HIP_CAP_* (quantiser capture layout)
 
 namespace mh {
 
@@ -74,6 +75,14 @@ __device__ __forceinline__ void quant_act_lds(float *act, float *da, int K) {
         act[i] = (float)q;
         if ((i & 31) == 0) da[i >> 5] = d;
     }
+}
+
+// Quantiser capture (tests only, moss_hip_llm_capture): the workgroup's 256 threads
+// copy n values of an LDS vector to dst.  A thread reads only the elements
+// quant_act_lds gives it (i = tix() + 256 k), so a copy made just before the
+// quantiser needs no barrier of its own.
+__device__ __forceinline__ void cap_copy(float *dst, const float *src, int n) {
+    for (int i = tix(); i < n; i += 256) dst[i] = src[i];
 }
 
 // Sum of a row's 16 lanes (lanes 16*bl + 4*kk + j for the row kk): every lane

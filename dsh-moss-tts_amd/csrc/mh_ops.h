@@ -389,6 +389,7 @@ struct GlobalArgs {
     unsigned *err = nullptr;            // set when a wait runs out
     int a8 = 0;                         // W8A8 GEMVs (activations quantised per 32-block), else W8A16
     int poll_budget = 0;                // poll rounds a wait may take before it gives up (kPollBudget)
+    float *cap = nullptr;               // W8A8 only: quantiser capture [kLayers][MOSS_HIP_CAP_STEP] (tests)
 };
 hipError_t launch_decode_global(const GlobalArgs &a, KvType kv, hipStream_t s);
 
@@ -421,6 +422,7 @@ struct LocalArgs {
                                        // frame's code counts, row[0] = slot and frame + 1 (sample_kernel's work)
     int a8 = 0;                        // W8A8 GEMVs (activations quantised per 32-block), else W8A16
     int poll_budget = 0;               // poll rounds a wait may take before it gives up (kPollBudget)
+    float *cap = nullptr;              // W8A8 only: quantiser capture [kLocalLen][MOSS_HIP_CAP_STEP] (tests)
 };
 hipError_t decode_local_occupancy(int *per_cu);
 hipError_t launch_decode_local(const LocalArgs &a, hipStream_t s);

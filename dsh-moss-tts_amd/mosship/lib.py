@@ -16,6 +16,15 @@ LIB_PATH = os.path.join(PKG_DIR, "libmoss_hip.so")
 OK, EINVAL, EDEVICE, EFORMAT, EUNSUPPORTED, ESTATE = 0, 1, 2, 3, 4, 5
 F32, F16 = 0, 1
 
+# Quantiser capture (moss_hip_llm_capture): kinds and the per-step float offsets of a decode
+# capture, as include/moss_hip.h declares them (name -> (offset, length)).
+CAP_GLOBAL, CAP_LOCAL, CAP_PREFILL = 0, 1, 2
+CAP_STEP = 17088
+CAP = {"xin": (0, 768), "ln1": (768, 768), "ln1_q": (1536, 768), "ln1_d": (2304, 24), "qkv": (2328, 2304),
+       "att": (4632, 768), "att_q": (5400, 768), "att_d": (6168, 24), "xm": (6192, 768), "ln2": (6960, 768),
+       "ln2_q": (7728, 768), "ln2_d": (8496, 24), "h": (8520, 3072), "h_q": (11592, 3072), "h_d": (14664, 96),
+       "xout": (14760, 768), "lnf": (15528, 768), "lnf_q": (16296, 768), "lnf_d": (17064, 24)}
+
 EXPORTED = [
     "moss_hip_last_error", "moss_hip_abi_version",
     "moss_hip_llm_create", "moss_hip_llm_create_from_file", "moss_hip_llm_destroy", "moss_hip_llm_reset",
@@ -23,7 +32,7 @@ EXPORTED = [
     "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
     "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
     "moss_hip_llm_gate_rows", "moss_hip_llm_fallbacks",
-    "moss_hip_llm_kv_export", "moss_hip_llm_kv_import",
+    "moss_hip_llm_kv_export", "moss_hip_llm_kv_import", "moss_hip_llm_capture", "moss_hip_llm_capture_read",
     "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
@@ -99,6 +108,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_llm_set_cancel_flag.argtypes = [vp, vp]
     L.moss_hip_llm_kv_export.argtypes = [vp, i32, vp, vp]
     L.moss_hip_llm_kv_import.argtypes = [vp, i32, vp, vp, vp]
+    L.moss_hip_llm_capture.argtypes = [vp, i32]
+    L.moss_hip_llm_capture_read.argtypes = [vp, i32, vp, C.c_size_t, C.POINTER(C.c_size_t)]
     L.moss_hip_gemv_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, i32, vp]
     L.moss_hip_gemv_q8x4_w8a8.argtypes = [vp, i32, i32, vp, vp, vp]
     L.moss_hip_gemm_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
@@ -287,6 +298,23 @@ class HipLLM:
 
     def restore_prefix(self):
         check(self.L.moss_hip_llm_restore_prefix(self._h))
+
+    def capture(self, on: bool = True):
+        """Quantiser capture (tests): W8A8 quantisers record their inputs and outputs."""
+        check(self.L.moss_hip_llm_capture(self._h, 1 if on else 0))
+
+    def capture_read(self, what: int) -> np.ndarray:
+        """Raw bytes of the last capture of `what` (CAP_GLOBAL / CAP_LOCAL / CAP_PREFILL)."""
+        n = C.c_size_t(0)
+        check(self.L.moss_hip_llm_capture_read(self._h, what, None, 0, C.byref(n)))
+        out = np.empty(n.value, np.uint8)
+        check(self.L.moss_hip_llm_capture_read(self._h, what, _ptr(out), out.size, None))
+        return out
+
+    def capture_steps(self, what: int) -> list:
+        """A decode capture as one dict per step (block or local position) of named float arrays."""
+        raw = self.capture_read(what).view(np.float32).reshape(-1, CAP_STEP)
+        return [{k: step[o:o + n].copy() for k, (o, n) in CAP.items()} for step in raw]
 
     def kv_export(self, n_pos: int):
         k = np.empty((12, n_pos, 768), np.float32)

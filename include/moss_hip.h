@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 6
+#define MOSS_HIP_ABI_VERSION 7
 
 enum {
     MOSS_HIP_OK = 0,
@@ -153,6 +153,57 @@ int moss_hip_llm_kv_export(moss_hip_llm *m, int n_pos, float *k, float *v);
 /* Import for load_prefix / load_state (llm.cpp:512-632): sets pos = n_pos and, when
  * hidden768 != NULL, the hidden state.  fp32 values are rounded to fp16 for an fp16 cache. */
 int moss_hip_llm_kv_import(moss_hip_llm *m, int n_pos, const float *k, const float *v, const float *hidden768);
+
+/* ---- Quantiser capture (test instrumentation).  No counterpart in the reference, whose
+ * activation quantiser is a plain function a test can call directly (quantize_row_q8_0_scaled,
+ * csrc/src/quant.cpp:28-54).  Here the W8A8 quantisers run inside other kernels -- the prefill's
+ * LayerNorm rows, attention epilogue and fc_in epilogue, and the in-LDS quantiser of every GEMV
+ * stage of the fused decode kernels -- so with capture on each of them also records the fp32
+ * vector it quantised, the int8 values and fp32 block scales it produced, and the stage outputs
+ * around it, for a test to check every quantiser bit for bit and every W8A8 stage on its own
+ * int8 inputs.  Capture costs memory (~130 MB for a 256-row prefill) and time: tests only.
+ * Only W8A8 paths record: the prefill without prefill_a16, the fused decode with decode_a8. */
+int moss_hip_llm_capture(moss_hip_llm *m, int on);
+
+enum {
+    MOSS_HIP_CAP_GLOBAL = 0,  /* the last fused global step: [12 blocks][MOSS_HIP_CAP_STEP] float */
+    MOSS_HIP_CAP_LOCAL = 1,   /* the last fused greedy local half: [17 positions][MOSS_HIP_CAP_STEP] float */
+    MOSS_HIP_CAP_PREFILL = 2  /* the last W8A8 prefill of m rows (M16 = m rounded up to 16), per layer:
+                                 float xin[m][768], ln1[m][768], att[m][768], xm[m][768], ln2[m][768],
+                                 h[m][3072], xout[m][768]; int8 ln1_q[M16 * 768], att_q[M16 * 768],
+                                 ln2_q[M16 * 768], h_q[M16 * 3072]; float ln1_d[M16 * 24], att_d[M16 * 24],
+                                 ln2_d[M16 * 24], h_d[M16 * 96] -- the int8 operands and scales exactly as
+                                 the GEMMs read them, in the matrix-core order (row m, column k of a K-wide
+                                 operand at byte ((m / 16) * (K / 32) + k / 32) * 512 + 8 * (m % 16 + 16 *
+                                 ((k % 32) / 8)) + k % 8; block b's scale at float ((m / 16) * (K / 32) +
+                                 b) * 16 + m % 16) */
+};
+/* Offsets (floats) within one decode step of a capture.  Int8 values are stored as floats. */
+enum {
+    MOSS_HIP_CAP_XIN = 0,       /* block input x (768) */
+    MOSS_HIP_CAP_LN1 = 768,     /* LN1(x): QKV's fp32 input (768), its int8 values, its 24 scales */
+    MOSS_HIP_CAP_LN1_Q = 1536,
+    MOSS_HIP_CAP_LN1_D = 2304,
+    MOSS_HIP_CAP_QKV = 2328,    /* q | k | v after bias and RoPE; k, v as the cache holds them (2304) */
+    MOSS_HIP_CAP_ATT = 4632,    /* attention output: proj's fp32 input, int8, scales */
+    MOSS_HIP_CAP_ATT_Q = 5400,
+    MOSS_HIP_CAP_ATT_D = 6168,
+    MOSS_HIP_CAP_XM = 6192,     /* x after the attention sub-block (768) */
+    MOSS_HIP_CAP_LN2 = 6960,    /* LN2(xm): fc_in's fp32 input, int8, scales */
+    MOSS_HIP_CAP_LN2_Q = 7728,
+    MOSS_HIP_CAP_LN2_D = 8496,
+    MOSS_HIP_CAP_H = 8520,      /* gelu(fc_in): fc_out's fp32 input (3072), int8 (3072), scales (96) */
+    MOSS_HIP_CAP_H_Q = 11592,
+    MOSS_HIP_CAP_H_D = 14664,
+    MOSS_HIP_CAP_XOUT = 14760,  /* block output (768) */
+    MOSS_HIP_CAP_LNF = 15528,   /* local positions >= 1: local ln_f(xout), the audio head's fp32 input, */
+    MOSS_HIP_CAP_LNF_Q = 16296, /*   int8, scales */
+    MOSS_HIP_CAP_LNF_D = 17064,
+    MOSS_HIP_CAP_STEP = 17088
+};
+/* Copies the last capture of `what` into out (bytes >= its size); *needed (may be NULL) receives
+ * the size.  out == NULL only reports the size.  ESTATE when nothing of that kind was captured. */
+int moss_hip_llm_capture_read(moss_hip_llm *m, int what, void *out, size_t bytes, size_t *needed);
 
 /* ------------------------------------------------------------------ batched streams */
 

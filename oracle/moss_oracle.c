@@ -239,6 +239,22 @@ void mo_gemm(const uint8_t *w, int rows, int cols, const float *x, int m, float 
     free(d);
 }
 
+/* The W8A8 product of gemm_par (reference csrc/src/gemv.cpp:281-309) on activations
+ * quantised elsewhere: row r of Y for activation row i is row_dot_q8_4x4's block sum
+ * (gemv_avx2.cpp:105-121) of q[i] with block scales d[i].  Lets a test evaluate a GPU
+ * stage on the GPU's own int8 operand. */
+void mo_gemm_w8a8_q(const uint8_t *w, int rows, int cols, const int8_t *q, const float *d, int m, float *y) {
+    int nb = cols / 32;
+#pragma omp parallel for schedule(static) if ((size_t)rows * m >= 4096)
+    for (int g = 0; g < rows / 4; ++g) {
+        const uint8_t *grp = w + (size_t)g * nb * 136;
+        for (int i = 0; i < m; ++i)
+            for (int k = 0; k < 4; ++k)
+                y[(size_t)i * rows + g * 4 + k] =
+                    mo_row_dot_w8a8(grp, nb, k, q + (size_t)i * cols, d + (size_t)i * nb);
+    }
+}
+
 /* ------------------------------------------------------------- elementwise */
 
 /* reference csrc/src/llm.cpp:22-25 */

@@ -61,6 +61,8 @@ float mo_row_dot_w8a8(const uint8_t *group, int nb, int k, const int8_t *qa, con
 void mo_gemv_a16(const uint8_t *w, int rows, int cols, const float *x, float *y);
 /* Y[m][rows] = X[m][cols] W^T, W8A8 (quantised activations) or A16 (reference gemv.cpp:276-309) */
 void mo_gemm(const uint8_t *w, int rows, int cols, const float *x, int m, float *y, int a16);
+/* W8A8 gemm on given int8 activations q[m][cols] and block scales d[m][cols/32] */
+void mo_gemm_w8a8_q(const uint8_t *w, int rows, int cols, const int8_t *q, const float *d, int m, float *y);
 
 /* ---- elementwise pieces (reference csrc/src/llm.cpp) ---- */
 float mo_gelu_new(float v);                                                    /* llm.cpp:22-25 */

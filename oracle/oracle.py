@@ -74,6 +74,7 @@ class Oracle:
         L.mo_row_dot_w8a8.argtypes = [_u8p, C.c_int, C.c_int, _i8p, _f32p]
         L.mo_gemv_a16.argtypes = [_u8p, C.c_int, C.c_int, _f32p, _f32p]
         L.mo_gemm.argtypes = [_u8p, C.c_int, C.c_int, _f32p, C.c_int, _f32p, C.c_int]
+        L.mo_gemm_w8a8_q.argtypes = [_u8p, C.c_int, C.c_int, _i8p, _f32p, C.c_int, _f32p]
         L.mo_gelu_new.restype = C.c_float
         L.mo_gelu_new.argtypes = [C.c_float]
         L.mo_layernorm.argtypes = [_f32p, _f32p, _f32p, _f32p]
@@ -145,6 +146,14 @@ class Oracle:
         x = _f32(x).reshape(-1, cols)
         y = np.empty((x.shape[0], rows), np.float32)
         self.lib.mo_gemm(_u8(w), rows, cols, x, x.shape[0], y, int(a16))
+        return y
+
+    def gemm_w8a8_q(self, w, rows, cols, q, d):
+        """W8A8 product on given int8 activations q [m][cols] and block scales d [m][cols/32]."""
+        q = np.ascontiguousarray(q, np.int8).reshape(-1, cols)
+        d = _f32(d).reshape(q.shape[0], cols // 32)
+        y = np.empty((q.shape[0], rows), np.float32)
+        self.lib.mo_gemm_w8a8_q(_u8(w), rows, cols, q, d, q.shape[0], y)
         return y
 
     def row_dot_w8a8(self, group, nb, k, x):

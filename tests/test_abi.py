@@ -22,7 +22,23 @@ def test_library_exports_every_declared_symbol():
     L = lib.load()
     missing = [s for s in declared_symbols() if not hasattr(L, s)]
     assert not missing, missing
-    assert L.moss_hip_abi_version() == 6
+    assert L.moss_hip_abi_version() == 7
+
+
+def test_capture_layout_matches_header():
+    """The binding's capture offsets are the header's MOSS_HIP_CAP_* values, and the
+    sections tile one step exactly."""
+    text = open(os.path.join(ROOT, "include", "moss_hip.h")).read()
+    vals = {m[0]: int(m[1]) for m in re.findall(r"\b(MOSS_HIP_CAP_\w+)\s*=\s*(\d+)", text)}
+    assert vals["MOSS_HIP_CAP_STEP"] == lib.CAP_STEP
+    assert (vals["MOSS_HIP_CAP_GLOBAL"], vals["MOSS_HIP_CAP_LOCAL"], vals["MOSS_HIP_CAP_PREFILL"]) == \
+        (lib.CAP_GLOBAL, lib.CAP_LOCAL, lib.CAP_PREFILL)
+    end = 0
+    for name, (off, n) in sorted(lib.CAP.items(), key=lambda kv: kv[1][0]):
+        assert vals["MOSS_HIP_CAP_" + name.upper()] == off
+        assert off == end, name
+        end = off + n
+    assert end == lib.CAP_STEP
 
 
 def test_error_paths_without_gpu():

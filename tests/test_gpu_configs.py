@@ -218,3 +218,56 @@ def test_64_streams_generate(torch_gpu, oracle, bench_model, streams_state):
     assert herr and max(herr) <= TOL
     b.close()
     g.close()
+
+
+def test_64_streams_128_frames_penalty(torch_gpu, oracle, bench_model, streams_state):
+    """The benchmarked run length: 128 lock-step greedy frames of the 64 streams, with
+    the reference's default repetition penalty 1.2 (capi.cpp:22), every count of the
+    streams' histories applied (sampler.cpp:13-28).  Free-running greedy decoding is
+    chaotic, so the check is teacher forcing on the GPU's own trajectory: on 8 streams
+    (the shortest context, the longest, 6 spread between) an oracle LlmModel is fed the
+    GPU's codes as forced rows (llm.cpp:634-733) and predicts each frame's 16 codes
+    from the same history; >= 99 % must equal the GPU's picks.  Every K/V row the 127
+    global steps wrote (all 12 layers) is compared (<= 1e-3), and the final hidden
+    state of each stream whose codes all agree.  The codes must repeat within some
+    channel's history, so the penalty path is exercised."""
+    blob = bench_model
+    ctx, k, v, hs = streams_state
+    n, frames, rep = len(ctx), 128, 1.2
+    cap = int(ctx.max()) + frames + 2
+    print(f"config 4: 64 streams x {frames} frames, penalty {rep}", flush=True)
+    g = HipLLM(blob)
+    b = HipBatch(g, max_streams=n, capacity=cap)
+    for s in range(n):
+        b.set_stream(s, k[:, :ctx[s]], v[:, :ctx[s]], hs[s])
+    out = b.generate(n, frames, SampleParams.make(greedy=True, min_frames=frames, repetition_penalty=rep))
+    assert (out["frames"] == frames).all()
+    order = np.argsort(ctx)
+    pick = sorted(set(order[np.linspace(0, n - 1, 8).round().astype(int)].tolist()))
+    assert int(ctx[pick[0]]) == int(ctx.min()) and int(ctx[pick[-1]]) == int(ctx.max()) and len(pick) == 8
+    agree, herr, kverr, repeats = [], [], [], 0
+    for s in pick:
+        c = int(ctx[s])
+        rows = out["rows"][:, s].copy()
+        rows[:, 0] = mf.SLOT
+        repeats += sum(frames - len(np.unique(rows[:, 1 + ch])) for ch in range(16))
+        m = _oracle_at(oracle, blob, k[:, :c], v[:, :c], hs[s], kv_f16=True, max_ctx=cap)
+        ref = m.generate(frames, OSP.make(greedy=True, min_frames=frames, repetition_penalty=rep), forced=rows)
+        eq = out["rows"][:, s, 1:] == ref["rows"][:, 1:]
+        agree.append(float(np.mean(eq)))
+        assert b.position(s) == m.position == c + frames - 1
+        bk, bv = b.kv_export(s, c + frames - 1)
+        ok, ov = m.kv_export(c + frames - 1)
+        kverr.append(max(max_rel(bk[:, c:], ok[:, c:]), max_rel(bv[:, c:], ov[:, c:])))
+        if eq.all():
+            herr.append(max_rel(b.hidden(s), m.hidden()))
+        print(f"  stream {s} ctx {c}: agreement {agree[-1]:.4f}, new K/V rows {kverr[-1]:.2e}", flush=True)
+    report("config4_128_frames_penalty", streams=n, checked=len(pick), frames=frames, penalty=rep,
+           ctx_checked=[int(ctx[s]) for s in pick], agreement=float(np.mean(agree)), min_agreement=min(agree),
+           kv_rows_max_rel=max(kverr), hidden_max_rel=max(herr) if herr else None, repeated_codes=repeats)
+    assert repeats > 0
+    assert np.mean(agree) >= 0.99
+    assert max(kverr) <= TOL
+    assert herr and max(herr) <= TOL
+    b.close()
+    g.close()

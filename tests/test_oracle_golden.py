@@ -23,6 +23,10 @@ def test_gemv_dequant_gemm_golden(oracle, name, rows, cols):
         assert np.float32(oracle.row_dot_w8a8(groups[r // 4], nb, r % 4, g["x"])) == g["w8a8"][r]
     assert np.array_equal(oracle.gemm(g["w"], rows, cols, g["xs"], a16=True), g["gemm_a16"])
     assert np.array_equal(oracle.gemm(g["w"], rows, cols, g["xs"], a16=False), g["gemm_w8a8"])
+    # the W8A8 product on operands quantised beforehand (what the GPU capture tests feed it)
+    qd = [oracle.quantize_row(x) for x in g["xs"]]
+    y = oracle.gemm_w8a8_q(g["w"], rows, cols, np.stack([q for q, _, _ in qd]), np.stack([d for _, _, d in qd]))
+    assert np.array_equal(y.view(np.uint32), g["gemm_w8a8"].view(np.uint32))
 
 
 def test_quantize_and_fp16_golden(oracle):

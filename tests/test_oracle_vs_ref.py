@@ -51,6 +51,22 @@ def test_sampler_bit_exact(oracle, ref):
         assert oracle.sample_token(logits, p, prev, seed=seed) == ref.sample_token(logits, p, prev, seed=seed)
 
 
+def test_greedy_nan_semantics(oracle, ref):
+    """The greedy scan (sampler.cpp:23-27) with NaN logits: a NaN elsewhere never wins, a
+    NaN at index 0 is never left (pick 0).  The GPU picks are tested against this."""
+    rng = np.random.default_rng(8)
+    p = SampleParams.make(greedy=True, repetition_penalty=1.2)
+    for case in range(4):
+        logits = rng.standard_normal(1024).astype(np.float32)
+        logits[[517, 900]] = np.nan
+        if case & 1:
+            logits[0] = np.nan
+        prev = rng.integers(0, 1024, 10).astype(np.int32) if case & 2 else None
+        got = oracle.sample_token(logits, p, prev)
+        assert got == ref.sample_token(logits, p, prev)
+        assert got == 0 if case & 1 else got not in (0, 517, 900)
+
+
 def test_model_steps_bit_exact(oracle, ref, golden_model):
     """Prefill (W8A8), then greedy frames with the 1.2 repetition penalty: rows and
     hidden state bit-identical between the restatement and the reference."""

@@ -60,9 +60,11 @@ def test_noalloc_matches_allocating_entry(torch_gpu):
 
 
 def test_noalloc_graph_replays(torch_gpu):
-    """Captured once and replayed with new inputs, eager calls of the allocating
-    entry point (other slice counts) between the replays: every replay equals the
-    eager result on its inputs."""
+    """Captured once and replayed with new inputs, eager no-allocation calls with other
+    key counts (other slice counts, so other grids on the same static scratch: its
+    arrival counts and generation stepped by a different launch) between the
+    replays: every replay equals the allocating entry point's result on its inputs,
+    and so does every eager call in between."""
     torch = torch_gpu
     ctx, stride, heads = 1500, 1500, 12
     rng = np.random.default_rng(12)
@@ -91,8 +93,9 @@ def test_noalloc_graph_replays(torch_gpu):
         assert np.array_equal(got, _run(torch, q, kc, vc, heads, stride, ctx, noalloc=False))
         assert max_rel(got, _ref(q, k, v, heads)) <= TOL
         n = 300 + 300 * rep
-        lib.attn_decode(q_d, k_d, v_d, heads, stride, n, side)
+        lib.attn_decode(q_d, k_d, v_d, heads, stride, n, side, noalloc=True)
         torch.cuda.synchronize()
+        assert np.array_equal(side.cpu().numpy(), _run(torch, q, kc, vc, heads, stride, n, noalloc=False))
 
 
 def test_noalloc_rejects_too_many_heads(torch_gpu):
