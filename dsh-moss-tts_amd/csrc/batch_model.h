@@ -31,6 +31,8 @@ public:
     int device() const { return model_.device(); }
     // Loads one stream's state: K/V [12][n_pos][768] fp32 (reference layout) and hidden[768].
     void set_stream(int s, int n_pos, const float *k, const float *v, const float *hidden);
+    // The same from a single-stream model's device state (its K/V, hidden, position), on the device.
+    void admit(int s, Model &src);
     void get_hidden(int s, float *out);
     void kv_export(int s, int n_pos, float *k, float *v);
     // One global step for streams [0, n): rows [n][17].

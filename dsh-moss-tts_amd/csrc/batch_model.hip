@@ -170,6 +170,38 @@ void Batch::set_stream(int s, int n_pos, const float *k, const float *v, const f
     pos_[s] = n_pos;
 }
 
+// Admission of a job prepared on a single-stream model (restore_prefix + prefill, the
+// reference's per-job flow, engine.cpp:447-470): its K/V rows go into the stream's pages
+// (converted to the batch's precision), its hidden state and position follow, all device to
+// device.  The model's last call has returned (calls are serialised), so its state is final
+// once its stream is drained.
+void Batch::admit(int s, Model &src) {
+    if (s < 0 || s >= S_) throw Status(MOSS_HIP_EINVAL, "stream out of range");
+    if (src.device() != model_.device()) throw Status(MOSS_HIP_EINVAL, "the model is on another device");
+    const Model::StateView v = src.state_view();
+    if (v.pos > cap_) throw Status(MOSS_HIP_EINVAL, "the model's position is above the batch capacity");
+    hip_check(hipSetDevice(model_.device()), "hipSetDevice");
+    hip_check(hipStreamSynchronize(src.stream()), "sync");
+    KvAdmit a;
+    a.k_src = v.k;
+    a.v_src = v.v;
+    a.src_layer_elems = v.layer_elems;
+    a.ctx_stride = v.ctx_stride;
+    a.src_kv = v.kv;
+    a.k_pool = kpool_;
+    a.v_pool = vpool_;
+    a.pool_layer_elems = layer_pool_elems_;
+    a.table_row = table_ + (size_t)s * pages_;
+    a.page_size = kPage;
+    a.pool_kv = kvt_;
+    hip_check(launch_kv_admit(a, v.pos, stream_), "kv admit");
+    hip_check(hipMemcpyAsync(hidden_ + (size_t)s * kHidden, v.hidden, kHidden * 4, hipMemcpyDeviceToDevice, stream_),
+              "hidden d2d");
+    hip_check(hipMemcpyAsync(pos_d_ + s, &v.pos, sizeof(int), hipMemcpyHostToDevice, stream_), "pos h2d");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    pos_[s] = v.pos;
+}
+
 void Batch::get_hidden(int s, float *out) {
     if (s < 0 || s >= S_) throw Status(MOSS_HIP_EINVAL, "stream out of range");
     hip_check(hipMemcpyAsync(out, hidden_ + (size_t)s * kHidden, kHidden * 4, hipMemcpyDeviceToHost, stream_), "d2h");

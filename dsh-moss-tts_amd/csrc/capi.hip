@@ -198,6 +198,8 @@ int moss_hip_llm_reset(moss_hip_llm *m) {
 int moss_hip_llm_position(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->position() : -1; }
 int moss_hip_llm_fallbacks(const moss_hip_llm *m) { return (m && m->impl) ? m->impl->fallbacks() : -1; }
 
+int moss_hip_fallbacks_total(void) { return mh::fallbacks_total.load(std::memory_order_relaxed); }
+
 int moss_hip_llm_get_hidden(moss_hip_llm *m, float *out) {
     return guard([&] {
         if (!out) throw Status(MOSS_HIP_EINVAL, "null output");
@@ -312,6 +314,10 @@ int moss_hip_batch_set_stream(moss_hip_batch *b, int stream, int n_pos, const fl
         if (n_pos > 0 && (!k || !v)) throw Status(MOSS_HIP_EINVAL, "null buffer");
         batch_of(b).set_stream(stream, n_pos, k, v, hidden);
     });
+}
+
+int moss_hip_batch_admit(moss_hip_batch *b, int stream, moss_hip_llm *model) {
+    return guard([&] { batch_of(b).admit(stream, model_of(model)); });
 }
 
 int moss_hip_batch_get_hidden(moss_hip_batch *b, int stream, float *out) {

@@ -817,7 +817,53 @@ __global__ void kv_export_paged_kernel(const void *pool, const int *table_row, i
     }
 }
 
+// grid (n_pos, layers, 2): position p of layer l of K (z = 0) or V (z = 1); thread t copies
+// element t of the 768 (head t / 64, dim t % 64) and t + 256, t + 512.
+template <int SK, int DK>
+__global__ __launch_bounds__(256) void kv_admit_kernel(KvAdmit a) {
+    const int p = blockIdx.x, l = blockIdx.y, z = blockIdx.z;
+    const uint8_t *src = static_cast<const uint8_t *>(z ? a.v_src : a.k_src) +
+                         (size_t)l * a.src_layer_elems * (SK == KV_F16 ? 2 : 4);
+    uint8_t *pool = static_cast<uint8_t *>(z ? a.v_pool : a.k_pool) + (size_t)l * a.pool_layer_elems * (DK == KV_F16 ? 2 : 4);
+    const size_t page_base = (size_t)a.table_row[p / a.page_size] * kHeads * a.page_size;
+    for (int e = threadIdx.x; e < kHidden; e += blockDim.x) {
+        const int h = e >> 6, d = e & 63;
+        const size_t si = ((size_t)h * a.ctx_stride + p) * kHeadDim + d;
+        const size_t di = ((page_base + (size_t)h * a.page_size) + p % a.page_size) * kHeadDim + d;
+        if constexpr (SK == DK) {
+            if constexpr (SK == KV_F16)
+                ((__half *)pool)[di] = ((const __half *)src)[si];
+            else
+                ((float *)pool)[di] = ((const float *)src)[si];
+        } else if constexpr (SK == KV_F32) {
+            ((__half *)pool)[di] = __float2half_rn(((const float *)src)[si]);
+        } else {
+            ((float *)pool)[di] = __half2float(((const __half *)src)[si]);
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_kv_admit(const KvAdmit &a, int n_pos, hipStream_t s) {
+    (void)hipGetLastError();  // report only this launch's error, not a stale one
+    if (n_pos <= 0) return hipSuccess;
+    if (!a.k_src || !a.v_src || !a.k_pool || !a.v_pool || !a.table_row || a.page_size <= 0 || n_pos > a.ctx_stride)
+        return hipErrorInvalidValue;
+    const dim3 grid(n_pos, kLayers, 2);
+    if (a.src_kv == KV_F16) {
+        if (a.pool_kv == KV_F16)
+            hipLaunchKernelGGL((kv_admit_kernel<KV_F16, KV_F16>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((kv_admit_kernel<KV_F16, KV_F32>), grid, dim3(256), 0, s, a);
+    } else {
+        if (a.pool_kv == KV_F16)
+            hipLaunchKernelGGL((kv_admit_kernel<KV_F32, KV_F16>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((kv_admit_kernel<KV_F32, KV_F32>), grid, dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_kv_import_paged(const float *src, int n_pos, void *pool, const int *table_row, int page_size,
                                   KvType kv, hipStream_t s) {

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <array>
+#include <atomic>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -24,6 +25,9 @@ struct Status : std::runtime_error {
 };
 
 void hip_check(hipError_t e, const char *what);
+
+// Fused decode launches redone per operator by every Model of the process.
+extern std::atomic<int> fallbacks_total;
 
 // One tensor of a .moss v1 index (reference csrc/src/weights.cpp:27-125).
 struct MossEntry {
@@ -94,6 +98,20 @@ public:
 
     int device() const { return device_; }
     hipStream_t stream() const { return stream_; }
+
+    // Where the state lives on the device (for a batch stream's admission, Batch::admit).
+    struct StateView {
+        const void *k, *v;         // layer 0 of K / V: [layer][head][ctx_stride][64]
+        size_t layer_elems;        // elements between layers
+        int ctx_stride;
+        KvType kv;
+        const float *hidden;       // [768]
+        int pos;
+    };
+    StateView state_view() const {
+        return StateView{kv_layer(0, 0), kv_layer(1, 0), (size_t)kHeads * max_ctx_ * kHeadDim, max_ctx_, kvt_,
+                         hidden_, pos_};
+    }
 
     // Quantiser capture (tests; moss_hip_llm_capture): W8A8 quantisers also record their
     // fp32 input, int8 output and scales, and the stage outputs around them.

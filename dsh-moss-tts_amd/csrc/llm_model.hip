@@ -2,6 +2,7 @@
 #include "llm_model.h"
 
 #include <algorithm>
+#include <atomic>
 
 #include <chrono>
 #include <cmath>
@@ -12,6 +13,9 @@
 #include <vector>
 
 namespace mh {
+
+// fused-launch recoveries of every model of the process (moss_hip_fallbacks_total)
+std::atomic<int> fallbacks_total{0};
 
 void hip_check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw Status(MOSS_HIP_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
@@ -672,6 +676,7 @@ void Model::global_step(const int32_t *row) {
         // the step is a function of the row, the position and the cache below it: redo it
         // per operator (it rewrites the K/V row at pos and the hidden state)
         ++fallbacks_;
+        fallbacks_total.fetch_add(1, std::memory_order_relaxed);
         hstate_->ll_err = 0;
         write_state_header();
         hip_check(hipMemcpyAsync(reinterpret_cast<uint8_t *>(state_) + kStateRowOff, row, 17 * sizeof(int32_t),
@@ -965,6 +970,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     auto recover = [&](int f) {
         hip_check(hipStreamSynchronize(stream_), "sync");
         ++fallbacks_;
+        fallbacks_total.fetch_add(1, std::memory_order_relaxed);
         fused_layers_ = false;
         DevState st = f == 0 ? start_state : hread_[(f - 1) & 1];
         st.ll_err = 0;
@@ -1023,6 +1029,7 @@ int Model::generate(int max_frames, const moss_hip_sample_params &p, uint64_t se
     if (hstate_->ll_err != 0 && frames > 0 && global_enq[(frames - 1) & 1] && fused_layers_ && can_fall_back()) {
         // the last frame's global step ran out: redo it per operator from the state after its local half
         ++fallbacks_;
+        fallbacks_total.fetch_add(1, std::memory_order_relaxed);
         fused_layers_ = false;
         DevState st = hread_[(frames - 1) & 1];
         st.ll_err = 0;

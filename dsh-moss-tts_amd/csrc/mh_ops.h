@@ -361,6 +361,22 @@ hipError_t launch_kv_import_paged(const float *src, int n_pos, void *pool, const
 hipError_t launch_kv_export_paged(const void *pool, const int *table_row, int page_size, int n_pos, KvType kv,
                                   float *dst, hipStream_t s);
 hipError_t launch_kv_export(const void *src, int n_pos, int ctx_stride, KvType kv, float *dst, hipStream_t s);
+// Device to device, every layer's K and V: positions [0, n_pos) of a contiguous cache
+// ([layer][head][ctx_stride][64], layer l of K at k_src + l * src_layer_elems) into the pages
+// of one stream (layer l of K at k_pool + l * pool_layer_elems), converted from src_kv to
+// pool_kv (fp32 -> fp16 rounds to nearest even, as launch_kv_import_paged does).
+struct KvAdmit {
+    const void *k_src = nullptr, *v_src = nullptr;
+    size_t src_layer_elems = 0;
+    int ctx_stride = 0;
+    KvType src_kv = KV_F16;
+    void *k_pool = nullptr, *v_pool = nullptr;
+    size_t pool_layer_elems = 0;
+    const int *table_row = nullptr;
+    int page_size = 0;
+    KvType pool_kv = KV_F16;
+};
+hipError_t launch_kv_admit(const KvAdmit &a, int n_pos, hipStream_t s);
 
 // ---- one transformer block of the single-stream decode in one launch (decode_layer.hip)
 constexpr int kLayerGrid = 192;          // workgroups, one per CU; all resident at once

@@ -31,9 +31,9 @@ EXPORTED = [
     "moss_hip_llm_position", "moss_hip_llm_get_hidden", "moss_hip_llm_set_hidden", "moss_hip_llm_prefill",
     "moss_hip_llm_global_step", "moss_hip_llm_generate", "moss_hip_llm_set_cancel_flag",
     "moss_hip_llm_snapshot_prefix", "moss_hip_llm_restore_prefix", "moss_hip_llm_prefix_pos",
-    "moss_hip_llm_gate_rows", "moss_hip_llm_fallbacks",
+    "moss_hip_llm_gate_rows", "moss_hip_llm_fallbacks", "moss_hip_fallbacks_total",
     "moss_hip_llm_kv_export", "moss_hip_llm_kv_import", "moss_hip_llm_capture", "moss_hip_llm_capture_read",
-    "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_get_hidden",
+    "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_admit", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
     "moss_hip_attn_decode_noalloc",
@@ -119,6 +119,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_batch_destroy.argtypes = [vp]
     L.moss_hip_batch_destroy.restype = None
     L.moss_hip_batch_set_stream.argtypes = [vp, i32, i32, vp, vp, vp]
+    L.moss_hip_batch_admit.argtypes = [vp, i32, vp]
     L.moss_hip_batch_get_hidden.argtypes = [vp, i32, vp]
     L.moss_hip_batch_position.argtypes = [vp, i32]
     L.moss_hip_batch_kv_export.argtypes = [vp, i32, i32, vp, vp]
@@ -351,6 +352,10 @@ class HipBatch:
         v = np.ascontiguousarray(v, np.float32)
         h = np.ascontiguousarray(hidden, np.float32)
         check(self.L.moss_hip_batch_set_stream(self._h, s, k.shape[1], _ptr(k), _ptr(v), _ptr(h)))
+
+    def admit(self, s: int, model: HipLLM):
+        """Stream s takes `model`'s state (K/V, hidden, position) device to device."""
+        check(self.L.moss_hip_batch_admit(self._h, s, model._h))
 
     def position(self, s: int) -> int:
         return self.L.moss_hip_batch_position(self._h, s)

@@ -135,6 +135,10 @@ int moss_hip_llm_gate_rows(const moss_hip_llm *m);
  * do not change beyond fp32 summation order.  No counterpart in the reference (its decode
  * has no such path); for monitoring. */
 int moss_hip_llm_fallbacks(const moss_hip_llm *m);
+/* The same count summed over every model of the process, destroyed ones included: what a
+ * caller that reaches the models only through the engine ABI (csrc/include/moss/tts.h) can
+ * read. */
+int moss_hip_fallbacks_total(void);
 
 /* LlmModel::set_cancel_flag (llm.h:86): a byte polled (relaxed) before each frame, as
  * llm.cpp:645 does; a flag raised in the on_frame callback of frame k ends generate after
@@ -221,6 +225,14 @@ void moss_hip_batch_destroy(moss_hip_batch *b);
 /* One stream's state, as load_state (csrc/src/llm.cpp:588-632): K/V [12][n_pos][768] fp32 and hidden[768]. */
 int moss_hip_batch_set_stream(moss_hip_batch *b, int stream, int n_pos, const float *k, const float *v,
                               const float *hidden768);
+/* The same from a single-stream model, device to device: K/V of positions [0, position) into the
+ * stream's pages (converted to the batch's KV precision: fp32 -> fp16 rounds to nearest even),
+ * the hidden state and the position.  This admits a job prepared by the reference's per-job
+ * flow on a moss_hip_llm (restore_prefix -> prefill, csrc/src/engine.cpp:447-470,
+ * csrc/src/llm.cpp:327-401,455-483) into the lock-step batch without a host round trip
+ * (~72 KB per position in fp32).  `model` must be on the batch's device and hold the batch's
+ * weights (normally the batch's own model); it is left unchanged. */
+int moss_hip_batch_admit(moss_hip_batch *b, int stream, moss_hip_llm *model);
 int moss_hip_batch_get_hidden(moss_hip_batch *b, int stream, float *out768);
 int moss_hip_batch_position(const moss_hip_batch *b, int stream);
 int moss_hip_batch_kv_export(moss_hip_batch *b, int stream, int n_pos, float *k, float *v);

@@ -157,3 +157,77 @@ def test_batch_capacity_and_errors(torch_gpu, oracle, setup):
     with pytest.raises(lib.MossHipError) as e:
         b.global_step(np.full((1, 17), 9, np.int32))  # stream 0 is at capacity
     assert e.value.code == lib.ESTATE
+
+
+@pytest.mark.parametrize("model_kv32,batch_kv32", [(False, False), (True, False), (True, True), (False, True)])
+def test_batch_admit_bit_exact(torch_gpu, setup, model_kv32, batch_kv32):
+    """moss_hip_batch_admit hands a model's state to a stream device to device: the stream's
+    K/V are the model's (kv_export), converted exactly to the batch's precision (fp32 -> fp16
+    by round to nearest even, fp16 -> fp32 exact); hidden and position follow; another
+    stream's pages are untouched."""
+    blob, lens, states = setup
+    print(f"admit model_kv32={model_kv32} batch_kv32={batch_kv32}", flush=True)
+    g = HipLLM(blob, kv_fp32=model_kv32, max_ctx=256)
+    k, v, h = states[3]  # 130 positions
+    g.kv_import(k, v, h)
+    g.global_step(np.array([mf.SLOT] + list(range(100, 116)), np.int32))  # one row the GPU computed
+    b = HipBatch(g, max_streams=4, capacity=256, kv_fp32=batch_kv32)
+    k1, v1, h1 = states[1]
+    b.set_stream(0, k1, v1, h1)
+    b.admit(2, g)
+    n = g.position
+    assert n == lens[3] + 1 and b.position(2) == n
+    mk, mv = g.kv_export(n)
+    bk, bv = b.kv_export(2, n)
+    if model_kv32 and not batch_kv32:
+        mk, mv = mk.astype(np.float16).astype(np.float32), mv.astype(np.float16).astype(np.float32)
+    assert np.array_equal(bk, mk) and np.array_equal(bv, mv)
+    assert np.array_equal(b.hidden(2), g.hidden())
+    ok, ov = b.kv_export(0, lens[1])
+    assert np.array_equal(ok, k1) and np.array_equal(ov, v1)
+    assert np.array_equal(b.hidden(0), h1)
+    b.close()
+    g.close()
+
+
+def test_batch_admit_then_generate(torch_gpu, oracle, golden_model):
+    """The reference's per-job flow feeding the batch (engine.cpp:447-470): a voice prefix is
+    prefilled once and snapshotted; per job the model restores it (restore_prefix) and
+    prefills the job's text rows after it, and the batch admits the job device to device.
+    Then 16 lock-step greedy frames with penalty 1.2 for the 3 jobs, each against its own
+    oracle LlmModel that ran the same prefix and prefill (A16): teacher-forced predictions on
+    the batch's codes >= 99 %, hidden states of the jobs whose codes all agree <= 1e-3."""
+    blob, _ = golden_model
+    rng = np.random.default_rng(23)
+    prefix = mf.text_rows(rng.integers(0, mf.VOCAB, 40))
+    prefix[10:30, 1:] = rng.integers(0, 1024, (20, 16))  # a voice prompt's audio rows
+    jobs = [mf.text_rows(rng.integers(0, mf.VOCAB, n)) for n in (9, 26, 47)]
+    g = HipLLM(blob, kv_fp32=True, prefill_a16=True, max_ctx=256)
+    g.prefill(prefix)
+    g.snapshot_prefix()
+    b = HipBatch(g, max_streams=4, capacity=256, kv_fp32=True)
+    for j, rows in enumerate(jobs):
+        g.restore_prefix()
+        assert g.position == len(prefix)
+        g.prefill(rows, start=len(prefix))
+        b.admit(j, g)
+        assert b.position(j) == len(prefix) + len(rows)
+    frames, rep = 16, 1.2
+    out = b.generate(len(jobs), frames, SampleParams.make(greedy=True, min_frames=frames, repetition_penalty=rep))
+    agree = []
+    for j, rows in enumerate(jobs):
+        m = oracle.model(blob, max_ctx=256)
+        m.prefill(prefix, a16=True)
+        m.prefill(rows, start=len(prefix), a16=True)
+        forced = out["rows"][:, j].copy()
+        forced[:, 0] = mf.SLOT
+        ref = m.generate(frames, OSP.make(greedy=True, min_frames=frames, repetition_penalty=rep), forced=forced)
+        eq = out["rows"][:, j, 1:] == ref["rows"][:, 1:]
+        agree.append(float(np.mean(eq)))
+        assert b.position(j) == m.position
+        if eq.all():
+            assert max_rel(b.hidden(j), m.hidden()) <= TOL
+    print("admitted jobs: agreement", agree, flush=True)
+    assert min(agree) >= 0.99
+    b.close()
+    g.close()
