@@ -316,6 +316,8 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     const size_t oi = (size_t)r * a.out_stride + h * kHeadDim + lane;
     if (a.out_hl != nullptr)  // for the next GEMM: hi / lo halves in the matrix-core order
         store_hl(a.out_hl, r, h * kHeadDim + lane, kHidden, res);
+    else if (a.out == nullptr)
+        ;  // only the W8A8 copy below is read
     else if (a.out_f16)
         ((__half *)a.out)[oi] = __float2half_rn(res);
     else
@@ -557,7 +559,8 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
 
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (a.heads <= 0 || a.rows <= 0 || a.max_keys <= 0 || a.page_size <= 0 || (!a.out && !a.part && !a.out_hl) ||
+    if (a.heads <= 0 || a.rows <= 0 || a.max_keys <= 0 || a.page_size <= 0 ||
+        (!a.out && !a.part && !a.out_hl && !a.q8) ||
         !a.q || !a.k_pool || !a.v_pool)
         return hipErrorInvalidValue;
     if (a.out_hl != nullptr && (a.part != nullptr || a.chunks != 0 || a.heads != kHeads)) return hipErrorInvalidValue;

@@ -6,7 +6,11 @@
 // global KV cache is paged (per layer a pool of 64-position pages, one block
 // table row per stream), attention runs per (head, stream) over that stream's
 // pages, and the local transformer, heads, greedy picks and end gate run per
-// stream.  Weights are the model's own device copy.
+// stream.  Weights are the model's own device copy.  The batch decodes in its model's
+// activation mode: W8A16 (fp32 activations), or W8A8 when the model was created with
+// decode_a8 (the reference with MOSS_A16 unset) -- then every GEMM input is quantised
+// per 32-block by the kernel that produces it and the GEMMs run on the int8 matrix
+// cores, the prefill's operand form.
 #pragma once
 
 #include <map>
@@ -33,6 +37,11 @@ public:
     void set_stream(int s, int n_pos, const float *k, const float *v, const float *hidden);
     // The same from a single-stream model's device state (its K/V, hidden, position), on the device.
     void admit(int s, Model &src);
+    bool a8() const { return a8_; }
+    // Attention capture of the W8A8 batch (tests): every attention of the frames run while on
+    // records its fp32 output and int8 operand (graphs are re-captured when this changes).
+    void set_capture(bool on);
+    size_t capture_read(void *out, size_t bytes);
     void get_hidden(int s, float *out);
     void kv_export(int s, int n_pos, float *k, float *v);
     // One global step for streams [0, n): rows [n][17].
@@ -49,9 +58,12 @@ private:
     };
     // attn = false: the step's attention output is already in o_ (the fused pick + attention)
     void enqueue_local_step(hipStream_t s, int n, const float *in, int in_stride, int lpos, bool attn = true);
+    // W8A8: proj -> LN2 -> fc_in -> fc_out -> ln_f of a local step, after its attention
+    void enqueue_local_step_a8(hipStream_t s, int n, const float *in, int in_stride);
     // greedy: channel picks fused with the next position's attention (greedy frames only)
     void enqueue_frame_local(hipStream_t s, int n, bool greedy);
     void enqueue_global(hipStream_t s, int n);
+    void enqueue_global_a8(hipStream_t s, int n);
     Graphs &graphs_for(int n);
     StreamState state() const;
     void write_ctrl(int min_frames, float rep, const SampleCfg &cfg);
@@ -77,6 +89,17 @@ private:
     float *xhl_ = nullptr;   // proj's output as hi / lo halves (fc_in's operand), rows padded to 16
     float *xst_ = nullptr;   // its per-16-column LayerNorm statistics [48][S][2]
     float *pairs_ = nullptr; // the audio head's greedy partials [S][64][2]
+    // W8A8 (a8_): the current GEMM's int8 operand in the matrix-core order, K = 768 (LN rows,
+    // attention outputs) and K = 3072 (fc_in's output), with their block scales; rows padded to 16
+    bool a8_ = false;
+    int8_t *q8a_ = nullptr, *q8h_ = nullptr;
+    float *d8a_ = nullptr, *d8h_ = nullptr;
+    // attention capture (tests; set_capture): after every attention of a frame, its fp32
+    // output rows and the W8A8 operand quantised from them, [kLayers + kNVq + 1] entries
+    bool capture_ = false;
+    uint8_t *acap_ = nullptr;
+    size_t acap_entry_ = 0;
+    void capture_attention(hipStream_t s, int n, int slot);
     BatchCtl *ctrl_ = nullptr;
     uint32_t *rng_ = nullptr;                   // [S][4]
     unsigned char *active_ = nullptr;

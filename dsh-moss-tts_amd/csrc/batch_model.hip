@@ -85,6 +85,15 @@ Batch::Batch(Model &model, int max_streams, int capacity, KvType kv)
     fm(&xhl_, s16 * kHidden);
     fm(&xst_, (size_t)(kHidden / 16) * S_ * 2);
     fm(&pairs_, (size_t)S_ * (kCodebook / 16) * 2);
+    a8_ = model.decode_a8();
+    if (a8_) {  // zeroed once: the GEMMs read the padding rows and never store them
+        hip_check(hipMalloc(&q8a_, s16 * kHidden), "hipMalloc(batch)");
+        hip_check(hipMalloc(&q8h_, s16 * kFF), "hipMalloc(batch)");
+        hip_check(hipMemset(q8a_, 0, s16 * kHidden), "memset(batch)");
+        hip_check(hipMemset(q8h_, 0, s16 * kFF), "memset(batch)");
+        fm(&d8a_, s16 * (kHidden / 32));
+        fm(&d8h_, s16 * (kFF / 32));
+    }
     hip_check(hipMalloc(&ctrl_, sizeof(BatchCtl)), "hipMalloc(ctrl)");
     hip_check(hipMalloc(&rng_, sizeof(uint32_t) * 4 * S_), "hipMalloc(rng)");
     hip_check(hipMemset(rng_, 0, sizeof(uint32_t) * 4 * S_), "memset(rng)");
@@ -106,7 +115,7 @@ Batch::~Batch() {
     }
     void *bufs[] = {kpool_, vpool_, lkv_, table_, rope_, x_, a_, q_, o_, h_, hidden_, lres_, next_in_, logits_,
                     gate_, pos_d_, codes_, row_, counts_, ctrl_, rng_, hist_codes_, active_, hist_active_, part_,
-                    xhl_,  xst_,  pairs_};
+                    xhl_,  xst_,  pairs_, q8a_, q8h_, d8a_, d8h_, acap_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (ctrl_h_) (void)hipHostFree(ctrl_h_);
@@ -251,13 +260,29 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
         q.ln_w = L.ln1_w; q.ln_b = L.ln1_b;
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = lk; q.v_pool = lv; q.page_size = kLocalLen;
         q.stream_stride = 1; q.pos0 = lpos; q.pos_stride = 0; q.rope_cos = rc; q.rope_sin = rs;
+        if (a8_) {  // LN1 and its int8 copy first, then the int8 GEMM
+            hip_check(launch_ln_rows(in, in_stride, L.ln1_w, L.ln1_b, nullptr, n, s, nullptr, q8a_, d8a_),
+                      "local ln1");
+            q.a = nullptr; q.ln_w = q.ln_b = nullptr; q.lda = kHidden;
+            q.a8 = q8a_; q.d8 = d8a_; q.a8_tiled = true;
+        }
         hip_check(launch_gemm(q, EPI_QKV, KV_F32, s), "local qkv");
     }
     if (attn) {
         AttnArgs t;
         t.q = q_; t.k_pool = lk; t.v_pool = lv; t.page_size = kLocalLen; t.stream_stride = 1;
-        t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen; t.out_hl = hl(o_);
+        t.pos0 = lpos; t.pos_stride = 0; t.rows = n; t.max_keys = kLocalLen;
+        if (a8_) {
+            t.out = o_; t.q8 = q8a_; t.d8 = d8a_;
+        } else {
+            t.out_hl = hl(o_);
+        }
         hip_check(launch_attn(t, KV_F32, s), "local attention");
+    }
+    if (a8_) {
+        capture_attention(s, n, kLayers + lpos);
+        enqueue_local_step_a8(s, n, in, in_stride);
+        return;
     }
     GemmArgs p;
     p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = hl(o_); p.lda = kHidden; p.M = n;
@@ -276,6 +301,79 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b,
                                    nullptr, nullptr, s, nullptr, nullptr, hl(a_)),
               "local fc_out reduce + ln_f");
+}
+
+// The W8A8 form of the local step after its attention (q8a_ holds the attention output's int8
+// copy): proj as split-K partials, reduced in a fixed order with bias and residual into lres_
+// by the kernel that also applies LN2 and quantises it; fc_in with gelu, quantised in its
+// epilogue; fc_out as split-K partials, reduced with bias and residual, then the local ln_f
+// quantised for the audio head -- the prefill's kernels and operand forms.
+void Batch::enqueue_local_step_a8(hipStream_t s, int n, const float *in, int in_stride) {
+    const LayerW &L = *w_.local;
+    GemmArgs p;
+    p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.lda = kHidden; p.M = n;
+    p.a8 = q8a_; p.d8 = d8a_; p.a8_tiled = true;
+    p.part = part_; p.ksplit = gemm_ksplit(n, kHidden, kHidden);
+    hip_check(launch_gemm(p, EPI_PART, KV_F32, s), "local proj");
+    hip_check(launch_resid_ln_rows(part_, p.ksplit, n, L.proj_b, in, in_stride, lres_, L.ln2_w, L.ln2_b, nullptr,
+                                   nullptr, s, q8a_, d8a_),
+              "local proj reduce + ln2");
+    GemmArgs f1;
+    f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.lda = kHidden; f1.M = n;
+    f1.a8 = q8a_; f1.d8 = d8a_; f1.a8_tiled = true;
+    f1.bias = L.fc_in_b; f1.q8_out = q8h_; f1.d8_out = d8h_;
+    hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
+    GemmArgs f2;
+    f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.lda = kFF; f2.M = n;
+    f2.a8 = q8h_; f2.d8 = d8h_; f2.a8_tiled = true;
+    f2.part = part_; f2.ksplit = std::max(gemm_ksplit(n, kHidden, kFF), kBatchFcOutSplit);
+    hip_check(launch_gemm(f2, EPI_PART, KV_F32, s), "local fc_out");
+    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b,
+                                   nullptr, nullptr, s, q8a_, d8a_),
+              "local fc_out reduce + ln_f");
+}
+
+// Attention capture (tests): the fp32 output rows o_ and their int8 copy q8a_ / d8a_ of the
+// attention just enqueued go to capture entry `slot` (0..11 global layers, 12..28 local
+// positions).  Device-to-device copies, so they are graph nodes like the kernels.
+void Batch::capture_attention(hipStream_t s, int n, int slot) {
+    if (!capture_ || !a8_) return;
+    const size_t s16 = (size_t)(S_ + 15) / 16 * 16;
+    uint8_t *e = acap_ + (size_t)slot * acap_entry_;
+    hip_check(hipMemcpyAsync(e, o_, sizeof(float) * (size_t)n * kHidden, hipMemcpyDeviceToDevice, s), "capture");
+    e += sizeof(float) * (size_t)S_ * kHidden;
+    hip_check(hipMemcpyAsync(e, q8a_, s16 * kHidden, hipMemcpyDeviceToDevice, s), "capture");
+    e += s16 * kHidden;
+    hip_check(hipMemcpyAsync(e, d8a_, sizeof(float) * s16 * (kHidden / 32), hipMemcpyDeviceToDevice, s), "capture");
+}
+
+void Batch::set_capture(bool on) {
+    if (on == capture_) return;
+    if (on && !a8_) throw Status(MOSS_HIP_ESTATE, "attention capture records the W8A8 batch only");
+    const size_t s16 = (size_t)(S_ + 15) / 16 * 16;
+    acap_entry_ = sizeof(float) * (size_t)S_ * kHidden + s16 * kHidden + sizeof(float) * s16 * (kHidden / 32);
+    if (on && !acap_) {
+        const size_t bytes = acap_entry_ * (kLayers + kLocalLen);
+        hip_check(hipMalloc(&acap_, bytes), "hipMalloc(capture)");
+        hip_check(hipMemset(acap_, 0, bytes), "memset(capture)");
+    }
+    capture_ = on;
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    for (auto &kv : graphs_) {  // re-captured with (or without) the copies
+        if (kv.second.local) (void)hipGraphExecDestroy(kv.second.local);
+        if (kv.second.local_greedy) (void)hipGraphExecDestroy(kv.second.local_greedy);
+        if (kv.second.global) (void)hipGraphExecDestroy(kv.second.global);
+    }
+    graphs_.clear();
+}
+
+size_t Batch::capture_read(void *out, size_t bytes) {
+    if (!acap_) return 0;
+    const size_t n = acap_entry_ * (kLayers + kLocalLen);
+    if (out == nullptr || bytes < n) return n;
+    hip_check(hipMemcpyAsync(out, acap_, n, hipMemcpyDeviceToHost, stream_), "capture d2h");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    return n;
 }
 
 // The local half of a frame for n streams (llm.cpp:648-698).  Greedy frames (the host knows
@@ -308,7 +406,11 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
             pa.lk = qkv.lk;
             pa.lv = qkv.lv;
             pa.lpos = ch + 1;
-            pa.o_hl = hl(o_);
+            if (a8_) {
+                pa.o = o_; pa.o_q8 = q8a_; pa.o_d8 = d8a_;
+            } else {
+                pa.o_hl = hl(o_);
+            }
             pa.pairs = pairs_;
             hip_check(launch_local_pick_attn(pa, n, s), "pick + local attention");
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1, false);
@@ -316,8 +418,13 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
             enqueue_local_step(s, n, next_in_, kHidden, ch + 1);
         }
         GemmArgs hd;  // the tied audio head on the local ln_f of the step's output
-        hd.w = w_.aemb[ch]; hd.wm = w_.aemb_m[ch]; hd.N = kCodebook; hd.K = kHidden; hd.a_hl = hl(a_); hd.lda = kHidden;
+        hd.w = w_.aemb[ch]; hd.wm = w_.aemb_m[ch]; hd.N = kCodebook; hd.K = kHidden; hd.lda = kHidden;
         hd.M = n;
+        if (a8_) {  // the local ln_f quantised by the reduce before it
+            hd.a8 = q8a_; hd.d8 = d8a_; hd.a8_tiled = true;
+        } else {
+            hd.a_hl = hl(a_);
+        }
         hd.y = logits_; hd.ldy = kCodebook;
         if (greedy && ch + 1 < kNVq) {  // the next launch picks this channel from per-16-code partials
             hd.pick_pairs = pairs_;
@@ -343,9 +450,13 @@ void Batch::enqueue_global(hipStream_t s, int n) {
     e.wte = w_.wte;
     for (int ch = 0; ch < kNVq; ++ch) e.aemb[ch] = w_.aemb[ch];
     hip_check(launch_embed_rows(e, row_, n, x_, s), "embed");
-    hip_check(launch_ln_rows(x_, kHidden, w_.global[0].ln1_w, w_.global[0].ln1_b, nullptr, n, s, nullptr, nullptr,
-                             nullptr, hl(a_)),
+    hip_check(launch_ln_rows(x_, kHidden, w_.global[0].ln1_w, w_.global[0].ln1_b, nullptr, n, s, nullptr,
+                             a8_ ? q8a_ : nullptr, a8_ ? d8a_ : nullptr, a8_ ? nullptr : hl(a_)),
               "ln1");
+    if (a8_) {
+        enqueue_global_a8(s, n);
+        return;
+    }
     const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
     for (int l = 0; l < kLayers; ++l) {
         const LayerW &L = w_.global[l];
@@ -381,6 +492,59 @@ void Batch::enqueue_global(hipStream_t s, int n) {
                                        last ? w_.lnf_w : w_.global[l + 1].ln1_w,
                                        last ? w_.lnf_b : w_.global[l + 1].ln1_b, last ? hidden_ : nullptr,
                                        last ? active_ : nullptr, s, nullptr, nullptr, last ? nullptr : hl(a_)),
+                  "fc_out reduce + ln");
+    }
+    hip_check(launch_advance_rows(st, n, s), "advance");
+}
+
+// The W8A8 global step after the embedding and LN1 (q8a_ holds LN1's int8 copy): per layer
+// the int8 QKV GEMM (bias, RoPE, paged K/V write), paged attention quantising its output, proj
+// as split-K partials reduced with bias and residual by the kernel that applies and quantises
+// LN2, fc_in with gelu quantised in its epilogue, fc_out as split-K partials reduced with
+// bias and residual before the next layer's LN1 (quantised) or ln_f.
+void Batch::enqueue_global_a8(hipStream_t s, int n) {
+    const StreamState st = state();
+    const float *rc = rope_, *rs = rope_ + (size_t)rope_n_ * kRopeHalf;
+    for (int l = 0; l < kLayers; ++l) {
+        const LayerW &L = w_.global[l];
+        void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
+        void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
+        GemmArgs q;
+        q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.lda = kHidden; q.M = n;
+        q.a8 = q8a_; q.d8 = d8a_; q.a8_tiled = true;
+        q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
+        q.page_table = table_; q.table_stride = pages_; q.page_size = kPage;
+        q.stream_stride = 1; q.row_pos = pos_d_; q.row_active = active_; q.rope_cos = rc; q.rope_sin = rs;
+        hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "qkv");
+        AttnArgs t;
+        t.q = q_; t.k_pool = kp; t.v_pool = vp; t.page_table = table_; t.table_stride = pages_; t.page_size = kPage;
+        t.stream_stride = 1; t.row_pos = pos_d_; t.rows = n; t.max_keys = cap_;
+        t.out = o_; t.q8 = q8a_; t.d8 = d8a_;
+        hip_check(launch_attn(t, kvt_, s), "attention");
+        capture_attention(s, n, l);
+        GemmArgs p;
+        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.lda = kHidden; p.M = n;
+        p.a8 = q8a_; p.d8 = d8a_; p.a8_tiled = true;
+        p.part = part_; p.ksplit = gemm_ksplit(n, kHidden, kHidden);
+        hip_check(launch_gemm(p, EPI_PART, kvt_, s), "proj");
+        hip_check(launch_resid_ln_rows(part_, p.ksplit, n, L.proj_b, x_, kHidden, x_, L.ln2_w, L.ln2_b, nullptr,
+                                       nullptr, s, q8a_, d8a_),
+                  "proj reduce + ln2");
+        GemmArgs f1;
+        f1.w = L.fc_in_w; f1.wm = L.fc_in_wm; f1.N = kFF; f1.K = kHidden; f1.lda = kHidden; f1.M = n;
+        f1.a8 = q8a_; f1.d8 = d8a_; f1.a8_tiled = true;
+        f1.bias = L.fc_in_b; f1.q8_out = q8h_; f1.d8_out = d8h_;
+        hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
+        GemmArgs f2;
+        f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.lda = kFF; f2.M = n;
+        f2.a8 = q8h_; f2.d8 = d8h_; f2.a8_tiled = true;
+        f2.part = part_; f2.ksplit = std::max(gemm_ksplit(n, kHidden, kFF), kBatchFcOutSplit);
+        hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
+        const bool last = l + 1 == kLayers;
+        hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, x_, kHidden, x_,
+                                       last ? w_.lnf_w : w_.global[l + 1].ln1_w,
+                                       last ? w_.lnf_b : w_.global[l + 1].ln1_b, last ? hidden_ : nullptr,
+                                       last ? active_ : nullptr, s, last ? nullptr : q8a_, last ? nullptr : d8a_),
                   "fc_out reduce + ln");
     }
     hip_check(launch_advance_rows(st, n, s), "advance");

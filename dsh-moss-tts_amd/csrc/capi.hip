@@ -316,6 +316,19 @@ int moss_hip_batch_set_stream(moss_hip_batch *b, int stream, int n_pos, const fl
     });
 }
 
+int moss_hip_batch_capture(moss_hip_batch *b, int on) {
+    return guard([&] { batch_of(b).set_capture(on != 0); });
+}
+
+int moss_hip_batch_capture_read(moss_hip_batch *b, void *out, size_t bytes, size_t *needed) {
+    return guard([&] {
+        const size_t n = batch_of(b).capture_read(out, bytes);
+        if (needed) *needed = n;
+        if (n == 0) throw Status(MOSS_HIP_ESTATE, "no capture taken");
+        if (out && bytes < n) throw Status(MOSS_HIP_EINVAL, "output buffer too small");
+    });
+}
+
 int moss_hip_batch_admit(moss_hip_batch *b, int stream, moss_hip_llm *model) {
     return guard([&] { batch_of(b).admit(stream, model_of(model)); });
 }

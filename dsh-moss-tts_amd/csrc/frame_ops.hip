@@ -773,10 +773,17 @@ __global__ __launch_bounds__(256) void local_pick_attn_kernel(const PickAttnArgs
 #pragma unroll
     for (int k = 0; k < kLocalLen; ++k)
         if (k < nk) o = fmaf(es[k], k == a.lpos ? vnew : vv[k], o);
+    const float res = o / l;
     if (a.o_hl != nullptr)  // for the proj GEMM: hi / lo halves in the matrix-core order
-        store_hl(a.o_hl, srow, h * kHeadDim + t, kHidden, o / l);
-    else
-        a.o[(size_t)srow * kHidden + h * kHeadDim + t] = o / l;
+        store_hl(a.o_hl, srow, h * kHeadDim + t, kHidden, res);
+    else if (a.o != nullptr)
+        a.o[(size_t)srow * kHidden + h * kHeadDim + t] = res;
+    if (a.o_q8 != nullptr) {  // W8A8 copy for the proj GEMM: this head's 64 outputs are two blocks of 32 lanes
+        float d;
+        const int q = quant_block32(res, &d);
+        a.o_q8[q8t_at(srow, h * kHeadDim + t, kHidden)] = (int8_t)q;
+        if ((t & 31) == 0) a.o_d8[d8t_at(srow, 2 * h + (t >> 5), kHidden)] = d;
+    }
 }
 
 __global__ void advance_rows_kernel(StreamState st, int streams) {
@@ -946,7 +953,8 @@ hipError_t launch_sample_rows(const float *logits, int ch, const uint8_t *aemb, 
 
 hipError_t launch_local_pick_attn(const PickAttnArgs &a, int streams, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
-    if (!a.logits || !a.aemb || !a.next_in || !a.rows || !a.lk || !a.lv || (!a.o && !a.o_hl) || streams <= 0 ||
+    if (!a.logits || !a.aemb || !a.next_in || !a.rows || !a.lk || !a.lv || (!a.o && !a.o_hl && !a.o_q8) ||
+        (a.o_q8 && !a.o_d8) || streams <= 0 ||
         a.ch < 0 ||
         a.ch >= kNVq - 1 || a.lpos != a.ch + 2)
         return hipErrorInvalidValue;

@@ -151,12 +151,12 @@ __device__ __forceinline__ void epi_load(const GemmArgs &g, const EpiRow &r, int
         if constexpr (EPI == EPI_RESID || EPI == EPI_GELU || EPI == EPI_QKV) o.b[t] = g.bias[n];
         if constexpr (EPI == EPI_RESID) o.res[t] = r.res[n];
         if constexpr (EPI == EPI_QKV) {
-            if (r.sec < 2) {  // uniform
-                const int d = n & 63;
-                o.bp[t] = g.bias[n ^ 1];
-                o.c[t] = r.rc[d >> 1];
-                o.sn[t] = r.rs[d >> 1];
-            }
+            // loaded for the v section too, where RoPE does not apply (the addresses are valid
+            // there as well): conditionally filled, the arrays were kept in private memory
+            const int d = n & 63;
+            o.bp[t] = g.bias[n ^ 1];
+            o.c[t] = r.rc[d >> 1];
+            o.sn[t] = r.rs[d >> 1];
         }
     }
 }

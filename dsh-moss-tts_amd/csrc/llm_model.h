@@ -98,6 +98,7 @@ public:
 
     int device() const { return device_; }
     hipStream_t stream() const { return stream_; }
+    bool decode_a8() const { return decode_a8_ != 0; }
 
     // Where the state lives on the device (for a batch stream's admission, Batch::admit).
     struct StateView {

@@ -342,6 +342,8 @@ struct PickAttnArgs {
     int lpos = 0;
     float *o = nullptr;             // [S][768] attention output
     uint8_t *o_hl = nullptr;        // or the output as hi / lo halves (hlt_at, rows padded to 16)
+    int8_t *o_q8 = nullptr;         // and / or its W8A8 copy in the matrix-core order (q8t_at / d8t_at)
+    float *o_d8 = nullptr;
     // greedy: the head GEMM's per-16-code partials of channel ch ([S][64] pairs,
     // GemmArgs::pick_pairs) instead of the logits and counts
     const float *pairs = nullptr;

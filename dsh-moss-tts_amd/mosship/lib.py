@@ -35,6 +35,7 @@ EXPORTED = [
     "moss_hip_llm_kv_export", "moss_hip_llm_kv_import", "moss_hip_llm_capture", "moss_hip_llm_capture_read",
     "moss_hip_batch_create", "moss_hip_batch_destroy", "moss_hip_batch_set_stream", "moss_hip_batch_admit", "moss_hip_batch_get_hidden",
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
+    "moss_hip_batch_capture", "moss_hip_batch_capture_read",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
     "moss_hip_attn_decode_noalloc",
     "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8", "moss_hip_gemv_q8x4_w8a8",
@@ -120,6 +121,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_batch_destroy.restype = None
     L.moss_hip_batch_set_stream.argtypes = [vp, i32, i32, vp, vp, vp]
     L.moss_hip_batch_admit.argtypes = [vp, i32, vp]
+    L.moss_hip_batch_capture.argtypes = [vp, i32]
+    L.moss_hip_batch_capture_read.argtypes = [vp, vp, C.c_size_t, C.POINTER(C.c_size_t)]
     L.moss_hip_batch_get_hidden.argtypes = [vp, i32, vp]
     L.moss_hip_batch_position.argtypes = [vp, i32]
     L.moss_hip_batch_kv_export.argtypes = [vp, i32, i32, vp, vp]
@@ -352,6 +355,28 @@ class HipBatch:
         v = np.ascontiguousarray(v, np.float32)
         h = np.ascontiguousarray(hidden, np.float32)
         check(self.L.moss_hip_batch_set_stream(self._h, s, k.shape[1], _ptr(k), _ptr(v), _ptr(h)))
+
+    def capture(self, on: bool = True):
+        """Attention capture of a W8A8 batch (tests)."""
+        check(self.L.moss_hip_batch_capture(self._h, 1 if on else 0))
+
+    def capture_attention(self, max_streams: int) -> list:
+        """The last frame's attention records: 29 dicts (12 global layers, local positions 0..16)
+        of out [max_streams][768] fp32 and the raw int8 / scale operand (matrix-core order)."""
+        n = C.c_size_t(0)
+        check(self.L.moss_hip_batch_capture_read(self._h, None, 0, C.byref(n)))
+        raw = np.empty(n.value, np.uint8)
+        check(self.L.moss_hip_batch_capture_read(self._h, _ptr(raw), raw.size, None))
+        s16 = (max_streams + 15) // 16 * 16
+        per = 4 * max_streams * 768 + s16 * 768 + 4 * s16 * 24
+        assert raw.size == 29 * per
+        out = []
+        for e in range(29):
+            b = e * per
+            out.append({"out": raw[b:b + 4 * max_streams * 768].view(np.float32).reshape(max_streams, 768),
+                        "q": raw[b + 4 * max_streams * 768: b + 4 * max_streams * 768 + s16 * 768],
+                        "d": raw[b + 4 * max_streams * 768 + s16 * 768: b + per]})
+        return out
 
     def admit(self, s: int, model: HipLLM):
         """Stream s takes `model`'s state (K/V, hidden, position) device to device."""

@@ -216,7 +216,10 @@ int moss_hip_llm_capture_read(moss_hip_llm *m, int what, void *out, size_t bytes
  * generate() per job, csrc/src/runtime.cpp:336); each stream here has exactly that
  * per-stream state and semantics (global KV, hidden, position, history, end gate).
  * The global KV cache is paged (64-position pages behind a block table).  A batch
- * shares `model`'s device weights and must be destroyed before it. */
+ * shares `model`'s device weights and must be destroyed before it.  It decodes in the
+ * model's activation mode (options.decode_a8): W8A16, or W8A8 -- every GEMM input
+ * quantised per 32-block by its producer (quantize_row_q8_0_scaled, quant.cpp:28-54), int8
+ * block dots scaled by d_w * d_a (row_dot_q8_4x4, gemv_avx2.cpp:105-121). */
 typedef struct moss_hip_batch moss_hip_batch;
 
 /* max_streams <= 1024; capacity = KV positions per stream (> 17); kv_dtype as in the options. */
@@ -244,6 +247,14 @@ int moss_hip_batch_global_step(moss_hip_batch *b, int n_streams, const int32_t *
  * with seed seeds[s] (seeds NULL = 0 for every stream). */
 int moss_hip_batch_generate(moss_hip_batch *b, int n_streams, int frames, const moss_hip_sample_params *p,
                             const uint64_t *seeds, int32_t *out_rows, int *out_frames, double *elapsed_ms);
+/* Attention capture of a W8A8 batch (test instrumentation, as moss_hip_llm_capture): while on,
+ * every attention of the frames run records its fp32 output rows and the int8 operand and block
+ * scales quantised from them for proj (ESTATE on a W8A16 batch).  moss_hip_batch_capture_read
+ * copies the last frame's records: 29 entries (12 global layers, then local positions 0..16),
+ * each float out[max_streams][768], int8 q[S16 * 768], float d[S16 * 24] with S16 = max_streams
+ * rounded up to 16, q and d in the matrix-core order of MOSS_HIP_CAP_PREFILL. */
+int moss_hip_batch_capture(moss_hip_batch *b, int on);
+int moss_hip_batch_capture_read(moss_hip_batch *b, void *out, size_t bytes, size_t *needed);
 
 /* ------------------------------------------------------------------ operator layer */
 

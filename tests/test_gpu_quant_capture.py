@@ -22,7 +22,7 @@ quantised and what it produced, and this module checks, stage by stage:
 """
 import numpy as np
 import pytest
-from conftest import max_rel
+from conftest import check_quant, d8t_rows, max_rel, q8t_rows
 
 from mosship import HipLLM, SampleParams, lib
 from mosship import moss_format as mf
@@ -30,6 +30,7 @@ from mosship import moss_format as mf
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
 H, FF = 768, 3072
+FLIPS = []  # int8 values of LN1 a full step apart when the oracle quantises its own LN1 output
 
 
 class Weights:
@@ -64,17 +65,6 @@ def gelu(v):  # gelu_new (llm.cpp:22-25), in float64
     return 0.5 * v * (1.0 + np.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))
 
 
-def check_quant(oracle, x, q, d, what):
-    """GPU int8 values q (any integer dtype or integer-valued floats) and fp32 scales d of x
-    against the oracle's quantize_row of x, bit for bit."""
-    qr, _, dr = oracle.quantize_row(np.ascontiguousarray(x, np.float32))
-    q = np.asarray(q)
-    assert np.all(q == np.round(q)), what
-    assert np.array_equal(q.astype(np.int32), qr.astype(np.int32)), f"{what}: int8 values differ"
-    assert np.array_equal(np.asarray(d, np.float32).view(np.uint32), dr.view(np.uint32)), f"{what}: scales differ"
-    return int(np.count_nonzero(np.abs(qr) == 127))
-
-
 def rope(oracle, vec, pos, tabs):
     return oracle.rope_apply(np.ascontiguousarray(vec, np.float32), pos, *tabs)
 
@@ -86,6 +76,10 @@ def check_block(oracle, W, pre, c, pos, keys, vals, kv32, what):
     ln1 = oracle.layernorm(c["xin"], W.vec(pre + "ln1.w"), W.vec(pre + "ln1.b"))
     assert max_rel(c["ln1"], ln1) <= TOL, what + " ln1"
     check_quant(oracle, c["ln1"], c["ln1_q"], c["ln1_d"], what + " ln1 quant")
+    # how the end-to-end W8A8 differences arise: the oracle's own LN1 of the same input, within
+    # ~1e-7, quantises to int8 values a full step away from the GPU's wherever a value sits on a
+    # rounding boundary
+    FLIPS.append(int(np.count_nonzero(oracle.quantize_row(ln1)[0] != c["ln1_q"].astype(np.int8))))
     qkv = w8a8(oracle, W, pre + "attn.w", c["ln1_q"], c["ln1_d"])[0] + W.vec(pre + "attn.b")
     q = rope(oracle, qkv[:H], pos, tabs)
     k = rope(oracle, qkv[H:2 * H], pos, tabs)
@@ -158,7 +152,9 @@ def test_fused_global_step_w8a8(torch_gpu, oracle, prefilled, kv32):
             clamps += check_block(oracle, W, f"g{l}.", caps[l], pos, keys[l], vals[l], kv32, f"step {step} block {l}")
         hid = oracle.layernorm(caps[11]["xout"], W.vec("lnf.w"), W.vec("lnf.b"))
         assert max_rel(g.hidden(), hid) <= TOL
-    print(f"  3 steps x 12 blocks pinned; {clamps} fc_in values at +-127", flush=True)
+    print(f"  3 steps x 12 blocks pinned; {clamps} fc_in values at +-127; LN1 int8 values one step apart "
+          f"from the oracle's quantisation of its own LN1: {sum(FLIPS)} of {len(FLIPS) * 768}", flush=True)
+    FLIPS.clear()
     g.close()
 
 
@@ -211,21 +207,6 @@ def test_fused_local_half_w8a8(torch_gpu, oracle, prefilled):
             assert max_rel(out["logits"][0, lpos - 1], logits) <= TOL, what + " head"
     print(f"  17 local positions pinned; codes {codes[:6].tolist()}...", flush=True)
     g.close()
-
-
-def q8t_rows(buf, m, K):
-    """Rows [m][K] of an int8 operand in the GEMMs' matrix-core order: row r, column k at
-    byte ((r // 16) * (K // 32) + k // 32) * 512 + 8 * (r % 16 + 16 * ((k % 32) // 8)) + k % 8."""
-    r = np.arange(m)[:, None]
-    k = np.arange(K)[None, :]
-    off = ((r // 16) * (K // 32) + k // 32) * 512 + 8 * (r % 16 + 16 * ((k % 32) // 8)) + k % 8
-    return buf.view(np.int8)[off]
-
-
-def d8t_rows(buf, m, K):
-    r = np.arange(m)[:, None]
-    b = np.arange(K // 32)[None, :]
-    return buf.view(np.float32)[((r // 16) * (K // 32) + b) * 16 + r % 16]
 
 
 def split_prefill_capture(raw, m):
