@@ -36,8 +36,12 @@ The audio codec decoder (decode_chunk, the engine's 8-frame chunks on a stream
 past every window; ms/frame and the real-time factor, 80 ms of audio per frame)
 is reported beside the reference AudioDecoder on min(6, share) host threads.
 
+The same frames with an fp32 KV cache (the reference's precision) are timed as well
+(decode_kv_fp32).  --mode gemm64 runs the 64-stream engine's GEMM shapes (M = 64) through
+the operator ABI eagerly, for hardware-counter passes.
+
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
-                       [--mode full|gemv|attn|decode|prefill|streams|codec]
+                       [--mode full|gemv|attn|decode|prefill|streams|codec|gemm64]
 """
 from __future__ import annotations
 
@@ -78,12 +82,13 @@ def make_state(seed: int = 2024):
     return k, v, hidden, rows
 
 
-def bench_decode(blob, state, steps, warmup):
+def bench_decode(blob, state, steps, warmup, kv_fp32: bool = False):
+    """The headline frame loop (fp16 KV), or with kv_fp32 the reference's own KV precision."""
     import torch
 
     from mosship import HipLLM, SampleParams
     k, v, hidden, _ = state
-    m = HipLLM(blob, device=0)
+    m = HipLLM(blob, device=0, kv_fp32=kv_fp32)
     m.kv_import(k, v, hidden)
     m.snapshot_prefix()
     p = SampleParams.make(greedy=True, min_frames=max(steps, warmup))
@@ -219,6 +224,47 @@ def bench_prefill(blob, reps: int = 20, a16: bool = False):
     # against the dense matrix-core peak of the arithmetic used: int8 (W8A8) or fp16 (W8A16)
     peak = MFMA_F16_PEAK_TFLOPS if a16 else MFMA_I8_PEAK_TOPS
     return {"ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / peak}
+
+
+GEMM64_SHAPES = ((2304, 768), (3072, 768), (768, 3072), (1024, 768))  # QKV, fc_in, fc_out, an audio head
+
+
+def bench_gemm64(reps: int = 20):
+    """The 64-stream engine's GEMM shapes (M = 64) through the operator ABI, eagerly (no graphs):
+    W8A16 (moss_hip_gemm_q8x4, fp32 activations) and W8A8 (moss_hip_gemm_q8x4_w8a8, int8
+    activations quantised by moss_hip_quantize_rows), `reps` calls each -- the launches a
+    hardware-counter pass profiles (rocprofv3 --pmc); times from HIP events on the stream."""
+    import torch
+
+    from mosship import lib
+    from mosship import moss_format as mf
+    M = 64
+    rng = np.random.default_rng(64)
+    s = torch.cuda.current_stream()
+    out = {}
+    for N, K in GEMM64_SHAPES:
+        w = torch.from_numpy(mf.synth_q8x4(rng, N, K).reshape(-1)).cuda()
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        d = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+        lib.quantize_rows(x, M, K, q, d)
+        res = {}
+        for mode in ("w8a16", "w8a8"):
+            call = (lambda: lib.gemm_q8x4(w, N, K, x, M, y)) if mode == "w8a16" else \
+                (lambda: lib.gemm_q8x4_w8a8(w, N, K, q, d, M, y))
+            call()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                call()
+            e1.record(s)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            res[mode] = {"us": round(us, 2), "TOP/s": round(2 * M * N * K / us / 1e6, 2)}
+        out[f"{N}x{K}"] = res
+    return out
 
 
 ATTN_CTX = (128, 512, 1024, 2048)
@@ -626,7 +672,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec"],
+    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec", "gemm64"],
                     default="full")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -646,6 +692,9 @@ def main():
         return
     if args.mode == "attn":
         print(json.dumps({"attention_decode": bench_attention()}), flush=True)
+        return
+    if args.mode == "gemm64":
+        print(json.dumps({"gemm64": bench_gemm64()}), flush=True)
         return
     if args.mode == "codec":
         cd = bench_codec()
@@ -669,6 +718,8 @@ def main():
         calibration_copy()
         print(json.dumps({"decode": d, "rooflines": roof}), flush=True)
         return
+    log("decode, fp32 KV")
+    d32 = bench_decode(blob, state, args.steps, args.warmup, kv_fp32=True)
     log("gemv roofline")
     g = bench_gemv()
     log("decode attention")
@@ -728,6 +779,10 @@ def main():
         "frames_per_s": round(1e3 / d["ms_per_frame"], 1),
         "global_step_ms": round(d["global_ms_event"], 4),
         "local_ms_per_frame": round(d["local_ms_event"], 4),
+        "decode_kv_fp32": {"ms_per_frame": round(d32["ms_per_frame"], 4),
+                           "global_step_ms": round(d32["global_ms_event"], 4),
+                           "local_ms_per_frame": round(d32["local_ms_event"], 4),
+                           "note": "the same frames with an fp32 KV cache, the reference's own KV precision"},
         "roofline": dom,
         "roofline_decode": roof,
         "roofline_gemv": gemv_roof,
