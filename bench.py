@@ -38,10 +38,11 @@ is reported beside the reference AudioDecoder on min(6, share) host threads.
 
 The same frames with an fp32 KV cache (the reference's precision) are timed as well
 (decode_kv_fp32).  --mode gemm64 runs the 64-stream engine's GEMM shapes (M = 64) through
-the operator ABI eagerly, for hardware-counter passes.
+the operator ABI eagerly, for hardware-counter passes; --mode mall runs global steps warm and
+with a 1 GiB sweep before each (Infinity Cache residency of the weights, A/B).
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
-                       [--mode full|gemv|attn|decode|prefill|streams|codec|gemm64]
+                       [--mode full|gemv|attn|decode|prefill|streams|codec|gemm64|mall]
 """
 from __future__ import annotations
 
@@ -227,6 +228,45 @@ def bench_prefill(blob, reps: int = 20, a16: bool = False):
 
 
 GEMM64_SHAPES = ((2304, 768), (3072, 768), (768, 3072), (1024, 768))  # QKV, fc_in, fc_out, an audio head
+SWEEP_BYTES = 1 << 30  # more than the 256 MB Infinity Cache (MALL) and every L2
+
+
+def bench_mall(blob, state, steps: int = 40):
+    """Infinity Cache residency of the global step's weights, shown by an A/B: `steps` global
+    steps back to back (warm: the 90 MB of layer weights stay in the 256 MB MALL between
+    steps), then `steps` more with a 1 GiB read-and-write sweep on the model's device before
+    each (cold: every weight byte comes from HBM).  Each step is one decode_global_kernel
+    launch; moss_hip_llm_global_step returns after it, so host time per step = launch and
+    copies + kernel, the same overhead in both halves.  The kernel's own duration per half
+    comes from a --kernel-trace run of this mode (launches in order: warm first)."""
+    import torch
+
+    from mosship import HipLLM
+    from mosship import moss_format as mf
+    k, v, hidden, _ = state
+    m = HipLLM(blob, device=0)
+    m.kv_import(k, v, hidden)
+    rng = np.random.default_rng(3)
+    rows = [np.array([mf.SLOT] + list(rng.integers(0, 1024, 16)), np.int32) for _ in range(2 * steps)]
+    sweep = torch.empty(SWEEP_BYTES // 4, dtype=torch.float32, device="cuda")
+    for r in rows[:4]:  # warm-up: the kernel and the weights resident
+        m.global_step(r)
+    m.kv_import(k, v, hidden)
+    out = {}
+    for mode in ("warm", "cold"):
+        ts = []
+        for r in rows[:steps] if mode == "warm" else rows[steps:]:
+            if mode == "cold":
+                sweep.add_(1.0)  # reads and writes 1 GiB: evicts the MALL and the L2s
+                torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            m.global_step(r)
+            ts.append(time.perf_counter() - t0)
+        out[mode] = {"host_us_per_step_median": round(float(np.median(ts)) * 1e6, 1)}
+    out["steps_each"] = steps
+    out["sweep_bytes"] = SWEEP_BYTES
+    m.close()
+    return out
 
 
 def bench_gemm64(reps: int = 20):
@@ -672,7 +712,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec", "gemm64"],
+    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec", "gemm64", "mall"],
                     default="full")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -710,6 +750,9 @@ def main():
         return
     if args.mode == "streams":
         print(json.dumps({"streams": bench_streams(blob)}), flush=True)
+        return
+    if args.mode == "mall":
+        print(json.dumps({"mall": bench_mall(blob, state)}), flush=True)
         return
     log("decode")
     d = bench_decode(blob, state, args.steps, args.warmup)
