@@ -39,10 +39,12 @@ is reported beside the reference AudioDecoder on min(6, share) host threads.
 The same frames with an fp32 KV cache (the reference's precision) are timed as well
 (decode_kv_fp32).  --mode gemm64 runs the 64-stream engine's GEMM shapes (M = 64) through
 the operator ABI eagerly, for hardware-counter passes; --mode mall runs global steps warm and
-with a 1 GiB sweep before each (Infinity Cache residency of the weights, A/B).
+with a 1 GiB sweep before each (Infinity Cache residency of the weights, A/B); --mode handoff
+times a cross-workgroup hand-off of 4-64 KB per workgroup inside one launch (LL words, fenced
+counter barriers) against a launch boundary (libmoss_probe.so).
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
-                       [--mode full|gemv|attn|decode|prefill|streams|codec|gemm64|mall]
+                       [--mode full|gemv|attn|decode|prefill|streams|codec|gemm64|mall|handoff]
 """
 from __future__ import annotations
 
@@ -266,6 +268,37 @@ def bench_mall(blob, state, steps: int = 40):
     out["steps_each"] = steps
     out["sweep_bytes"] = SWEEP_BYTES
     m.close()
+    return out
+
+
+HANDOFF_MODES = (("launch per round (graph)", 3), ("LL words, one launch", 2),
+                 ("fence in every thread, one launch", 0), ("fence in one thread per workgroup, one launch", 1))
+HANDOFF_BYTES = (4096, 16384, 65536)
+
+
+def bench_handoff(rounds: int = 50):
+    """Cost of handing bulk data from each of 256 workgroups to a workgroup on another XCD,
+    per round, four ways: a kernel boundary (one launch per round, replayed from a graph),
+    LL words inside one persistent launch, and a counter barrier with __threadfence() in every
+    thread or in one thread per workgroup (libmoss_probe.so, csrc/probe_handoff.hip); 4, 16
+    and 64 KB per workgroup.  Every value is checked; device time from HIP events."""
+    import ctypes as C
+
+    import torch
+    torch.zeros(1, device="cuda")
+    lib = C.CDLL(os.path.join(ROOT, "dsh-moss-tts_amd", "libmoss_probe.so"))
+    lib.moss_probe_handoff.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
+    out = {}
+    for name, mode in HANDOFF_MODES:
+        row = {}
+        for nbytes in HANDOFF_BYTES:
+            us = C.c_double(0.0)
+            rc = lib.moss_probe_handoff(mode, rounds, nbytes // 4, C.byref(us))
+            if rc != 0:
+                raise RuntimeError(f"handoff probe {name}, {nbytes} B: error {rc}")
+            row[f"{nbytes // 1024}KB"] = round(us.value, 2)
+        out[name] = row
+    out["unit"] = "us per round, 256 workgroups"
     return out
 
 
@@ -712,8 +745,8 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec", "gemm64", "mall"],
-                    default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec", "gemm64", "mall",
+                                       "handoff"], default="full")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -735,6 +768,9 @@ def main():
         return
     if args.mode == "gemm64":
         print(json.dumps({"gemm64": bench_gemm64()}), flush=True)
+        return
+    if args.mode == "handoff":
+        print(json.dumps({"handoff": bench_handoff()}), flush=True)
         return
     if args.mode == "codec":
         cd = bench_codec()
