@@ -30,7 +30,9 @@ AVX2 attention on one host core; the 256-row prefill (ms; W8A8 as the
 reference's prefill, against the 5.0 POP/s int8 MFMA peak, and W8A16 against
 the 2.5 PFLOP/s fp16 peak) and 64 streams with contexts ~ U[64, 1024] decoded
 128 frames in lock-step (aggregate frames/s), each next to the reference on the
-host cores.
+host cores; the 64-stream engine's paged global attention alone
+(attention_paged_64, moss_hip_attn_paged at those contexts and at their mean,
+GB/s against the 8 TB/s HBM peak).
 
 The audio codec decoder (decode_chunk, the engine's 8-frame chunks on a stream
 past every window; ms/frame and the real-time factor, 80 ms of audio per frame)
@@ -44,7 +46,7 @@ times a cross-workgroup hand-off of 4-64 KB per workgroup inside one launch (LL 
 counter barriers) against a launch boundary (libmoss_probe.so).
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--no-cpu]
-                       [--mode full|gemv|attn|decode|prefill|streams|codec|gemm64|mall|handoff]
+                       [--mode full|gemv|attn|attn64|decode|prefill|streams|codec|gemm64|mall|handoff]
 """
 from __future__ import annotations
 
@@ -387,6 +389,58 @@ def bench_attention(reps: int = 100):
         r["frac_cold"] = round(r["GBps_cold"] / HBM_PEAK_GBS, 4)
         res[str(ctx)] = r
         del kv
+    return res
+
+
+def bench_attn64(reps: int = 20):
+    """The 64-stream engine's paged global attention through moss_hip_attn_paged: 64 rows
+    (one per stream, contexts ~ U[64, 1024] as the 64-stream workload), 12 heads x 64, fp16
+    pages of 64 positions laid out as the engine lays them (page j of stream s at j * 64 + s),
+    fp32 q and output.  12 launches per replay, one per layer's pools (2.3 GB in all, so
+    every launch reads its pages from HBM, as a frame's 12 layers do), `reps` replays of a
+    captured graph timed with HIP events on the capture stream.  Algorithmic bytes per
+    launch: the rows' K and V (2 * 2 * 768 bytes per key) + q and output (2 * 64 * 768 * 4).
+    Also timed: every row at the mean context (same bytes, no ragged tail)."""
+    import torch
+
+    from mosship import lib
+    ctx = stream_contexts()
+    rows, layers, page = STREAMS, 12, 64
+    per = -(-int(ctx.max()) // page)
+    g = torch.Generator(device="cuda").manual_seed(64)
+    k = torch.randn((layers, per * rows, 12, page, 64), generator=g, device="cuda").to(torch.float16)
+    v = torch.randn((layers, per * rows, 12, page, 64), generator=g, device="cuda").to(torch.float16)
+    table = (torch.arange(per, device="cuda", dtype=torch.int32)[None, :] * rows +
+             torch.arange(rows, device="cuda", dtype=torch.int32)[:, None]).contiguous()
+    q = torch.randn((rows, 768), generator=g, device="cuda")
+    out = torch.empty((rows, 768), dtype=torch.float32, device="cuda")
+    cap = torch.cuda.Stream()
+    res = {}
+    for kind, keys in (("ragged", ctx), ("uniform", np.full_like(ctx, int(round(ctx.mean()))))):
+        pos = torch.from_numpy((keys - 1).astype(np.int32)).cuda()
+        mk = int(keys.max())
+        algo = int(3072 * keys.sum()) + 2 * rows * 768 * 4
+        with torch.cuda.stream(cap):
+            for l in range(layers):
+                lib.attn_paged(q, k[l], v[l], 12, table, per, page, pos, mk, out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            for l in range(layers):
+                lib.attn_paged(q, k[l], v[l], 12, table, per, page, pos, mk, out)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(cap):
+            e0.record(cap)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(cap)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+        res[kind] = {"keys_total": int(keys.sum()), "keys_max": mk, "algo_bytes": algo, "us": round(us, 3),
+                     "GBps": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del k, v
     return res
 
 
@@ -745,8 +799,8 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["full", "gemv", "attn", "decode", "prefill", "streams", "codec", "gemm64", "mall",
-                                       "handoff"], default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "attn", "attn64", "decode", "prefill", "streams", "codec", "gemm64",
+                                       "mall", "handoff"], default="full")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -768,6 +822,9 @@ def main():
         return
     if args.mode == "gemm64":
         print(json.dumps({"gemm64": bench_gemm64()}), flush=True)
+        return
+    if args.mode == "attn64":
+        print(json.dumps({"attention_paged_64": bench_attn64()}), flush=True)
         return
     if args.mode == "handoff":
         print(json.dumps({"handoff": bench_handoff()}), flush=True)
@@ -808,6 +865,8 @@ def main():
     pf16 = bench_prefill(blob, a16=True)
     log("64 streams")
     st = bench_streams(blob)
+    log("64-stream paged attention")
+    a64 = bench_attn64()
     log("codec decoder")
     cd = bench_codec()
     cblob = cd.pop("blob")
@@ -876,6 +935,7 @@ def main():
         "streams_64": {"frames_per_s": round(st["frames_per_s"], 1), "ms_per_step": round(st["ms_per_step"], 4),
                        "global_stack_GBps": round(st["global_stack_GBps"], 1), "cpu_ref": cpu_st or None,
                        "vs_cpu": round(st["frames_per_s"] / best_st["frames_per_s"], 1) if best_st else None},
+        "attention_paged_64": a64,
         "codec": dict(cd, cpu_ref=cpu_cd,
                       vs_cpu=round(cpu_cd["ms_per_frame"] / cd["ms_per_frame"], 1) if cpu_cd else None),
         "host_cpu": host,

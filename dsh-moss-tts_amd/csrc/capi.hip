@@ -524,6 +524,39 @@ int moss_hip_attn_decode_noalloc(const float *q, const void *k_cache, const void
     });
 }
 
+int moss_hip_attn_paged(const float *q, const void *k_pool, const void *v_pool, int kv_dtype, int heads,
+                        const int32_t *page_table, int table_stride, int page_size, int rows,
+                        const int32_t *row_stream, const int32_t *row_pos, int max_keys, void *out, int out_dtype,
+                        void *stream) {
+    return guard([&] {
+        if (!q || !k_pool || !v_pool || !page_table || !row_pos || !out) throw Status(MOSS_HIP_EINVAL, "null pointer");
+        if (heads <= 0 || rows <= 0 || max_keys <= 0 || page_size <= 0 || table_stride <= 0 ||
+            (long long)table_stride * page_size < max_keys)
+            throw Status(MOSS_HIP_EINVAL, "need heads, rows, max_keys, page_size > 0 and table_stride * page_size >= max_keys");
+        if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
+            throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
+        mh::AttnArgs a;
+        a.q = q;
+        a.q_stride = heads * mh::kHeadDim;
+        a.k_pool = k_pool;
+        a.v_pool = v_pool;
+        a.page_table = page_table;
+        a.table_stride = table_stride;
+        a.page_size = page_size;
+        a.heads = heads;
+        a.row_stream = row_stream;
+        a.stream_stride = 1;
+        a.row_pos = row_pos;
+        a.rows = rows;
+        a.max_keys = max_keys;
+        a.out = out;
+        a.out_stride = heads * mh::kHeadDim;
+        a.out_f16 = out_dtype == MOSS_HIP_F16;
+        const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
+        mh::hip_check(mh::launch_attn(a, kv, static_cast<hipStream_t>(stream)), "attention launch");
+    });
+}
+
 int moss_hip_codec_create(const void *blob, size_t bytes, const moss_hip_codec_options *opt, moss_hip_codec **out) {
     return guard([&] {
         if (out == nullptr || blob == nullptr) throw Status(MOSS_HIP_EINVAL, "null argument");

@@ -37,7 +37,7 @@ EXPORTED = [
     "moss_hip_batch_position", "moss_hip_batch_kv_export", "moss_hip_batch_global_step", "moss_hip_batch_generate",
     "moss_hip_batch_capture", "moss_hip_batch_capture_read",
     "moss_hip_gemv_q8x4", "moss_hip_gemm_q8x4", "moss_hip_dequant_rows_q8x4", "moss_hip_attn_decode",
-    "moss_hip_attn_decode_noalloc",
+    "moss_hip_attn_decode_noalloc", "moss_hip_attn_paged",
     "moss_hip_quantize_rows", "moss_hip_gemm_q8x4_w8a8", "moss_hip_gemv_q8x4_w8a8",
     "moss_hip_codec_create", "moss_hip_codec_create_from_file", "moss_hip_codec_destroy",
     "moss_hip_codec_samples_per_frame", "moss_hip_codec_reset_stream", "moss_hip_codec_decode_chunk",
@@ -131,6 +131,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.moss_hip_dequant_rows_q8x4.argtypes = [vp, i32, i32, vp, i32, vp, vp]
     L.moss_hip_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
     L.moss_hip_attn_decode_noalloc.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, i32, vp]
+    L.moss_hip_attn_paged.argtypes = [vp, vp, vp, i32, i32, vp, i32, i32, i32, vp, vp, i32, vp, i32, vp]
     L.moss_hip_codec_create.argtypes = [vp, C.c_size_t, C.POINTER(CodecOptions), C.POINTER(vp)]
     L.moss_hip_codec_create_from_file.argtypes = [C.c_char_p, C.POINTER(CodecOptions), C.POINTER(vp)]
     L.moss_hip_codec_destroy.argtypes = [vp]
@@ -210,6 +211,20 @@ def attn_decode(q, k_cache, v_cache, heads: int, ctx_stride: int, n_keys: int, o
     fn = L.moss_hip_attn_decode_noalloc if noalloc else L.moss_hip_attn_decode
     check(fn(C.c_void_p(q.data_ptr()), C.c_void_p(k_cache.data_ptr()), C.c_void_p(v_cache.data_ptr()),
              dt[k_cache.dtype], heads, ctx_stride, n_keys, C.c_void_p(out.data_ptr()), dt[out.dtype], _stream(stream)))
+
+
+def attn_paged(q, k_pool, v_pool, heads: int, page_table, table_stride: int, page_size: int, row_pos, max_keys: int,
+               out, row_stream=None, stream=None) -> None:
+    """moss_hip_attn_paged: row r (stream row_stream[r], or r) attends its keys 0 .. row_pos[r]."""
+    import torch
+    dt = {torch.float32: F32, torch.float16: F16}
+    L = load()
+    rows = q.shape[0]
+    check(L.moss_hip_attn_paged(C.c_void_p(q.data_ptr()), C.c_void_p(k_pool.data_ptr()), C.c_void_p(v_pool.data_ptr()),
+                                dt[k_pool.dtype], heads, C.c_void_p(page_table.data_ptr()), table_stride, page_size,
+                                rows, C.c_void_p(row_stream.data_ptr()) if row_stream is not None else None,
+                                C.c_void_p(row_pos.data_ptr()), max_keys, C.c_void_p(out.data_ptr()), dt[out.dtype],
+                                _stream(stream)))
 
 
 # ---------------------------------------------------------------- model

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOSS_HIP_ABI_VERSION 7
+#define MOSS_HIP_ABI_VERSION 8
 
 enum {
     MOSS_HIP_OK = 0,
@@ -302,6 +302,22 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
  * streams do not share it. */
 int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cache, int kv_dtype, int heads,
                          int ctx_stride, int n_keys, void *out, int out_dtype, void *stream);
+
+/* Single-query attention of a batch of streams over paged K/V: the 64-stream engine's global
+ * attention (csrc/batch_model.hip) on caller-owned pages.  Per row it is attention_core
+ * (reference csrc/src/llm.cpp:189-217: scores q . k * 0.125, softmax, weighted sum of v); the
+ * batch over streams and the paging have no reference counterpart (the reference decodes one
+ * stream).  Pools are [page][heads][page_size][64] (kv_dtype MOSS_HIP_F16 or MOSS_HIP_F32); row
+ * r is the query of stream row_stream[r] (r when row_stream is NULL) at position row_pos[r]
+ * and attends that stream's keys 0 .. row_pos[r], whose j-th page of page_size positions is
+ * page_table[stream * table_stride + j].  q: [rows][heads * 64] fp32 (RoPE applied); out:
+ * [rows][heads * 64] (out_dtype).  max_keys bounds every row's key count (row_pos[r] + 1 is
+ * clamped to it) and sizes the launch.  page_table, row_stream and row_pos are device arrays.
+ * No scratch, no allocation: one workgroup per (head, row). */
+int moss_hip_attn_paged(const float *q, const void *k_pool, const void *v_pool, int kv_dtype, int heads,
+                        const int32_t *page_table, int table_stride, int page_size, int rows,
+                        const int32_t *row_stream, const int32_t *row_pos, int max_keys, void *out, int out_dtype,
+                        void *stream);
 
 /* moss_hip_attn_decode without any allocation.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under hipGraph capture, tight serving

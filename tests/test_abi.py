@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     L = lib.load()
     missing = [s for s in declared_symbols() if not hasattr(L, s)]
     assert not missing, missing
-    assert L.moss_hip_abi_version() == 7
+    assert L.moss_hip_abi_version() == 8
 
 
 def test_capture_layout_matches_header():
