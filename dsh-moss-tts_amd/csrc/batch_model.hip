@@ -294,13 +294,12 @@ void Batch::enqueue_local_step(hipStream_t s, int n, const float *in, int in_str
     f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b; f1.ln_stats = xst_;
     f1.y_hl = hl(h_); f1.bias = L.fc_in_b;
     hip_check(launch_gemm(f1, EPI_GELU, KV_F32, s), "local fc_in");
-    GemmArgs f2;  // split K: the reduce adds bias and residual, then the local ln_f for the head
+    GemmArgs f2;  // x += fc_out + b (lres_: the gate's input at lpos 0), pre-split with its LN
+                  // statistics: the audio head applies the local ln_f
     f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = hl(h_); f2.lda = kFF; f2.M = n;
-    f2.part = part_; f2.ksplit = std::max(gemm_ksplit(n, kHidden, kFF), kBatchFcOutSplit);
-    hip_check(launch_gemm(f2, EPI_PART, KV_F32, s), "local fc_out");
-    hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, lres_, kHidden, lres_, w_.llnf_w, w_.llnf_b,
-                                   nullptr, nullptr, s, nullptr, nullptr, hl(a_)),
-              "local fc_out reduce + ln_f");
+    f2.y = lres_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
+    f2.y_hl = hl(a_); f2.y_stats = xst_;
+    hip_check(launch_gemm(f2, EPI_RESID, KV_F32, s), "local fc_out");
 }
 
 // The W8A8 form of the local step after its attention (q8a_ holds the attention output's int8
@@ -422,8 +421,9 @@ void Batch::enqueue_frame_local(hipStream_t s, int n, bool greedy) {
         hd.M = n;
         if (a8_) {  // the local ln_f quantised by the reduce before it
             hd.a8 = q8a_; hd.d8 = d8a_; hd.a8_tiled = true;
-        } else {
+        } else {  // the step's output, pre-split by fc_out: the local ln_f applied here
             hd.a_hl = hl(a_);
+            hd.ln_w = w_.llnf_w; hd.ln_b = w_.llnf_b; hd.ln_stats = xst_;
         }
         hd.y = logits_; hd.ldy = kCodebook;
         if (greedy && ch + 1 < kNVq) {  // the next launch picks this channel from per-16-code partials
@@ -462,8 +462,12 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         const LayerW &L = w_.global[l];
         void *kp = static_cast<uint8_t *>(kpool_) + l * layer_pool_elems_ * esize_;
         void *vp = static_cast<uint8_t *>(vpool_) + l * layer_pool_elems_ * esize_;
-        GemmArgs q;  // on LN1(x) in a_ (hi / lo halves)
+        GemmArgs q;  // layer 0: on LN1(x) in a_ (hi / lo halves); later layers: on x in a_, LN1 applied
+                     // with the statistics the previous fc_out wrote
         q.w = L.attn_w; q.wm = L.attn_wm; q.N = 3 * kHidden; q.K = kHidden; q.a_hl = hl(a_); q.lda = kHidden; q.M = n;
+        if (l > 0) {
+            q.ln_w = L.ln1_w; q.ln_b = L.ln1_b; q.ln_stats = xst_;
+        }
         q.bias = L.attn_b; q.q_out = q_; q.k_pool = kp; q.v_pool = vp;
         q.page_table = table_; q.table_stride = pages_; q.page_size = kPage;
         q.stream_stride = 1; q.row_pos = pos_d_; q.row_active = active_; q.rope_cos = rc; q.rope_sin = rs;
@@ -482,17 +486,23 @@ void Batch::enqueue_global(hipStream_t s, int n) {
         f1.ln_w = L.ln2_w; f1.ln_b = L.ln2_b; f1.ln_stats = xst_;
         f1.y_hl = hl(h_); f1.bias = L.fc_in_b;
         hip_check(launch_gemm(f1, EPI_GELU, kvt_, s), "fc_in");
-        GemmArgs f2;  // split K; the reduce adds bias and residual
+        GemmArgs f2;
         f2.w = L.fc_out_w; f2.wm = L.fc_out_wm; f2.N = kHidden; f2.K = kFF; f2.a_hl = hl(h_); f2.lda = kFF; f2.M = n;
-        f2.part = part_; f2.ksplit = std::max(gemm_ksplit(n, kHidden, kFF), kBatchFcOutSplit);
-        hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
-        // then LN1 of the next layer into a_, or ln_f into hidden (active streams only)
-        const bool last = l + 1 == kLayers;
-        hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, x_, kHidden, x_,
-                                       last ? w_.lnf_w : w_.global[l + 1].ln1_w,
-                                       last ? w_.lnf_b : w_.global[l + 1].ln1_b, last ? hidden_ : nullptr,
-                                       last ? active_ : nullptr, s, nullptr, nullptr, last ? nullptr : hl(a_)),
-                  "fc_out reduce + ln");
+        if (l + 1 < kLayers) {
+            // x += fc_out + b in one launch (8 waves split K in the workgroup), written also
+            // pre-split with its LN statistics: the next layer's QKV applies LN1
+            f2.y = x_; f2.ldy = kHidden; f2.bias = L.fc_out_b;
+            f2.y_hl = hl(a_); f2.y_stats = xst_;
+            hip_check(launch_gemm(f2, EPI_RESID, kvt_, s), "fc_out");
+        } else {
+            // split K; the reduce adds bias and residual and writes ln_f into hidden (active
+            // streams only)
+            f2.part = part_; f2.ksplit = std::max(gemm_ksplit(n, kHidden, kFF), kBatchFcOutSplit);
+            hip_check(launch_gemm(f2, EPI_PART, kvt_, s), "fc_out");
+            hip_check(launch_resid_ln_rows(part_, f2.ksplit, n, L.fc_out_b, x_, kHidden, x_, w_.lnf_w, w_.lnf_b,
+                                           hidden_, active_, s, nullptr, nullptr, nullptr),
+                      "fc_out reduce + ln_f");
+        }
     }
     hip_check(launch_advance_rows(st, n, s), "advance");
 }

@@ -412,11 +412,14 @@ __device__ __forceinline__ float2 ln_rows_from_stats(const GemmArgs &g, int m_ba
     return rstat[l16];
 }
 
-template <int EPI, int KV, int NT, bool A8, bool LN, bool TL, bool AT>
-__global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
+// WV: waves per workgroup, 4, or 8 for a long K with the residual epilogue (fc_out, K = 3072:
+// 3 blocks per wave, so the sum needs no second kernel); waves 4..7 only contribute partials.
+template <int EPI, int KV, int NT, bool A8, bool LN, bool TL, bool AT, int WV = 4>
+__global__ __launch_bounds__(64 * WV) void gemm_wk_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
+    static_assert(WV == 4 || (WV == 8 && EPI == EPI_RESID && !LN), "8 waves: the residual epilogue only");
     GT_START
-    __shared__ floatx4 red[4][NT][64];
+    __shared__ floatx4 red[WV][NT][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int l16 = lane & 15, kq = lane >> 4;  // kq: which 8-column quarter of the block
     const int m_base = blockIdx.y * 16;
@@ -425,13 +428,13 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
     // K slice z: blocks [z * nb_all / Z, (z + 1) * nb_all / Z); wave w its w-th quarter
     const int z0 = (int)((blockIdx.z * (unsigned)nb_all) / gridDim.z);
     const int nbz = (int)(((blockIdx.z + 1) * (unsigned)nb_all) / gridDim.z) - z0;
-    const int kb0 = z0 + (wave * nbz) / 4;
-    const int nb = z0 + ((wave + 1) * nbz) / 4 - kb0;  // 0 when the slice has fewer than 4 blocks
+    const int kb0 = z0 + (wave * nbz) / WV;
+    const int nb = z0 + ((wave + 1) * nbz) / WV - kb0;  // 0 when the slice has fewer than WV blocks
     const int arow = min(m_base + l16, g.M - 1);      // rows past M read row M-1, never stored
     const int krow = l16 & 3;
     // the epilogue: wave w finishes row 4kq + w of every column subtile; its operands
     // are requested first (loads complete in order, so these never delay the operands')
-    const int erow = m_base + 4 * kq + wave;
+    const int erow = m_base + 4 * kq + (wave & 3);
     const EpiRow er = epi_row<EPI, KV>(g, erow, n_base);
     EpiOps<NT> eo;
     epi_load<EPI, NT>(g, er, n_base, l16, eo);
@@ -653,16 +656,16 @@ __global__ __launch_bounds__(256) void gemm_wk_kernel(GemmArgs g) {
             return;
         }
     }
+    if (WV > 4 && wave >= 4) return;  // (uniform) their partials are in LDS
     // component w of each lane's partials: one 4-byte LDS read each, at an offset
-    // uniform in the wave
+    // uniform in the wave; the waves' partials summed in wave order
     const int i = wave, m = erow;
     const float *redf = (const float *)&red[0][0][lane] + i;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         float v = redf[4 * (t * 64)];
-        v += redf[4 * ((NT + t) * 64)];
-        v += redf[4 * ((2 * NT + t) * 64)];
-        v += redf[4 * ((3 * NT + t) * 64)];
+#pragma unroll
+        for (int w = 1; w < WV; ++w) v += redf[4 * ((w * NT + t) * 64)];
         const int n = n_base + 16 * t + l16;
         const float partner = xshfl<1>(v);  // column n ^ 1, same row
         if (m < g.M) gemm_finish<EPI, KV, NT>(er, eo, t, n, v, partner);
@@ -728,6 +731,16 @@ template <int EPI, int KV, bool A8, bool LN, bool TL, bool AT>
 hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     const int mt = (g.M + 15) / 16;
+    if constexpr (EPI == EPI_RESID && !LN) {
+        // a long K (fc_out, K = 3072) in one workgroup of 8 waves, 16 columns a tile: each wave
+        // takes 3 blocks and the residual epilogue completes the rows (no split-K reduce)
+        // (32-column tiles, half the workgroups: 64 streams 56.4k -> 54.4k frames/s)
+        if (g.K >= 2048) {
+            hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN, TL, AT, 8>), dim3(g.N / 16, mt, 1), dim3(512), 0, s,
+                               g);
+            return hipGetLastError();
+        }
+    }
     const int kz = EPI == EPI_PART ? (g.ksplit > 0 ? g.ksplit : gemm_ksplit(g.M, g.N, g.K)) : 1;
     // the widest column tile that still gives ~192 workgroups (a quantising epilogue needs
     // whole 32-blocks in a tile: at least 32 columns)
@@ -746,7 +759,7 @@ hipError_t launch_l(const GemmArgs &g, hipStream_t s) {
     if (g.a8 != nullptr)
         return g.a8_tiled ? launch_nt<EPI, KV, true, false, TL, true>(g, s)
                           : launch_nt<EPI, KV, true, false, TL, false>(g, s);
-    if constexpr (EPI == EPI_GELU) {
+    if constexpr (EPI == EPI_GELU || EPI == EPI_QKV || EPI == EPI_F32) {
         if (g.a_hl != nullptr && g.ln_w != nullptr) return launch_nt<EPI, KV, false, true, TL, true>(g, s);
     }
     if (g.a_hl != nullptr) return launch_nt<EPI, KV, false, false, TL, true>(g, s);
@@ -802,9 +815,9 @@ hipError_t launch_gemm(const GemmArgs &g, Epilogue epi, KvType kv, hipStream_t s
     if (g.a8 != nullptr && (!g.d8 || g.lda % 32)) return hipErrorInvalidValue;
     if (g.a8_tiled && (g.a8 == nullptr || g.lda != g.K)) return hipErrorInvalidValue;
     if (g.a_hl != nullptr && (g.a8 != nullptr || g.lda != g.K)) return hipErrorInvalidValue;
-    // LN of pre-split rows: statistics from a producer's y_stats, fc_in's shape
+    // LN of pre-split rows: statistics from a producer's y_stats, K = 768 (fc_in, QKV, the heads)
     if (g.a_hl != nullptr && g.ln_w != nullptr &&
-        (!g.ln_stats || !g.ln_b || epi != EPI_GELU || g.K != kHidden))
+        (!g.ln_stats || !g.ln_b || (epi != EPI_GELU && epi != EPI_QKV && epi != EPI_F32) || g.K != kHidden))
         return hipErrorInvalidValue;
     if (g.ln_stats != nullptr && (g.a_hl == nullptr || g.ln_w == nullptr)) return hipErrorInvalidValue;
     if (g.y_hl != nullptr && ((epi != EPI_GELU && epi != EPI_RESID) || g.q8_out != nullptr || g.N % 32))

@@ -181,8 +181,8 @@ struct GemmArgs {
     // sum of squared deviations at y_stats[2 * (j * M + m)] -- the next LayerNorm's row
     // statistics, combined in a fixed order by the GEMM that reads them (ln_stats)
     float *y_stats = nullptr;
-    // with a_hl and ln_w (EPI_GELU, K = 768): LN of the pre-split rows, the rows' statistics
-    // combined from ln_stats (a producer's y_stats) instead of formed from the rows
+    // with a_hl and ln_w (EPI_GELU, EPI_QKV, EPI_F32; K = 768): LN of the pre-split rows, the
+    // rows' statistics combined from ln_stats (a producer's y_stats) instead of formed from the rows
     const float *ln_stats = nullptr;
     // LayerNorm prologue: the GEMM multiplies LN(a_row) = (a - mean) * inv * ln_w + ln_b
     // (llm.cpp:159-171) when ln_w is non-null -- over fp32 rows `a` (K <= 1024, no K
