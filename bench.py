@@ -416,18 +416,21 @@ def bench_attn64(reps: int = 20):
     out = torch.empty((rows, 768), dtype=torch.float32, device="cuda")
     cap = torch.cuda.Stream()
     res = {}
-    for kind, keys in (("ragged", ctx), ("uniform", np.full_like(ctx, int(round(ctx.mean()))))):
-        pos = torch.from_numpy((keys - 1).astype(np.int32)).cuda()
+    order = np.argsort(-ctx, kind="stable").astype(np.int32)
+    for kind, keys, rs in (("ragged", ctx, None), ("uniform", np.full_like(ctx, int(round(ctx.mean()))), None),
+                           ("ragged_longest_first", ctx, order)):
+        pos = torch.from_numpy(((keys if rs is None else keys[rs]) - 1).astype(np.int32)).cuda()
+        rsd = None if rs is None else torch.from_numpy(rs).cuda()
         mk = int(keys.max())
         algo = int(3072 * keys.sum()) + 2 * rows * 768 * 4
         with torch.cuda.stream(cap):
             for l in range(layers):
-                lib.attn_paged(q, k[l], v[l], 12, table, per, page, pos, mk, out)
+                lib.attn_paged(q, k[l], v[l], 12, table, per, page, pos, mk, out, row_stream=rsd)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=cap):
             for l in range(layers):
-                lib.attn_paged(q, k[l], v[l], 12, table, per, page, pos, mk, out)
+                lib.attn_paged(q, k[l], v[l], 12, table, per, page, pos, mk, out, row_stream=rsd)
         graph.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

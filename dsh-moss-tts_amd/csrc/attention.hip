@@ -108,7 +108,9 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
     // PART: one 64-key span per workgroup (blockIdx.y), one row
     // w is wave-uniform; saying so keeps span bases in SGPRs (loads then take a
     // scalar base and a 32-bit lane offset)
-    const int h = blockIdx.x, r = (PART || CHUNK) ? 0 : blockIdx.y, lane = threadIdx.x & 63;
+    const int h = blockIdx.x, lane = threadIdx.x & 63;
+    const int r = (PART || CHUNK) ? 0
+                                  : __builtin_amdgcn_readfirstlane(a.row_order ? a.row_order[blockIdx.y] : (int)blockIdx.y);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = __builtin_amdgcn_readfirstlane(a.row_stream ? a.row_stream[r] : r * a.stream_stride);
     // keys of this row, never past the capacity the caches were built for (a
@@ -565,6 +567,7 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
         return hipErrorInvalidValue;
     if (a.out_hl != nullptr && (a.part != nullptr || a.chunks != 0 || a.heads != kHeads)) return hipErrorInvalidValue;
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
+    if (a.row_order != nullptr && (a.part != nullptr || a.chunks != 0)) return hipErrorInvalidValue;
     if (a.q8 != nullptr && (!a.d8 || a.part != nullptr || a.heads != kHeads)) return hipErrorInvalidValue;
     // every slice holds at least one live span and reaches the end of the kernel (no stop
     // flag), so every workgroup of a sliced launch arrives at the generation counter

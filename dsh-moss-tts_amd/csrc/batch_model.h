@@ -85,6 +85,10 @@ private:
     float *x_ = nullptr, *a_ = nullptr, *q_ = nullptr, *o_ = nullptr, *h_ = nullptr;
     float *hidden_ = nullptr, *lres_ = nullptr, *next_in_ = nullptr, *logits_ = nullptr;
     int *pos_d_ = nullptr, *codes_ = nullptr, *row_ = nullptr, *counts_ = nullptr;
+    // the streams longest context first, the order of the paged attention's workgroups
+    // (set from pos_ at every generate / global_step call), and its pinned host staging
+    int *order_ = nullptr, *order_h_ = nullptr;
+    void upload_order(int n);
     float *part_ = nullptr;                     // [16][S][768] split-K partials
     float *xhl_ = nullptr;   // proj's output as hi / lo halves (fc_in's operand), rows padded to 16
     float *xst_ = nullptr;   // its per-16-column LayerNorm statistics [48][S][2]

@@ -86,6 +86,10 @@ struct AttnArgs {
     const int *row_pos = nullptr;  // keys of row r = row_pos[r] + 1 (pos0 + r * pos_stride + 1 when null)
     int pos0 = 0, pos_stride = 1;
     int rows = 1;
+    // workgroups (blockIdx.y) take the rows in this order when set (the batch engine passes its
+    // streams longest context first, so the longest rows start first and share no CU round
+    // with each other); row y when null.  Rows of one launch, not split-KV or sliced launches.
+    const int *row_order = nullptr;
     int max_keys = 0;              // key capacity: sizes the launch and caps every row's key count
     void *out = nullptr;           // row r: out + r * out_stride
     int out_stride = kHidden;
