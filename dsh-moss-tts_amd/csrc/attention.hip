@@ -375,7 +375,10 @@ __device__ __forceinline__ floatx4 mfma_f32x4(float a, float b, floatx4 c) {
 // so the lane with row l%16 holds S^T for keys kb + 4g + i and O for columns 16g..16g+15
 // (g = l/16).  The waves merge through LDS; the output is normalised (and, under W8A8,
 // quantised per 32-block as quant_block32 does) and written as the row-per-workgroup kernel
-// writes it.
+// writes it -- or, in the prefill (proj_part), multiplied by the head's 64 columns of proj
+// on the matrix cores (int8 under W8A8, fp16 hi / lo otherwise, the proj GEMM's per-block
+// arithmetic) and written as split-K partial h: one launch fewer per layer (the tile's
+// kernel time grows 9.7 -> 14.3 us against the 6.1 us proj GEMM it replaces).
 template <int KV>
 __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
     __shared__ float red[4][16 * 64 + 32];
@@ -500,6 +503,40 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
     }
     lrun += xshfl<16>(lrun);
     lrun += xshfl<32>(lrun);
+    // proj in the same launch (a.proj_part): wave w takes proj's 16-column subtiles w, w + 4,
+    // ..., 12 of the 48; their units for this head's two blocks are requested now, so that they
+    // arrive during the merge (the barriers up to the proj MFMAs order LDS only; requested
+    // before the key blocks instead, they delay those: 256-row prefill 0.62 -> 0.63 ms)
+    const bool fuse = a.proj_part != nullptr;  // uniform
+    constexpr int kPS = kHidden / 16 / 4;     // subtiles per wave
+    uint2 pq[kPS][2];
+    uint16_t pd[kPS][2];
+    if (fuse) {
+        // B operand of lane c16 + 16 kq: row n = 16 s + c16 of proj, columns 8 kq .. 8 kq + 7 of
+        // block 2h + bb, and the row's block scale -- one unit of the matrix-core order, or the
+        // row's 32-byte run in its 4-row group's 136-byte block (Q8_0_4X4)
+        const int c16 = lane & 15, kq = lane >> 4;
+        constexpr int nb = kHidden / 32;
+#pragma unroll
+        for (int i = 0; i < kPS; ++i)
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const int sub = wave + 4 * i, blk = 2 * h + bb;
+                const uint8_t *qp, *dp;
+                if (a.proj_tiled) {
+                    const uint8_t *unit = a.proj_w + ((size_t)sub * nb + blk) * kTileBytes;
+                    qp = unit + 8 * lane;
+                    dp = unit + 512 + 2 * c16;
+                } else {
+                    const int n = 16 * sub + c16;
+                    const uint8_t *b4 = a.proj_w + ((size_t)(n >> 2) * nb + blk) * kBlockBytes;
+                    qp = b4 + 8 + 32 * (n & 3) + 8 * kq;
+                    dp = b4 + 2 * (n & 3);
+                }
+                pq[i][bb] = *reinterpret_cast<const uint2 *>(qp);
+                pd[i][bb] = *reinterpret_cast<const uint16_t *>(dp);
+            }
+    }
     float *R = red[wave];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -509,7 +546,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
         R[1024 + col] = mrun;
         R[1040 + col] = lrun;
     }
-    __syncthreads();
+    lds_barrier();
     // thread t: row q = t / 16, columns 4 (t % 16) .. + 3 of the head
     const int q = t >> 4, d4 = t & 15, m = m0 + q;
     float mx = -INFINITY;
@@ -528,22 +565,107 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(const AttnArgs a) {
     float ov[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) ov[e] = acc[e] * inv;
-    if (a.q8 != nullptr) {  // uniform: W8A8 copy, quant_block32's arithmetic over 8 threads x 4 values
+    // W8A8 operand: quant_block32's arithmetic over 8 threads x 4 values (a 32-column block)
+    const bool quant = a.q8 != nullptr || (fuse && a.proj_a8);  // uniform
+    uint32_t qword = 0;  // the 4 int8 values, column 4 d4 + e in byte e
+    float dq = 0.0f;
+    if (quant) {
         float amax = fmaxf(fmaxf(fabsf(ov[0]), fabsf(ov[1])), fmaxf(fabsf(ov[2]), fabsf(ov[3])));
         amax = fmaxf(amax, xshfl<1>(amax));
         amax = fmaxf(amax, xshfl<2>(amax));
         amax = fmaxf(amax, xshfl<4>(amax));
-        const float d = amax / 127.0f;
-        const float id = d > 0.0f ? 1.0f / d : 0.0f;
-        if (m < a.rows) {
-            // 4 consecutive columns: one aligned 4-byte run of the matrix-core order
-            int8_t *qrun = a.q8 + q8t_at(m, h * kHeadDim + 4 * d4, kHidden);
+        dq = amax / 127.0f;
+        const float id = dq > 0.0f ? 1.0f / dq : 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                int qq = (int)rintf(ov[e] * id);
-                qrun[e] = (int8_t)(qq < -127 ? -127 : (qq > 127 ? 127 : qq));
+        for (int e = 0; e < 4; ++e) {
+            int qq = (int)rintf(ov[e] * id);
+            qq = qq < -127 ? -127 : (qq > 127 ? 127 : qq);
+            qword |= (uint32_t)(qq & 0xff) << (8 * e);
+        }
+        if (a.q8 != nullptr && m < a.rows) {
+            // 4 consecutive columns: one aligned 4-byte run of the matrix-core order
+            *reinterpret_cast<uint32_t *>(a.q8 + q8t_at(m, h * kHeadDim + 4 * d4, kHidden)) = qword;
+            if ((d4 & 7) == 0) a.d8[d8t_at(m, 2 * h + (d4 >> 3), kHidden)] = dq;
+        }
+    }
+    if (fuse) {
+        // proj's A operand for the head's two blocks in the MFMA lane order: lane q + 16 j of
+        // block b takes row q, columns 8j .. 8j + 7 of the block (thread (q, d4): block d4 / 8,
+        // j = (d4 % 8) / 2, the 4 columns at (d4 % 2) * 4); W8A8: int8 and the rows' block
+        // scales, A16: fp16 hi / lo halves (store_hl's split)
+        __shared__ uint2 pa8[2][64];
+        __shared__ float pda[2][16];
+        __shared__ uint4 pah[2][64], pal[2][64];
+        const int bb = d4 >> 3, L = q + 16 * ((d4 & 7) >> 1), half = d4 & 1;
+        if (a.proj_a8) {
+            reinterpret_cast<uint32_t *>(&pa8[bb][L])[half] = qword;
+            if ((d4 & 7) == 0) pda[bb][q] = dq;
+        } else {
+            const auto h01 = __builtin_amdgcn_cvt_pkrtz(ov[0], ov[1]);
+            const auto h23 = __builtin_amdgcn_cvt_pkrtz(ov[2], ov[3]);
+            const auto l01 = __builtin_amdgcn_cvt_pkrtz(ov[0] - (float)h01[0], ov[1] - (float)h01[1]);
+            const auto l23 = __builtin_amdgcn_cvt_pkrtz(ov[2] - (float)h23[0], ov[3] - (float)h23[1]);
+            uint2 hw, lw;
+            hw.x = __builtin_bit_cast(uint32_t, h01);
+            hw.y = __builtin_bit_cast(uint32_t, h23);
+            lw.x = __builtin_bit_cast(uint32_t, l01);
+            lw.y = __builtin_bit_cast(uint32_t, l23);
+            reinterpret_cast<uint2 *>(&pah[bb][L])[half] = hw;
+            reinterpret_cast<uint2 *>(&pal[bb][L])[half] = lw;
+        }
+        lds_barrier();
+        // wave w: subtiles w + 4i, both blocks, in block order per output (the GEMM's
+        // per-block scale-then-accumulate); lane holds rows 4 kq + r, column c16
+        const int kq = lane >> 4, c16 = lane & 15;
+        float acc[kPS][4];
+#pragma unroll
+        for (int i = 0; i < kPS; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][r] = 0.0f;
+        if (a.proj_a8) {
+            const uint2 a0 = pa8[0][lane], a1 = pa8[1][lane];
+            float da[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                da[0][r] = pda[0][4 * kq + r];
+                da[1][r] = pda[1][4 * kq + r];
             }
-            if ((d4 & 7) == 0) a.d8[d8t_at(m, 2 * h + (d4 >> 3), kHidden)] = d;
+#pragma unroll
+            for (int i = 0; i < kPS; ++i)
+#pragma unroll
+                for (int b2 = 0; b2 < 2; ++b2) {
+                    const uint2 av = b2 ? a1 : a0;
+                    const long al = (long)(((uint64_t)av.y << 32) | av.x);
+                    const long bl = (long)(((uint64_t)pq[i][b2].y << 32) | pq[i][b2].x);
+                    const intx4 p = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bl, intx4{0, 0, 0, 0}, 0, 0, 0);
+                    const float dw = h2f(pd[i][b2]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][r] = fmaf((float)p[r], dw * da[b2][r], acc[i][r]);
+                }
+        } else {
+            const half8 h0 = __builtin_bit_cast(half8, pah[0][lane]), l0 = __builtin_bit_cast(half8, pal[0][lane]);
+            const half8 h1 = __builtin_bit_cast(half8, pah[1][lane]), l1 = __builtin_bit_cast(half8, pal[1][lane]);
+#pragma unroll
+            for (int i = 0; i < kPS; ++i)
+#pragma unroll
+                for (int b2 = 0; b2 < 2; ++b2) {
+                    const half8 bw = i8x8_to_h8(pq[i][b2]);
+                    floatx4 blk = floatx4{0.f, 0.f, 0.f, 0.f};
+                    blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(b2 ? h1 : h0, bw, blk, 0, 0, 0);
+                    blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(b2 ? l1 : l0, bw, blk, 0, 0, 0);
+                    const float dw = h2f(pd[i][b2]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(blk[r], dw, acc[i][r]);
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int mr = m0 + 4 * kq + r;
+            if (mr < a.rows) {
+                float *prow = a.proj_part + ((size_t)h * a.rows + mr) * kHidden + c16;
+#pragma unroll
+                for (int i = 0; i < kPS; ++i) prow[16 * (wave + 4 * i)] = acc[i][r];
+            }
         }
     }
     if (m >= a.rows) return;
@@ -582,11 +704,11 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
 hipError_t launch_attn_tiles(const AttnArgs &a, KvType kv, hipStream_t s) {
     (void)hipGetLastError();  // report only this launch's error, not a stale one
     if (a.heads != kHeads || a.rows <= 0 || a.max_keys <= 0 || a.page_size < a.max_keys ||
-        (!a.out && !a.q8 && !a.out_hl) ||
+        (!a.out && !a.q8 && !a.out_hl && !a.proj_part) ||
         a.out_f16 ||
         !a.q || !a.k_pool || !a.v_pool || a.part || a.page_table || a.row_pos || a.row_stream || a.chunks ||
         a.pos_stride != 1 || a.pos0 < 0 || a.pos0 + a.rows > a.max_keys || a.q_stride % 4 || a.out_stride % 4 ||
-        (a.q8 != nullptr && !a.d8))
+        (a.q8 != nullptr && !a.d8) || (a.proj_part != nullptr && !a.proj_w))
         return hipErrorInvalidValue;
     const dim3 grid((a.rows + 15) / 16, kHeads);
     if (kv == KV_F16)

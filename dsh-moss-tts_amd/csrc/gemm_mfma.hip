@@ -40,7 +40,6 @@ __device__ unsigned long long mh_gemm_ts[8192][2];
 #endif
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 #ifndef MH_GEMM_KB
@@ -50,7 +49,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // GEMMs (K = 768: 6 per wave, or 3 per wave in two K slices; K = 3072: 24 or 12)
 constexpr int KB = MH_GEMM_KB;
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // x = hi + lo: hi rounds toward zero (v_cvt_pkrtz, two values per
 // instruction), so x - hi is exact in fp32; lo keeps the next ~10 bits.
@@ -64,25 +62,6 @@ __device__ __forceinline__ void split_hi_lo(const float (&x)[8], half8 &hi, half
         lo[2 * i] = (_Float16)l[0];
         lo[2 * i + 1] = (_Float16)l[1];
     }
-}
-
-// int8 -> fp16, exactly: the half with bits 0x64 : (q ^ 0x80) is 1024 + (q + 128),
-// built two at a time with v_perm_b32; subtracting 1152 leaves q.
-__device__ __forceinline__ half8 i8x8_to_h8(uint2 q) {
-    const uint32_t a = q.x ^ 0x80808080u, b = q.y ^ 0x80808080u;
-    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
-                           __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
-                           __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
-    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    half8 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const half2v v = __builtin_bit_cast(half2v, w[i]) - bias;
-        r[2 * i] = v[0];
-        r[2 * i + 1] = v[1];
-    }
-    return r;
 }
 
 // What the epilogue needs of a lane's row, computed once: a lane stores one row
@@ -218,7 +197,6 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
 // rows' fp16 scales.  A column-subtile load is 4 whole 128-byte lines; in the
 // Q8_0_4X4 order it gathers 4 groups' 128-byte runs that start 8 bytes into
 // 136-byte blocks (8 lines), plus 4 more lines for the scales.
-constexpr int kTileBytes = 544;
 
 template <bool A8>
 struct Src {
@@ -300,7 +278,6 @@ __device__ __forceinline__ void load_chunk(Chunk<NT, A8, AT> &c, int b0, const S
     load_chunk_b<NT, A8, AT, TL>(c, b0, s);
 }
 
-typedef int intx4 __attribute__((ext_vector_type(4)));
 
 template <int NT, bool A8, bool AT>
 __device__ __forceinline__ void mfma_chunk(const Chunk<NT, A8, AT> &c, int b0, int nb, int kq, floatx4 (&acc)[NT]) {

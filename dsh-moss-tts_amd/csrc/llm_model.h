@@ -200,7 +200,7 @@ private:
     float *text_logits_ = nullptr;       // [16384] text head of gate-dump frames
     int *rows_dev_ = nullptr;            // prefill rows [n][17]
     int rows_cap_ = 0;
-    float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_o_ = nullptr, *pre_h_ = nullptr;  // prefill rows
+    float *pre_x_ = nullptr, *pre_a_ = nullptr, *pre_q_ = nullptr, *pre_h_ = nullptr;  // prefill rows
     float *pre_part_ = nullptr;          // split-K partials of the prefill proj / fc_out GEMMs
     int8_t *pre_q8_ = nullptr;           // W8A8 prefill: the current GEMM's int8 activations [m][<=768]
     float *pre_d8_ = nullptr;            //   and their block scales [m][<=24]

@@ -270,7 +270,7 @@ Model::~Model() {
     if (g_global_) (void)hipGraphExecDestroy(g_global_);
     if (g_local_) (void)hipGraphExecDestroy(g_local_);
     if (g_local_fused_) (void)hipGraphExecDestroy(g_local_fused_);
-    void *bufs[] = {blob_, wm_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_, cap_dec_, cap_pre_};
+    void *bufs[] = {blob_, wm_, kv_, lkv_, rope_, x_, q_, mlp_, hidden_, lres_, next_in_, slot_in_, attn_out_, attn_part_, pre_x_, pre_a_, pre_q_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_, logits_, counts_, forced_, text_logits_, rows_dev_, state_, snap_, ll_, qkv_table_, layer_args_, cap_dec_, cap_pre_};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (hstate_) (void)hipHostFree(hstate_);
@@ -711,27 +711,26 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     if (m <= 0) return;
     check_rows(rows, m);
     if (m > rows_cap_) {
-        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_o_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_};
+        void *bufs[] = {rows_dev_, pre_x_, pre_a_, pre_q_, pre_h_, pre_part_, pre_q8_, pre_d8_, pre_q8h_, pre_d8h_};
         for (void *p : bufs)
             if (p) hip_check(hipFree(p), "free prefill buffers");
         rows_dev_ = nullptr;
-        pre_x_ = pre_a_ = pre_q_ = pre_o_ = pre_h_ = pre_part_ = pre_d8_ = pre_d8h_ = nullptr;
+        pre_x_ = pre_a_ = pre_q_ = pre_h_ = pre_part_ = pre_d8_ = pre_d8h_ = nullptr;
         pre_q8_ = pre_q8h_ = nullptr;
         rows_cap_ = 0;
         hip_check(hipMalloc(&rows_dev_, sizeof(int) * 17 * (size_t)m), "hipMalloc(rows)");
-        // pre_a_, pre_o_, pre_h_: GEMM inputs, as fp16 hi / lo halves in the matrix-core
+        // pre_a_, pre_h_: GEMM inputs, as fp16 hi / lo halves in the matrix-core
         // order under A16 (hlt_at: 4 bytes a value, rows padded to 16)
         const size_t mp = (size_t)(m + 15) / 16 * 16;
         hip_check(hipMalloc(&pre_x_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
         hip_check(hipMalloc(&pre_a_, sizeof(float) * kHidden * mp), "hipMalloc(prefill)");
         hip_check(hipMalloc(&pre_q_, sizeof(float) * kHidden * (size_t)m), "hipMalloc(prefill)");
-        hip_check(hipMalloc(&pre_o_, sizeof(float) * kHidden * mp), "hipMalloc(prefill)");
         hip_check(hipMalloc(&pre_h_, sizeof(float) * kFF * mp), "hipMalloc(prefill)");
         hip_check(hipMemsetAsync(pre_a_, 0, sizeof(float) * kHidden * mp, stream_), "memset(prefill)");
-        hip_check(hipMemsetAsync(pre_o_, 0, sizeof(float) * kHidden * mp, stream_), "memset(prefill)");
         hip_check(hipMemsetAsync(pre_h_, 0, sizeof(float) * kFF * mp, stream_), "memset(prefill)");
+        // split-K partials: proj's (one per head when the attention applies proj) and fc_out's
         const int kz = std::max(std::max(gemm_ksplit(m, kHidden, kHidden), gemm_ksplit(m, kHidden, kFF)),
-                                kPrefillFcOutSplit);
+                                std::max(kPrefillFcOutSplit, kHeads));
         hip_check(hipMalloc(&pre_part_, sizeof(float) * kHidden * (size_t)m * kz), "hipMalloc(prefill)");
         // W8A8 operands in the matrix-core order: rows padded to 16 (the padding rows are
         // read by the GEMMs and never stored; zeroed once)
@@ -806,7 +805,6 @@ void Model::prefill(const int32_t *rows, int n, int start) {
     // the GEMMs read their inputs in the matrix-core order, written so by the kernel
     // before: int8 + block scales under W8A8, fp16 hi / lo halves under A16
     uint8_t *a_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_a_);
-    uint8_t *o_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_o_);
     uint8_t *h_hl = a8 ? nullptr : reinterpret_cast<uint8_t *>(pre_h_);
     hip_check(launch_ln_rows(pre_x_, kHidden, g_[0].ln1_w, g_[0].ln1_b, cap_f(0, 1), m, s, nullptr, q8, d8, a_hl),
               "prefill ln1");
@@ -823,19 +821,20 @@ void Model::prefill(const int32_t *rows, int n, int start) {
         hip_check(launch_gemm(q, EPI_QKV, kvt_, s), "prefill qkv");
         AttnArgs t;
         t.q = pre_q_; t.k_pool = q.k_pool; t.v_pool = q.v_pool; t.page_size = max_ctx_;
-        t.pos0 = start; t.rows = m; t.max_keys = start + m; t.out_hl = o_hl;
-        t.q8 = q8; t.d8 = d8;
+        t.pos0 = start; t.rows = m; t.max_keys = start + m;
         t.out = cap_f(l, 2);
+        // the attention applies proj itself: each head's tile writes split-K partial h (12
+        // partials, reduced in head order with the bias and the residual below)
+        t.proj_w = L.proj_wm ? L.proj_wm : L.proj_w; t.proj_tiled = L.proj_wm ? 1 : 0;
+        t.proj_part = pre_part_; t.proj_a8 = a8 ? 1 : 0;
+        if (cap) {  // the int8 operand, for the capture only
+            t.q8 = q8; t.d8 = d8;
+        }
         hip_check(launch_attn_tiles(t, kvt_, s), "prefill attention");
         cap_copy_q(l, 1, pre_q8_, pre_d8_);
-        GemmArgs p;  // split-K partials, reduced with the residual and LN2 by the next kernel
-        p.w = L.proj_w; p.wm = L.proj_wm; p.N = kHidden; p.K = kHidden; p.a_hl = o_hl; p.lda = kHidden; p.M = m;
-        p.part = pre_part_; p.ksplit = gemm_ksplit(m, kHidden, kHidden);
-        operand(p);
-        hip_check(launch_gemm(p, EPI_PART, kvt_, s), "prefill proj");
-        hip_check(launch_resid_ln_rows(pre_part_, p.ksplit, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
+        hip_check(launch_resid_ln_rows(pre_part_, kHeads, m, L.proj_b, pre_x_, kHidden, pre_x_, L.ln2_w, L.ln2_b,
                                        cap_f(l, 4), nullptr, s, q8, d8, a_hl),
-                  "prefill proj reduce + ln2");
+                  "prefill attention + proj reduce + ln2");
         cap_copy_x(l, 3);
         cap_copy_q(l, 2, pre_q8_, pre_d8_);
         GemmArgs f1;

@@ -27,6 +27,9 @@ constexpr int kRopeHalf = kHeadDim / 2;
 // then 4 x 32 int8 (row k at byte 8 + 32k): 136 bytes per block
 // (reference csrc/src/quant.cpp:56-65, tools/export_weights.py:160-179).
 constexpr int kBlockBytes = 136;
+// a weight matrix in the matrix-core order (the GEMMs' copy): one unit per 16 rows and scale
+// block, the 512 quants in MFMA lane order then the 16 rows' fp16 scales
+constexpr int kTileBytes = 544;
 
 constexpr int kWave = 64;
 
@@ -215,6 +218,39 @@ __device__ __forceinline__ float q8x4_elem(const uint8_t *w, int nb, int r, int 
 // the lowest index winning ties; kCodebook when every value is NaN (the caller
 // maps that to 0, where the reference's scan stays).  bv / bi: 4 LDS slots.
 // The loads (issued first, so later loads do not delay them) and the reduction.
+// MFMA operand vectors
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+
+// int8 -> fp16, exactly: the half with bits 0x64 : (q ^ 0x80) is 1024 + (q + 128),
+// built two at a time with v_perm_b32; subtracting 1152 leaves q.
+__device__ __forceinline__ half8 i8x8_to_h8(uint2 q) {
+    const uint32_t a = q.x ^ 0x80808080u, b = q.y ^ 0x80808080u;
+    const uint32_t w[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
+                           __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
+    const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    half8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v v = __builtin_bit_cast(half2v, w[i]) - bias;
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+// Workgroup barrier for LDS traffic only: each wave waits for its own LDS operations, not
+// for its global loads in flight (__syncthreads() orders global memory too, so it waits for
+// every outstanding load -- a weight prefetch included -- before the barrier).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 struct PickIn {
     float vals[kCodebook / 256];
     int cnt[kCodebook / 256];

@@ -106,6 +106,16 @@ struct AttnArgs {
     // for the next GEMM's a_hl, instead of out (no split-KV or sliced launches)
     uint8_t *out_hl = nullptr;
     const DevState *state = nullptr;
+    // prefill tiles (launch_attn_tiles): proj applied to the tile's output in the same launch.
+    // proj_w is the proj matrix (768 x 768), in the matrix-core order (544-byte units) when
+    // proj_tiled, else Q8_0_4X4; head h's 64 columns of it times the head's output give
+    // split-K partial h, written to proj_part[(h * rows + m) * 768 + n] -- the reduce that
+    // follows sums the 12 partials in head order.  Under W8A8 (proj_a8) the operand is the
+    // output quantised per 32-block (the int8 copy q8 / d8 holds), else its fp16 hi / lo halves.
+    const uint8_t *proj_w = nullptr;
+    int proj_tiled = 0;
+    float *proj_part = nullptr;
+    int proj_a8 = 0;
     // single row, long context: the keys are cut into `chunks` slices of 256 (one workgroup of
     // 4 waves each, more spans per wave past kMaxChunks); slices 1.. write their partial
     // (o[64], m, l) as LL words to chunk_part[(h * chunks + c) * kPartStride], and slice 0 of
