@@ -828,6 +828,7 @@ def main():
         return
     if args.mode == "attn64":
         print(json.dumps({"attention_paged_64": bench_attn64()}), flush=True)
+        calibration_copy()  # scales the byte counters of a counter pass over this mode
         return
     if args.mode == "handoff":
         print(json.dumps({"handoff": bench_handoff()}), flush=True)
