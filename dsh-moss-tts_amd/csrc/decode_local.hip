@@ -7,12 +7,13 @@
 // LL words (mh_ll.h), as in decode_layer.hip:
 //   Q  lpos 0 only, b < 144: LN1 + QKV of the block input (the global hidden
 //      state), RoPE, k/v into the local cache                  -> LL q|k|v
-//   P  b < 192: the step's input -- for lpos >= 2 the code of the previous
-//      channel, picked here (greedy: penalised argmax of its logits, or the
-//      forced code) or written by the sampler -- and its q|k|v: from the
-//      QKV stage (lpos 0) or from the precomputed row of (lpos, code); the
-//      local attention over keys 0..lpos (every workgroup computes all 12
-//      heads: at most 17 keys); proj + residual                -> LL x + attn
+//   A  b < 12: head h = b: the step's input -- for lpos >= 2 the code of the
+//      previous channel, picked here (greedy: penalised argmax of its logits,
+//      or the forced code) or written by the sampler -- and the head's q|k|v:
+//      from the QKV stage (lpos 0) or from the precomputed row of (lpos,
+//      code); k/v into the local cache; the head's attention over keys
+//      0..lpos (at most 17)                                    -> LL attn + code
+//   P  b < 192: proj + residual (the raw input row is aemb[ch][code]) -> LL x + attn
 //   M  b < 192: LN2 + fc_in + gelu_new                          -> LL h
 //   F  b < 192: fc_out + residual -> x_out (memory) and, with a head, LL x_out
 //   H  b < 64, with a head: local ln_f + the audio head GEMV   -> logits (memory)
