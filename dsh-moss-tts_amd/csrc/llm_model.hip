@@ -44,6 +44,9 @@ std::unordered_map<std::string, MossEntry> parse_moss_index(const uint8_t *blob,
         std::memcpy(&en.off, e + 64, 8);
         std::memcpy(&en.nbytes, e + 72, 8);
         if (en.off + en.nbytes > bytes) throw Status(MOSS_HIP_EFORMAT, std::string("tensor out of range: ") + name);
+        // the format aligns every tensor to 32 bytes; the kernels copy weight runs by
+        // 16-byte DMA, which needs it
+        if (en.off % 32) throw Status(MOSS_HIP_EFORMAT, std::string("tensor not 32-byte aligned: ") + name);
         out[name] = en;
     }
     return out;

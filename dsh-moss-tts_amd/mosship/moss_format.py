@@ -33,6 +33,7 @@ NVQ, CODEBOOK, AUDIO_PAD, SLOT, END = 16, 1024, 1024, 9, 7
 MAX_CTX, LOCAL_LEN, LAYERS = 768, 17, 12
 
 DT_F16, DT_Q8_0, DT_Q4_0, DT_F32, DT_Q8X4, DT_Q4X4 = 0, 1, 2, 3, 4, 5
+DATA_ALIGN = 32  # payload alignment of every tensor (tools/export_weights.py:32,254)
 BLOCK_BYTES = 136
 
 _FNV_OFFSET = 1469598103934665603
@@ -117,7 +118,7 @@ def write_moss(entries: list[tuple[str, int, int, int, bytes]]) -> bytes:
     table = bytearray()
     payload = bytearray()
     for name, dtype, rows, cols, blob in entries:
-        pad = (-(data_start + len(payload))) % 32
+        pad = (-(data_start + len(payload))) % DATA_ALIGN
         payload += b"\x00" * pad
         offset = data_start + len(payload)
         nb = name.encode("ascii")
@@ -145,6 +146,8 @@ def read_moss_index(blob: bytes) -> dict[str, tuple[int, int, int, int, int]]:
         off, nbytes = struct.unpack_from("<QQ", blob, base + 64)
         if off + nbytes > len(blob):
             raise ValueError(f"tensor out of range: {name}")
+        if off % DATA_ALIGN:  # the exporter pads every tensor to it; the GPU loader requires it
+            raise ValueError(f"tensor not {DATA_ALIGN}-byte aligned: {name}")
         out[name] = (dtype, d0, d1, off, nbytes)
     return out
 

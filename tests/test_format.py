@@ -66,3 +66,19 @@ def test_missing_tensor_rejected(oracle):
     blob = mf.synth_model(2, drop="g3.proj.b")
     with pytest.raises(RuntimeError, match="g3.proj.b"):
         oracle.model(blob)
+
+
+def test_misaligned_tensor_rejected(golden_model):
+    """Every tensor of a .moss file sits on a 32-byte boundary (the exporter pads to it,
+    tools/export_weights.py:254); an index entry moved off it is rejected."""
+    blob, _ = golden_model
+    mf.read_moss_index(blob)
+    bad = bytearray(blob)
+    n = int.from_bytes(bad[8:12], "little")
+    for i in range(n):
+        e0 = 16 + 80 * i
+        if bytes(bad[e0:e0 + 48]).rstrip(b"\0") == b"g5.fc_in.w":
+            off = int.from_bytes(bad[e0 + 64:e0 + 72], "little")
+            bad[e0 + 64:e0 + 72] = (off + 4).to_bytes(8, "little")
+    with pytest.raises(ValueError, match="aligned"):
+        mf.read_moss_index(bytes(bad))

@@ -301,6 +301,17 @@ def test_model_errors(torch_gpu, golden_model):
     with pytest.raises(lib.MossHipError) as e:
         HipLLM(mf.synth_model(3, drop="g5.fc_in.b"))
     assert e.value.code == lib.EFORMAT and "g5.fc_in.b" in str(e.value)
+    # a tensor off the format's 32-byte alignment (its offset moved by 4 bytes)
+    shifted = bytearray(blob)
+    n = int.from_bytes(shifted[8:12], "little")
+    for i in range(n):
+        e0 = 16 + 80 * i
+        if bytes(shifted[e0:e0 + 48]).rstrip(b"\0") == b"g5.fc_in.w":
+            off = int.from_bytes(shifted[e0 + 64:e0 + 72], "little")
+            shifted[e0 + 64:e0 + 72] = (off + 4).to_bytes(8, "little")
+    with pytest.raises(lib.MossHipError) as e:
+        HipLLM(bytes(shifted))
+    assert e.value.code == lib.EFORMAT and "aligned" in str(e.value)
     g = HipLLM(blob)
     bad = np.full((2, 17), 2000, np.int32)
     with pytest.raises(lib.MossHipError) as e:
