@@ -350,6 +350,19 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
         return hipGetLastError();
     }
     const dim3 grid(a.heads, a.rows);
+    if (a.rows == 1 && a.page_table == nullptr && spans > 2) {
+        // one query row (the single-query operator): one workgroup per head, a wave per
+        // 64-key span (every K/V load in flight at once), merged in LDS -- no hand-off
+        // between workgroups; fp32 caches at most 8 waves (their span needs ~170 VGPRs)
+        if (spans <= 4)
+            hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false>), grid, dim3(256), 0, s, a);
+        else if (KV == KV_F32 || spans <= 8)
+            hipLaunchKernelGGL((attn_rows_kernel<KV, 8, false>), grid, dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL((attn_rows_kernel<KV, KV == KV_F16 ? 16 : 8, false>), grid, dim3(KV == KV_F16 ? 1024 : 512), 0,
+                               s, a);
+        return hipGetLastError();
+    }
     if (spans <= 1)
         hipLaunchKernelGGL((attn_rows_kernel<KV, 1, false>), grid, dim3(64), 0, s, a);
     else if (KV == KV_F16 && a.page_table != nullptr)  // the batch engine's paged fp16 caches

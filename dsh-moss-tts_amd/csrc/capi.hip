@@ -493,7 +493,9 @@ void attn_decode(const float *q, const void *k_cache, const void *v_cache, int k
     a.out_f16 = out_dtype == MOSS_HIP_F16;
     const auto kv = kv_dtype == MOSS_HIP_F32 ? mh::KV_F32 : mh::KV_F16;
     const int spans = (n_keys + 63) / 64;
-    if (spans > mh::kOneWgSpans) {  // slices of kSliceWaves spans across workgroups
+    // one workgroup per head (a wave per span) up to kOneWgSpans spans; fp32 caches up to 8
+    const int one_wg = kv == mh::KV_F16 ? mh::kOneWgSpans : std::min(mh::kOneWgSpans, 8);
+    if (spans > one_wg) {  // slices of kSliceWaves spans across workgroups
         uint8_t *sc = scratch_of(static_cast<hipStream_t>(stream), heads);
         const int chunks = (spans + mh::kSliceWaves - 1) / mh::kSliceWaves;
         a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;

@@ -141,7 +141,7 @@ constexpr size_t chunk_scratch_bytes(int heads) {
 #define MH_SLICE_WAVES 4
 #endif
 #ifndef MH_ONE_WG_SPANS
-#define MH_ONE_WG_SPANS 4
+#define MH_ONE_WG_SPANS 8
 #endif
 // single-row slices: waves per slice workgroup (one 64-key span each); the keys
 // stay in one workgroup up to kOneWgSpans spans
