@@ -61,7 +61,12 @@ void frame_trampoline(void *user, int frame, const int32_t row[17]) {
 LlmModel::LlmModel(int threads) { (void)threads; }
 
 LlmModel::~LlmModel() {
-    if (h_) moss_hip_llm_destroy(h_);
+    if (!h_) return;
+    // MOSS_HIP_REPORT set: one JSON line on stderr with the model's count of fused launches
+    // redone on the per-operator path (co-residency lost at run time, e.g. to another stream)
+    if (const char *r = std::getenv("MOSS_HIP_REPORT"); r && *r && std::strcmp(r, "0") != 0)
+        std::fprintf(stderr, "{\"moss_hip_fallbacks\": %d}\n", moss_hip_llm_fallbacks(h_));
+    moss_hip_llm_destroy(h_);
 }
 
 void LlmModel::require_loaded() const {

@@ -12,8 +12,9 @@
 //
 // usage: engine_{gpu,cpu} LLM.moss DECODER.moss TOKENIZER.mossvocab WORKDIR TEXT SEED GREEDY MAX_FRAMES
 // writes WORKDIR/run{1,2,3}.pcm (interleaved float32: the codec's output of the LLM's
-// codes, frame by frame) and prints one JSON line per run.
+// codes, frame by frame) and prints one JSON line per run (with its wall time, "ms").
 #include <atomic>
+#include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -88,16 +89,18 @@ int main(int argc, char **argv) {
             if (run == 3) cancel.store(true);
         };
         moss::SynthStats st;
+        const auto t0 = std::chrono::steady_clock::now();
         if (!engine.synthesize(text, so, &st, &err)) {
             std::fprintf(stderr, "synthesize: %s\n", err.c_str());
             return 1;
         }
+        const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         const std::string base = workdir + "/run" + std::to_string(run);
         if (!write_file(base + ".pcm", pcm.data(), pcm.size() * sizeof(float))) return 1;
         std::printf("{\"run\": %d, \"chunks\": %d, \"text_tokens\": %d, \"frames\": %d, \"samples\": %zu, "
-                    "\"prefix_cache_hit\": %s, \"cancelled\": %s}\n",
+                    "\"prefix_cache_hit\": %s, \"cancelled\": %s, \"ms\": %.2f}\n",
                     run, st.chunks, st.text_tokens, st.frames, pcm.size() / 2, st.prefix_cache_hit ? "true" : "false",
-                    st.cancelled ? "true" : "false");
+                    st.cancelled ? "true" : "false", ms);
         std::fflush(stdout);
     }
     return 0;

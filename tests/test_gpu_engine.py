@@ -59,6 +59,10 @@ def run_engine(exe, weights, workdir, seed, greedy, frames, env_extra):
     assert p.returncode == 0, p.stderr[-2000:]
     runs = [json.loads(ln) for ln in p.stdout.splitlines() if ln.startswith('{"run"')]
     assert [r["run"] for r in runs] == [1, 2, 3]
+    # the GPU drop-in's count of fused launches redone per operator (MOSS_HIP_REPORT=1)
+    fb = [json.loads(ln)["moss_hip_fallbacks"] for ln in p.stderr.splitlines() if ln.startswith('{"moss_hip_fallbacks"')]
+    for r in runs:
+        r["fallbacks"] = fb
     pcm = [np.fromfile(os.path.join(workdir, f"run{i}.pcm"), np.float32) for i in (1, 2, 3)]
     return runs, pcm
 
@@ -90,11 +94,19 @@ def test_engine_release_mode(torch_gpu, weights, tmp_path):
 def test_engine_gpu_codec_matches_cpu(torch_gpu, weights, tmp_path):
     """Both drop-ins (A16 mode, so the codes are the CPU engine's): the engine's runs
     match the CPU engine's, and the PCM from the GPU codec matches the reference codec's
-    to <= 1e-3 (max |diff| / max |pcm| per run; the measured error is printed)."""
+    to <= 1e-3 (max |diff| / max |pcm| per run; the measured error is printed).  The GPU
+    LLM's fused launches share the GPU with the codec's graphs here: the drop-in reports
+    how many it had to redo per operator (co-residency lost), and each run's wall time
+    is printed beside the CPU engine's."""
     if not os.path.exists(os.path.join(REF_DIR, "engine_gpu_codec")):
         pytest.skip("oracle/_ref/engine_gpu_codec not built")
-    gr, gp = run_engine("engine_gpu_codec", weights, str(tmp_path / "gpuc"), 0, True, 8, ENV)
+    gr, gp = run_engine("engine_gpu_codec", weights, str(tmp_path / "gpuc"), 0, True, 8,
+                        dict(ENV, MOSS_HIP_REPORT="1"))
     cr, cp = run_engine("engine_cpu", weights, str(tmp_path / "cpu"), 0, True, 8, ENV)
+    for g, c in zip(gr, cr):
+        print(f"run {g['run']}: {g['frames']} frames, GPU LLM + GPU codec {g['ms']:.1f} ms, "
+              f"CPU engine {c['ms']:.1f} ms; fused-launch fallbacks {g['fallbacks']}", flush=True)
+    assert len(gr[0]["fallbacks"]) == 1  # one LLM per engine, reported at its destruction
     _compare(gr, gp, cr, cp, 8, exact=False)
     for i in range(3):
         assert gp[i].shape == cp[i].shape
