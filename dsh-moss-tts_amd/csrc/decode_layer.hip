@@ -151,6 +151,13 @@ __device__ __forceinline__ float rawk(const SpanRaw<KV> &r, int c, int e) {  // 
     }
 }
 
+// Stages Q and M (one wave per 4-row group) read their weights from LDS, copied in by
+// wave 3 a stage ahead (Q's at the end of the previous block, M's at the end of stage P);
+// the gathers before them are waves 0..2's, so none of their polls completes behind a
+// copy (at the first, 0.1753 -> 0.1720 ms per global step)
+using QStage = LdsGemvStage<6, kHidden>;
+constexpr int kDmaWave = 3;
+
 // A8: every GEMV in W8A8 (the activation quantised per 32-block in LDS, quant_act_lds),
 // the reference's decode with MOSS_A16 unset (csrc/src/gemv.cpp:23-48,245-274).
 template <int KV, bool A8>
@@ -167,6 +174,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
     __shared__ float4 po[4][16];
     __shared__ float pm[4], pl[4];
     __shared__ float part[4][4];
+    __shared__ __attribute__((aligned(16))) uint8_t wq_lds[QStage::kBytes];  // stage Q's weights
+    __shared__ __attribute__((aligned(16))) uint8_t wm_lds[QStage::kBytes];  // stage M's
 
     __shared__ int wait_failed;  // set when a wait of this workgroup runs out
     if (threadIdx.x == 0) wait_failed = 0;
@@ -177,6 +186,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
     const int pos = g.state->pos;
     const int t = threadIdx.x;
     const int b = blockIdx.x;
+    if (b < kAttnBase && (t >> 6) == kDmaWave) QStage::issue_wave(g.layers[0].attn_w, b, wq_lds);
     int budget = g.poll_budget > 0 ? g.poll_budget : kPollBudget;
     uint64_t *LL = g.ll;
 
@@ -209,10 +219,6 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
         __syncthreads();
     }
 
-    // stage Q's weight prefetch, reissued at every block's start (declared out here:
-    // with the attention workgroups' input skip below, 0.176 -> 0.1735 ms per step,
-    // against 0.175 declared inside the loop)
-    GemvStage<1, 6, kHidden> gq;
     QkvEpi eq;
     int rq = 0;
 #pragma unroll 1
@@ -230,7 +236,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
         // spans (stage A).  (Requesting stage Q's a block ahead, during stage F,
         // measured 0.178 -> 0.188 ms per step.)
         if (b < kAttnBase) {
-            gq.prefetch(a.attn_w, b);
+            QStage gq;
+            gq.setup(b, wq_lds);
             rq = gq.row();
             if (gq.storer()) eq.load(a.attn_b, a.rope_cos, a.rope_sin, rq, pos);
         }
@@ -279,7 +286,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
         // the residuals of their 4 proj rows, which stage P polls
         if (layer > 0 && !attn_wg) {
             const uint32_t prev = ((uint32_t)(pos + 1) << 5) | (uint32_t)(layer - 1);
-            const bool ok = ll_gather<3>(LL + kLLO, kHidden, prev, xin, budget);
+            // waves 0..2: wave 3's loads end with the copy of this block's QKV weights
+            const bool ok = wave == kDmaWave || ll_gather_by<4, 192>(LL + kLLO, kHidden, prev, xin, budget, t);
             if (sync_failed(!ok, &wait_failed)) {
                 if (t == 0) atomicOr(g.err, 1u);
                 return;
@@ -289,7 +297,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
 
         // ---- stage Q: LN1 + QKV, one wave per group
         if (b < kAttnBase) {
-            const GemvStage<1, 6, kHidden> &gs = gq;
+            QStage gs;
+            gs.setup(b, wq_lds);
             const int r = rq;
             const QkvEpi &e = eq;
             float o[3], lw[3], lb[3];
@@ -316,7 +325,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 }
             }
             STAGE_TS(1);
-            const float yv = gs.template dot<A8>(act, part, da);
+            const float yv = gs.template dot<A8>(act, da);
             const float partner = xshfl<4>(yv);
             if (gs.storer()) {  // bias, RoPE (llm.cpp:234-236), KV write (llm.cpp:224-225)
                 float out = e.apply(r, yv, partner);
@@ -590,6 +599,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             }
             STAGE_TS(7);
             const float yv = gs.template dot<A8>(act, part, da);
+            // stage M's weights, after this wave's last read of them a block ago (barriers since)
+            if (wave == kDmaWave) QStage::issue_wave(a.fc_in_w, b, wm_lds);
             if (gs.storer()) {
                 ll_put(LL + kLLX + r, eres + (yv + eb), tag);  // llm.cpp:239
                 if constexpr (A8)
@@ -600,8 +611,8 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
 
         // ---- stage M: LN2 + fc_in + gelu_new, one wave per group, every workgroup
         {
-            GemvStage<1, 6, kHidden> gs;
-            gs.prefetch(a.fc_in_w, b);
+            QStage gs;
+            gs.setup(b, wm_lds);
             const int r = gs.row();
             const float eb = gs.storer() ? a.fc_in_b[r] : 0.0f;
             float lw[3], lb[3];
@@ -610,7 +621,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 lw[i] = a.ln2_w[t + 256 * i];
                 lb[i] = a.ln2_b[t + 256 * i];
             }
-            const bool ok = ll_gather<3>(LL + kLLX, kHidden, tag, xm, budget);
+            const bool ok = wave == kDmaWave || ll_gather_by<4, 192>(LL + kLLX, kHidden, tag, xm, budget, t);
             if (sync_failed(!ok, &wait_failed)) {
                 if (t == 0) atomicOr(g.err, 1u);
                 return;
@@ -632,7 +643,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 }
             }
             STAGE_TS(10);
-            const float yv = gs.template dot<A8>(act, part, da);
+            const float yv = gs.template dot<A8>(act, da);
             if (gs.storer()) {
                 ll_put(LL + kLLH + r, gelu_new(yv + eb), tag);  // llm.cpp:243
                 if constexpr (A8)
@@ -670,6 +681,10 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             }
             STAGE_TS(13);
             if (layer == kLayers - 2) STAGE_TS(15);
+            // the next block's QKV weights, after this wave's last use of stage Q's (barriers
+            // since) and behind no gather of its own: the block-input gather is waves 0..2's
+            if (wave == kDmaWave && b < kAttnBase && layer + 1 < kLayers)
+                QStage::issue_wave(g.layers[layer + 1].attn_w, b, wq_lds);
         }
 
     }  // layer

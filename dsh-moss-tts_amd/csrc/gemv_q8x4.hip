@@ -412,8 +412,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-typedef __attribute__((address_space(3))) void *lds_ptr;
-
 #ifndef MH_STREAM_CPOL
 #define MH_STREAM_CPOL 2  // non-temporal: the weights are read once per pass
 #endif

@@ -31,6 +31,9 @@ constexpr int kBlockBytes = 136;
 // block, the 512 quants in MFMA lane order then the 16 rows' fp16 scales
 constexpr int kTileBytes = 544;
 
+// LDS pointer type of the direct global -> LDS loads (__builtin_amdgcn_global_load_lds)
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
 constexpr int kWave = 64;
 
 // Device-resident decode state, read by every kernel of a captured step so the

@@ -95,6 +95,79 @@ __device__ __forceinline__ float row_lane_sum(float acc) {
     return acc;
 }
 
+// A GEMV stage of a fused launch whose weights wait in LDS: GemvStage's rows,
+// lanes and summation order, but the workgroup's rows of the stage (one contiguous
+// run of 4-row groups, kBytes) are copied into LDS by direct DMA (global_load_lds,
+// 16 bytes per lane), issued by one wave a stage or more ahead.  Loads complete in
+// issue order per wave, so a gather by the other waves never waits behind the
+// copy; the copy must follow a workgroup barrier after the previous use's dot, and
+// dot() a __syncthreads() after the copy (its s_waitcnt vmcnt(0) completes it).
+template <int NB, int K>
+struct LdsGemvStage {
+    static constexpr int nb = K / 32, per = nb;
+    static constexpr int kGroupBytes = nb * kBlockBytes;
+    static constexpr int kBytes = 4 * kGroupBytes;  // a group per wave
+    static_assert(per <= 4 * NB && kGroupBytes % 16 == 0, "one batch per wave, whole chunks");
+    const uint8_t *base;
+    int g;
+
+    // the rows of workgroup b of w (16-byte aligned) into lds (kBytes, 16-byte aligned),
+    // by the calling wave alone
+    static __device__ __forceinline__ void issue_wave(const uint8_t *w, int b, uint8_t *lds) {
+        constexpr int chunks = kBytes / 16;
+        const int lane = tix() & 63;
+        const uint8_t *src = w + (size_t)b * kBytes;
+#pragma unroll
+        for (int i = 0; i < (chunks + 63) / 64; ++i)
+            if (64 * i + lane < chunks)
+                __builtin_amdgcn_global_load_lds((const void *)(src + 16 * (64 * i + lane)), (lds_ptr)(lds + 1024 * i), 16,
+                                                 0, 0);
+    }
+    __device__ __forceinline__ void setup(int b, const uint8_t *lds) {
+        const int wave = tix() >> 6;
+        g = 4 * b + wave;
+        base = lds + wave * kGroupBytes;
+    }
+    __device__ __forceinline__ int row() const { return 4 * g + ((tix() & 15) >> 2); }
+    __device__ __forceinline__ bool storer() const {
+        const int lane = tix() & 63;
+        return lane < 16 && (lane & 3) == 0;
+    }
+    // GemvStage<1, NB, K>::dot with the weights read from LDS (same order)
+    template <bool A8 = false>
+    __device__ __forceinline__ float dot(const float *act, const float *da = nullptr) const {
+        const int lane = tix() & 63, u = lane & 15, kk = u >> 2, j = u & 3;
+        const int first = lane >> 4;
+        float acc = 0.0f;
+#pragma unroll
+        for (int it = 0; it < NB; ++it) {
+            const int b = first + 4 * it;
+            if (b < per) {
+                const uint8_t *blk = base + b * kBlockBytes;
+                const uint2 q = *(const uint2 *)(blk + 8 + 8 * u);
+                const float dw = h2f(*(const uint16_t *)(blk + 2 * kk));
+                const float4 x0 = *(const float4 *)(act + b * 32 + 8 * j);
+                const float4 x1 = *(const float4 *)(act + b * 32 + 8 * j + 4);
+                float s = (float)(int8_t)(q.x) * x0.x;
+                s = fmaf((float)(int8_t)(q.x >> 8), x0.y, s);
+                s = fmaf((float)(int8_t)(q.x >> 16), x0.z, s);
+                s = fmaf((float)(int8_t)(q.x >> 24), x0.w, s);
+                s = fmaf((float)(int8_t)(q.y), x1.x, s);
+                s = fmaf((float)(int8_t)(q.y >> 8), x1.y, s);
+                s = fmaf((float)(int8_t)(q.y >> 16), x1.z, s);
+                s = fmaf((float)(int8_t)(q.y >> 24), x1.w, s);
+                if constexpr (A8) {
+                    const float scale = dw * da[b];
+                    acc = fmaf(s, scale, acc);
+                } else {
+                    acc = fmaf(s, dw, acc);
+                }
+            }
+        }
+        return row_lane_sum(acc);
+    }
+};
+
 // QKV epilogue of row r at position pos (llm.cpp:234-236): bias, then RoPE on
 // the q and k sections, which pairs row r with its neighbour r ^ 1 (the
 // partner's raw sum comes from the caller).  load() before the dot, apply()
