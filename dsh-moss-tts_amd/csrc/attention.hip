@@ -700,6 +700,8 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
         (!a.out && !a.part && !a.out_hl && !a.q8) ||
         !a.q || !a.k_pool || !a.v_pool)
         return hipErrorInvalidValue;
+    // a 64-key span is read from one page: paged caches need whole spans per page
+    if (a.page_table != nullptr && a.page_size % 64 != 0) return hipErrorInvalidValue;
     if (a.out_hl != nullptr && (a.part != nullptr || a.chunks != 0 || a.heads != kHeads)) return hipErrorInvalidValue;
     if (a.part != nullptr && (a.rows != 1 || a.page_table != nullptr)) return hipErrorInvalidValue;
     if (a.row_order != nullptr && (a.part != nullptr || a.chunks != 0)) return hipErrorInvalidValue;

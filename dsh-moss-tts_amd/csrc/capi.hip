@@ -535,6 +535,8 @@ int moss_hip_attn_paged(const float *q, const void *k_pool, const void *v_pool, 
         if (heads <= 0 || rows <= 0 || max_keys <= 0 || page_size <= 0 || table_stride <= 0 ||
             (long long)table_stride * page_size < max_keys)
             throw Status(MOSS_HIP_EINVAL, "need heads, rows, max_keys, page_size > 0 and table_stride * page_size >= max_keys");
+        if (page_size % 64 != 0)  // the kernel reads 64-key spans, each from one page
+            throw Status(MOSS_HIP_EINVAL, "page_size must be a multiple of 64");
         if ((kv_dtype != MOSS_HIP_F32 && kv_dtype != MOSS_HIP_F16) || (out_dtype != MOSS_HIP_F32 && out_dtype != MOSS_HIP_F16))
             throw Status(MOSS_HIP_EINVAL, "dtype must be MOSS_HIP_F32 or MOSS_HIP_F16");
         mh::AttnArgs a;

@@ -308,7 +308,8 @@ int moss_hip_attn_decode(const float *q, const void *k_cache, const void *v_cach
  * attention (csrc/batch_model.hip) on caller-owned pages.  Per row it is attention_core
  * (reference csrc/src/llm.cpp:189-217: scores q . k * 0.125, softmax, weighted sum of v); the
  * batch over streams and the paging have no reference counterpart (the reference decodes one
- * stream).  Pools are [page][heads][page_size][64] (kv_dtype MOSS_HIP_F16 or MOSS_HIP_F32); row
+ * stream).  Pools are [page][heads][page_size][64] (kv_dtype MOSS_HIP_F16 or MOSS_HIP_F32;
+ * page_size a multiple of 64, else MOSS_HIP_EINVAL: keys are read in 64-key spans); row
  * r is the query of stream row_stream[r] (r when row_stream is NULL) at position row_pos[r]
  * and attends that stream's keys 0 .. row_pos[r], whose j-th page of page_size positions is
  * page_table[stream * table_stride + j].  q: [rows][heads * 64] fp32 (RoPE applied); out:

@@ -95,3 +95,6 @@ def test_attn_paged_rejects_bad_arguments(torch_gpu):
     with pytest.raises(lib.MossHipError) as e:  # 2 pages of 64 cannot hold 200 keys
         lib.attn_paged(z.view(1, 768), z, z, 12, i, 2, 64, i, 200, z.view(1, 768))
     assert e.value.code == lib.EINVAL
+    with pytest.raises(lib.MossHipError) as e:  # a 64-key span would cross a page of 100
+        lib.attn_paged(z.view(1, 768), z, z, 12, i, 4, 100, i, 200, z.view(1, 768))
+    assert e.value.code == lib.EINVAL and "multiple of 64" in str(e.value)
