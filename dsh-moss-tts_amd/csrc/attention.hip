@@ -345,8 +345,10 @@ hipError_t launch_kv(const AttnArgs &a, hipStream_t s) {
         return hipGetLastError();
     }
     if (a.chunks > 0) {  // one row, slices of 4 spans merged by the last slice of each head
-        hipLaunchKernelGGL((attn_rows_kernel<KV, kSliceWaves, false, true>), dim3(a.heads, a.chunks),
-                           dim3(64 * kSliceWaves), 0, s, a);
+        if (a.chunk_waves == 2)
+            hipLaunchKernelGGL((attn_rows_kernel<KV, 2, false, true>), dim3(a.heads, a.chunks), dim3(128), 0, s, a);
+        else
+            hipLaunchKernelGGL((attn_rows_kernel<KV, 4, false, true>), dim3(a.heads, a.chunks), dim3(256), 0, s, a);
         return hipGetLastError();
     }
     const dim3 grid(a.heads, a.rows);
@@ -711,7 +713,8 @@ hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s) {
     if (a.chunks != 0 && (a.chunks < 0 || a.chunks > kMaxChunks || a.rows != 1 || a.part != nullptr ||
                           a.page_table != nullptr || a.row_pos != nullptr || a.q8 != nullptr ||
                           a.state != nullptr || !a.chunk_part || !a.chunk_gen ||
-                          kSliceWaves * 64 * (a.chunks - 1) >= a.max_keys))
+                          (a.chunk_waves != 2 && a.chunk_waves != 4) ||
+                          a.chunk_waves * 64 * (a.chunks - 1) >= a.max_keys))
         return hipErrorInvalidValue;
     return kv == KV_F16 ? launch_kv<KV_F16>(a, s) : launch_kv<KV_F32>(a, s);
 }

@@ -495,9 +495,10 @@ void attn_decode(const float *q, const void *k_cache, const void *v_cache, int k
     const int spans = (n_keys + 63) / 64;
     // one workgroup per head (a wave per span) up to kOneWgSpans spans; fp32 caches up to 8
     const int one_wg = kv == mh::KV_F16 ? mh::kOneWgSpans : std::min(mh::kOneWgSpans, 8);
-    if (spans > one_wg) {  // slices of kSliceWaves spans across workgroups
+    if (spans > one_wg) {  // slices of slice_waves(spans) spans across workgroups
         uint8_t *sc = scratch_of(static_cast<hipStream_t>(stream), heads);
-        const int chunks = (spans + mh::kSliceWaves - 1) / mh::kSliceWaves;
+        a.chunk_waves = mh::slice_waves(spans);
+        const int chunks = (spans + a.chunk_waves - 1) / a.chunk_waves;
         a.chunks = chunks < mh::kMaxChunks ? chunks : mh::kMaxChunks;
         a.chunk_gen = reinterpret_cast<uint32_t *>(sc);
         a.chunk_part = reinterpret_cast<uint64_t *>(sc + mh::kChunkHeader);

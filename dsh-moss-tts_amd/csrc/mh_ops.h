@@ -116,8 +116,9 @@ struct AttnArgs {
     int proj_tiled = 0;
     float *proj_part = nullptr;
     int proj_a8 = 0;
-    // single row, long context: the keys are cut into `chunks` slices of 256 (one workgroup of
-    // 4 waves each, more spans per wave past kMaxChunks); slices 1.. write their partial
+    // single row, long context: the keys are cut into `chunks` slices of 64 * chunk_waves
+    // keys (one workgroup of chunk_waves waves each, one 64-key span per wave, more spans
+    // per wave past kMaxChunks); slices 1.. write their partial
     // (o[64], m, l) as LL words to chunk_part[(h * chunks + c) * kPartStride], and slice 0 of
     // each head waits for them, merges all in slice order and writes the output.  The words
     // carry a tag made from the launch generation chunk_gen[0], which every workgroup reads at
@@ -126,6 +127,7 @@ struct AttnArgs {
     // replays included) never share a tag, and a partial left by a launch whose merge gave up
     // is never read as current.  Both words start at zero.
     int chunks = 0;
+    int chunk_waves = 4;  // 2 or 4
     uint64_t *chunk_part = nullptr;
     uint32_t *chunk_gen = nullptr;
 };
@@ -137,16 +139,13 @@ constexpr int kMaxChunks = 64;
 constexpr size_t chunk_scratch_bytes(int heads) {
     return kChunkHeader + sizeof(uint64_t) * (size_t)heads * kMaxChunks * kPartStride;
 }
-#ifndef MH_SLICE_WAVES
-#define MH_SLICE_WAVES 4
-#endif
 #ifndef MH_ONE_WG_SPANS
 #define MH_ONE_WG_SPANS 8
 #endif
-// single-row slices: waves per slice workgroup (one 64-key span each); the keys
-// stay in one workgroup up to kOneWgSpans spans
-constexpr int kSliceWaves = MH_SLICE_WAVES;
+// single-row attention: the keys stay in one workgroup up to kOneWgSpans 64-key spans;
+// past that, slices of slice_waves(spans) waves (one span each), about 8 slices per head
 constexpr int kOneWgSpans = MH_ONE_WG_SPANS;
+constexpr int slice_waves(int spans) { return spans <= 16 ? 2 : 4; }
 hipError_t launch_attn(const AttnArgs &a, KvType kv, hipStream_t s);
 // The prefill's form on the matrix cores: 16 rows x one head per workgroup, rows r at
 // positions pos0 + r of one cache page (no page table, per-row positions or split output).

@@ -296,7 +296,8 @@ int moss_hip_dequant_rows_q8x4(const void *w, int mat_rows, int cols, const int3
  * q [heads*64] fp32 (post-RoPE); k_cache/v_cache [heads][ctx_stride][64] of kv_dtype; the
  * first n_keys positions are attended.  out [heads*64] of out_dtype.  Up to 512 keys one
  * workgroup per head attends them (a wave per 64 keys, merged in LDS); past 512 the keys are
- * cut into slices of 256 (at most 64 per head) attended by separate workgroups and merged by
+ * cut into slices of 128 keys (up to 1,024 keys) or 256 (at most 64 slices per head)
+ * attended by separate workgroups and merged by
  * the first slice of each head (log-sum-exp, slice order); the partials live in a scratch block
  * the library allocates once per (device, stream) on the first call on that stream (which must
  * not be under graph capture), so calls on one stream are ordered and calls on different
