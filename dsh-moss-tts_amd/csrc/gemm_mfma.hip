@@ -390,7 +390,7 @@ __device__ __forceinline__ float2 ln_rows_from_stats(const GemmArgs &g, int m_ba
 }
 
 // WV: waves per workgroup, 4, or 8 for a long K with the residual epilogue (fc_out, K = 3072:
-// 3 blocks per wave, so the sum needs no second kernel); waves 4..7 only contribute partials.
+// 12 blocks per wave, so the sum needs no second kernel); waves 4..7 only contribute partials.
 template <int EPI, int KV, int NT, bool A8, bool LN, bool TL, bool AT, int WV = 4>
 __global__ __launch_bounds__(64 * WV) void gemm_wk_kernel(GemmArgs g) {
 #pragma clang fp contract(off)
@@ -710,8 +710,9 @@ hipError_t launch_nt(const GemmArgs &g, hipStream_t s) {
     const int mt = (g.M + 15) / 16;
     if constexpr (EPI == EPI_RESID && !LN) {
         // a long K (fc_out, K = 3072) in one workgroup of 8 waves, 16 columns a tile: each wave
-        // takes 3 blocks and the residual epilogue completes the rows (no split-K reduce)
-        // (32-column tiles, half the workgroups: 64 streams 56.4k -> 54.4k frames/s)
+        // takes 12 blocks (4 chunks of 3) and the residual epilogue completes the rows (no
+        // split-K reduce) (32-column tiles, half the workgroups: 64 streams 56.4k -> 54.4k
+        // frames/s; 16 waves of 6 blocks: 56.66k -> 56.59k)
         if (g.K >= 2048) {
             hipLaunchKernelGGL((gemm_wk_kernel<EPI, KV, 1, A8, LN, TL, AT, 8>), dim3(g.N / 16, mt, 1), dim3(512), 0, s,
                                g);
