@@ -15,21 +15,21 @@ TOL = 1e-3
 PAGE = 64
 
 
-def _case(rng, keys, heads, npdt):
-    """Pools [page][heads][PAGE][64] holding each stream's keys on shuffled pages, the table,
+def _case(rng, keys, heads, npdt, page=PAGE):
+    """Pools [page][heads][page][64] holding each stream's keys on shuffled pages, the table,
     and the rows [n][heads * 64] of K and V each stream holds (as the pool stores them)."""
     streams = len(keys)
-    per = (max(keys) + PAGE - 1) // PAGE
+    per = (max(keys) + page - 1) // page
     n_pages = streams * per + 3  # a few pages nobody owns
     perm = rng.permutation(n_pages)[: streams * per].reshape(streams, per).astype(np.int32)
-    kp = rng.standard_normal((n_pages, heads, PAGE, 64)).astype(npdt)
-    vp = rng.standard_normal((n_pages, heads, PAGE, 64)).astype(npdt)
+    kp = rng.standard_normal((n_pages, heads, page, 64)).astype(npdt)
+    vp = rng.standard_normal((n_pages, heads, page, 64)).astype(npdt)
     kr, vr = [], []
     for s, n in enumerate(keys):
         pos = np.arange(n)
-        pg = perm[s, pos // PAGE]
-        kr.append(kp[pg, :, pos % PAGE, :].reshape(n, heads * 64).astype(np.float32))
-        vr.append(vp[pg, :, pos % PAGE, :].reshape(n, heads * 64).astype(np.float32))
+        pg = perm[s, pos // page]
+        kr.append(kp[pg, :, pos % page, :].reshape(n, heads * 64).astype(np.float32))
+        vr.append(vp[pg, :, pos % page, :].reshape(n, heads * 64).astype(np.float32))
     return kp, vp, perm, per, kr, vr
 
 
@@ -98,3 +98,21 @@ def test_attn_paged_rejects_bad_arguments(torch_gpu):
     with pytest.raises(lib.MossHipError) as e:  # a 64-key span would cross a page of 100
         lib.attn_paged(z.view(1, 768), z, z, 12, i, 4, 100, i, 200, z.view(1, 768))
     assert e.value.code == lib.EINVAL and "multiple of 64" in str(e.value)
+
+
+def test_attn_paged_pages_of_128(torch_gpu, oracle):
+    """Pages of 128 positions: each page holds two 64-key spans, at offsets 0 and 64."""
+    torch = torch_gpu
+    rng = np.random.default_rng(128)
+    keys = [1, 64, 65, 127, 128, 129, 255, 256, 257, 600, 1000]
+    kp, vp, table, per, kr, vr = _case(rng, keys, 12, np.float16, page=128)
+    rows = len(keys)
+    row_pos = np.array([n - 1 for n in keys], np.int32)
+    q = rng.standard_normal((rows, 768)).astype(np.float32)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = torch.full((rows, 768), float("nan"), dtype=torch.float32, device="cuda")
+    lib.attn_paged(dev(q), dev(kp), dev(vp), 12, dev(table), per, 128, dev(row_pos), max(keys), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        assert max_rel(got[r], oracle.attention(kr[r], vr[r], q[r])) <= TOL, (r, keys[r])
