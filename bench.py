@@ -39,7 +39,8 @@ past every window; ms/frame and the real-time factor, 80 ms of audio per frame)
 is reported beside the reference AudioDecoder on min(6, share) host threads.
 
 The same frames with an fp32 KV cache (the reference's precision) are timed as well
-(decode_kv_fp32).  --mode gemm64 runs the 64-stream engine's GEMM shapes (M = 64) through
+(decode_kv_fp32), and the W8A8 decode from the same state (decode_w8a8: the reference's
+decode when MOSS_A16 is unset).  --mode gemm64 runs the 64-stream engine's GEMM shapes (M = 64) through
 the operator ABI eagerly, for hardware-counter passes; --mode mall runs global steps warm and
 with a 1 GiB sweep before each (Infinity Cache residency of the weights, A/B); --mode handoff
 times a cross-workgroup hand-off of 4-64 KB per workgroup inside one launch (LL words, fenced
@@ -87,13 +88,14 @@ def make_state(seed: int = 2024):
     return k, v, hidden, rows
 
 
-def bench_decode(blob, state, steps, warmup, kv_fp32: bool = False):
-    """The headline frame loop (fp16 KV), or with kv_fp32 the reference's own KV precision."""
+def bench_decode(blob, state, steps, warmup, kv_fp32: bool = False, a8: bool = False):
+    """The headline frame loop (fp16 KV), or with kv_fp32 the reference's own KV precision, or
+    with a8 the W8A8 decode (the reference's with MOSS_A16 unset)."""
     import torch
 
     from mosship import HipLLM, SampleParams
     k, v, hidden, _ = state
-    m = HipLLM(blob, device=0, kv_fp32=kv_fp32)
+    m = HipLLM(blob, device=0, kv_fp32=kv_fp32, decode_a8=a8)
     m.kv_import(k, v, hidden)
     m.snapshot_prefix()
     p = SampleParams.make(greedy=True, min_frames=max(steps, warmup))
@@ -860,6 +862,8 @@ def main():
         return
     log("decode, fp32 KV")
     d32 = bench_decode(blob, state, args.steps, args.warmup, kv_fp32=True)
+    log("decode, W8A8")
+    da8 = bench_decode(blob, state, args.steps, args.warmup, a8=True)
     log("gemv roofline")
     g = bench_gemv()
     log("decode attention")
@@ -925,6 +929,11 @@ def main():
                            "global_step_ms": round(d32["global_ms_event"], 4),
                            "local_ms_per_frame": round(d32["local_ms_event"], 4),
                            "note": "the same frames with an fp32 KV cache, the reference's own KV precision"},
+        "decode_w8a8": {"ms_per_frame": round(da8["ms_per_frame"], 4),
+                        "global_step_ms": round(da8["global_ms_event"], 4),
+                        "local_ms_per_frame": round(da8["local_ms_event"], 4),
+                        "note": "W8A8 decode (int8 activations, the reference's decode with MOSS_A16 unset), "
+                                "fp16 KV, from the same state; its codes differ from the W8A16 run's"},
         "roofline": dom,
         "roofline_decode": roof,
         "roofline_gemv": gemv_roof,

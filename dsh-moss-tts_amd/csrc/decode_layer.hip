@@ -316,8 +316,9 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_XIN, xin, kHidden);
                     cap_copy(cp + MOSS_HIP_CAP_LN1, act, kHidden);
+                    __syncthreads();  // before the quantiser rewrites runs other threads copy
                 }
-                quant_act_lds(act, da, kHidden);
+                quant_act_lds_k<kHidden>(act, da);
                 __syncthreads();
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_LN1_Q, act, kHidden);
@@ -589,8 +590,11 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             }
             if constexpr (A8) {
                 float *cp = b == 0 ? cap : nullptr;
-                if (cp) cap_copy(cp + MOSS_HIP_CAP_ATT, act, kHidden);
-                quant_act_lds(act, da, kHidden);
+                if (cp) {  // a barrier before the quantiser rewrites runs other threads copy
+                    cap_copy(cp + MOSS_HIP_CAP_ATT, act, kHidden);
+                    __syncthreads();
+                }
+                quant_act_lds_k<kHidden>(act, da);
                 __syncthreads();
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_ATT_Q, act, kHidden);
@@ -634,8 +638,11 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
             __syncthreads();
             if constexpr (A8) {
                 float *cp = b == 0 ? cap : nullptr;
-                if (cp) cap_copy(cp + MOSS_HIP_CAP_LN2, act, kHidden);
-                quant_act_lds(act, da, kHidden);
+                if (cp) {  // a barrier before the quantiser rewrites runs other threads copy
+                    cap_copy(cp + MOSS_HIP_CAP_LN2, act, kHidden);
+                    __syncthreads();
+                }
+                quant_act_lds_k<kHidden>(act, da);
                 __syncthreads();
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_LN2_Q, act, kHidden);
@@ -665,7 +672,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 return;
             }
             if constexpr (A8) {
-                quant_act_lds(act, da, kFF);
+                quant_act_lds_k<kFF>(act, da);
                 __syncthreads();
                 if (b == 0 && cap) {
                     cap_copy(cap + MOSS_HIP_CAP_H_Q, act, kFF);

@@ -174,8 +174,9 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                     if (cp) {
                         cap_copy(cp + MOSS_HIP_CAP_XIN, xm, kHidden);
                         cap_copy(cp + MOSS_HIP_CAP_LN1, act, kHidden);
+                        __syncthreads();  // before the quantiser rewrites runs other threads copy
                     }
-                    quant_act_lds(act, da, kHidden);
+                    quant_act_lds_k<kHidden>(act, da);
                     __syncthreads();
                     if (cp) {
                         cap_copy(cp + MOSS_HIP_CAP_LN1_Q, act, kHidden);
@@ -355,8 +356,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 eres = q8x4_elem(aemb_in, kHidden / 32, __float_as_int(act[kHidden]), r);
             if constexpr (A8) {  // act[0, 768) only: the code at act[kHidden] stays
                 float *cp = b == 0 ? cap : nullptr;
-                if (cp) cap_copy(cp + MOSS_HIP_CAP_ATT, act, kHidden);
-                quant_act_lds(act, da, kHidden);
+                if (cp) {  // a barrier before the quantiser rewrites runs other threads copy
+                    cap_copy(cp + MOSS_HIP_CAP_ATT, act, kHidden);
+                    __syncthreads();
+                }
+                quant_act_lds_k<kHidden>(act, da);
                 __syncthreads();
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_ATT_Q, act, kHidden);
@@ -398,8 +402,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             __syncthreads();
             if constexpr (A8) {
                 float *cp = b == 0 ? cap : nullptr;
-                if (cp) cap_copy(cp + MOSS_HIP_CAP_LN2, act, kHidden);
-                quant_act_lds(act, da, kHidden);
+                if (cp) {  // a barrier before the quantiser rewrites runs other threads copy
+                    cap_copy(cp + MOSS_HIP_CAP_LN2, act, kHidden);
+                    __syncthreads();
+                }
+                quant_act_lds_k<kHidden>(act, da);
                 __syncthreads();
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_LN2_Q, act, kHidden);
@@ -428,7 +435,7 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
                 return;
             }
             if constexpr (A8) {
-                quant_act_lds(act, da, kFF);
+                quant_act_lds_k<kFF>(act, da);
                 __syncthreads();
                 if (b == 0 && cap) {
                     cap_copy(cap + MOSS_HIP_CAP_H_Q, act, kFF);
@@ -472,8 +479,11 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             __syncthreads();
             if constexpr (A8) {
                 float *cp = b == 0 ? cap : nullptr;
-                if (cp) cap_copy(cp + MOSS_HIP_CAP_LNF, act, kHidden);
-                quant_act_lds(act, da, kHidden);
+                if (cp) {  // a barrier before the quantiser rewrites runs other threads copy
+                    cap_copy(cp + MOSS_HIP_CAP_LNF, act, kHidden);
+                    __syncthreads();
+                }
+                quant_act_lds_k<kHidden>(act, da);
                 __syncthreads();
                 if (cp) {
                     cap_copy(cp + MOSS_HIP_CAP_LNF_Q, act, kHidden);

@@ -66,9 +66,67 @@ __device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1
 // The W8A8 activation (quantize_row_q8_0_scaled, reference csrc/src/quant.cpp:28-54,
 // via quantize_activation, quant.cpp:45) in place: act[0, K) becomes its int8 values
 // (as floats, exact) and da[K / 32] the fp32 block scales d = amax / 127.  Called
-// by all 256 threads of the workgroup between two barriers; K % 256 == 0, so each
-// block of 32 values is 32 consecutive lanes of one wave.
+// by all 256 threads of the workgroup between two barriers; K % 256 == 0.
+//
+// For a K known at compile time: quant_block32's arithmetic on runs of 8 consecutive values
+// (4 threads per block of 32; thread t takes runs t, t + 256, ...), in registers: a block's
+// amax from the run's 8 values and two lane exchanges (every lane of the 4 ends with it),
+// then d = amax / 127 and 1 / d in those 4 lanes (not in all 32 lanes of the block), then
+// the 8 values scaled and written back.  No barrier inside: the caller's barriers before
+// and after order it, and a copy of act made just before it (the capture) needs a barrier
+// of its own.  A stage's quantiser measured 0.7 -> ~0.2 us at K = 768 and 2.6 -> ~0.5 us at
+// K = 3072 against the loop form below (an LDS round trip per value, 5 exchanges and 2
+// divisions per value).
+template <int K>
+__device__ __forceinline__ void quant_act_lds_k(float *act, float *da) {
+#pragma clang fp contract(off)
+    static_assert(K % 256 == 0, "whole waves");
+    constexpr int R = K / 8, N = (R + 255) / 256;  // runs of 8, runs per thread
+    const int t = tix();
+    float4 x[N][2];
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+        if (t + 256 * j < R) {
+            const float4 *p = (const float4 *)(act + 8 * (t + 256 * j));
+            x[j][0] = p[0];
+            x[j][1] = p[1];
+        }
+    auto qv = [](float v, float id) {
+        int q = (int)rintf(v * id);
+        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+        return (float)q;
+    };
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const int g = t + 256 * j;
+        // R is a multiple of 4: the run test holds for whole 4-lane groups, so the
+        // exchanges stay inside active groups
+        if (g < R) {
+            float amax = fmaxf(fmaxf(fabsf(x[j][0].x), fabsf(x[j][0].y)), fmaxf(fabsf(x[j][0].z), fabsf(x[j][0].w)));
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[j][1].x), fabsf(x[j][1].y)), fmaxf(fabsf(x[j][1].z), fabsf(x[j][1].w))));
+            amax = fmaxf(amax, xshfl<1>(amax));
+            amax = fmaxf(amax, xshfl<2>(amax));
+            const float d = amax / 127.0f;
+            const float id = d > 0.0f ? 1.0f / d : 0.0f;
+            float4 *p = (float4 *)(act + 8 * g);
+            p[0] = make_float4(qv(x[j][0].x, id), qv(x[j][0].y, id), qv(x[j][0].z, id), qv(x[j][0].w, id));
+            p[1] = make_float4(qv(x[j][1].x, id), qv(x[j][1].y, id), qv(x[j][1].z, id), qv(x[j][1].w, id));
+            if ((g & 3) == 0) da[g >> 2] = d;
+        }
+    }
+}
+
+// Any K (the GEMV operators): the compile-time forms for the model's widths, else a loop
+// of quant_block32.  K is the same for every thread of the workgroup.
 __device__ __forceinline__ void quant_act_lds(float *act, float *da, int K) {
+    if (K == 768) {
+        quant_act_lds_k<768>(act, da);
+        return;
+    }
+    if (K == 3072) {
+        quant_act_lds_k<3072>(act, da);
+        return;
+    }
     for (int i = tix(); i < K; i += 256) {
         float d;
         const int q = quant_block32(act[i], &d);
@@ -78,9 +136,8 @@ __device__ __forceinline__ void quant_act_lds(float *act, float *da, int K) {
 }
 
 // Quantiser capture (tests only, moss_hip_llm_capture): the workgroup's 256 threads
-// copy n values of an LDS vector to dst.  A thread reads only the elements
-// quant_act_lds gives it (i = tix() + 256 k), so a copy made just before the
-// quantiser needs no barrier of its own.
+// copy n values of an LDS vector to dst.  A copy made just before quant_act_lds_k needs a
+// barrier between them (the quantiser rewrites runs other threads copy).
 __device__ __forceinline__ void cap_copy(float *dst, const float *src, int n) {
     for (int i = tix(); i < n; i += 256) dst[i] = src[i];
 }
