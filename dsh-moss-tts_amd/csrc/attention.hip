@@ -102,7 +102,9 @@ struct SpanRaw {
 // NT: the K/V spans are read non-temporally (the batch engine's paged caches)
 template <int KV, int NW, bool PART, bool CHUNK = false, bool NT = false>
 __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
-    __shared__ float sc[NW][64];
+    // a span's softmax weights, key k at (k % 4) * 16 + k / 4: the 16 keys pg + 4t a lane's
+    // value pass takes are then 16 consecutive floats (four 16-byte LDS reads)
+    __shared__ __attribute__((aligned(16))) float sc[NW][64];
     __shared__ float4 po[NW][16];
     __shared__ float pm[NW], pl[NW];
     // PART: one 64-key span per workgroup (blockIdx.y), one row
@@ -176,15 +178,18 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_kernel(AttnArgs a) {
         o.y *= rescale;
         o.z *= rescale;
         o.w *= rescale;
-        sc[w][kl] = e;
+        sc[w][(kl & 3) * 16 + (kl >> 2)] = e;
         // sc[w][*] is written and read by different lanes of this one wave
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         __builtin_amdgcn_wave_barrier();
+        float ev[16];
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) *(float4 *)&ev[4 * t4] = *(const float4 *)&sc[w][pg * 16 + 4 * t4];
         // o[d] += sum_p e_p v_p[d]: lane = 16*pg + dg covers dims 4dg..4dg+3 of every 4th key
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             const float4 v = raw.vf(t);
-            const float ei = sc[w][pg + 4 * t];
+            const float ei = ev[t];
             o.x = fmaf(ei, v.x, o.x);
             o.y = fmaf(ei, v.y, o.y);
             o.z = fmaf(ei, v.z, o.z);

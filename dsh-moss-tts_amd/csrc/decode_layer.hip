@@ -170,7 +170,9 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
     __shared__ float pbuf[kMaxUnits * 66];     // gathered attention partials
     __shared__ float qkn[3 * kHeadDim];        // q, k, v of the new position for this head
     __shared__ float hw[kHeads][kLayerMaxQuarters + 1];  // per-head merge weights and denominator
-    __shared__ float sc[4][kAttnSpansPerWave<KV>][64];
+    // a span's softmax weights, key k at (k % 4) * 16 + k / 4: the 16 keys pg + 4q a lane's
+    // value pass takes are then 16 consecutive floats (four 16-byte LDS reads)
+    __shared__ __attribute__((aligned(16))) float sc[4][kAttnSpansPerWave<KV>][64];
     __shared__ float4 po[4][16];
     __shared__ float pm[4], pl[4];
     __shared__ float part[4][4];
@@ -228,7 +230,9 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
         // W8A8 quantiser capture of this block (tests only; null in the library's own use)
         float *const cap = A8 && g.cap ? g.cap + (size_t)layer * MOSS_HIP_CAP_STEP : nullptr;
         // per-block copies of the indices: nothing derived from them is held across blocks
-        const int t = tix(), wave = t >> 6, lane = t & 63;
+        // the wave index as a wave-uniform (scalar) value, so that per-span and per-wave
+        // conditions below are branches rather than selects executed by every wave
+        const int t = tix(), wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
         const int b = bix();
 
         // ---- loads that do not depend on this block's input, issued before
@@ -414,7 +418,7 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 for (int i = 0; i < NS; ++i) {
                     const float e = kl < cnt[i] ? expf(dot[i] - m_new) : 0.0f;
                     esum += e;
-                    sc[wave][i][kl] = e;
+                    sc[wave][i][(kl & 3) * 16 + (kl >> 2)] = e;
                 }
                 l = l * rescale + wave_sum(esum);
                 STAGE_TS(21);
@@ -426,10 +430,14 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 for (int i = 0; i < NS; ++i) {
                     os[i] = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (cnt[i] == 0) continue;
+                    float ev[16];
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4)
+                        *(float4 *)&ev[4 * q4] = *(const float4 *)&sc[wave][i][pg * 16 + 4 * q4];
 #pragma unroll
                     for (int q = 0; q < 16; ++q) {
                         const float4 v = raw4<KV>(raw[i].v[q]);
-                        const float ei = sc[wave][i][pg + 4 * q];
+                        const float ei = ev[q];
                         os[i].x = fmaf(ei, v.x, os[i].x);
                         os[i].y = fmaf(ei, v.y, os[i].y);
                         os[i].z = fmaf(ei, v.z, os[i].z);
