@@ -83,30 +83,36 @@ def test_global_step_vs_oracle(torch_gpu, oracle, prefilled, kv32, graphs, per_o
     g.close()
 
 
+@pytest.mark.parametrize("kv32", [False, True])
 @pytest.mark.parametrize("per_op", [False, True])
-@pytest.mark.parametrize("ctx", [0, 1, 63, 64, 65, 255, 256, 300, 765, 766, 767, 1021])
-def test_global_step_long_context(torch_gpu, oracle, golden_model, ctx, per_op):
+@pytest.mark.parametrize("ctx", [0, 1, 63, 64, 65, 255, 256, 300, 511, 765, 766, 767, 1021])
+def test_global_step_long_context(torch_gpu, oracle, golden_model, ctx, per_op, kv32):
     """Split-KV attention at span boundaries (64 keys) and at the boundaries of
     the fused kernel's attention workgroups (256 keys), up to the last positions:
     per-span workgroups merged in the proj prologue (per_op) and 4-span
     workgroups merged in the fused block launch.  ctx 766 / 767 step through
     768 keys (12 spans: one workgroup per head, its last span full) to 769 (13
     spans: two workgroups per head, merged by proj); 1021 ends at 1023 keys of
-    a 1024-position cache (the default cache holds 768)."""
+    a 1024-position cache (the default cache holds 768).  With an fp32 cache a
+    wave holds one span, so the fused launch adds a workgroup per head every
+    256 keys (ctx 255, 511, 767 step across 256, 512, 768)."""
     blob, _ = golden_model
     rng = np.random.default_rng(ctx)
-    k = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
-    v = rng.standard_normal((12, ctx, 768), dtype=np.float32).astype(np.float16).astype(np.float32)
+    k = rng.standard_normal((12, ctx, 768), dtype=np.float32)
+    v = rng.standard_normal((12, ctx, 768), dtype=np.float32)
+    if not kv32:
+        k, v = k.astype(np.float16).astype(np.float32), v.astype(np.float16).astype(np.float32)
     h = rng.standard_normal(768, dtype=np.float32)
     cap = 1024 if ctx + 2 > 768 else 0  # 0: the default capacity
-    print(f"global step at ctx {ctx} per_op={per_op} max_ctx={cap}", flush=True)
-    g = HipLLM(blob, per_op=per_op, max_ctx=cap)
+    print(f"global step at ctx {ctx} per_op={per_op} kv32={kv32} max_ctx={cap}", flush=True)
+    g = HipLLM(blob, per_op=per_op, max_ctx=cap, kv_fp32=kv32)
+    extra = {"max_ctx": cap} if cap else {}
     if ctx:
         g.kv_import(k, v, h)
-        m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=True, **({"max_ctx": cap} if cap else {}))
+        m = _oracle_from_state(oracle, blob, k, v, h, kv_f16=not kv32, **extra)
     else:  # the first position of an empty cache
         g.set_hidden(h)
-        m = oracle.model(blob, kv_f16=True)
+        m = oracle.model(blob, kv_f16=not kv32, **extra)
         m.set_hidden(h)
     for step in range(2):
         row = np.array([mf.SLOT] + list(rng.integers(0, 1024, 16)), np.int32)
