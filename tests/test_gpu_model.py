@@ -267,6 +267,44 @@ def test_prefill_vs_oracle(torch_gpu, oracle, golden_model, a16):
     gm.close()
 
 
+def test_prefill_clamps_and_truncates(torch_gpu, oracle, golden_model):
+    """The reference's prefill limits (llm.cpp:327-331): start clamped to [0, max_ctx],
+    rows past the cache dropped, nothing done for no rows; and generate stops at a
+    full cache (llm.cpp:643-644).  A 96-position cache, A16 prefill, against the
+    oracle, which restates the same rules."""
+    blob, _ = golden_model
+    cap = 96
+    rng = np.random.default_rng(31)
+    rows = mf.text_rows(rng.integers(0, mf.VOCAB, 70))
+    rows[5:25, 1:] = rng.integers(0, 1024, (20, 16))
+    gm = HipLLM(blob, max_ctx=cap, kv_fp32=True, prefill_a16=True)
+    m = oracle.model(blob, max_ctx=cap)
+    print("prefill: empty, negative start, past the cache", flush=True)
+    gm.prefill(rows[:0])
+    assert gm.position == 0
+    gm.prefill(rows[:40], start=-5)  # start 0
+    m.prefill(rows[:40], start=-5, a16=True)
+    assert gm.position == m.position == 40
+    gm.prefill(rows[40:], start=cap + 3)  # start clamped to max_ctx: nothing fits
+    m.prefill(rows[40:], start=cap + 3, a16=True)
+    assert gm.position == m.position == 40
+    assert max_rel(gm.hidden(), m.hidden()) <= TOL
+    print("prefill: 70 rows at 40, 56 fit", flush=True)
+    gm.prefill(rows, start=40)
+    m.prefill(rows, start=40, a16=True)
+    assert gm.position == m.position == cap
+    assert max_rel(gm.hidden(), m.hidden()) <= TOL
+    gk, gv = gm.kv_export(cap)
+    ok, ov = m.kv_export(cap)
+    assert max_rel(gk, ok) <= TOL and max_rel(gv, ov) <= TOL
+    print("generate on a full cache", flush=True)
+    out = gm.generate(4, SampleParams.make(greedy=True, min_frames=4))
+    ref = m.generate(4, OSP.make(greedy=True, min_frames=4))
+    assert len(out["rows"]) == len(ref["rows"]) == 0
+    assert gm.position == cap
+    gm.close()
+
+
 @pytest.mark.parametrize("a16", [False, True])
 def test_prefill_tiled_weights_bit_identical(torch_gpu, golden_model, monkeypatch, a16):
     """The prefill GEMMs read a copy of the matrices in the matrix-core order made at load;
