@@ -429,21 +429,27 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             gs.prefetch(a.fc_out_w, b);
             const int r = gs.row();
             const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
-            const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
-            if (sync_failed(!ok, &wait_failed)) {
-                if (t == 0) atomicOr(a.err, 1u);
-                return;
-            }
-            if constexpr (A8) {
+            if constexpr (A8) {  // the quantiser's runs span the K slices: the whole vector first
+                const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
+                if (sync_failed(!ok, &wait_failed)) {
+                    if (t == 0) atomicOr(a.err, 1u);
+                    return;
+                }
                 quant_act_lds_k<kFF>(act, da);
                 __syncthreads();
                 if (b == 0 && cap) {
                     cap_copy(cap + MOSS_HIP_CAP_H_Q, act, kFF);
                     cap_copy(cap + MOSS_HIP_CAP_H_D, da, kFF / 32);
                 }
+            } else {
+                ll_gather_slice<kFF>(LL + kLH, tag, act, budget, &wait_failed);
             }
             STAGE_TS(7);
             const float yv = gs.template dot<A8>(act, part, da);
+            if (!A8 && *(volatile int *)&wait_failed) {  // read after the dot's barriers
+                if (t == 0) atomicOr(a.err, 1u);
+                return;
+            }
             if (gs.storer()) {
                 const float xo = xm[r] + (yv + eb);  // llm.cpp:245
                 a.x_out[r] = xo;

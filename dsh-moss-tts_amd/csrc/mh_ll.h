@@ -109,6 +109,22 @@ __device__ __forceinline__ bool sync_failed(bool failed, volatile int *flag) {
     return *flag != 0;
 }
 
+// The gather before a row dot split in K over the 4 waves of a workgroup (GemvStage<4, NB, N>):
+// wave w reads only K slice w, [w N / 4, (w + 1) N / 4), of the activation, so it gathers that
+// slice itself and starts its dot when the slice is in, with no workgroup barrier in between.
+// A failed wait sets *flag, which the caller tests after the dot's barriers.
+template <int N>
+__device__ __forceinline__ void ll_gather_slice(const uint64_t *src, uint32_t tag, float *dst, int &budget,
+                                                volatile int *flag) {
+    constexpr int S = N / 4;
+    static_assert(S % 64 == 0 && S / 64 <= 32, "whole rounds of 64 lanes");
+    const int w = __builtin_amdgcn_readfirstlane(tix() >> 6), lane = tix() & 63;
+    if (!ll_gather_by<S / 64, 64>(src + S * w, S, tag, dst + S * w, budget, lane)) *flag = 1;
+    // the slice's LDS writes before any lane of this wave reads them
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 // One word per thread (threads with active == false return true at once).
 __device__ __forceinline__ bool ll_wait1(const uint64_t *src, bool active, uint32_t tag, float *dst, int &budget) {
     if (!active) return true;
