@@ -117,7 +117,7 @@ template <int N>
 __device__ __forceinline__ void ll_gather_slice(const uint64_t *src, uint32_t tag, float *dst, int &budget,
                                                 volatile int *flag) {
     constexpr int S = N / 4;
-    static_assert(S % 64 == 0 && S / 64 <= 32, "whole rounds of 64 lanes");
+    static_assert(S % 64 == 0 && S / 64 <= 32, "a whole number of words per lane, at most 32");
     const int w = __builtin_amdgcn_readfirstlane(tix() >> 6), lane = tix() & 63;
     if (!ll_gather_by<S / 64, 64>(src + S * w, S, tag, dst + S * w, budget, lane)) *flag = 1;
     // the slice's LDS writes before any lane of this wave reads them
