@@ -524,6 +524,11 @@ __global__ __launch_bounds__(256) void decode_global_kernel(GlobalArgs g) {
                 else
                     eres = xin[r];
             }
+            // workgroups without attention work wait ~0.85 us (2,048 clocks) before polling for
+            // its output when an attention wave has more than one span (over 1.5 us of work
+            // after its query arrives): their polls would share the coherent path with the
+            // query hand-off meanwhile (global step 1.5-1.8 us shorter at ctx 512..767)
+            if (!attn_wg && spans > 4) __builtin_amdgcn_s_sleep(32);
             if (Qs == 1) {  // the heads' outputs, ready to use
                 const bool ok = ll_gather<3>(LL + kLLA, kHidden, tag, act, budget);
                 if (sync_failed(!ok, &wait_failed)) {
