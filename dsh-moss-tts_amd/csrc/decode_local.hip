@@ -429,24 +429,21 @@ __global__ __launch_bounds__(256) void decode_local_kernel(LocalArgs a) {
             gs.prefetch(a.fc_out_w, b);
             const int r = gs.row();
             const float eb = gs.storer() ? a.fc_out_b[r] : 0.0f;
-            if constexpr (A8) {  // the quantiser's runs span the K slices: the whole vector first
-                const bool ok = ll_gather<kFF / 256>(LL + kLH, kFF, tag, act, budget);
-                if (sync_failed(!ok, &wait_failed)) {
-                    if (t == 0) atomicOr(a.err, 1u);
-                    return;
-                }
-                quant_act_lds_k<kFF>(act, da);
-                __syncthreads();
+            ll_gather_slice<kFF>(LL + kLH, tag, act, budget, &wait_failed);
+            if constexpr (A8) {  // the slice's 24 blocks, quantised by the wave that reads them
+                const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+                quant_act_lds_k<kFF / 4, 64>(act + (kFF / 4) * w, da + (kFF / 128) * w, t & 63);
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
                 if (b == 0 && cap) {
+                    __syncthreads();
                     cap_copy(cap + MOSS_HIP_CAP_H_Q, act, kFF);
                     cap_copy(cap + MOSS_HIP_CAP_H_D, da, kFF / 32);
                 }
-            } else {
-                ll_gather_slice<kFF>(LL + kLH, tag, act, budget, &wait_failed);
             }
             STAGE_TS(7);
             const float yv = gs.template dot<A8>(act, part, da);
-            if (!A8 && *(volatile int *)&wait_failed) {  // read after the dot's barriers
+            if (*(volatile int *)&wait_failed) {  // read after the dot's barriers
                 if (t == 0) atomicOr(a.err, 1u);
                 return;
             }

@@ -77,17 +77,18 @@ __device__ __forceinline__ float dot_batch(const float *act, int first_b, int b1
 // of its own.  A stage's quantiser measured 0.7 -> ~0.2 us at K = 768 and 2.6 -> ~0.5 us at
 // K = 3072 against the loop form below (an LDS round trip per value, 5 exchanges and 2
 // divisions per value).
-template <int K>
-__device__ __forceinline__ void quant_act_lds_k(float *act, float *da) {
+// NT threads (t = 0 .. NT - 1) share the vector: the whole workgroup by default, one
+// wave (NT = 64, t = its lane) for a K slice that wave alone reads.
+template <int K, int NT = 256>
+__device__ __forceinline__ void quant_act_lds_k(float *act, float *da, int t = tix()) {
 #pragma clang fp contract(off)
-    static_assert(K % 256 == 0, "whole waves");
-    constexpr int R = K / 8, N = (R + 255) / 256;  // runs of 8, runs per thread
-    const int t = tix();
+    static_assert(K % NT == 0 && NT % 64 == 0, "whole waves");
+    constexpr int R = K / 8, N = (R + NT - 1) / NT;  // runs of 8, runs per thread
     float4 x[N][2];
 #pragma unroll
     for (int j = 0; j < N; ++j)
-        if (t + 256 * j < R) {
-            const float4 *p = (const float4 *)(act + 8 * (t + 256 * j));
+        if (t + NT * j < R) {
+            const float4 *p = (const float4 *)(act + 8 * (t + NT * j));
             x[j][0] = p[0];
             x[j][1] = p[1];
         }
@@ -98,7 +99,7 @@ __device__ __forceinline__ void quant_act_lds_k(float *act, float *da) {
     };
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-        const int g = t + 256 * j;
+        const int g = t + NT * j;
         // R is a multiple of 4: the run test holds for whole 4-lane groups, so the
         // exchanges stay inside active groups
         if (g < R) {
